@@ -1,0 +1,296 @@
+"""Benchmark of the paged attention path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--no-cpu] [--only cfg2]
+
+A "step" is one pass of the path over one batch of synthetic input:
+  decode  (cfg2/cfg4/cfg5): store_kvcache of the new token + paged decode
+  prefill (cfg3):           store_kvcache of the new tokens + causal varlen prefill
+Inputs are resident in HBM before timing starts.  Decode steps alternate
+between two independent KV pools (each larger than the 256 MB MALL), so no
+step re-reads KV the previous step left in the Infinity Cache.
+
+The headline (``value``) is cfg2's algorithmic HBM bandwidth in GB/s; cfg3's
+TFLOP/s and the other decode configurations are reported under ``extra``.
+``roofline`` covers the dominant kernel of the headline workload (paged
+decode: main kernel + split-K merge), timed with HIP events on the stream
+the kernels run on.  ``cpu_baseline`` times the CPU restatement of the path
+(torch gather + repeat_interleave + scaled_dot_product_attention) on the
+host cores for a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def _events_time(fn, steps, warmup):
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(warmup + i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per step
+
+
+def _second_pool(case):
+    import torch
+    k2 = torch.empty_like(case["k_cache"])
+    v2 = torch.empty_like(case["v_cache"])
+    k2.view(torch.uint8).copy_(case["k_cache"].view(torch.uint8).roll(1, 0))
+    v2.view(torch.uint8).copy_(case["v_cache"].view(torch.uint8).roll(1, 0))
+    return k2, v2
+
+
+def bench_decode(name, steps, warmup, seed=0):
+    import torch
+    from nano_qwen_amd import kernels
+    from oracle.inputs import decode_bytes, decode_flops, make_decode_case
+
+    dev = torch.device("cuda:0")
+    case = make_decode_case(name, seed=seed, device=dev)
+    pools = [(case["k_cache"], case["v_cache"]), _second_pool(case)]
+    out = torch.empty(case["batch"], 1, case["hq"], case["d"], dtype=case["q"].dtype, device=dev)
+    q = case["q"].unsqueeze(1)
+
+    def step(i):
+        kc, vc = pools[i % 2]
+        kernels.store_kvcache(case["k_new"], case["v_new"], kc, vc, case["slot_mapping"], case["k_scale"],
+                              case["v_scale"])
+        kernels.paged_decode(q, kc, vc, case["context_lens"], case["block_tables"], case["scale"],
+                             case["k_scale"], case["v_scale"], out=out)
+
+    def attn_only(i):
+        kc, vc = pools[i % 2]
+        kernels.paged_decode(q, kc, vc, case["context_lens"], case["block_tables"], case["scale"],
+                             case["k_scale"], case["v_scale"], out=out)
+
+    ms = _events_time(step, steps, warmup)
+    ms_attn = _events_time(attn_only, steps, warmup)
+    nbytes = decode_bytes(case)
+    store_bytes = 2 * case["batch"] * case["hkv"] * case["d"] * (case["q"].element_size() +
+                                                                 case["k_cache"].element_size())
+    attn_bytes = nbytes - store_bytes
+    W = case["block_tables"].shape[1]
+    ns, st = kernels.decode_plan(case["batch"], case["hq"], case["hkv"], W, case["block_size"],
+                                 case["k_cache"].dtype)
+    res = dict(
+        ms_per_step=ms, gbs=nbytes / (ms * 1e-3) / 1e9, tokens_per_s=case["batch"] / (ms * 1e-3),
+        hbm_frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, bytes_per_step=nbytes,
+        tflops=decode_flops(case) / (ms * 1e-3) / 1e12,
+        attn_ms=ms_attn, attn_gbs=attn_bytes / (ms_attn * 1e-3) / 1e9, attn_bytes=attn_bytes,
+        splits=ns, split_tokens=st, batch=case["batch"], hq=case["hq"], hkv=case["hkv"],
+        kv_dtype=str(case["k_cache"].dtype).replace("torch.", ""),
+        sum_ctx=int(case["context_lens"].sum()))
+    return res, case
+
+
+def bench_prefill(name, steps, warmup, seed=0):
+    import torch
+    from nano_qwen_amd import kernels
+    from oracle.inputs import make_prefill_case, prefill_bytes, prefill_flops
+
+    dev = torch.device("cuda:0")
+    case = make_prefill_case(name, seed=seed, device=dev)
+    out = torch.empty_like(case["q"])
+
+    def attn(i):
+        kernels.varlen_prefill(case["q"], case["k_cache"], case["v_cache"], case["cu_seqlens_q"],
+                               case["cu_seqlens_k"], case["max_seqlen_q"], case["max_seqlen_k"], case["scale"],
+                               causal=True, block_table=case["block_tables"], out=out)
+
+    def step(i):
+        kernels.store_kvcache(case["k_new"], case["v_new"], case["k_cache"], case["v_cache"],
+                              case["slot_mapping"])
+        attn(i)
+
+    ms = _events_time(step, steps, warmup)
+    ms_attn = _events_time(attn, steps, warmup)
+    fl = prefill_flops(case)
+    return dict(ms_per_step=ms, tflops=fl / (ms * 1e-3) / 1e12, attn_ms=ms_attn,
+                attn_tflops=fl / (ms_attn * 1e-3) / 1e12, mfma_frac=fl / (ms_attn * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                flops=fl, tokens_per_s=sum(case["lq"]) / (ms * 1e-3), total_q=sum(case["lq"]),
+                gbs=prefill_bytes(case) / (ms * 1e-3) / 1e9), case
+
+
+def cpu_baseline_decode(case, n_seqs=8, reps=5):
+    """Median wall time of the CPU path on the first n_seqs sequences."""
+    import torch
+    from oracle import sdpa_path
+    from oracle.inputs import decode_bytes
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    ids = list(range(n_seqs))
+    bs = case["block_size"]
+    ctx = case["context_lens"][:n_seqs].cpu()
+    nblk = [(int(c) + bs - 1) // bs for c in ctx]
+    blocks = torch.cat([case["block_tables"][i, :nblk[i]].long() for i in ids])
+    kc = case["k_cache"].index_select(0, blocks.to(case["k_cache"].device)).cpu()
+    vc = case["v_cache"].index_select(0, blocks.to(case["v_cache"].device)).cpu()
+    bt = torch.full((n_seqs, max(nblk)), -1, dtype=torch.int32)
+    off = 0
+    for i in ids:
+        bt[i, :nblk[i]] = torch.arange(off, off + nblk[i], dtype=torch.int32)
+        off += nblk[i]
+    slot = torch.tensor([int(bt[i, (int(ctx[i]) - 1) // bs]) * bs + (int(ctx[i]) - 1) % bs for i in ids],
+                        dtype=torch.int32)
+    q = case["q"][:n_seqs].cpu()
+    kn, vn = case["k_new"][:n_seqs].cpu(), case["v_new"][:n_seqs].cpu()
+    ks = None if case["k_scale"] is None else case["k_scale"].cpu()
+    vs = None if case["v_scale"] is None else case["v_scale"].cpu()
+
+    def run():
+        sdpa_path.store_kvcache(kn, vn, kc, vc, slot, ks, vs)
+        sdpa_path.paged_decode(q, kc, vc, bt, ctx, case["scale"], ks, vs)
+
+    run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    sub = dict(case, batch=n_seqs, context_lens=ctx, q=q)
+    nbytes = decode_bytes(sub)
+    return dict(value=nbytes / t / 1e9, unit="GB/s", cores=cores, kind="port",
+                sample=f"{case['name']} first {n_seqs} of {case['batch']} sequences (sum ctx "
+                       f"{int(ctx.sum())}), store + decode, torch {torch.__version__} CPU, median of {reps}",
+                seconds=t, cpu=platform.processor() or platform.machine())
+
+
+def cpu_baseline_prefill(case, n_seqs=2, reps=3):
+    import torch
+    from oracle import sdpa_path
+    from oracle.inputs import prefill_flops
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    ids = list(range(n_seqs))
+    lq, lk = case["lq"][:n_seqs], case["lk"][:n_seqs]
+    cq = torch.tensor([0] + list(torch.tensor(lq).cumsum(0).tolist()), dtype=torch.int32)
+    ck = torch.tensor([0] + list(torch.tensor(lk).cumsum(0).tolist()), dtype=torch.int32)
+    bs = case["block_size"]
+    nblk = [(x + bs - 1) // bs for x in lk]
+    blocks = torch.cat([case["block_tables"][i, :nblk[i]].long() for i in ids])
+    kc = case["k_cache"].index_select(0, blocks.to(case["k_cache"].device)).cpu()
+    vc = case["v_cache"].index_select(0, blocks.to(case["v_cache"].device)).cpu()
+    bt = torch.full((n_seqs, max(nblk)), -1, dtype=torch.int32)
+    off = 0
+    for i in ids:
+        bt[i, :nblk[i]] = torch.arange(off, off + nblk[i], dtype=torch.int32)
+        off += nblk[i]
+    q = case["q"][: int(cq[-1])].cpu()
+
+    def run():
+        sdpa_path.varlen_prefill(q, kc, vc, cq, ck, case["scale"], block_tables=bt)
+
+    run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    fl = prefill_flops(dict(case, lq=lq, lk=lk))
+    return dict(value=fl / t / 1e12, unit="TFLOP/s", cores=cores, kind="port",
+                sample=f"{case['name']} first {n_seqs} of {case['nseq']} sequences (Lq {lq}, Lk {lk}), "
+                       f"attention only, median of {reps}", seconds=t)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default=None, help="run one config (cfg2|cfg3|cfg4|cfg5)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures the paged attention path on ONE GPU; "
+              "multi-GPU runs are not part of it (see DESIGN.md for how the path shards)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from nano_qwen_amd._lib import lib
+    lib()
+    torch.cuda.set_device(0)
+
+    extra = {}
+    head = None
+    todo = [args.only] if args.only else ["cfg2", "cfg3", "cfg4", "cfg5"]
+    cpu = None
+    for name in todo:
+        print(f"[bench] {name} ...", file=sys.stderr, flush=True)
+        if name == "cfg3":
+            r, case = bench_prefill(name, args.steps, args.warmup)
+            if not args.no_cpu:
+                r["cpu_baseline"] = cpu_baseline_prefill(case)
+        else:
+            r, case = bench_decode(name, args.steps, args.warmup)
+            if name == "cfg2":
+                head = r
+                if not args.no_cpu:
+                    cpu = cpu_baseline_decode(case)
+        extra[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+        print(f"[bench] {name}: {json.dumps(extra[name])}", file=sys.stderr, flush=True)
+        del case
+        torch.cuda.empty_cache()
+
+    if head is None:  # --only on a non-headline config: report it as the line
+        name = todo[0]
+        r = extra[name]
+        head_ms = r["ms_per_step"]
+        value = r.get("gbs") if name != "cfg3" else r["tflops"]
+        unit = "GB/s" if name != "cfg3" else "TFLOP/s"
+    else:
+        head_ms, value, unit = head["ms_per_step"], head["gbs"], "GB/s"
+    line = {
+        "metric": "decode attn HBM GB/s (% of 8 TB/s) + prefill attn TFLOP/s, Qwen3-8B shape",
+        "value": round(value, 2),
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) K/V pools, random block permutation)",
+        "config": {
+            "workload": "cfg2: Qwen3-8B-shaped bf16 paged decode step (store_kvcache + decode), B=64, "
+                        "ctx U[1024,4096], Hq=32, Hkv=8, D=128, block_size=256",
+            "batch": 64, "num_q_heads": 32, "num_kv_heads": 8, "head_dim": 128, "block_size": 256,
+        },
+    }
+    if head is not None:
+        line["roofline"] = {
+            "bound": "hbm", "kernel": "paged_decode (main + split-K merge)",
+            "achieved": round(head["attn_gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(head["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+            "attn_ms": round(head["attn_ms"], 5), "algorithmic_bytes": head["attn_bytes"],
+        }
+    if "cfg3" in extra:
+        line["prefill_tflops"] = extra["cfg3"]["attn_tflops"]
+        line["prefill_mfma_frac"] = extra["cfg3"]["mfma_frac"]
+    line["cpu_baseline"] = cpu
+    line["extra"] = extra
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

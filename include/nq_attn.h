@@ -1,0 +1,165 @@
+/*
+ * nq_attn.h -- C ABI of the MI355X (gfx950) paged attention library
+ * (libnq_attn.so).
+ *
+ * The library replaces the device work of nano_qwen's paged attention path:
+ * the Triton KV scatter and flash_attn's prefill/decode calls made by
+ * layers/attention.py, and the Triton decode-metadata kernel of
+ * engine/decode_init.py.  All entry points:
+ *
+ *   - take device pointers, plain integers and floats, and a hipStream_t
+ *     passed as `void *` (NULL = the default stream); no torch types;
+ *   - enqueue work asynchronously on that stream: they never allocate, free
+ *     or synchronise, so they may be captured into a HIP graph;
+ *   - return NQ_OK (0) or a negative status; nq_last_error() then returns a
+ *     message for the calling thread.
+ *
+ * Element types are NQ_F32 / NQ_F16 / NQ_BF16 / NQ_FP8_E4M3 (OCP e4m3fn).
+ * Strides are in elements of the tensor's own type.
+ *
+ * KV cache layout (engine/model_runner.py:198): one tensor per layer and
+ * per K/V, [num_blocks, block_size, num_kv_heads, head_dim], contiguous;
+ * cache row `slot` = block * block_size + offset.
+ */
+#ifndef NQ_ATTN_H
+#define NQ_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NQ_ABI_VERSION 1
+
+#define NQ_OK 0
+#define NQ_EINVAL (-1)       /* bad pointer, shape, stride or alignment */
+#define NQ_EUNSUPPORTED (-2) /* dtype / head_dim / block_size not built */
+#define NQ_ELAUNCH (-3)      /* the HIP launch itself failed */
+
+enum nq_dtype { NQ_F32 = 0, NQ_F16 = 1, NQ_BF16 = 2, NQ_FP8_E4M3 = 3 };
+
+/* Version of this ABI (NQ_ABI_VERSION). */
+int nq_abi_version(void);
+
+/* Message for the last non-zero status returned on this thread. */
+const char *nq_last_error(void);
+
+/*
+ * Slot-mapped KV scatter.
+ * Replaces store_kvcache / store_kvcache_kernel (layers/attention.py:10-40).
+ *
+ * For each token i < num_tokens with slot = slot_mapping[i] in
+ * [0, num_slots): copy the num_kv_heads*head_dim elements of key row i
+ * (at key + i*key_row_stride) to k_cache row `slot`, and likewise value ->
+ * v_cache.  slot == -1 (and any slot outside [0, num_slots)) skips the token,
+ * as the reference skips -1 (:23).  key/value rows must be contiguous over
+ * (head, dim) -- the reference asserts stride(1) == head_dim and
+ * stride(-1) == 1 (:36-37).
+ *
+ * in_dtype == cache_dtype: a byte-exact copy.
+ * cache_dtype == NQ_FP8_E4M3 (in_dtype F32/F16/BF16): each element x of kv
+ * head h is stored as e4m3fn(RNE(clamp(float(x) * (1.0f / scale[h]), +-448)))
+ * with k_scale / v_scale float[num_kv_heads] device arrays.
+ */
+int nq_store_kvcache(const void *key, int64_t key_row_stride,
+                     const void *value, int64_t value_row_stride,
+                     void *k_cache, void *v_cache,
+                     const int32_t *slot_mapping, int64_t num_tokens,
+                     int64_t num_slots, int num_kv_heads, int head_dim,
+                     int in_dtype, int cache_dtype,
+                     const float *k_scale, const float *v_scale,
+                     void *stream);
+
+/*
+ * Split-K plan for nq_paged_decode, chosen from host-known shapes only (so
+ * it is fixed under graph capture): fills *num_splits and *split_tokens
+ * (a multiple of 128; split s covers tokens [s*split_tokens, (s+1)*split_tokens)).
+ */
+int nq_decode_plan(int batch, int num_q_heads, int num_kv_heads,
+                   int max_blocks_per_seq, int block_size, int kv_dtype,
+                   int *num_splits, int *split_tokens);
+
+/* Bytes of device workspace nq_paged_decode needs for a plan (0 if one split). */
+int64_t nq_decode_workspace_bytes(int batch, int num_q_heads, int head_dim,
+                                  int num_splits);
+
+/*
+ * Paged decode attention (one query token per sequence).
+ * Replaces flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
+ *   cache_seqlens=context_lens, block_table=block_tables,
+ *   softmax_scale=scale, causal=True)   (layers/attention.py:71-74).
+ *
+ * q   [batch, num_q_heads, head_dim] with strides (q_batch_stride,
+ *     q_head_stride, 1); out likewise.  q and out have type q_dtype
+ *     (F16/BF16).  k_cache/v_cache have type kv_dtype (== q_dtype, or
+ *     NQ_FP8_E4M3 with k_scale/v_scale float[num_kv_heads]).
+ * block_tables [batch, >= max_blocks_per_seq] int32 with row stride
+ * bt_stride; context_lens [batch] int32 counts the cached tokens including
+ * the one just stored.  Query head h reads kv head h / (num_q_heads /
+ * num_kv_heads).  Entries past ceil(context_len / block_size) are never
+ * read; rows with context_len <= 0 produce zeros.
+ * num_splits/split_tokens come from nq_decode_plan; workspace (>=
+ * nq_decode_workspace_bytes, 256-byte aligned) is caller-owned.
+ */
+int nq_paged_decode(const void *q, int64_t q_batch_stride, int64_t q_head_stride,
+                    const void *k_cache, const void *v_cache,
+                    const int32_t *block_tables, int64_t bt_stride,
+                    int max_blocks_per_seq, const int32_t *context_lens,
+                    void *out, int64_t out_batch_stride, int64_t out_head_stride,
+                    int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                    int block_size, int64_t num_blocks, float softmax_scale,
+                    int num_splits, int split_tokens,
+                    void *workspace, int64_t workspace_bytes,
+                    int q_dtype, int kv_dtype,
+                    const float *k_scale, const float *v_scale, void *stream);
+
+/*
+ * Causal varlen prefill attention, optionally over paged K/V.
+ * Replaces flash_attn_varlen_func(q, k, v, cu_seqlens_q=..., cu_seqlens_k=...,
+ *   max_seqlen_q=..., max_seqlen_k=..., softmax_scale=scale, causal=True,
+ *   block_table=block_tables)   (layers/attention.py:64-70).
+ *
+ * q [total_q, num_q_heads, head_dim] (strides q_row_stride, q_head_stride, 1),
+ * out likewise.  Sequence s owns query rows [cu_q[s], cu_q[s+1]) and
+ * Lk = cu_k[s+1]-cu_k[s] keys; query row i (0-based in s) sees keys
+ * j <= i + Lk - Lq (bottom-right causal) when causal != 0, all Lk keys
+ * otherwise.
+ * block_tables == NULL: k/v are packed [total_k, num_kv_heads, head_dim]
+ *   with row stride kv_row_stride; key j of s is row cu_k[s] + j.
+ * block_tables != NULL: k/v are the paged caches; key j of s is cache row
+ *   block_tables[s*bt_stride + j/block_size]*block_size + j%block_size.
+ * kv_dtype == q_dtype (F16/BF16), or NQ_FP8_E4M3 with k_scale/v_scale.
+ */
+int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_head_stride,
+                      const void *k, const void *v, int64_t kv_row_stride,
+                      const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k,
+                      int max_seqlen_q, int max_seqlen_k,
+                      const int32_t *block_tables, int64_t bt_stride,
+                      int max_blocks_per_seq, int64_t num_blocks,
+                      void *out, int64_t out_row_stride, int64_t out_head_stride,
+                      int num_seqs, int num_q_heads, int num_kv_heads,
+                      int head_dim, int block_size, float softmax_scale,
+                      int causal, int q_dtype, int kv_dtype,
+                      const float *k_scale, const float *v_scale, void *stream);
+
+/*
+ * Decode metadata on the device.
+ * Replaces _prepare_decode_kernel (engine/decode_init.py:6-65):
+ *   input_ids[i]    = sampled_token_ids[batch_slots[i]]
+ *   positions[i]    = seq_lens[i] - 1
+ *   context_lens[i] = seq_lens[i]
+ *   slot_mapping[i] = last_block_ids[i]*block_size + (seq_lens[i]-1) % block_size
+ * for i < num_seqs.
+ */
+int nq_prepare_decode(const int64_t *sampled_token_ids, const int64_t *batch_slots,
+                      const int32_t *seq_lens, const int32_t *last_block_ids,
+                      int64_t *input_ids, int64_t *positions,
+                      int32_t *context_lens, int32_t *slot_mapping,
+                      int num_seqs, int block_size, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NQ_ATTN_H */

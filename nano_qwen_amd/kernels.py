@@ -1,0 +1,169 @@
+"""Python entry points of the HIP paged attention kernels.
+
+Thin wrappers over the C ABI (include/nq_attn.h): they check shapes and
+strides, pick dtype codes, pass raw device pointers and torch's current
+stream, and raise ``RuntimeError`` on a non-zero status.  The argument names
+and meanings follow the calls the reference makes:
+
+* ``store_kvcache``   -- layers/attention.py:33-40
+* ``varlen_prefill``  -- flash_attn_varlen_func at layers/attention.py:67-70
+* ``paged_decode``    -- flash_attn_with_kvcache at layers/attention.py:72-74
+* ``prepare_decode``  -- engine/decode_init.py:39-65
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import check, dtype_code, lib, ptr, require_cuda, stream_of
+
+_workspaces: dict[int, torch.Tensor] = {}
+
+
+def store_kvcache(key, value, k_cache, v_cache, slot_mapping, k_scale=None, v_scale=None):
+    """Scatter ``key/value [N, Hkv, D]`` into cache rows ``slot_mapping [N]``.
+
+    Same-dtype caches get a byte-exact copy; a ``float8_e4m3fn`` cache is
+    quantized with ``k_scale/v_scale [Hkv]`` (``x * (1/scale)``, saturate to
+    +-448, round to nearest even).
+    """
+    require_cuda(key, value, k_cache, v_cache, slot_mapping, what="store_kvcache")
+    n, hkv, d = key.shape
+    if slot_mapping.dtype != torch.int32:
+        raise RuntimeError("store_kvcache: slot_mapping must be int32")
+    fp8 = k_cache.dtype == torch.float8_e4m3fn
+    if fp8 and (k_scale is None or v_scale is None):
+        raise RuntimeError("store_kvcache: an fp8 cache needs k_scale and v_scale")
+    if not fp8 and k_cache.dtype != key.dtype:
+        raise RuntimeError(f"store_kvcache: cache dtype {k_cache.dtype} != key dtype {key.dtype}")
+    num_slots = k_cache.numel() // (hkv * d)
+    rc = lib().nq_store_kvcache(
+        ptr(key), key.stride(0), ptr(value), value.stride(0), ptr(k_cache), ptr(v_cache),
+        ptr(slot_mapping), n, num_slots, hkv, d, dtype_code(key.dtype), dtype_code(k_cache.dtype),
+        ptr(k_scale) if fp8 else None, ptr(v_scale) if fp8 else None, stream_of(key))
+    check(rc, "store_kvcache")
+
+
+def decode_plan(batch, num_q_heads, num_kv_heads, max_blocks_per_seq, block_size, kv_dtype):
+    """(num_splits, split_tokens) chosen from host-known shapes only."""
+    ns, st = ctypes.c_int(), ctypes.c_int()
+    rc = lib().nq_decode_plan(batch, num_q_heads, num_kv_heads, max_blocks_per_seq, block_size,
+                              dtype_code(kv_dtype), ctypes.byref(ns), ctypes.byref(st))
+    check(rc, "decode_plan")
+    return ns.value, st.value
+
+
+def decode_workspace(device, nbytes: int) -> torch.Tensor | None:
+    """Persistent, grow-only split-K workspace for ``device``.
+
+    Kept across calls so a captured HIP graph keeps a fixed pointer; growing
+    it inside a capture allocates from the capture's pool, which torch keeps
+    alive with the graph.
+    """
+    if nbytes <= 0:
+        return None
+    idx = torch.device(device).index or 0
+    ws = _workspaces.get(idx)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[idx] = ws
+    return ws
+
+
+def paged_decode(q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale,
+                 k_scale=None, v_scale=None, out=None):
+    """Paged decode attention: ``q [B, 1, Hq, D]`` (or ``[B, Hq, D]``).
+
+    Returns ``out`` shaped like ``q`` (``[B, 1, Hq, D]`` as
+    flash_attn_with_kvcache does).  ``cache_seqlens [B] int32`` counts the
+    cached tokens including the new one; ``block_table [B, W] int32``.
+    """
+    require_cuda(q, k_cache, v_cache, cache_seqlens, block_table, what="paged_decode")
+    q3 = q.squeeze(1) if q.dim() == 4 else q
+    if q3.dim() != 3 or q3.stride(-1) != 1:
+        raise RuntimeError("paged_decode: q must be [B, 1, Hq, D] / [B, Hq, D] with a contiguous last dim")
+    B, hq, d = q3.shape
+    nb, bs, hkv, d2 = k_cache.shape
+    if d2 != d or v_cache.shape != k_cache.shape:
+        raise RuntimeError("paged_decode: cache shape mismatch")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise RuntimeError("paged_decode: caches must be contiguous [num_blocks, block_size, Hkv, D]")
+    if cache_seqlens.dtype != torch.int32 or block_table.dtype != torch.int32:
+        raise RuntimeError("paged_decode: cache_seqlens and block_table must be int32")
+    if block_table.stride(-1) != 1:
+        raise RuntimeError("paged_decode: block_table rows must be contiguous")
+    fp8 = k_cache.dtype == torch.float8_e4m3fn
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    o3 = out.squeeze(1) if out.dim() == 4 else out
+    W = block_table.shape[1]
+    ns, st = decode_plan(B, hq, hkv, W, bs, k_cache.dtype)
+    wsb = lib().nq_decode_workspace_bytes(B, hq, d, ns)
+    ws = decode_workspace(q.device, wsb)
+    rc = lib().nq_paged_decode(
+        ptr(q3), q3.stride(0), q3.stride(1), ptr(k_cache), ptr(v_cache), ptr(block_table),
+        block_table.stride(0), W, ptr(cache_seqlens), ptr(o3), o3.stride(0), o3.stride(1),
+        B, hq, hkv, d, bs, nb, float(softmax_scale), ns, st, ptr(ws), 0 if ws is None else ws.numel(),
+        dtype_code(q.dtype), dtype_code(k_cache.dtype), ptr(k_scale) if fp8 else None,
+        ptr(v_scale) if fp8 else None, stream_of(q))
+    check(rc, "paged_decode")
+    return out
+
+
+def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
+                   causal=True, block_table=None, k_scale=None, v_scale=None, out=None):
+    """Causal varlen attention; ``q [Tq, Hq, D]`` -> ``[Tq, Hq, D]``.
+
+    Without ``block_table``: ``k, v [Tk, Hkv, D]`` packed by ``cu_seqlens_k``.
+    With it: ``k, v`` are the paged caches ``[num_blocks, block_size, Hkv, D]``.
+    """
+    require_cuda(q, k, v, cu_seqlens_q, cu_seqlens_k, block_table, what="varlen_prefill")
+    tq, hq, d = q.shape
+    if q.stride(-1) != 1:
+        raise RuntimeError("varlen_prefill: q needs a contiguous last dim")
+    if cu_seqlens_q.dtype != torch.int32 or cu_seqlens_k.dtype != torch.int32:
+        raise RuntimeError("varlen_prefill: cu_seqlens must be int32")
+    n = cu_seqlens_q.numel() - 1
+    if block_table is None:
+        tk, hkv, d2 = k.shape
+        if k.stride(-1) != 1 or k.stride(1) != d or k.stride(0) != v.stride(0) or v.stride(1) != d:
+            raise RuntimeError("varlen_prefill: packed k/v must be [Tk, Hkv, D] with equal strides")
+        kv_rs, bs, nb, W, bt_stride = k.stride(0), 0, 0, 0, 0
+    else:
+        if block_table.dtype != torch.int32 or block_table.stride(-1) != 1:
+            raise RuntimeError("varlen_prefill: block_table must be int32 with contiguous rows")
+        nb, bs, hkv, d2 = k.shape
+        if not (k.is_contiguous() and v.is_contiguous()):
+            raise RuntimeError("varlen_prefill: paged caches must be contiguous")
+        kv_rs, W, bt_stride = hkv * d, block_table.shape[1], block_table.stride(0)
+    if d2 != d:
+        raise RuntimeError("varlen_prefill: head_dim mismatch")
+    fp8 = k.dtype == torch.float8_e4m3fn
+    if out is None:
+        out = torch.empty(tq, hq, d, dtype=q.dtype, device=q.device)
+    rc = lib().nq_varlen_prefill(
+        ptr(q), q.stride(0), q.stride(1), ptr(k), ptr(v), kv_rs, ptr(cu_seqlens_q), ptr(cu_seqlens_k),
+        int(max_seqlen_q), int(max_seqlen_k), ptr(block_table), bt_stride, W, nb, ptr(out),
+        out.stride(0), out.stride(1), n, hq, hkv, d, bs, float(softmax_scale), 1 if causal else 0,
+        dtype_code(q.dtype), dtype_code(k.dtype), ptr(k_scale) if fp8 else None,
+        ptr(v_scale) if fp8 else None, stream_of(q))
+    check(rc, "varlen_prefill")
+    return out
+
+
+def prepare_decode(sampled_token_ids, batch_slots, seq_lens, last_block_ids, input_ids, positions,
+                   context_lens, slot_mapping, num_seqs, block_size):
+    """Decode metadata kernel; same arguments as engine/decode_init.py:39-52."""
+    require_cuda(seq_lens, last_block_ids, positions, context_lens, slot_mapping,
+                 what="prepare_decode")
+    rc = lib().nq_prepare_decode(
+        ptr(sampled_token_ids), ptr(batch_slots), ptr(seq_lens), ptr(last_block_ids), ptr(input_ids),
+        ptr(positions), ptr(context_lens), ptr(slot_mapping), int(num_seqs), int(block_size),
+        stream_of(seq_lens))
+    check(rc, "prepare_decode")
+
+
+__all__ = ["store_kvcache", "paged_decode", "varlen_prefill", "prepare_decode", "decode_plan",
+           "decode_workspace", "_lib"]

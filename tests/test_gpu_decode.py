@@ -1,0 +1,207 @@
+"""Paged decode on the GPU vs the float64 oracle (layers/attention.py:71-74).
+
+Every case runs the full decode step -- store_kvcache of the new token, then
+paged decode over context_lens tokens -- and the oracle replays the same step
+from the cache contents taken before the store.
+"""
+import numpy as np
+import pytest
+import torch
+
+from nano_qwen_amd import kernels
+from oracle.inputs import make_decode_case
+from tests.parity import TOL_BF16, TOL_FP8, assert_close, decode_reference, f64, snapshot_decode
+
+pytestmark = pytest.mark.gpu
+
+
+def run_step(case):
+    kernels.store_kvcache(case["k_new"], case["v_new"], case["k_cache"], case["v_cache"],
+                          case["slot_mapping"], case["k_scale"], case["v_scale"])
+    out = kernels.paged_decode(case["q"].unsqueeze(1), case["k_cache"], case["v_cache"],
+                               case["context_lens"], case["block_tables"], case["scale"],
+                               case["k_scale"], case["v_scale"])
+    torch.cuda.synchronize()
+    return out
+
+
+def check(case, seq_ids, tol):
+    print(f"[decode] {case['name']} B={case['batch']} Hq={case['hq']} Hkv={case['hkv']} "
+          f"kv={case['k_cache'].dtype} seqs={list(seq_ids)[:8]}", flush=True)
+    snapshot_decode(case, seq_ids)
+    out = run_step(case)
+    assert out.shape == (case["batch"], 1, case["hq"], case["d"])
+    ref = decode_reference(case, seq_ids)
+    return assert_close(f64(out[list(seq_ids), 0]), ref, **tol, what=case["name"])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_cfg1_shape(cuda, dtype):
+    case = make_decode_case("cfg1", seed=0, device=cuda, dtype=dtype)
+    check(case, range(case["batch"]), TOL_BF16)
+
+
+@pytest.mark.parametrize("split", [128, 512, 4096])
+@pytest.mark.parametrize("seed", [0, 1])
+def test_decode_cfg2_small_splits(cuda, split, seed, monkeypatch):
+    monkeypatch.setenv("NQ_DECODE_SPLIT_TOKENS", str(split))
+    case = make_decode_case("cfg2", seed=seed, device=cuda, batch=6, ctx=(1, 1300))
+    check(case, range(6), TOL_BF16)
+
+
+@pytest.mark.parametrize("G", [1, 2, 8, 16])
+def test_decode_group_sizes(cuda, G):
+    case = make_decode_case("cfg2", seed=3, device=cuda, batch=3, ctx=(200, 700), hq=2 * G, hkv=2)
+    check(case, range(3), TOL_BF16)
+
+
+def test_decode_edge_lengths(cuda):
+    # lengths at and around block / step / split boundaries, plus ctx = 1
+    case = make_decode_case("cfg2", seed=4, device=cuda, batch=10, ctx=(1, 1))
+    lens = torch.tensor([1, 2, 31, 32, 33, 255, 256, 257, 512, 513], dtype=torch.int32)
+    bs = case["block_size"]
+    pool = case["num_blocks"]
+    need = int(sum((int(c) + bs - 1) // bs for c in lens))
+    perm = torch.randperm(max(pool, need + 2), generator=torch.Generator().manual_seed(1))
+    case["k_cache"] = torch.randn(len(perm), bs, 8, 128, device=cuda).mul_(0.5).to(torch.bfloat16)
+    case["v_cache"] = torch.randn(len(perm), bs, 8, 128, device=cuda).mul_(0.5).to(torch.bfloat16)
+    W = int(max((int(c) + bs - 1) // bs for c in lens)) + 2
+    bt = torch.full((10, W), -1, dtype=torch.int32)
+    off = 0
+    for b, c in enumerate(lens.tolist()):
+        n = (c + bs - 1) // bs
+        bt[b, :n] = perm[off:off + n].to(torch.int32)
+        off += n
+    bt[:, -1] = 10 ** 6         # stale / out-of-range entries past ctx are never read
+    slot = [int(bt[b, (c - 1) // bs]) * bs + (c - 1) % bs for b, c in enumerate(lens.tolist())]
+    case.update(block_tables=bt.to(cuda), context_lens=lens.to(cuda),
+                slot_mapping=torch.tensor(slot, dtype=torch.int32, device=cuda), num_blocks=len(perm))
+    check(case, range(10), TOL_BF16)
+
+
+def test_decode_ctx1_returns_new_value(cuda):
+    case = make_decode_case("cfg2", seed=5, device=cuda, batch=4, ctx=(1, 1))
+    out = run_step(case)
+    G = case["hq"] // case["hkv"]
+    want = case["v_new"].repeat_interleave(G, dim=1)
+    assert torch.equal(out[:, 0], want), "softmax over a single key must return that value exactly"
+
+
+def test_decode_zero_context_rows(cuda):
+    case = make_decode_case("cfg2", seed=6, device=cuda, batch=5, ctx=(300, 900))
+    ctx = case["context_lens"].clone()
+    ctx[1] = 0
+    ctx[3] = 0
+    case["context_lens"] = ctx
+    slot = case["slot_mapping"].clone()
+    slot[1] = -1
+    slot[3] = -1
+    case["slot_mapping"] = slot
+    snapshot_decode(case, [0, 2, 4])
+    out = run_step(case)
+    assert torch.all(out[1] == 0) and torch.all(out[3] == 0)
+    ref = decode_reference(case, [0, 2, 4])
+    assert_close(f64(out[[0, 2, 4], 0]), ref, **TOL_BF16, what="zero-ctx batch")
+
+
+def test_decode_block_permutation_bit_identical(cuda):
+    case = make_decode_case("cfg2", seed=7, device=cuda, batch=4, ctx=(500, 1500))
+    out1 = run_step(case)
+    nb = case["k_cache"].shape[0]
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(3)).to(cuda)
+    inv = torch.argsort(perm)
+    k2, v2 = case["k_cache"][perm].contiguous(), case["v_cache"][perm].contiguous()
+    bt = case["block_tables"].long()
+    bt2 = torch.where(bt >= 0, inv[bt.clamp(min=0)], -1).to(torch.int32)
+    out2 = kernels.paged_decode(case["q"].unsqueeze(1), k2, v2, case["context_lens"], bt2, case["scale"])
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+
+
+def test_decode_hip_graph_replay(cuda):
+    """Capture store + decode once, replay with new metadata in the static
+    buffers, as the reference's graph decode does (engine/model_runner.py:319-336)."""
+    mk = lambda seed: make_decode_case("cfg2", seed=seed, device=cuda, batch=8, ctx=(100, 2000), min_pool=200)
+    case = mk(8)
+    W = 11                                   # static table width > any ceil(2000/256)
+    static_bt = torch.zeros(8, W, dtype=torch.int32, device=cuda)
+    static_ctx = torch.zeros(8, dtype=torch.int32, device=cuda)
+    static_slot = torch.full((8,), -1, dtype=torch.int32, device=cuda)
+    static_q = torch.zeros_like(case["q"])
+    static_k = torch.zeros_like(case["k_new"])
+    static_v = torch.zeros_like(case["v_new"])
+    out = torch.zeros(8, 1, case["hq"], 128, dtype=case["q"].dtype, device=cuda)
+
+    def step():
+        kernels.store_kvcache(static_k, static_v, case["k_cache"], case["v_cache"], static_slot)
+        kernels.paged_decode(static_q.unsqueeze(1), case["k_cache"], case["v_cache"], static_ctx,
+                             static_bt, case["scale"], out=out)
+
+    step()  # warm-up: the split-K workspace is allocated outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for rep, seed in enumerate([8, 9, 10, 11]):
+        c = mk(seed)
+        assert c["num_blocks"] == case["num_blocks"]
+        c["k_cache"], c["v_cache"] = case["k_cache"], case["v_cache"]   # one persistent pool
+        snapshot_decode(c, list(range(8)))
+        static_bt.fill_(-1)
+        static_bt[:, :c["block_tables"].shape[1]] = c["block_tables"]
+        static_ctx.copy_(c["context_lens"])
+        static_slot.copy_(c["slot_mapping"])
+        static_q.copy_(c["q"])
+        static_k.copy_(c["k_new"])
+        static_v.copy_(c["v_new"])
+        g.replay()
+        torch.cuda.synchronize()
+        ref = decode_reference(c, list(range(8)))
+        assert_close(f64(out[:, 0]), ref, **TOL_BF16, what=f"graph replay {rep}")
+        # an eager decode of the same state agrees bit for bit
+        eager = kernels.paged_decode(static_q.unsqueeze(1), case["k_cache"], case["v_cache"], static_ctx,
+                                     static_bt, case["scale"])
+        torch.cuda.synchronize()
+        assert torch.equal(eager, out)
+
+
+@pytest.mark.slow
+def test_decode_cfg2_full(cuda):
+    case = make_decode_case("cfg2", seed=0, device=cuda)
+    seqs = np.random.default_rng(0).choice(case["batch"], 12, replace=False).tolist()
+    check(case, seqs, TOL_BF16)
+
+
+@pytest.mark.slow
+def test_decode_cfg4_full_split_k(cuda):
+    case = make_decode_case("cfg4", seed=0, device=cuda)
+    check(case, [0, 5], TOL_BF16)
+
+
+@pytest.mark.slow
+def test_decode_cfg5_full_fp8(cuda):
+    case = make_decode_case("cfg5", seed=0, device=cuda)
+    seqs = np.random.default_rng(1).choice(case["batch"], 10, replace=False).tolist()
+    check(case, seqs, TOL_FP8)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_fp8_small(cuda, dtype):
+    case = make_decode_case("cfg5", seed=2, device=cuda, batch=6, ctx=(1, 1500), dtype=dtype)
+    check(case, range(6), TOL_FP8)
+
+
+def test_decode_fp8_vs_bf16_dequantized_reference(cuda):
+    """The target's stated fp8 reference: attention in fp32 over K/V
+    dequantized to bf16 (code value * scale, rounded to bf16)."""
+    from oracle import paged as P
+    from tests.parity import subpool
+    case = make_decode_case("cfg5", seed=3, device=cuda, batch=4, ctx=(600, 2000))
+    out = run_step(case)
+    k = (case["k_cache"].float() * case["k_scale"].view(1, 1, -1, 1)).to(torch.bfloat16)
+    v = (case["v_cache"].float() * case["v_scale"].view(1, 1, -1, 1)).to(torch.bfloat16)
+    ids = list(range(4))
+    ks, vs, table, _ = subpool(k, v, case["block_tables"], case["context_lens"].cpu(), ids)
+    ref = P.paged_decode(f64(case["q"]).astype(np.float32), f64(ks).astype(np.float32),
+                         f64(vs).astype(np.float32), table, case["context_lens"].cpu().numpy(), case["scale"])
+    assert_close(f64(out[ids, 0]), ref, **TOL_FP8, what="fp8 vs bf16-dequantized fp32 reference")

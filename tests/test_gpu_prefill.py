@@ -1,0 +1,130 @@
+"""Causal varlen prefill on the GPU vs the float64 oracle (layers/attention.py:64-70).
+
+Each case runs the reference's prefill step: store the new K/V through
+slot_mapping, then attend -- over the packed new K/V when no sequence has a
+prefix-cache hit, otherwise over the whole paged cache through block_tables.
+"""
+import numpy as np
+import pytest
+import torch
+
+from nano_qwen_amd import kernels
+from oracle.inputs import make_prefill_case
+from tests.parity import TOL_BF16, TOL_FP8, assert_close, f64, prefill_reference, snapshot_prefill
+
+pytestmark = pytest.mark.gpu
+
+
+def run_step(case):
+    kernels.store_kvcache(case["k_new"], case["v_new"], case["k_cache"], case["v_cache"],
+                          case["slot_mapping"], case["k_scale"], case["v_scale"])
+    if case["block_tables"] is None:
+        k, v, ks, vs = case["k_new"], case["v_new"], None, None
+    else:
+        k, v, ks, vs = case["k_cache"], case["v_cache"], case["k_scale"], case["v_scale"]
+    out = kernels.varlen_prefill(case["q"], k, v, case["cu_seqlens_q"], case["cu_seqlens_k"],
+                                 case["max_seqlen_q"], case["max_seqlen_k"], case["scale"], causal=True,
+                                 block_table=case["block_tables"], k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    return out
+
+
+def check(case, seq_ids, tol, rows_per_seq=None):
+    print(f"[prefill] {case['name']} n={case['nseq']} lq={case['lq'][:6]} prefix={case['prefix'][:6]} "
+          f"kv={case['k_cache'].dtype} paged={case['block_tables'] is not None}", flush=True)
+    snapshot_prefill(case, seq_ids)
+    out = run_step(case)
+    assert out.shape == case["q"].shape
+    rows, ref = prefill_reference(case, seq_ids, rows_per_seq)
+    return assert_close(f64(out[torch.from_numpy(rows).to(out.device)]), ref, **tol, what=case["name"])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_packed_no_prefix(cuda, dtype):
+    case = make_prefill_case("cfg3", seed=0, device=cuda, nseq=5, lq=(1, 400), prefix_blocks=(0, 0),
+                             dtype=dtype)
+    assert case["block_tables"] is None
+    check(case, range(5), TOL_BF16)
+
+
+def test_prefill_packed_tile_edges(cuda):
+    case = make_prefill_case("cfg3", seed=1, device=cuda, nseq=8, lq=(1, 1), prefix_blocks=(0, 0))
+    # replace lengths by tile-boundary values and rebuild the packed metadata
+    lens = [1, 2, 63, 64, 65, 127, 128, 129]
+    tot = sum(lens)
+    g = torch.Generator(device=cuda).manual_seed(3)
+    case["q"] = torch.randn(tot, 32, 128, generator=g, device=cuda).to(torch.bfloat16)
+    case["k_new"] = torch.randn(tot, 8, 128, generator=g, device=cuda).to(torch.bfloat16)
+    case["v_new"] = torch.randn(tot, 8, 128, generator=g, device=cuda).to(torch.bfloat16)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=cuda)
+    case.update(lq=lens, lk=lens, prefix=[0] * 8, cu_seqlens_q=cu, cu_seqlens_k=cu,
+                max_seqlen_q=max(lens), max_seqlen_k=max(lens),
+                slot_mapping=torch.full((tot,), -1, dtype=torch.int32, device=cuda))
+    check(case, range(8), TOL_BF16)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_prefill_paged_prefix(cuda, seed):
+    case = make_prefill_case("cfg3", seed=seed, device=cuda, nseq=4, lq=(1, 700), prefix_blocks=(1, 3))
+    assert case["block_tables"] is not None
+    check(case, range(4), TOL_BF16)
+
+
+def test_prefill_chunked_unaligned_prefix(cuda):
+    """A chunked prefill leaves num_cached_tokens off block boundaries
+    (scheduler/scheduler.py:47-51): P = Lk - Lq need not be a multiple of 256."""
+    case = make_prefill_case("cfg3", seed=4, device=cuda, nseq=3, lq=(50, 300), prefix_blocks=(1, 2))
+    bs = 256
+    pre = [37, 0, 300]
+    lq = case["lq"]
+    lk = [p + q for p, q in zip(pre, lq)]
+    nb = case["num_blocks"]
+    need = sum((x + bs - 1) // bs for x in lk)
+    assert need <= nb
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(2))
+    W = max((x + bs - 1) // bs for x in lk)
+    bt = torch.full((3, W), -1, dtype=torch.int32)
+    off = 0
+    slots = []
+    for i in range(3):
+        n = (lk[i] + bs - 1) // bs
+        bt[i, :n] = perm[off:off + n].to(torch.int32)
+        off += n
+        slots += [int(bt[i, p // bs]) * bs + p % bs for p in range(pre[i], lk[i])]
+    cu_k = torch.tensor(np.concatenate([[0], np.cumsum(lk)]), dtype=torch.int32, device=cuda)
+    case.update(prefix=pre, lk=lk, cu_seqlens_k=cu_k, max_seqlen_k=max(lk), block_tables=bt.to(cuda),
+                slot_mapping=torch.tensor(slots, dtype=torch.int32, device=cuda))
+    check(case, range(3), TOL_BF16)
+
+
+def test_prefill_group_sizes(cuda):
+    for G, hkv in ((1, 4), (2, 4), (8, 2), (16, 1)):
+        case = make_prefill_case("cfg3", seed=5, device=cuda, nseq=3, lq=(20, 300), prefix_blocks=(1, 1),
+                                 hq=G * hkv, hkv=hkv)
+        check(case, range(3), TOL_BF16)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_fp8_paged(cuda, dtype):
+    case = make_prefill_case("cfg3", seed=6, device=cuda, nseq=4, lq=(1, 600), prefix_blocks=(1, 2),
+                             kv="fp8", dtype=dtype)
+    check(case, range(4), TOL_FP8)
+
+
+def test_decode_equals_last_prefill_row(cuda):
+    """Cross-kernel invariant: the decode output of a sequence equals the last
+    row of the causal prefill over the same keys."""
+    case = make_prefill_case("cfg3", seed=7, device=cuda, nseq=4, lq=(5, 900), prefix_blocks=(1, 2))
+    out = run_step(case)
+    last = (case["cu_seqlens_q"][1:] - 1).long()
+    lk = torch.tensor(case["lk"], dtype=torch.int32, device=cuda)
+    dec = kernels.paged_decode(case["q"][last].unsqueeze(1), case["k_cache"], case["v_cache"], lk,
+                               case["block_tables"], case["scale"])
+    torch.cuda.synchronize()
+    assert_close(f64(dec[:, 0]), f64(out[last]), max_abs=1e-2, mean_abs=1e-3, what="decode vs prefill last row")
+
+
+@pytest.mark.slow
+def test_prefill_cfg3_full(cuda):
+    case = make_prefill_case("cfg3", seed=0, device=cuda)
+    check(case, list(range(16)), TOL_BF16, rows_per_seq=24)

@@ -1,0 +1,140 @@
+"""Host-side logic and the C ABI surface, on the CPU (no device calls)."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import nano_qwen_amd
+from nano_qwen_amd import _lib, kernels
+from nano_qwen_amd.engine import ModelRunner, Sequence
+from nano_qwen_amd.layers import Attention, store_kvcache
+from nano_qwen_amd.utils import context as C
+from oracle import metadata
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def header_functions():
+    text = (ROOT / "include" / "nq_attn.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(nq_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_loads_and_exports_every_header_symbol():
+    lib = _lib.lib()
+    names = header_functions()
+    assert "nq_paged_decode" in names and "nq_varlen_prefill" in names and "nq_store_kvcache" in names
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/nq_attn.h but not exported"
+    assert set(names) == set(_lib.EXPORTED), "ctypes signatures out of sync with the header"
+    assert lib.nq_abi_version() == 1
+
+
+def test_abi_rejects_bad_arguments_without_launching():
+    lib = _lib.lib()
+    # head_dim 64 is not built: NQ_EUNSUPPORTED before any device work
+    rc = lib.nq_paged_decode(None, 0, 0, None, None, None, 0, 1, None, None, 0, 0, 2, 8, 2, 64, 256, 1,
+                             0.1, 1, 256, None, 0, 2, 2, None, None, None)
+    assert rc == -2 and b"head_dim" in lib.nq_last_error()
+    rc = lib.nq_paged_decode(None, 0, 0, None, None, None, 0, 1, None, None, 0, 0, 2, 6, 4, 128, 256, 1,
+                             0.1, 1, 256, None, 0, 2, 2, None, None, None)
+    assert rc == -1  # 6 q heads over 4 kv heads
+    rc = lib.nq_store_kvcache(None, 0, None, 0, None, None, None, 3, 10, 8, 128, 2, 2, None, None, None)
+    assert rc == -1 and b"null" in lib.nq_last_error()
+    assert lib.nq_store_kvcache(None, 0, None, 0, None, None, None, 0, 10, 8, 128, 2, 2, None, None, None) == 0
+    rc = lib.nq_varlen_prefill(None, 0, 0, None, None, 0, None, None, 10, 10, None, 0, 0, 0, None, 0, 0, 1, 32, 8,
+                               128, 256, 0.1, 1, 2, 1, None, None, None)
+    assert rc == -2  # bf16 q with f16 kv
+
+
+def test_decode_plan_covers_table_and_respects_env(monkeypatch):
+    for W, B in ((1, 1), (16, 64), (128, 8), (32, 128), (3, 5)):
+        ns, st = kernels.decode_plan(B, 32, 8, W, 256, torch.bfloat16)
+        assert st % 128 == 0 and ns * st >= W * 256 and (ns - 1) * st < W * 256
+    monkeypatch.setenv("NQ_DECODE_SPLIT_TOKENS", "1024")
+    ns, st = kernels.decode_plan(8, 64, 8, 128, 256, torch.bfloat16)
+    assert (ns, st) == (32, 1024)
+    assert _lib.lib().nq_decode_workspace_bytes(8, 64, 128, 1) == 0
+    assert _lib.lib().nq_decode_workspace_bytes(8, 64, 128, 32) >= 8 * 64 * 32 * (128 + 1) * 4
+
+
+def test_context_roundtrip():
+    C.reset_context()
+    assert C.get_context().is_prefill is False and C.get_context().block_tables is None
+    C.set_context(True, torch.tensor([0, 3]), torch.tensor([0, 5]), 3, 5, torch.tensor([1, 2, 3]))
+    ctx = C.get_context()
+    assert ctx.is_prefill and ctx.max_seqlen_k == 5 and ctx.context_lens is None
+    assert [f for f in C.Context.__slots__] == ["is_prefill", "cu_seqlens_q", "cu_seqlens_k", "max_seqlen_q",
+                                               "max_seqlen_k", "slot_mapping", "context_lens", "block_tables",
+                                               "state_indices"]
+    C.reset_context()
+    assert C.get_context().cu_seqlens_q is None
+
+
+def test_attention_module_contract():
+    a = Attention(32, 128, 128 ** -0.5, 8)
+    assert (a.num_heads, a.head_dim, a.num_kv_heads) == (32, 128, 8)
+    assert a.k_cache.numel() == 0 and a.v_cache.numel() == 0
+    assert nano_qwen_amd.Attention is Attention
+
+
+def test_no_cpu_fallback():
+    key = torch.zeros(2, 8, 128, dtype=torch.bfloat16)
+    cache = torch.zeros(1, 256, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        store_kvcache(key, key, cache, cache, torch.tensor([0, 1], dtype=torch.int32))
+    q = torch.zeros(2, 1, 32, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        kernels.paged_decode(q, cache, cache, torch.tensor([1, 1], dtype=torch.int32),
+                             torch.zeros(2, 1, dtype=torch.int32), 0.1)
+
+
+def test_store_kvcache_keeps_reference_asserts():
+    key = torch.zeros(2, 8, 128, dtype=torch.bfloat16)
+    cache = torch.zeros(1, 256, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):
+        store_kvcache(key.transpose(1, 2).contiguous().transpose(1, 2), key, cache, cache,
+                      torch.tensor([0, 1], dtype=torch.int32))
+    with pytest.raises(AssertionError):
+        store_kvcache(key, key, cache, cache, torch.tensor([0], dtype=torch.int32))
+
+
+def test_runner_prepare_prefill_on_cpu_matches_oracle():
+    runner = ModelRunner(block_size=256, max_num_seqs=8, device="cpu")
+    rng = np.random.default_rng(3)
+    seqs = []
+    for i in range(4):
+        n = int(rng.integers(1, 1200))
+        cached = 256 * int(rng.integers(0, (n - 1) // 256 + 1)) if i % 2 else 0
+        sched = n - cached if i != 1 else max(1, (n - cached) // 2)
+        seqs.append(Sequence(list(rng.integers(0, 999, n)), block_table=list(rng.permutation(64)[:(n + 255) // 256]),
+                             num_cached_tokens=cached, num_scheduled_tokens=sched))
+    input_ids, positions = runner.prepare_prefill(seqs)
+    md = metadata.prepare_prefill(seqs, 256)
+    ctx = C.get_context()
+    assert input_ids.tolist() == md["input_ids"] and positions.tolist() == md["positions"]
+    assert ctx.slot_mapping.tolist() == md["slot_mapping"]
+    assert ctx.cu_seqlens_q.tolist() == md["cu_seqlens_q"] and ctx.cu_seqlens_k.tolist() == md["cu_seqlens_k"]
+    assert (ctx.max_seqlen_q, ctx.max_seqlen_k) == (md["max_seqlen_q"], md["max_seqlen_k"])
+    want = md["block_tables"]
+    assert (ctx.block_tables is None) == (want is None)
+    if want is not None:
+        assert ctx.block_tables.tolist() == want
+    assert ctx.slot_mapping.dtype == torch.int32 and ctx.cu_seqlens_q.dtype == torch.int32
+    C.reset_context()
+
+
+def test_runner_allocate_kv_cache_binds_layers():
+    class M(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.a = Attention(4, 128, 0.1, 2)
+            self.b = Attention(4, 128, 0.1, 2)
+    m = M()
+    r = ModelRunner(block_size=256, max_num_seqs=4, device="cpu")
+    assert r.allocate_kv_cache(m, 2, 3, 2, 128, torch.bfloat16, kv_cache_dtype=torch.float8_e4m3fn) == 2
+    assert r.kv_cache.shape == (2, 2, 3, 256, 2, 128)
+    assert m.b.k_cache.data_ptr() == r.kv_cache[0, 1].data_ptr()
+    assert m.a.k_scale.shape == (2,) and m.b.v_scale.data_ptr() == r.kv_scales[1, 1].data_ptr()
