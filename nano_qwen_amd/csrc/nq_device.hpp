@@ -83,18 +83,76 @@ __device__ inline u32x4 load16_stream(const void *p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
 }
 
-// Wave-level LDS ordering: make this wave's LDS writes visible to its own
-// later LDS reads from other lanes (no cross-wave barrier needed).
+// Buffer resource over [base, base + num_bytes): raw buffer loads outside the
+// range return 0 without touching memory.  Dword 3 is the gfx9-family raw
+// (untyped, 32-bit data format) descriptor word.
+// The fields are forced into scalar registers (readfirstlane): the caller
+// guarantees they are wave-uniform, and a descriptor the compiler cannot
+// prove uniform would be wrapped in a per-load waterfall loop.
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t num_bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32));
+  const uint32_t n = __builtin_amdgcn_readfirstlane(num_bytes);
+  void *ub = reinterpret_cast<void *>((static_cast<uint64_t>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ub, static_cast<short>(0), static_cast<int>(n), 0x00020000);
+}
+// 16-byte raw buffer load with the non-temporal (streaming) hint.
+__device__ inline u32x4 buffer_load16_nt(__amdgpu_buffer_rsrc_t r, int voffset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 2));
+}
+
+// Wave-level LDS ordering between lanes of ONE wave.  The LDS executes a
+// wave's DS instructions in issue order, so a read issued after a write (by
+// any lane of the same wave) sees it; only the compiler must be kept from
+// reordering across this point.  (A memory-model fence here makes the
+// backend wait for every outstanding global load, which would serialize the
+// prefetch pipeline.)
 __device__ inline void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  asm volatile("" ::: "memory");
 }
 
 __device__ inline float xor_max(float v, int mask) {
   return fmaxf(v, __shfl_xor(v, mask, 64));
 }
 __device__ inline float xor_sum(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
+
+// Butterflies across lane l and l^16 / l^32 with gfx950 permlane swaps (one
+// VALU op each, no LDS round trip).  With both operands = v, the swap returns
+// {v, partner} in some order on every lane.
+__device__ inline float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+__device__ inline uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+__device__ inline float max16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(f2u(v), f2u(v), false, false);
+  const uint32_t a = r[0], b = r[1];
+  return fmaxf(u2f(a), u2f(b));
+}
+__device__ inline float max32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(f2u(v), f2u(v), false, false);
+  const uint32_t a = r[0], b = r[1];
+  return fmaxf(u2f(a), u2f(b));
+}
+__device__ inline float sum16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(f2u(v), f2u(v), false, false);
+  const uint32_t a = r[0], b = r[1];
+  return u2f(a) + u2f(b);
+}
+__device__ inline float sum32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(f2u(v), f2u(v), false, false);
+  const uint32_t a = r[0], b = r[1];
+  return u2f(a) + u2f(b);
+}
+
+// Transposing LDS read (ds_read_b64_tr_b16).  Within each 16-lane group,
+// lanes 4k..4k+3 address the four 8-byte pieces of "row" k (16 consecutive
+// 16-bit elements); lane i receives element i of rows 0..3, packed in order.
+__device__ inline u32x2 lds_read_tr16(const uint16_t *p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4 *)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();

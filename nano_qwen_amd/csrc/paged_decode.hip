@@ -7,16 +7,17 @@
 // context_lens[b] cached tokens of kv head h / G, gathered through
 // block_tables[b, t / block_size].
 //
-// Design (one workgroup = 4 waves = one (sequence, kv head, split)):
+// Design (one workgroup = up to 8 waves = the kv heads of one (sequence, split)):
 //  * GQA sharing: the G query heads of a kv head are the 16 columns of one
 //    MFMA tile, so every K/V byte is read from HBM exactly once.
-//  * S^T[token, head] = K . Q^T on v_mfma_f32_16x16x32 (K is the A operand,
-//    loaded straight from HBM as 16-byte vectors in operand layout).  The
-//    C layout (lane = head column, 4 token rows) is already the B-operand
+//  * K/V are streamed in full 128-byte lines per load instruction (the
+//    access pattern that sustains HBM bandwidth) and each wave rearranges its
+//    32-token tile through a swizzled LDS tile into MFMA operands.
+//  * S^T[token, head] = K . Q^T on v_mfma_f32_16x16x32 (K is the A operand).
+//    The C layout (lane = head column, 4 token rows) is already the B-operand
 //    layout of the PV product, so P never leaves registers.
-//  * O^T[dim, head] += V^T . P^T: V needs token-contiguous operands, so each
-//    wave stages its 32-token V tile through LDS (row-major) and reads it
-//    back transposed.
+//  * O^T[dim, head] += V^T . P^T: the token-contiguous V^T operands come from
+//    the row-major tile through ds_read_b64_tr_b16 (gfx950 transposing read).
 //  * Online softmax in the log2 domain per head; the row max is reduced over
 //    the 4 lane groups with two cross-lane exchanges.
 //  * Split-K: split s of a sequence covers tokens [s*T, (s+1)*T); a split
@@ -36,8 +37,6 @@
 namespace nq {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kStep = 32;  // tokens per wave step (two 16-token MFMA tiles)
 
 struct DecodeArgs {
@@ -61,106 +60,122 @@ struct DecodeArgs {
   const float *v_scale;
 };
 
-// Per-head-dim constants.  16-bit K/V: lane group g holds dims 8g + 32kk + [0,8)
-// of its token for MFMA kk; fp8 K/V: dims (D/4)g + 8kk + [0,8) so one lane's
-// bytes are contiguous.
+// Per-head-dim geometry.  K/V are streamed from HBM in "full-line" layout:
+// one 16-byte load instruction covers whole 128-byte cache lines of a few
+// tokens (a 16-bit token row of one kv head is 2*D bytes = D/8 chunks of 16 B;
+// an fp8 row is D/16 chunks).  Measured on MI355X this reaches ~6.2-6.6 TB/s
+// where the MFMA-operand layout (16 tokens x 64 B per instruction) stalls near
+// 4-5.6 TB/s.  Each wave then rearranges the 32-token tile through its own
+// LDS tile into MFMA operands.
 template <int D, bool FP8>
 struct Geo {
-  static constexpr int NKK = D / 32;                   // QK MFMAs per 16-token tile
-  static constexpr int NJ = D / 16;                    // PV output blocks
-  static constexpr int KLOADS = FP8 ? D / 64 : D / 32;  // 16-byte loads per lane per tile
-  static constexpr int VROW = D + 4;                   // LDS V row stride (16-bit elems)
-  static constexpr int ESZ = FP8 ? 1 : 2;
-  __device__ static inline int lane_off(int g) { return FP8 ? (D / 4) * g : 8 * g; }  // elems
-  __device__ static inline int load_stride() { return FP8 ? 16 : 32; }                 // elems
-  __device__ static inline int dim0(int g, int kk) { return FP8 ? (D / 4) * g + 8 * kk : 8 * g + 32 * kk; }
+  static constexpr int NKK = D / 32;           // QK MFMAs per 16-token tile
+  static constexpr int NJ = D / 16;            // PV output blocks
+  static constexpr int ROWB = D * 2;           // LDS tile row: one token, 16-bit elements
+  static constexpr int CHUNKS = ROWB / 16;     // 16-byte chunks per LDS row
+  static constexpr int SRC_ROWB = FP8 ? D : D * 2;       // bytes of one token's head piece in HBM
+  static constexpr int SRC_CHUNKS = SRC_ROWB / 16;
+  static constexpr int TOK_PER_LOAD = 64 / SRC_CHUNKS;   // tokens covered by one load instruction
+  static constexpr int RAW = kStep / TOK_PER_LOAD;       // load instructions per 32-token step
+  static constexpr int TILE_B = kStep * ROWB;            // LDS bytes per wave
+  static_assert(CHUNKS == 16, "swizzle below assumes 16 chunks per row (D = 128)");
 };
 
-template <int D, bool FP8>
-struct StepRegs {
-  u32x4 k[2][Geo<D, FP8>::KLOADS];
-  u32x4 v[2][Geo<D, FP8>::KLOADS];
-};
+// XOR swizzle of 16-byte chunks within an LDS row (row index mod 16).  It is
+// a bijection, so a row written by 16 lanes stays conflict-free, and it makes
+// both operand reads conflict-free: 16 rows x one logical chunk (K fragments,
+// ds_read_b128) and 4 rows x 2 adjacent chunks (V^T fragments, ds_read_b64_tr_b16).
+__device__ inline int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1) | (row & 8); }
 
 template <class T, bool FP8, int D>
 struct DecodeWave {
   using Gm = Geo<D, FP8>;
-  static constexpr int LDS_PER_WAVE_B =
-      (kStep * Gm::VROW * 2 > (16 * D + 32) * 4) ? kStep * Gm::VROW * 2 : (16 * D + 32) * 4;
+  static constexpr int LDS_PER_WAVE_B = Gm::TILE_B;
 
-  // Issue the K/V loads of one 32-token step (tokens t0 .. t0+31 of the split).
-  __device__ static inline void load(const DecodeArgs &a, const int32_t *bt_row, int kvh, int t0,
-                                     int t_end, int m, int g, StepRegs<D, FP8> &r) {
-    const int blk = bt_row[t0 / a.block_size];
-    const bool ok = blk >= 0 && blk < a.num_blocks;
-    const int64_t row0 = static_cast<int64_t>(blk) * a.block_size + (t0 % a.block_size);
+  // Cache row of token t0 of a step (t0 % 32 == 0, so the step stays inside
+  // one block), or -1 if the table entry is not a valid block.  The split's
+  // table entries were loaded once into `bt_lane` (lane i holds entry
+  // first_blk + i), so no memory access -- and no wait on the vector-memory
+  // counter, which would also wait for the K/V prefetch -- happens here.
+  __device__ static inline int64_t step_row(const DecodeArgs &a, int bt_lane, int first_blk, int t0) {
+    const int blk = __builtin_amdgcn_readlane(bt_lane, t0 / a.block_size - first_blk);
+    if (blk < 0 || blk >= a.num_blocks) return -1;
+    return static_cast<int64_t>(blk) * a.block_size + (t0 % a.block_size);
+  }
+
+  // Lane's byte offset, within a step's rows, of its chunk for load c = 0
+  // (load c adds c * TOK_PER_LOAD rows).
+  __device__ static inline int lane_voff(const DecodeArgs &a, int kvh, int lane) {
+    const int tl = lane / Gm::SRC_CHUNKS, ch = lane % Gm::SRC_CHUNKS;
+    return (tl * a.Hkv + kvh) * Gm::SRC_ROWB + ch * 16;
+  }
+
+  // Issue the loads of one 32-token step of K (or V): load c, lane l ->
+  // token c*TOK_PER_LOAD + l/SRC_CHUNKS, chunk l%SRC_CHUNKS of kv head kvh.
+  // One scalar buffer descriptor spans exactly the step's valid tokens, so
+  // tokens past t_end (or a missing block) read as zeros with no branches.
+  __device__ static inline void load(const uint8_t *base, const DecodeArgs &a, int64_t row0, int t0, int t_end,
+                                     int voff0, u32x4 (&r)[Gm::RAW]) {
+    const int row_b = a.Hkv * Gm::SRC_ROWB;
+    const int nvalid = row0 >= 0 ? max(0, min(kStep, t_end - t0)) : 0;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + (row0 >= 0 ? row0 : 0) * row_b,
+                                                static_cast<uint32_t>(nvalid * row_b));
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const bool valid = ok && (t0 + 16 * i + m < t_end);
-      const int64_t off =
-          (((row0 + 16 * i + m) * a.Hkv + kvh) * D + Gm::lane_off(g)) * Gm::ESZ;
+    for (int c = 0; c < Gm::RAW; ++c) r[c] = buffer_load16_nt(rs, voff0 + c * Gm::TOK_PER_LOAD * row_b);
+  }
+
+  // Write one raw step into the wave's LDS tile (row-major tokens x D, 16-bit,
+  // swizzled chunks); fp8 is converted to the operand type on the way.
+  __device__ static inline void stage(uint8_t *tile, const u32x4 (&r)[Gm::RAW], int lane) {
+    const int tl = lane / Gm::SRC_CHUNKS, ch = lane % Gm::SRC_CHUNKS;
 #pragma unroll
-      for (int c = 0; c < Gm::KLOADS; ++c) {
-        const int64_t o2 = off + static_cast<int64_t>(c) * Gm::load_stride() * Gm::ESZ;
-        r.k[i][c] = valid ? load16_stream(a.k_cache + o2) : u32x4{0, 0, 0, 0};
-        r.v[i][c] = valid ? load16_stream(a.v_cache + o2) : u32x4{0, 0, 0, 0};
+    for (int c = 0; c < Gm::RAW; ++c) {
+      const int row = c * Gm::TOK_PER_LOAD + tl;
+      uint8_t *rp = tile + row * Gm::ROWB;
+      if constexpr (!FP8) {
+        *reinterpret_cast<u32x4 *>(rp + ((ch ^ swz(row)) << 4)) = r[c];
+      } else {
+        const u32x4 &w = r[c];
+        const u32x4 lo{T::template fp8x2<false>(w[0]), T::template fp8x2<true>(w[0]),
+                       T::template fp8x2<false>(w[1]), T::template fp8x2<true>(w[1])};
+        const u32x4 hi{T::template fp8x2<false>(w[2]), T::template fp8x2<true>(w[2]),
+                       T::template fp8x2<false>(w[3]), T::template fp8x2<true>(w[3])};
+        *reinterpret_cast<u32x4 *>(rp + (((2 * ch) ^ swz(row)) << 4)) = lo;
+        *reinterpret_cast<u32x4 *>(rp + (((2 * ch + 1) ^ swz(row)) << 4)) = hi;
       }
     }
   }
 
-  // K operand of MFMA kk of tile i, in operand type.
-  __device__ static inline u32x4 kfrag(const StepRegs<D, FP8> &r, int i, int kk) {
-    if constexpr (!FP8) {
-      return r.k[i][kk];
-    } else {
-      const u32x4 &w = r.k[i][kk / 2];
-      const uint32_t w0 = w[(kk % 2) * 2], w1 = w[(kk % 2) * 2 + 1];
-      return u32x4{T::template fp8x2<false>(w0), T::template fp8x2<true>(w0), T::template fp8x2<false>(w1),
-                   T::template fp8x2<true>(w1)};
-    }
-  }
-
-  // Write this wave's V tile (32 tokens x D, operand type) to LDS row-major.
-  __device__ static inline void stage_v(uint16_t *vt, const StepRegs<D, FP8> &r, int m, int g) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      uint16_t *row = vt + (16 * i + m) * Gm::VROW;
-#pragma unroll
-      for (int c = 0; c < Gm::KLOADS; ++c) {
-        if constexpr (!FP8) {
-          const u32x4 &w = r.v[i][c];
-          uint16_t *p = row + Gm::dim0(g, c);
-          *reinterpret_cast<u32x2 *>(p) = u32x2{w[0], w[1]};
-          *reinterpret_cast<u32x2 *>(p + 4) = u32x2{w[2], w[3]};
-        } else {
-          const u32x4 &w = r.v[i][c];
-          uint16_t *p = row + Gm::lane_off(g) + 16 * c;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            *reinterpret_cast<u32x2 *>(p + 4 * t) = u32x2{T::template fp8x2<false>(w[t]), T::template fp8x2<true>(w[t])};
-          }
-        }
-      }
-    }
+  // K operand of MFMA kk of tile i: lane (m, g) = token 16i + m, dims
+  // 8(g + 4kk) .. +8 (logical chunk g + 4kk).
+  __device__ static inline u32x4 kfrag(const uint8_t *tile, int i, int kk, int m, int g) {
+    const int row = 16 * i + m;
+    return *reinterpret_cast<const u32x4 *>(tile + row * Gm::ROWB + (((g + 4 * kk) ^ swz(row)) << 4));
   }
 
   // V^T operand for output block j: lane (m, g) takes V[psi(g, i)][16j + m],
-  // psi(g, i) = 4g + i (i < 4, tile 0) or 16 + 4g + i - 4 (tile 1).
-  __device__ static inline u32x4 vfrag(const uint16_t *vt, int j, int m, int g) {
-    const uint16_t *c0 = vt + (4 * g) * Gm::VROW + 16 * j + m;
-    const uint16_t *c1 = c0 + 16 * Gm::VROW;
-    uint32_t e[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      e[i] = c0[i * Gm::VROW];
-      e[4 + i] = c1[i * Gm::VROW];
-    }
-    return u32x4{e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16)};
+  // psi(g, i) = 4g + i (i < 4) or 16 + 4g + i - 4.  Two transposing reads:
+  // lane 16g + 4k + q addresses row psi(g, k) (resp. psi(g, 4 + k)) at
+  // elements 16j + 4q .. +3.
+  __device__ static inline u32x4 vfrag(const uint8_t *tile, int j, int lane) {
+    const int g = lane >> 4, k = (lane >> 2) & 3, q = lane & 3;
+    const int r0 = 4 * g + k, r1 = r0 + 16;
+    const int lc = 2 * j + (q >> 1), sub = (q & 1) * 8;
+    const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t *>(
+        tile + r0 * Gm::ROWB + ((lc ^ swz(r0)) << 4) + sub));
+    const u32x2 hi = lds_read_tr16(reinterpret_cast<const uint16_t *>(
+        tile + r1 * Gm::ROWB + ((lc ^ swz(r1)) << 4) + sub));
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
   }
 };
 
-template <class T, bool FP8, int D, bool PIPE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PIPE ? 2 : 3)))
+// One workgroup = HPW waves = HPW consecutive kv heads of one (sequence,
+// split); wave w owns kv head blockIdx.y * HPW + w.  The waves of a workgroup
+// step through the same tokens together, so the workgroup streams whole
+// contiguous cache rows, and no cross-wave merge is needed: each wave owns
+// its heads' softmax state.
+template <class T, bool FP8, int D, int HPW>
+__global__ __launch_bounds__(64 * HPW) __attribute__((amdgpu_waves_per_eu(3)))
 void paged_decode_kernel(const DecodeArgs a) {
   using W = DecodeWave<T, FP8, D>;
   using Gm = Geo<D, FP8>;
@@ -168,14 +183,16 @@ void paged_decode_kernel(const DecodeArgs a) {
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m = lane & 15, g = lane >> 4;  // m: token row / head column, g: lane group
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int split = blockIdx.x, b = blockIdx.z;
+  const int kvh = blockIdx.y * HPW + wave;
+  if (kvh >= a.Hkv) return;  // whole wave; the kernel has no workgroup barrier
   const int G = a.G;
   const int ctx = min(a.context_lens[b], a.max_tokens);
   const int t_begin = split * a.split_tokens;
 
   if (ctx <= 0) {  // padded graph row: defined zeros, no KV reads
     if (split == 0) {
-      for (int it = threadIdx.x; it < G * D / 4; it += kThreads) {
+      for (int it = lane; it < G * D / 4; it += 64) {
         const int h = it / (D / 4), d4 = it % (D / 4);
         uint8_t *o = a.out + b * a.o_bs + (kvh * G + h) * a.o_hs + d4 * 8;
         *reinterpret_cast<u32x2 *>(o) = u32x2{0, 0};
@@ -190,48 +207,69 @@ void paged_decode_kernel(const DecodeArgs a) {
   const float kscale = FP8 ? a.k_scale[kvh] : 1.0f;
   const float vscale = FP8 ? a.v_scale[kvh] : 1.0f;
   const float sl2 = a.scale_log2 * kscale;
+  const int32_t *bt_row = a.block_tables + b * a.bt_stride;
 
-  // Q^T operand: lane (m, g) = head column m, dims dim0(g, kk) + [0, 8).
+  // Q^T operand: lane (m, g) = head column m, dims 8(g + 4kk) .. +8.
   u32x4 qf[Gm::NKK];
   {
     const bool hv = m < G;
     const uint8_t *qp = a.q + b * a.q_bs + (kvh * G + (hv ? m : 0)) * a.q_hs;
 #pragma unroll
-    for (int kk = 0; kk < Gm::NKK; ++kk)
-      qf[kk] = hv ? load16(qp + Gm::dim0(g, kk) * 2) : u32x4{0, 0, 0, 0};
+    for (int kk = 0; kk < Gm::NKK; ++kk) qf[kk] = hv ? load16(qp + (8 * g + 32 * kk) * 2) : u32x4{0, 0, 0, 0};
   }
 
-  const int32_t *bt_row = a.block_tables + b * a.bt_stride;
-  uint16_t *vt = reinterpret_cast<uint16_t *>(smem + wave * W::LDS_PER_WAVE_B);
+  // Raw K and V of the current step live in registers; each is refilled with
+  // the next step's loads as soon as it has been copied to LDS, so those
+  // loads are in flight during the rest of the step.  The refill is issued
+  // unconditionally (past the split it is an empty descriptor: zeros, no
+  // memory traffic) so the vector-memory wait counts are the same on every
+  // iteration and never drain the prefetch.
+  int t0 = t_begin;
+  const int first_blk = t_begin / a.block_size;
+  const int n_blk = (t_end - 1) / a.block_size - first_blk + 1;  // <= 64 (host plan)
+  const int bt_lane = lane < n_blk ? bt_row[first_blk + lane] : -1;
+  u32x4 kraw[Gm::RAW], vraw[Gm::RAW];
+  int64_t row0 = W::step_row(a, bt_lane, first_blk, t0);
+  const int voff0 = W::lane_voff(a, kvh, lane);
+  W::load(a.k_cache, a, row0, t0, t_end, voff0, kraw);
+  W::load(a.v_cache, a, row0, t0, t_end, voff0, vraw);
+
+  uint8_t *tile = smem + wave * W::LDS_PER_WAVE_B;
 
   float m_run = kNegInf, l_run = 0.f;
   f32x4 o[Gm::NJ];
 #pragma unroll
   for (int j = 0; j < Gm::NJ; ++j) o[j] = f32x4{0, 0, 0, 0};
 
-  auto compute = [&](int t0, const StepRegs<D, FP8> &r) {
-    wave_lds_sync();  // previous step's V^T reads are done before overwriting
-    W::stage_v(vt, r, m, g);
+  for (; t0 < t_end; t0 += kStep) {
+    const int t1 = t0 + kStep;
+    const int64_t row1 = (t1 < t_end) ? W::step_row(a, bt_lane, first_blk, t1) : -1;
+    wave_lds_sync();  // the previous step's V^T reads are issued before the tile is overwritten
+    W::stage(tile, kraw, lane);
+    W::load(a.k_cache, a, row1, t1, t_end, voff0, kraw);  // empty past t_end
+    wave_lds_sync();
     f32x4 s[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       s[i] = f32x4{0, 0, 0, 0};
 #pragma unroll
-      for (int kk = 0; kk < Gm::NKK; ++kk) s[i] = T::mfma16x16x32(W::kfrag(r, i, kk), qf[kk], s[i]);
+      for (int kk = 0; kk < Gm::NKK; ++kk) s[i] = T::mfma16x16x32(W::kfrag(tile, i, kk, m, g), qf[kk], s[i]);
     }
+    wave_lds_sync();  // K operand reads are issued before V overwrites the tile
+    W::stage(tile, vraw, lane);
+    W::load(a.v_cache, a, row1, t1, t_end, voff0, vraw);
     float x[8];
     float mloc = kNegInf;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const bool valid = t0 + 16 * i + 4 * g + rr < t_end;
+        const bool valid = row0 >= 0 && t0 + 16 * i + 4 * g + rr < t_end;
         const float v = valid ? s[i][rr] * sl2 : kNegInf;
         x[4 * i + rr] = v;
         mloc = fmaxf(mloc, v);
       }
-    mloc = xor_max(mloc, 16);
-    mloc = xor_max(mloc, 32);
+    mloc = max32(max16(mloc));
     const float m_new = fmaxf(m_run, mloc);
     const float m_use = (m_new == kNegInf) ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
@@ -251,77 +289,29 @@ void paged_decode_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int j = 0; j < Gm::NJ; ++j) {
       o[j] *= alpha;
-      o[j] = T::mfma16x16x32(W::vfrag(vt, j, m, g), pb, o[j]);
+      o[j] = T::mfma16x16x32(W::vfrag(tile, j, lane), pb, o[j]);
     }
-  };
+    row0 = row1;
+  }
 
-  // Token loop: waves take interleaved 32-token steps.  With PIPE, step
-  // n+1's loads are in flight while step n computes (two register sets,
-  // fewer waves); without, latency is hidden by more resident waves.
-  const int stride = kWaves * kStep;
-  int t0 = t_begin + wave * kStep;
-  if constexpr (PIPE) {
-    StepRegs<D, FP8> ra, rb;
-    if (t0 < t_end) W::load(a, bt_row, kvh, t0, t_end, m, g, ra);
-    while (t0 < t_end) {
-      int t1 = t0 + stride;
-      if (t1 < t_end) W::load(a, bt_row, kvh, t1, t_end, m, g, rb);
-      compute(t0, ra);
-      t0 = t1;
-      if (t0 >= t_end) break;
-      t1 = t0 + stride;
-      if (t1 < t_end) W::load(a, bt_row, kvh, t1, t_end, m, g, ra);
-      compute(t0, rb);
-      t0 = t1;
+  // ---- epilogue: lane (m, g) holds O^T[16j + 4g + r][head m]
+  const float L = sum32(sum16(l_run));
+  if (m >= G) return;
+  const int head = kvh * G + m;
+  const float inv = (L > 0.f) ? vscale / L : 0.f;
+  if (single) {
+    uint8_t *op = a.out + b * a.o_bs + head * a.o_hs;
+#pragma unroll
+    for (int j = 0; j < Gm::NJ; ++j) {
+      const f32x4 v = o[j] * inv;
+      *reinterpret_cast<u32x2 *>(op + (16 * j + 4 * g) * 2) = u32x2{T::pack2(v[0], v[1]), T::pack2(v[2], v[3])};
     }
   } else {
-    for (; t0 < t_end; t0 += stride) {
-      StepRegs<D, FP8> r;
-      W::load(a, bt_row, kvh, t0, t_end, m, g, r);
-      compute(t0, r);
-    }
-  }
-
-  // ---- merge the 4 waves of the workgroup through LDS
-  l_run = xor_sum(l_run, 16);
-  l_run = xor_sum(l_run, 32);
-  __syncthreads();  // every wave is done with its V tile (the merge buffers alias it)
-  float *cb = reinterpret_cast<float *>(smem + wave * W::LDS_PER_WAVE_B);
+    const int64_t idx = (static_cast<int64_t>(b) * a.Hq + head) * a.num_splits + split;
+    float *wp = a.ws_o + idx * D;
 #pragma unroll
-  for (int j = 0; j < Gm::NJ; ++j) *reinterpret_cast<f32x4 *>(cb + m * D + 16 * j + 4 * g) = o[j];
-  if (g == 0) {
-    cb[16 * D + m] = m_run;
-    cb[16 * D + 16 + m] = l_run;
-  }
-  __syncthreads();
-  for (int it = threadIdx.x; it < G * D / 4; it += kThreads) {
-    const int h = it / (D / 4), d4 = it % (D / 4);
-    float mw[kWaves], M = kNegInf;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      mw[w] = reinterpret_cast<const float *>(smem + w * W::LDS_PER_WAVE_B)[16 * D + h];
-      M = fmaxf(M, mw[w]);
-    }
-    float L = 0.f;
-    f32x4 acc{0, 0, 0, 0};
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float *cw = reinterpret_cast<const float *>(smem + w * W::LDS_PER_WAVE_B);
-      const float e = (mw[w] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(mw[w] - M);
-      L += cw[16 * D + 16 + h] * e;
-      acc += *reinterpret_cast<const f32x4 *>(cw + h * D + 4 * d4) * e;
-    }
-    const float inv = (L > 0.f) ? vscale / L : 0.f;
-    acc *= inv;
-    const int head = kvh * G + h;
-    if (single) {
-      uint8_t *op = a.out + b * a.o_bs + head * a.o_hs + d4 * 8;
-      *reinterpret_cast<u32x2 *>(op) = u32x2{T::pack2(acc[0], acc[1]), T::pack2(acc[2], acc[3])};
-    } else {
-      const int64_t idx = (static_cast<int64_t>(b) * a.Hq + head) * a.num_splits + split;
-      *reinterpret_cast<f32x4 *>(a.ws_o + idx * D + 4 * d4) = acc;
-      if (d4 == 0) a.ws_lse[idx] = (L > 0.f) ? M + __log2f(L) : kNegInf;
-    }
+    for (int j = 0; j < Gm::NJ; ++j) *reinterpret_cast<f32x4 *>(wp + 16 * j + 4 * g) = o[j] * inv;
+    if (g == 0) a.ws_lse[idx] = (L > 0.f) ? m_run + __log2f(L) : kNegInf;
   }
 }
 
@@ -364,13 +354,14 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeArgs a, 
 template <class T, bool FP8, int D>
 int launch_decode(const DecodeArgs &a, int batch, hipStream_t s) {
   using W = DecodeWave<T, FP8, D>;
-  const size_t lds = static_cast<size_t>(kWaves) * W::LDS_PER_WAVE_B;
-  dim3 grid(a.num_splits, a.Hkv, batch);
-  static const bool pipe = env_int("NQ_DECODE_PIPE", 1) != 0;
-  if (pipe)
-    paged_decode_kernel<T, FP8, D, true><<<grid, kThreads, lds, s>>>(a);
+  const int hpw_env = env_int("NQ_DECODE_HPW", 0);
+  const int hpw = hpw_env == 4 || hpw_env == 8 ? hpw_env : (a.Hkv >= 8 ? 8 : 4);
+  dim3 grid(a.num_splits, (a.Hkv + hpw - 1) / hpw, batch);
+  const size_t lds = static_cast<size_t>(hpw) * W::LDS_PER_WAVE_B;
+  if (hpw == 8)
+    paged_decode_kernel<T, FP8, D, 8><<<grid, 64 * 8, lds, s>>>(a);
   else
-    paged_decode_kernel<T, FP8, D, false><<<grid, kThreads, lds, s>>>(a);
+    paged_decode_kernel<T, FP8, D, 4><<<grid, 64 * 4, lds, s>>>(a);
   int rc = check_launch("paged_decode");
   if (rc != NQ_OK || a.num_splits <= 1) return rc;
   constexpr int per_block = 256 / (D / 4);
@@ -395,6 +386,9 @@ extern "C" int nq_decode_plan(int batch, int num_q_heads, int num_kv_heads, int 
   int64_t split = env_int("NQ_DECODE_SPLIT_TOKENS", 512);
   split = (split + 127) / 128 * 128;
   if (split < 128) split = 128;
+  // a split's block-table entries are held one per lane: at most 63 blocks
+  const int64_t max_split = (63LL * block_size) / 128 * 128;
+  if (split > max_split) split = max_split;
   if (max_tokens <= split) {
     *num_splits = 1;
     *split_tokens = static_cast<int>((max_tokens + 127) / 128 * 128);
