@@ -174,9 +174,10 @@ struct DecodeWave {
 // step through the same tokens together, so the workgroup streams whole
 // contiguous cache rows, and no cross-wave merge is needed: each wave owns
 // its heads' softmax state.
-template <class T, bool FP8, int D, int HPW>
-__global__ __launch_bounds__(64 * HPW) __attribute__((amdgpu_waves_per_eu(3)))
+template <class T, bool FP8, int D, int HPW, int DEPTH, int WPE>
+__global__ __launch_bounds__(64 * HPW) __attribute__((amdgpu_waves_per_eu(WPE)))
 void paged_decode_kernel(const DecodeArgs a) {
+  static_assert(DEPTH == 1 || DEPTH == 2, "prefetch depth");
   using W = DecodeWave<T, FP8, D>;
   using Gm = Geo<D, FP8>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -218,21 +219,26 @@ void paged_decode_kernel(const DecodeArgs a) {
     for (int kk = 0; kk < Gm::NKK; ++kk) qf[kk] = hv ? load16(qp + (8 * g + 32 * kk) * 2) : u32x4{0, 0, 0, 0};
   }
 
-  // Raw K and V of the current step live in registers; each is refilled with
-  // the next step's loads as soon as it has been copied to LDS, so those
-  // loads are in flight during the rest of the step.  The refill is issued
-  // unconditionally (past the split it is an empty descriptor: zeros, no
-  // memory traffic) so the vector-memory wait counts are the same on every
-  // iteration and never drain the prefetch.
-  int t0 = t_begin;
+  // Raw K and V of DEPTH steps live in registers (one set per step in
+  // flight); a set is refilled with the step DEPTH ahead as soon as it has
+  // been copied to LDS, so those loads are in flight while the wave works
+  // through the steps before it.  The refill is issued unconditionally (past
+  // the split it is an empty descriptor: zeros, no memory traffic) so the
+  // vector-memory wait counts are identical on every iteration and never
+  // drain the prefetch.
   const int first_blk = t_begin / a.block_size;
   const int n_blk = (t_end - 1) / a.block_size - first_blk + 1;  // <= 64 (host plan)
   const int bt_lane = lane < n_blk ? bt_row[first_blk + lane] : -1;
-  u32x4 kraw[Gm::RAW], vraw[Gm::RAW];
-  int64_t row0 = W::step_row(a, bt_lane, first_blk, t0);
   const int voff0 = W::lane_voff(a, kvh, lane);
-  W::load(a.k_cache, a, row0, t0, t_end, voff0, kraw);
-  W::load(a.v_cache, a, row0, t0, t_end, voff0, vraw);
+  u32x4 kraw[DEPTH][Gm::RAW], vraw[DEPTH][Gm::RAW];
+  int64_t rows[DEPTH];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    const int td = t_begin + d * kStep;
+    rows[d] = td < t_end ? W::step_row(a, bt_lane, first_blk, td) : -1;
+    W::load(a.k_cache, a, rows[d], td, t_end, voff0, kraw[d]);
+    W::load(a.v_cache, a, rows[d], td, t_end, voff0, vraw[d]);
+  }
 
   uint8_t *tile = smem + wave * W::LDS_PER_WAVE_B;
 
@@ -241,12 +247,14 @@ void paged_decode_kernel(const DecodeArgs a) {
 #pragma unroll
   for (int j = 0; j < Gm::NJ; ++j) o[j] = f32x4{0, 0, 0, 0};
 
-  for (; t0 < t_end; t0 += kStep) {
-    const int t1 = t0 + kStep;
-    const int64_t row1 = (t1 < t_end) ? W::step_row(a, bt_lane, first_blk, t1) : -1;
+  // One 32-token step on register set (kr, vr) holding tokens t0..t0+31 of
+  // cache row `row`; returns the row of the step that refilled the set.
+  auto step = [&](int t0, int64_t row, u32x4 (&kr)[Gm::RAW], u32x4 (&vr)[Gm::RAW]) -> int64_t {
+    const int tn = t0 + DEPTH * kStep;
+    const int64_t rown = (tn < t_end) ? W::step_row(a, bt_lane, first_blk, tn) : -1;
     wave_lds_sync();  // the previous step's V^T reads are issued before the tile is overwritten
-    W::stage(tile, kraw, lane);
-    W::load(a.k_cache, a, row1, t1, t_end, voff0, kraw);  // empty past t_end
+    W::stage(tile, kr, lane);
+    W::load(a.k_cache, a, rown, tn, t_end, voff0, kr);  // empty past t_end
     wave_lds_sync();
     f32x4 s[2];
 #pragma unroll
@@ -256,15 +264,15 @@ void paged_decode_kernel(const DecodeArgs a) {
       for (int kk = 0; kk < Gm::NKK; ++kk) s[i] = T::mfma16x16x32(W::kfrag(tile, i, kk, m, g), qf[kk], s[i]);
     }
     wave_lds_sync();  // K operand reads are issued before V overwrites the tile
-    W::stage(tile, vraw, lane);
-    W::load(a.v_cache, a, row1, t1, t_end, voff0, vraw);
+    W::stage(tile, vr, lane);
+    W::load(a.v_cache, a, rown, tn, t_end, voff0, vr);
     float x[8];
     float mloc = kNegInf;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const bool valid = row0 >= 0 && t0 + 16 * i + 4 * g + rr < t_end;
+        const bool valid = row >= 0 && t0 + 16 * i + 4 * g + rr < t_end;
         const float v = valid ? s[i][rr] * sl2 : kNegInf;
         x[4 * i + rr] = v;
         mloc = fmaxf(mloc, v);
@@ -291,7 +299,15 @@ void paged_decode_kernel(const DecodeArgs a) {
       o[j] *= alpha;
       o[j] = T::mfma16x16x32(W::vfrag(tile, j, lane), pb, o[j]);
     }
-    row0 = row1;
+    return rown;
+  };
+
+  for (int t0 = t_begin; t0 < t_end; t0 += DEPTH * kStep) {
+    rows[0] = step(t0, rows[0], kraw[0], vraw[0]);
+    if constexpr (DEPTH > 1) {
+      if (t0 + kStep >= t_end) break;
+      rows[1] = step(t0 + kStep, rows[1], kraw[1], vraw[1]);
+    }
   }
 
   // ---- epilogue: lane (m, g) holds O^T[16j + 4g + r][head m]
@@ -351,17 +367,34 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeArgs a, 
   *reinterpret_cast<u32x2 *>(op) = u32x2{T::pack2(acc[0], acc[1]), T::pack2(acc[2], acc[3])};
 }
 
+// kv heads (= waves) per workgroup: 4 for 16-bit caches, 8 for fp8
+// (measured best on MI355X); NQ_DECODE_HPW=4|8 overrides for tuning.
+int decode_heads_per_wg(int hkv, bool fp8) {
+  const int env = env_int("NQ_DECODE_HPW", 0);
+  if (env == 4 || env == 8) return env;
+  return (fp8 && hkv >= 8) ? 8 : 4;
+}
+
 template <class T, bool FP8, int D>
 int launch_decode(const DecodeArgs &a, int batch, hipStream_t s) {
   using W = DecodeWave<T, FP8, D>;
-  const int hpw_env = env_int("NQ_DECODE_HPW", 0);
-  const int hpw = hpw_env == 4 || hpw_env == 8 ? hpw_env : (a.Hkv >= 8 ? 8 : 4);
+  const int hpw = decode_heads_per_wg(a.Hkv, FP8);
   dim3 grid(a.num_splits, (a.Hkv + hpw - 1) / hpw, batch);
   const size_t lds = static_cast<size_t>(hpw) * W::LDS_PER_WAVE_B;
-  if (hpw == 8)
-    paged_decode_kernel<T, FP8, D, 8><<<grid, 64 * 8, lds, s>>>(a);
-  else
-    paged_decode_kernel<T, FP8, D, 4><<<grid, 64 * 4, lds, s>>>(a);
+  // Register budget per wave = in-flight K/V (DEPTH steps) + state: two
+  // steps deep (bf16: 2 waves/SIMD, fp8: 3); NQ_DECODE_DEPTH=1 trades depth
+  // for occupancy.
+  const int depth_env = env_int("NQ_DECODE_DEPTH", 0);
+  const int depth = depth_env == 1 || depth_env == 2 ? depth_env : 2;
+#define NQ_DECODE_LAUNCH(H, DP, WP) paged_decode_kernel<T, FP8, D, H, DP, WP><<<grid, 64 * H, lds, s>>>(a)
+  if (hpw == 8) {
+    if (depth == 2) NQ_DECODE_LAUNCH(8, 2, FP8 ? 3 : 2);
+    else NQ_DECODE_LAUNCH(8, 1, FP8 ? 4 : 3);
+  } else {
+    if (depth == 2) NQ_DECODE_LAUNCH(4, 2, FP8 ? 3 : 2);
+    else NQ_DECODE_LAUNCH(4, 1, FP8 ? 4 : 3);
+  }
+#undef NQ_DECODE_LAUNCH
   int rc = check_launch("paged_decode");
   if (rc != NQ_OK || a.num_splits <= 1) return rc;
   constexpr int per_block = 256 / (D / 4);
@@ -375,15 +408,44 @@ int launch_decode(const DecodeArgs &a, int batch, hipStream_t s) {
 
 using namespace nq;
 
+namespace nq {
+namespace {
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+}  // namespace
+}  // namespace nq
+
+// Split size: one split per workgroup should carry enough tokens that the
+// workgroup's fixed costs (Q load, first-step latency, partial write) stay
+// small, while the grid still spreads over every CU.  Measured on MI355X:
+// 2048-token splits are best for the benchmark shapes; smaller batches get
+// smaller splits (down to 512) so the grid keeps ~one workgroup per CU at the
+// longest context the table allows.
 extern "C" int nq_decode_plan(int batch, int num_q_heads, int num_kv_heads, int max_blocks_per_seq,
                               int block_size, int kv_dtype, int *num_splits, int *split_tokens) {
   if (!num_splits || !split_tokens || batch <= 0 || num_kv_heads <= 0 || max_blocks_per_seq <= 0 ||
       block_size <= 0)
     return fail(NQ_EINVAL, "decode_plan: bad arguments");
   (void)num_q_heads;
-  (void)kv_dtype;
   const int64_t max_tokens = static_cast<int64_t>(max_blocks_per_seq) * block_size;
-  int64_t split = env_int("NQ_DECODE_SPLIT_TOKENS", 512);
+  const int hpw = decode_heads_per_wg(num_kv_heads, kv_dtype == NQ_FP8_E4M3);
+  const int64_t groups = (num_kv_heads + hpw - 1) / hpw;
+  int64_t split = env_int("NQ_DECODE_SPLIT_TOKENS", 0);
+  if (split <= 0) {
+    const int64_t per_cu = static_cast<int64_t>(batch) * groups * max_tokens / device_cus();
+    split = 512;
+    while (split < 2048 && split * 2 <= per_cu) split *= 2;
+  }
   split = (split + 127) / 128 * 128;
   if (split < 128) split = 128;
   // a split's block-table entries are held one per lane: at most 63 blocks
