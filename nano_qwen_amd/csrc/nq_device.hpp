@@ -32,9 +32,10 @@ struct BF16 {
   __device__ static inline float to_float(uint16_t h) {
     return __builtin_bit_cast(float, static_cast<uint32_t>(h) << 16);
   }
-  // two fp32 -> packed pair (lo = a)
+  // two fp32 -> packed pair (lo = a), one v_cvt_pk_bf16_f32 (RNE)
   __device__ static inline uint32_t pack2(float a, float b) {
-    return static_cast<uint32_t>(from_float(a)) | (static_cast<uint32_t>(from_float(b)) << 16);
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
   }
   // two fp8 e4m3 (bytes 0,1 of w, or 2,3 when HI) -> packed pair, exact
   template <bool HI>
@@ -102,6 +103,28 @@ __device__ inline u32x4 buffer_load16_nt(__amdgpu_buffer_rsrc_t r, int voffset) 
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 2));
 }
 
+// Direct global -> LDS copy (gfx950 LDS DMA, 16 bytes per lane): lane l's 16
+// bytes land at lds + 16 * l.  Completion is tracked by the vector-memory
+// counter only -- the compiler inserts no wait for it -- so callers pair it
+// with wait_vmcnt() and a workgroup barrier before reading the LDS.
+__device__ inline void dma16(const void *src, void *lds) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(lds), 16, 0, 0);
+}
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ inline void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// Workgroup barrier without the memory-model fence __syncthreads() implies
+// (which would wait for every outstanding load, including in-flight DMA).
+__device__ inline void raw_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Wave-level LDS ordering between lanes of ONE wave.  The LDS executes a
 // wave's DS instructions in issue order, so a read issued after a write (by
 // any lane of the same wave) sees it; only the compiler must be kept from
@@ -152,6 +175,18 @@ __device__ inline u32x2 lds_read_tr16(const uint16_t *p) {
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) s16x4 *)(p));
   return __builtin_bit_cast(u32x2, v);
+}
+// The same read issued as an opaque instruction: the compiler neither waits
+// for it nor for in-flight LDS DMA before it (the builtin carries no alias
+// information, so the backend would drain every outstanding DMA copy first).
+// The caller must wait for it with an s_waitcnt lgkmcnt(0) that names the
+// result registers as operands (so no consumer is scheduled above the wait).
+__device__ inline u32x2 lds_read_tr16_async(const void *p) {
+  u32x2 v;
+  const uint32_t a = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) const void *)(p)));
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(a));
+  return v;
 }
 
 constexpr float kLog2e = 1.4426950408889634f;

@@ -9,18 +9,26 @@
 // block table (any prefix hit in the batch, engine/model_runner.py:275-276)
 // K/V are the whole paged cache (layers/attention.py:65-66).
 //
-// Design (one workgroup = 4 waves = 128 query rows of one (sequence, head)):
-//  * grid (Hq * num_seqs, ceil(max_seqlen_q / 128)), q tiles dispatched
-//    last-row-first so the tiles with the most keys start earliest; tiles
-//    past a sequence's end exit at once.
-//  * K and V tiles of 64 keys are staged in LDS (fp8 caches are converted to
-//    the operand type while staging); each wave keeps its 32 query rows in
-//    registers as the B operand of S^T = K . Q^T (v_mfma_f32_16x16x32).
-//  * The S^T accumulator layout is the B-operand layout of O^T += V^T . P^T,
-//    so probabilities stay in registers; V^T operands are read transposed
-//    from the row-major LDS tile.
-//  * Online softmax in the log2 domain; key tiles beyond a wave's causal
-//    limit are skipped, the diagonal tile is masked element-wise.
+// Design (one workgroup = 4 waves; each wave = one query head x 32 rows):
+//  * GQA sharing in LDS: the waves of a workgroup are query heads of the SAME
+//    kv head (G4 = min(G, 4) heads x 4/G4 row blocks), so every K/V tile
+//    staged in LDS serves all of them; heads of one group also share the
+//    causal structure, so the waves run identical trip counts.
+//  * K/V tiles of 32 keys, double-buffered in LDS: the loads of tile j+1 are
+//    in flight while tile j is computed (one barrier per tile).  A tile never
+//    crosses a cache block (block_size % 32 == 0), so one scalar buffer
+//    descriptor covers it and keys past the causal limit read as zeros.  The
+//    sequence's block-table row is copied to LDS once.
+//  * S^T = K . Q^T and O^T += V^T . P^T on v_mfma_f32_16x16x32 with Q in
+//    registers; P stays in registers (the S^T accumulator layout is the PV
+//    B-operand layout); V^T comes from the row-major tile through
+//    ds_read_b64_tr_b16.  Chunks of a tile row are XOR-swizzled so the
+//    operand reads are bank-conflict free.
+//  * Online softmax in the log2 domain with lazy rescaling: O and l are only
+//    rescaled when a row maximum grows by more than 2^8, so P <= 256.
+//  * Grid order: last query tiles first (most keys), and XCD-aware: the
+//    consecutive tiles of one (sequence, kv head) run on the same XCD and
+//    share its L2.
 #include "nq_device.hpp"
 
 namespace nq {
@@ -28,8 +36,10 @@ namespace {
 
 constexpr int kPWaves = 4;
 constexpr int kPThreads = 64 * kPWaves;
-constexpr int kBM = 128;  // query rows per workgroup (32 per wave)
-constexpr int kBN = 64;   // keys per LDS tile
+constexpr int kRows = 32;    // query rows per wave
+constexpr int kKeys = 32;    // keys per LDS tile
+constexpr int kMaxBt = 4096;  // block-table entries staged in LDS (1M tokens at 256)
+constexpr float kRescale = 8.0f;  // log2 growth of a row max that forces a rescale
 
 struct PrefillArgs {
   const uint8_t *q;
@@ -45,131 +55,150 @@ struct PrefillArgs {
   int64_t num_blocks;
   uint8_t *out;
   int64_t o_rs, o_hs;  // bytes
-  int Hq, Hkv, G, block_size, num_seqs, n_qtiles;
+  int Hq, Hkv, G, G4, quads, block_size, num_seqs, n_qtiles, n_qtiles_dma;
   int causal;
   float scale_log2;
   const float *k_scale;
   const float *v_scale;
 };
 
+__device__ inline int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1) | (row & 8); }
+
 template <class T, bool FP8, int D>
-struct PrefillTile {
-  static constexpr int ROW = D + 8;  // LDS row stride in 16-bit elements (16-byte aligned rows)
+struct PTile {
+  static_assert(D == 128, "tile layout assumes head_dim 128");
+  static constexpr int ROWB = D * 2;            // LDS row: one key, 16-bit elements
+  static constexpr int TILE_B = kKeys * ROWB;   // one K (or V) tile
+  static constexpr int SRC_ROWB = FP8 ? D : D * 2;
+  static constexpr int SRC_CHUNKS = SRC_ROWB / 16;
+  static constexpr int LOADS = kKeys * SRC_CHUNKS / kPThreads;  // 16-byte loads per thread per tile
   static constexpr int NKK = D / 32;
   static constexpr int NJ = D / 16;
-  static constexpr int TILE_ELEMS = kBN * ROW;
-  static constexpr int LDS_BYTES = 2 * TILE_ELEMS * 2;
+  static constexpr int LDS_BYTES = 4 * TILE_B + kMaxBt * 4;  // K,V x 2 buffers + block table
 
-  // Cache/packed row of key j of the sequence, or -1 when unavailable.
-  __device__ static inline int64_t key_row(const PrefillArgs &a, int s, int k0, int j) {
-    if (a.block_tables == nullptr) return static_cast<int64_t>(k0) + j;
-    if (j / a.block_size >= a.max_blocks) return -1;
-    const int blk = a.block_tables[s * a.bt_stride + j / a.block_size];
-    if (blk < 0 || blk >= a.num_blocks) return -1;
-    return static_cast<int64_t>(blk) * a.block_size + j % a.block_size;
-  }
-
-  // Stage K and V rows [kbase, kbase+64) of kv head kvh into LDS; keys at or
-  // past key_end are zero.
-  __device__ static inline void stage(const PrefillArgs &a, uint16_t *kt, uint16_t *vt, int s, int k0,
-                                      int kvh, int kbase, int key_end) {
-    if constexpr (!FP8) {
-      constexpr int CH = D / 8;  // 16-byte chunks per row
-      for (int c = threadIdx.x; c < kBN * CH; c += kPThreads) {
-        const int r = c / CH, col = (c % CH) * 8;
-        const int j = kbase + r;
-        u32x4 kw{0, 0, 0, 0}, vw{0, 0, 0, 0};
-        if (j < key_end) {
-          const int64_t row = key_row(a, s, k0, j);
-          if (row >= 0) {
-            const int64_t off = row * a.kv_rs + (static_cast<int64_t>(kvh) * D + col) * 2;
-            kw = load16(a.k + off);
-            vw = load16(a.v + off);
-          }
-        }
-        *reinterpret_cast<u32x4 *>(kt + r * ROW + col) = kw;
-        *reinterpret_cast<u32x4 *>(vt + r * ROW + col) = vw;
-      }
+  // Issue the loads of key tile [kbase, kbase + 32) of kv head kvh; keys at or
+  // past key_end (or in a missing block) read as zeros.
+  __device__ static inline void load(const PrefillArgs &a, const int32_t *lds_bt, int k0, int kvh, int kbase,
+                                     int key_end, u32x4 (&kr)[LOADS], u32x4 (&vr)[LOADS]) {
+    int64_t row0;
+    if (a.block_tables == nullptr) {
+      row0 = static_cast<int64_t>(k0) + kbase;
     } else {
-      constexpr int CH = D / 16;  // 16-byte fp8 chunks per row
-      for (int c = threadIdx.x; c < kBN * CH; c += kPThreads) {
-        const int r = c / CH, col = (c % CH) * 16;
-        const int j = kbase + r;
-        u32x4 kw{0, 0, 0, 0}, vw{0, 0, 0, 0};
-        if (j < key_end) {
-          const int64_t row = key_row(a, s, k0, j);
-          if (row >= 0) {
-            const int64_t off = row * a.kv_rs + static_cast<int64_t>(kvh) * D + col;
-            kw = load16(a.k + off);
-            vw = load16(a.v + off);
-          }
-        }
-        u32x4 k0w, k1w, v0w, v1w;
-        k0w = u32x4{T::template fp8x2<false>(kw[0]), T::template fp8x2<true>(kw[0]),
-                    T::template fp8x2<false>(kw[1]), T::template fp8x2<true>(kw[1])};
-        k1w = u32x4{T::template fp8x2<false>(kw[2]), T::template fp8x2<true>(kw[2]),
-                    T::template fp8x2<false>(kw[3]), T::template fp8x2<true>(kw[3])};
-        v0w = u32x4{T::template fp8x2<false>(vw[0]), T::template fp8x2<true>(vw[0]),
-                    T::template fp8x2<false>(vw[1]), T::template fp8x2<true>(vw[1])};
-        v1w = u32x4{T::template fp8x2<false>(vw[2]), T::template fp8x2<true>(vw[2]),
-                    T::template fp8x2<false>(vw[3]), T::template fp8x2<true>(vw[3])};
-        *reinterpret_cast<u32x4 *>(kt + r * ROW + col) = k0w;
-        *reinterpret_cast<u32x4 *>(kt + r * ROW + col + 8) = k1w;
-        *reinterpret_cast<u32x4 *>(vt + r * ROW + col) = v0w;
-        *reinterpret_cast<u32x4 *>(vt + r * ROW + col + 8) = v1w;
+      const int blk = __builtin_amdgcn_readfirstlane(lds_bt[kbase / a.block_size]);
+      row0 = (blk >= 0 && blk < a.num_blocks) ? static_cast<int64_t>(blk) * a.block_size + kbase % a.block_size : -1;
+    }
+    const int nvalid = row0 >= 0 ? max(0, min(kKeys, key_end - kbase)) : 0;
+    const int64_t base_off = (row0 >= 0 ? row0 : 0) * a.kv_rs + static_cast<int64_t>(kvh) * SRC_ROWB;
+    const uint32_t nbytes = nvalid > 0 ? static_cast<uint32_t>((nvalid - 1) * a.kv_rs + SRC_ROWB) : 0u;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k + base_off, nbytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v + base_off, nbytes);
+#pragma unroll
+    for (int c = 0; c < LOADS; ++c) {
+      const int idx = threadIdx.x + c * kPThreads;
+      const int row = idx / SRC_CHUNKS, ch = idx % SRC_CHUNKS;
+      const int off = static_cast<int>(row * a.kv_rs) + ch * 16;
+      kr[c] = buffer_load16_nt(rk, off);
+      vr[c] = buffer_load16_nt(rv, off);
+    }
+  }
+
+  // Write a loaded tile into LDS (row = key, 16-bit elements, swizzled chunks).
+  __device__ static inline void stage(uint8_t *kt, uint8_t *vt, const u32x4 (&kr)[LOADS],
+                                      const u32x4 (&vr)[LOADS]) {
+#pragma unroll
+    for (int c = 0; c < LOADS; ++c) {
+      const int idx = threadIdx.x + c * kPThreads;
+      const int row = idx / SRC_CHUNKS, ch = idx % SRC_CHUNKS;
+      uint8_t *kp = kt + row * ROWB, *vp = vt + row * ROWB;
+      if constexpr (!FP8) {
+        *reinterpret_cast<u32x4 *>(kp + ((ch ^ swz(row)) << 4)) = kr[c];
+        *reinterpret_cast<u32x4 *>(vp + ((ch ^ swz(row)) << 4)) = vr[c];
+      } else {
+        const u32x4 &k = kr[c], &v = vr[c];
+        *reinterpret_cast<u32x4 *>(kp + (((2 * ch) ^ swz(row)) << 4)) =
+            u32x4{T::template fp8x2<false>(k[0]), T::template fp8x2<true>(k[0]), T::template fp8x2<false>(k[1]),
+                  T::template fp8x2<true>(k[1])};
+        *reinterpret_cast<u32x4 *>(kp + (((2 * ch + 1) ^ swz(row)) << 4)) =
+            u32x4{T::template fp8x2<false>(k[2]), T::template fp8x2<true>(k[2]), T::template fp8x2<false>(k[3]),
+                  T::template fp8x2<true>(k[3])};
+        *reinterpret_cast<u32x4 *>(vp + (((2 * ch) ^ swz(row)) << 4)) =
+            u32x4{T::template fp8x2<false>(v[0]), T::template fp8x2<true>(v[0]), T::template fp8x2<false>(v[1]),
+                  T::template fp8x2<true>(v[1])};
+        *reinterpret_cast<u32x4 *>(vp + (((2 * ch + 1) ^ swz(row)) << 4)) =
+            u32x4{T::template fp8x2<false>(v[2]), T::template fp8x2<true>(v[2]), T::template fp8x2<false>(v[3]),
+                  T::template fp8x2<true>(v[3])};
       }
     }
   }
 
-  // K operand: lane (m, g) = key row `r0 + m`, dims 8g + 32kk + [0, 8).
-  __device__ static inline u32x4 kfrag(const uint16_t *kt, int r0, int kk, int m, int g) {
-    return *reinterpret_cast<const u32x4 *>(kt + (r0 + m) * ROW + 8 * g + 32 * kk);
+  // K operand: lane (m, g) = key row 16*ks + m, dims 8(g + 4kk) .. +8.
+  __device__ static inline u32x4 kfrag(const uint8_t *kt, int ks, int kk, int m, int g) {
+    const int row = 16 * ks + m;
+    return *reinterpret_cast<const u32x4 *>(kt + row * ROWB + (((g + 4 * kk) ^ swz(row)) << 4));
   }
 
-  // V^T operand of output block j over keys r0 .. r0+31:
-  // lane (m, g) takes V[r0 + psi(g, i)][16j + m].
-  __device__ static inline u32x4 vfrag(const uint16_t *vt, int r0, int j, int m, int g) {
-    const uint16_t *c0 = vt + (r0 + 4 * g) * ROW + 16 * j + m;
-    const uint16_t *c1 = c0 + 16 * ROW;
-    uint32_t e[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      e[i] = c0[i * ROW];
-      e[4 + i] = c1[i * ROW];
-    }
-    return u32x4{e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16)};
+  // V^T operand of output block j over the tile's 32 keys: lane (m, g) takes
+  // V[psi(g, i)][16j + m], psi(g, i) = 4g + i (i < 4) or 16 + 4g + i - 4.
+  __device__ static inline u32x4 vfrag(const uint8_t *vt, int j, int lane) {
+    const int g = lane >> 4, k = (lane >> 2) & 3, q = lane & 3;
+    const int r0 = 4 * g + k, r1 = r0 + 16;
+    const int lc = 2 * j + (q >> 1), sub = (q & 1) * 8;
+    const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t *>(vt + r0 * ROWB + ((lc ^ swz(r0)) << 4) + sub));
+    const u32x2 hi = lds_read_tr16(reinterpret_cast<const uint16_t *>(vt + r1 * ROWB + ((lc ^ swz(r1)) << 4) + sub));
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
   }
 };
 
 template <class T, bool FP8, int D>
-__global__ __launch_bounds__(kPThreads) void varlen_prefill_kernel(const PrefillArgs a) {
-  using PT = PrefillTile<T, FP8, D>;
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void varlen_prefill_kernel(const PrefillArgs a) {
+  using PT = PTile<T, FP8, D>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint16_t *kt = reinterpret_cast<uint16_t *>(smem);
-  uint16_t *vt = kt + PT::TILE_ELEMS;
+  int32_t *lds_bt = reinterpret_cast<int32_t *>(smem + 4 * PT::TILE_B);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m = lane & 15, g = lane >> 4;
-  const int h = blockIdx.x % a.Hq, s = blockIdx.x / a.Hq;
-  const int qt = a.n_qtiles - 1 - static_cast<int>(blockIdx.y);
+
+  // ---- XCD-aware, longest-first work mapping.  Hardware places workgroup L
+  // on XCD L % 8; logical index Lg = (L % 8) * per + L / 8 makes consecutive
+  // logical indices -- consecutive query tiles of one (sequence, kv-head
+  // quad) -- run on one XCD.
+  const int n_x = a.n_qtiles, n_y = a.Hkv * a.quads;
+  const int total = n_x * n_y * a.num_seqs;
+  const int L = blockIdx.x;
+  const int per = (total + 7) / 8;
+  const int Lg = (L % 8) * per + L / 8;
+  if (Lg >= total) return;
+  const int xt = Lg % n_x;
+  const int yz = Lg / n_x;
+  const int y = yz % n_y, s = yz / n_y;
+  const int qt = n_x - 1 - xt;  // last tiles first: they have the most keys
+  const int kvh = y / a.quads, quad = y % a.quads;
+  const int rb = 4 / a.G4;  // row blocks of 32 per workgroup
+  const int head = kvh * a.G + quad * 4 + (wave % a.G4);
   const int q0 = a.cu_q[s], Lq = a.cu_q[s + 1] - q0;
-  const int row_begin = qt * kBM;
+  const int row_begin = qt * kRows * rb;
   if (row_begin >= Lq) return;
   const int k0 = a.cu_k[s], Lk = a.cu_k[s + 1] - k0;
   const int P = Lk - Lq;
-  const int kvh = h / a.G;
-  const int row_last = min(row_begin + kBM, Lq) - 1;
+  const int row_last = min(row_begin + kRows * rb, Lq) - 1;
   const int key_end = a.causal ? max(0, min(Lk, row_last + P + 1)) : Lk;
-  const int n_kt = (key_end + kBN - 1) / kBN;
+  const int n_kt = (key_end + kKeys - 1) / kKeys;
 
   const float kscale = FP8 ? a.k_scale[kvh] : 1.0f;
   const float vscale = FP8 ? a.v_scale[kvh] : 1.0f;
   const float sl2 = a.scale_log2 * kscale;
 
+  // stage the sequence's block-table entries once
+  if (a.block_tables != nullptr) {
+    const int n_bt = min(min((key_end + a.block_size - 1) / a.block_size, a.max_blocks), kMaxBt);
+    for (int i = threadIdx.x; i < n_bt; i += kPThreads) lds_bt[i] = a.block_tables[s * a.bt_stride + i];
+  }
+
   // This wave's rows: wrow0 .. wrow0+31 (two 16-row sub-tiles).
-  const int wrow0 = row_begin + 32 * wave;
+  const int wrow0 = row_begin + kRows * (wave / a.G4);
   const bool wave_live = wrow0 < Lq;
-  const int wrow_last = min(wrow0 + 31, Lq - 1);
+  const int wrow_last = min(wrow0 + kRows - 1, Lq - 1);
   const int wave_key_end = a.causal ? min(Lk, wrow_last + P + 1) : Lk;
 
   u32x4 qf[2][PT::NKK];
@@ -177,29 +206,33 @@ __global__ __launch_bounds__(kPThreads) void varlen_prefill_kernel(const Prefill
   for (int qs = 0; qs < 2; ++qs) {
     const int r = wrow0 + 16 * qs + m;
     const bool ok = r < Lq;
-    const uint8_t *qp = a.q + static_cast<int64_t>(q0 + (ok ? r : 0)) * a.q_rs + static_cast<int64_t>(h) * a.q_hs;
+    const uint8_t *qp = a.q + static_cast<int64_t>(q0 + (ok ? r : 0)) * a.q_rs + static_cast<int64_t>(head) * a.q_hs;
 #pragma unroll
-    for (int kk = 0; kk < PT::NKK; ++kk)
-      qf[qs][kk] = ok ? load16(qp + (8 * g + 32 * kk) * 2) : u32x4{0, 0, 0, 0};
+    for (int kk = 0; kk < PT::NKK; ++kk) qf[qs][kk] = ok ? load16(qp + (8 * g + 32 * kk) * 2) : u32x4{0, 0, 0, 0};
   }
 
-  float m_run[2] = {kNegInf, kNegInf}, l_run[2] = {0.f, 0.f};
+  float m_use[2] = {kNegInf, kNegInf}, l_run[2] = {0.f, 0.f};
   f32x4 o[2][PT::NJ];
 #pragma unroll
   for (int qs = 0; qs < 2; ++qs)
 #pragma unroll
     for (int j = 0; j < PT::NJ; ++j) o[qs][j] = f32x4{0, 0, 0, 0};
 
-  for (int ktile = 0; ktile < n_kt; ++ktile) {
-    const int kbase = ktile * kBN;
-    __syncthreads();
-    PT::stage(a, kt, vt, s, k0, kvh, kbase, key_end);
-    __syncthreads();
-    if (!wave_live) continue;
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const int kb = kbase + 32 * hh;
-      if (kb >= wave_key_end) break;
+  __syncthreads();  // block table visible
+  u32x4 kr[PT::LOADS], vr[PT::LOADS];
+  if (n_kt > 0) {
+    PT::load(a, lds_bt, k0, kvh, 0, key_end, kr, vr);
+    PT::stage(smem, smem + PT::TILE_B, kr, vr);
+  }
+  __syncthreads();
+
+  for (int jt = 0; jt < n_kt; ++jt) {
+    const int kbase = jt * kKeys;
+    const uint8_t *kt = smem + (jt & 1) * 2 * PT::TILE_B;
+    const uint8_t *vt = kt + PT::TILE_B;
+    const bool more = jt + 1 < n_kt;
+    if (more) PT::load(a, lds_bt, k0, kvh, kbase + kKeys, key_end, kr, vr);
+    if (wave_live && kbase < wave_key_end) {
       f32x4 sc[2][2];
 #pragma unroll
       for (int qs = 0; qs < 2; ++qs)
@@ -209,14 +242,14 @@ __global__ __launch_bounds__(kPThreads) void varlen_prefill_kernel(const Prefill
       for (int kk = 0; kk < PT::NKK; ++kk) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          const u32x4 kf = PT::kfrag(kt, 32 * hh + 16 * ks, kk, m, g);
+          const u32x4 kf = PT::kfrag(kt, ks, kk, m, g);
 #pragma unroll
           for (int qs = 0; qs < 2; ++qs) sc[qs][ks] = T::mfma16x16x32(kf, qf[qs][kk], sc[qs][ks]);
         }
       }
-      const bool need_mask = kb + 31 > wrow0 + P || kb + 31 >= Lk;
+      // mask only where the tile crosses the causal diagonal or the key end
+      const bool need_mask = kbase + kKeys - 1 > wrow0 + P || kbase + kKeys > Lk;
       u32x4 pb[2];
-      float alpha[2];
 #pragma unroll
       for (int qs = 0; qs < 2; ++qs) {
         const int row = wrow0 + 16 * qs + m;
@@ -227,51 +260,287 @@ __global__ __launch_bounds__(kPThreads) void varlen_prefill_kernel(const Prefill
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) {
-            const int j = kb + 16 * ks + 4 * g + rr;
+            const int j = kbase + 16 * ks + 4 * g + rr;
             float v = sc[qs][ks][rr] * sl2;
             if (need_mask && j > lim) v = kNegInf;
             x[4 * ks + rr] = v;
             mloc = fmaxf(mloc, v);
           }
-        mloc = xor_max(mloc, 16);
-        mloc = xor_max(mloc, 32);
-        const float m_new = fmaxf(m_run[qs], mloc);
-        const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-        alpha[qs] = __builtin_amdgcn_exp2f(m_run[qs] - m_use);
+        mloc = max32(max16(mloc));
+        // lazy rescale: only when some row of the wave grew by > 2^kRescale
+        if (__builtin_amdgcn_ballot_w64(mloc > m_use[qs] + kRescale) != 0) {
+          const float m_new = fmaxf(m_use[qs], mloc);
+          const float alpha = (m_use[qs] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(m_use[qs] - m_new);
+          l_run[qs] *= alpha;
+#pragma unroll
+          for (int j = 0; j < PT::NJ; ++j) o[qs][j] *= alpha;
+          m_use[qs] = m_new;
+        }
+        const float mref = (m_use[qs] == kNegInf) ? 0.f : m_use[qs];
         float psum = 0.f;
         uint32_t pw[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const float p0 = __builtin_amdgcn_exp2f(x[2 * t] - m_use);
-          const float p1 = __builtin_amdgcn_exp2f(x[2 * t + 1] - m_use);
+          const float p0 = __builtin_amdgcn_exp2f(x[2 * t] - mref);
+          const float p1 = __builtin_amdgcn_exp2f(x[2 * t + 1] - mref);
           psum += p0 + p1;
           pw[t] = T::pack2(p0, p1);
         }
-        l_run[qs] = l_run[qs] * alpha[qs] + psum;
-        m_run[qs] = m_new;
+        l_run[qs] += psum;
         pb[qs] = u32x4{pw[0], pw[1], pw[2], pw[3]};
       }
 #pragma unroll
       for (int j = 0; j < PT::NJ; ++j) {
-        const u32x4 vf = PT::vfrag(vt, 32 * hh, j, m, g);
+        const u32x4 vf = PT::vfrag(vt, j, lane);
 #pragma unroll
-        for (int qs = 0; qs < 2; ++qs) {
-          o[qs][j] *= alpha[qs];
-          o[qs][j] = T::mfma16x16x32(vf, pb[qs], o[qs][j]);
-        }
+        for (int qs = 0; qs < 2; ++qs) o[qs][j] = T::mfma16x16x32(vf, pb[qs], o[qs][j]);
       }
     }
+    if (more) {
+      uint8_t *nk = smem + ((jt + 1) & 1) * 2 * PT::TILE_B;
+      PT::stage(nk, nk + PT::TILE_B, kr, vr);
+    }
+    __syncthreads();
   }
 
   if (!wave_live) return;
 #pragma unroll
   for (int qs = 0; qs < 2; ++qs) {
-    float l = xor_sum(l_run[qs], 16);
-    l = xor_sum(l, 32);
+    const float l = sum32(sum16(l_run[qs]));
     const int row = wrow0 + 16 * qs + m;
     if (row >= Lq) continue;
     const float inv = l > 0.f ? vscale / l : 0.f;
-    uint8_t *op = a.out + static_cast<int64_t>(q0 + row) * a.o_rs + static_cast<int64_t>(h) * a.o_hs;
+    uint8_t *op = a.out + static_cast<int64_t>(q0 + row) * a.o_rs + static_cast<int64_t>(head) * a.o_hs;
+#pragma unroll
+    for (int j = 0; j < PT::NJ; ++j) {
+      const f32x4 v = o[qs][j] * inv;
+      *reinterpret_cast<u32x2 *>(op + (16 * j + 4 * g) * 2) = u32x2{T::pack2(v[0], v[1]), T::pack2(v[2], v[3])};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit K/V: 8-wave workgroups fed by an LDS DMA ring.
+//
+// K/V tiles of 32 keys go HBM/L2 -> LDS directly (global_load_lds_dwordx4,
+// no VGPRs), into a ring of kStages slots, so kStages-1 tiles are in flight
+// while one is computed.  Each wave copies 4 rows of K and 4 of V per tile;
+// it waits for its own copies (vmcnt) and a raw workgroup barrier makes the
+// whole tile visible.  The chunk swizzle of the LDS tile is produced by the
+// source address each lane fetches.
+constexpr int kNW = 8;  // waves per workgroup
+constexpr int kStages = 4;
+
+template <class T, int D>
+struct DTile {
+  static_assert(D == 128, "tile layout assumes head_dim 128");
+  static constexpr int ROWB = D * 2;
+  static constexpr int TILE_B = kKeys * ROWB;   // 8 KiB per K (or V) tile
+  static constexpr int SLOT_B = 2 * TILE_B;     // K + V
+  static constexpr int LDS_BYTES = kStages * SLOT_B + kMaxBt * 4;
+};
+
+template <class T, int D>
+__global__ __launch_bounds__(64 * kNW) __attribute__((amdgpu_waves_per_eu(2)))
+void varlen_prefill_dma_kernel(const PrefillArgs a) {
+  using DT = DTile<T, D>;
+  using PT = PTile<T, false, D>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  int32_t *lds_bt = reinterpret_cast<int32_t *>(smem + kStages * DT::SLOT_B);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m = lane & 15, g = lane >> 4;
+
+  // XCD-aware, longest-first work mapping (see varlen_prefill_kernel).
+  const int n_x = a.n_qtiles, n_y = a.Hkv * a.quads;
+  const int total = n_x * n_y * a.num_seqs;
+  const int L = blockIdx.x;
+  const int per = (total + 7) / 8;
+  const int Lg = (L % 8) * per + L / 8;
+  if (Lg >= total) return;
+  const int xt = Lg % n_x;
+  const int yz = Lg / n_x;
+  const int y = yz % n_y, s = yz / n_y;
+  const int qt = n_x - 1 - xt;
+  const int kvh = y / a.quads, quad = y % a.quads;
+  const int rb = kNW / a.G4;  // row blocks of 32 per workgroup
+  const int head = kvh * a.G + quad * 4 + (wave % a.G4);
+  const int q0 = a.cu_q[s], Lq = a.cu_q[s + 1] - q0;
+  const int row_begin = qt * kRows * rb;
+  if (row_begin >= Lq) return;
+  const int k0 = a.cu_k[s], Lk = a.cu_k[s + 1] - k0;
+  const int P = Lk - Lq;
+  const int row_last = min(row_begin + kRows * rb, Lq) - 1;
+  const int key_end = a.causal ? max(0, min(Lk, row_last + P + 1)) : Lk;
+  const int n_kt = (key_end + kKeys - 1) / kKeys;
+  const float sl2 = a.scale_log2;
+
+  if (a.block_tables != nullptr) {
+    const int n_bt = min(min((key_end + a.block_size - 1) / a.block_size, a.max_blocks), kMaxBt);
+    for (int i = threadIdx.x; i < n_bt; i += 64 * kNW) lds_bt[i] = a.block_tables[s * a.bt_stride + i];
+  }
+
+  const int wrow0 = row_begin + kRows * (wave / a.G4);
+  const bool wave_live = wrow0 < Lq;
+  const int wrow_last = min(wrow0 + kRows - 1, Lq - 1);
+  const int wave_key_end = a.causal ? min(Lk, wrow_last + P + 1) : Lk;
+
+  u32x4 qf[2][PT::NKK];
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    const int r = wrow0 + 16 * qs + m;
+    const bool ok = r < Lq;
+    const uint8_t *qp = a.q + static_cast<int64_t>(q0 + (ok ? r : 0)) * a.q_rs + static_cast<int64_t>(head) * a.q_hs;
+#pragma unroll
+    for (int kk = 0; kk < PT::NKK; ++kk) qf[qs][kk] = ok ? load16(qp + (8 * g + 32 * kk) * 2) : u32x4{0, 0, 0, 0};
+  }
+
+  __syncthreads();  // block table in LDS
+
+  // This lane's DMA row within a tile (wave w copies rows 4w..4w+3) and the
+  // logical chunk it fetches for its fixed LDS position.
+  const int drow = 4 * wave + (lane >> 4);
+  const int dchunk = (lane & 15) ^ swz(drow);
+  // Copy tile jt (clamped: a slot past the last tile is refilled with the
+  // last tile, which is never read) into ring slot `slot`.
+  auto issue = [&](int jt, int slot) {
+    jt = min(jt, n_kt - 1);
+    const int kbase = jt * kKeys;
+    const int nvalid = min(kKeys, key_end - kbase);  // >= 1
+    const int r = min(drow, nvalid - 1);              // rows past the end repeat a valid key (masked)
+    int64_t row;
+    if (a.block_tables == nullptr) {
+      row = static_cast<int64_t>(k0) + kbase + r;
+    } else {
+      const int blk = __builtin_amdgcn_readfirstlane(lds_bt[kbase / a.block_size]);
+      const int bb = (blk >= 0 && blk < a.num_blocks) ? blk : 0;  // a missing block reads block 0 (masked below)
+      row = static_cast<int64_t>(bb) * a.block_size + kbase % a.block_size + r;
+    }
+    const int64_t off = row * a.kv_rs + static_cast<int64_t>(kvh) * DT::ROWB + dchunk * 16;
+    uint8_t *dst = smem + slot * DT::SLOT_B + wave * 1024;
+    dma16(a.k + off, dst);
+    dma16(a.v + off, dst + DT::TILE_B);
+  };
+
+  float m_use[2] = {kNegInf, kNegInf}, l_run[2] = {0.f, 0.f};
+  f32x4 o[2][PT::NJ];
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+    for (int j = 0; j < PT::NJ; ++j) o[qs][j] = f32x4{0, 0, 0, 0};
+
+  if (n_kt > 0) {
+#pragma unroll
+    for (int st = 0; st < kStages - 1; ++st) issue(st, st);
+  }
+  for (int jt = 0; jt < n_kt; ++jt) {
+    wait_vmcnt<2 * (kStages - 2)>();  // this wave's copies of tile jt have landed
+    wait_lgkmcnt0();                   // and its reads of tile jt-1 are done
+    raw_barrier();                     // tile jt complete; slot of tile jt-1 free
+    issue(jt + kStages - 1, (jt + kStages - 1) % kStages);
+    const int kbase = jt * kKeys;
+    const uint8_t *kt = smem + (jt % kStages) * DT::SLOT_B;
+    const uint8_t *vt = kt + DT::TILE_B;
+    bool blk_ok = true;
+    if (a.block_tables != nullptr) {
+      const int blk = __builtin_amdgcn_readfirstlane(lds_bt[kbase / a.block_size]);
+      blk_ok = blk >= 0 && blk < a.num_blocks;
+    }
+    if (wave_live && kbase < wave_key_end) {
+      f32x4 sc[2][2];
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = f32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int kk = 0; kk < PT::NKK; ++kk) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const u32x4 kf = PT::kfrag(kt, ks, kk, m, g);
+#pragma unroll
+          for (int qs = 0; qs < 2; ++qs) sc[qs][ks] = T::mfma16x16x32(kf, qf[qs][kk], sc[qs][ks]);
+        }
+      }
+      const bool need_mask = !blk_ok || kbase + kKeys - 1 > wrow0 + P || kbase + kKeys > Lk;
+      u32x4 pb[2];
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) {
+        const int row = wrow0 + 16 * qs + m;
+        int lim = a.causal ? min(Lk - 1, row + P) : Lk - 1;  // last visible key
+        if (!blk_ok) lim = -1;
+        float x[8];
+        float mloc = kNegInf;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const int j = kbase + 16 * ks + 4 * g + rr;
+            float v = sc[qs][ks][rr] * sl2;
+            if (need_mask && j > lim) v = kNegInf;
+            x[4 * ks + rr] = v;
+            mloc = fmaxf(mloc, v);
+          }
+        mloc = max32(max16(mloc));
+        if (__builtin_amdgcn_ballot_w64(mloc > m_use[qs] + kRescale) != 0) {
+          const float m_new = fmaxf(m_use[qs], mloc);
+          const float alpha = (m_use[qs] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(m_use[qs] - m_new);
+          l_run[qs] *= alpha;
+#pragma unroll
+          for (int j = 0; j < PT::NJ; ++j) o[qs][j] *= alpha;
+          m_use[qs] = m_new;
+        }
+        const float mref = (m_use[qs] == kNegInf) ? 0.f : m_use[qs];
+        float psum = 0.f;
+        uint32_t pw[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float p0 = __builtin_amdgcn_exp2f(x[2 * t] - mref);
+          const float p1 = __builtin_amdgcn_exp2f(x[2 * t + 1] - mref);
+          psum += p0 + p1;
+          pw[t] = T::pack2(p0, p1);
+        }
+        l_run[qs] += psum;
+        pb[qs] = u32x4{pw[0], pw[1], pw[2], pw[3]};
+      }
+      // V^T operands: all 16 transposing reads issued back to back (opaque to
+      // the compiler, so it does not drain the DMA ring), one LDS wait.
+      u32x4 vf[PT::NJ];
+      {
+        const int vg = lane >> 4, vk = (lane >> 2) & 3, vq = lane & 3;
+        const int r0 = 4 * vg + vk, r1 = r0 + 16;
+#pragma unroll
+        for (int j = 0; j < PT::NJ; ++j) {
+          const int lc = 2 * j + (vq >> 1), sub = (vq & 1) * 8;
+          const u32x2 lo = lds_read_tr16_async(vt + r0 * PT::ROWB + ((lc ^ swz(r0)) << 4) + sub);
+          const u32x2 hi = lds_read_tr16_async(vt + r1 * PT::ROWB + ((lc ^ swz(r1)) << 4) + sub);
+          vf[j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+      }
+      // The wait names the fragments as in/out operands, so no consumer can
+      // be scheduled above it.
+      static_assert(PT::NJ == 8, "operand list below");
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(vf[0]), "+v"(vf[1]), "+v"(vf[2]), "+v"(vf[3]), "+v"(vf[4]), "+v"(vf[5]), "+v"(vf[6]),
+                     "+v"(vf[7])
+                   :
+                   : "memory");
+#pragma unroll
+      for (int j = 0; j < PT::NJ; ++j) {
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) o[qs][j] = T::mfma16x16x32(vf[j], pb[qs], o[qs][j]);
+      }
+    }
+  }
+  wait_vmcnt<0>();  // drain the clamped tail copies before the workgroup can exit
+
+  if (!wave_live) return;
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    const float l = sum32(sum16(l_run[qs]));
+    const int row = wrow0 + 16 * qs + m;
+    if (row >= Lq) continue;
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    uint8_t *op = a.out + static_cast<int64_t>(q0 + row) * a.o_rs + static_cast<int64_t>(head) * a.o_hs;
 #pragma unroll
     for (int j = 0; j < PT::NJ; ++j) {
       const f32x4 v = o[qs][j] * inv;
@@ -281,10 +550,21 @@ __global__ __launch_bounds__(kPThreads) void varlen_prefill_kernel(const Prefill
 }
 
 template <class T, bool FP8, int D>
-int launch_prefill(const PrefillArgs &a, hipStream_t s) {
-  using PT = PrefillTile<T, FP8, D>;
-  dim3 grid(a.Hq * a.num_seqs, a.n_qtiles);
-  varlen_prefill_kernel<T, FP8, D><<<grid, kPThreads, PT::LDS_BYTES, s>>>(a);
+int launch_prefill(PrefillArgs a, hipStream_t s) {
+  if constexpr (!FP8) {
+    using DT = DTile<T, D>;
+    a.n_qtiles = a.n_qtiles_dma;
+    const int64_t total = static_cast<int64_t>(a.n_qtiles) * a.Hkv * a.quads * a.num_seqs;
+    if (total > 0x7fffffff) return fail(NQ_EINVAL, "varlen_prefill: grid too large");
+    const int grid = static_cast<int>((total + 7) / 8 * 8);
+    varlen_prefill_dma_kernel<T, D><<<grid, 64 * kNW, DT::LDS_BYTES, s>>>(a);
+  } else {
+    using PT = PTile<T, FP8, D>;
+    const int64_t total = static_cast<int64_t>(a.n_qtiles) * a.Hkv * a.quads * a.num_seqs;
+    if (total > 0x7fffffff) return fail(NQ_EINVAL, "varlen_prefill: grid too large");
+    const int grid = static_cast<int>((total + 7) / 8 * 8);
+    varlen_prefill_kernel<T, FP8, D><<<grid, kPThreads, PT::LDS_BYTES, s>>>(a);
+  }
   return check_launch("varlen_prefill");
 }
 
@@ -307,6 +587,9 @@ extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_
   if (num_q_heads % num_kv_heads != 0)
     return fail(NQ_EINVAL, "varlen_prefill: num_q_heads %d not a multiple of num_kv_heads %d", num_q_heads,
                 num_kv_heads);
+  const int G = num_q_heads / num_kv_heads;
+  if (G > 4 && G % 4 != 0) return fail(NQ_EUNSUPPORTED, "varlen_prefill: GQA group %d (need <= 4 or a multiple of 4)", G);
+  if (G == 3) return fail(NQ_EUNSUPPORTED, "varlen_prefill: GQA group 3");
   if (head_dim != 128) return fail(NQ_EUNSUPPORTED, "varlen_prefill: head_dim %d (built: 128)", head_dim);
   if (q_dtype != NQ_BF16 && q_dtype != NQ_F16)
     return fail(NQ_EUNSUPPORTED, "varlen_prefill: q dtype %d (need f16/bf16)", q_dtype);
@@ -316,21 +599,22 @@ extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_
   if (fp8 && (!k_scale || !v_scale)) return fail(NQ_EINVAL, "varlen_prefill: fp8 K/V needs scales");
   if (!q || !k || !v || !cu_seqlens_q || !cu_seqlens_k || !out) return fail(NQ_EINVAL, "varlen_prefill: null pointer");
   if (block_tables) {
-    if (block_size <= 0 || block_size % kBN != 0)
-      return fail(NQ_EUNSUPPORTED, "varlen_prefill: block_size %d must be a multiple of %d", block_size, kBN);
+    if (block_size <= 0 || block_size % kKeys != 0)
+      return fail(NQ_EUNSUPPORTED, "varlen_prefill: block_size %d must be a multiple of %d", block_size, kKeys);
     if (max_blocks_per_seq <= 0 || bt_stride < max_blocks_per_seq)
       return fail(NQ_EINVAL, "varlen_prefill: block table width");
     if (static_cast<int64_t>(max_blocks_per_seq) * block_size < max_seqlen_k)
       return fail(NQ_EINVAL, "varlen_prefill: block table narrower than max_seqlen_k");
+    if ((max_seqlen_k + block_size - 1) / block_size > kMaxBt)
+      return fail(NQ_EUNSUPPORTED, "varlen_prefill: max_seqlen_k %d needs more than %d table entries", max_seqlen_k,
+                  kMaxBt);
   }
   const int qsz = 2, ksz = fp8 ? 1 : 2;
   if ((q_row_stride * qsz) % 16 || (q_head_stride * qsz) % 16 || !aligned(q, 16) || (kv_row_stride * ksz) % 16 ||
       !aligned(k, 16) || !aligned(v, 16) || (out_row_stride * qsz) % 8 || (out_head_stride * qsz) % 8 ||
       !aligned(out, 8))
     return fail(NQ_EINVAL, "varlen_prefill: q/k/v/out alignment");
-  const int n_qtiles = (max_seqlen_q + kBM - 1) / kBM;
-  if (n_qtiles > 65535 || static_cast<int64_t>(num_q_heads) * num_seqs > 0x7fffffff)
-    return fail(NQ_EINVAL, "varlen_prefill: grid too large");
+  if (kv_row_stride * ksz > (1 << 20)) return fail(NQ_EINVAL, "varlen_prefill: K/V row stride too large");
   PrefillArgs a{};
   a.q = static_cast<const uint8_t *>(q);
   a.q_rs = q_row_stride * qsz;
@@ -349,10 +633,15 @@ extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_
   a.o_hs = out_head_stride * qsz;
   a.Hq = num_q_heads;
   a.Hkv = num_kv_heads;
-  a.G = num_q_heads / num_kv_heads;
+  a.G = G;
+  a.G4 = G < 4 ? G : 4;
+  a.quads = G < 4 ? 1 : G / 4;
   a.block_size = block_size;
   a.num_seqs = num_seqs;
-  a.n_qtiles = n_qtiles;
+  const int rows_per_wg = kRows * (4 / a.G4);
+  a.n_qtiles = (max_seqlen_q + rows_per_wg - 1) / rows_per_wg;
+  const int rows_per_wg_dma = kRows * (kNW / a.G4);
+  a.n_qtiles_dma = (max_seqlen_q + rows_per_wg_dma - 1) / rows_per_wg_dma;
   a.causal = causal;
   a.scale_log2 = softmax_scale * kLog2e;
   a.k_scale = k_scale;

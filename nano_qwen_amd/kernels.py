@@ -60,7 +60,7 @@ def decode_workspace(device, nbytes: int) -> torch.Tensor | None:
 
     Kept across calls so a captured HIP graph keeps a fixed pointer; growing
     it inside a capture allocates from the capture's pool, which torch keeps
-    alive with the graph.
+    alive with the graph.  Calls that share it must not overlap (one stream).
     """
     if nbytes <= 0:
         return None
