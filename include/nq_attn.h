@@ -130,6 +130,10 @@ int nq_paged_decode(const void *q, int64_t q_batch_stride, int64_t q_head_stride
  * block_tables != NULL: k/v are the paged caches; key j of s is cache row
  *   block_tables[s*bt_stride + j/block_size]*block_size + j%block_size.
  * kv_dtype == q_dtype (F16/BF16), or NQ_FP8_E4M3 with k_scale/v_scale.
+ * workspace: >= nq_prefill_workspace_bytes() bytes, 4-byte aligned, all zero
+ * before its first use; every completed call leaves it zero again, so it is
+ * allocated and cleared once and then reused (also under graph replay).
+ * Calls that share a workspace must not run concurrently.
  */
 int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_head_stride,
                       const void *k, const void *v, int64_t kv_row_stride,
@@ -141,7 +145,11 @@ int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_head_stride
                       int num_seqs, int num_q_heads, int num_kv_heads,
                       int head_dim, int block_size, float softmax_scale,
                       int causal, int q_dtype, int kv_dtype,
-                      const float *k_scale, const float *v_scale, void *stream);
+                      const float *k_scale, const float *v_scale,
+                      void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Bytes of device workspace nq_varlen_prefill needs (work-queue counters). */
+int64_t nq_prefill_workspace_bytes(void);
 
 /*
  * Decode metadata on the device.

@@ -39,7 +39,8 @@ _SIGS = {
     "nq_varlen_prefill": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p,
                                   c_void_p, c_int, c_int, c_void_p, c_int64, c_int, c_int64, c_void_p,
                                   c_int64, c_int64, c_int, c_int, c_int, c_int, c_int, c_float, c_int,
-                                  c_int, c_int, c_void_p, c_void_p, c_void_p]),
+                                  c_int, c_int, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+    "nq_prefill_workspace_bytes": (c_int64, []),
     "nq_prepare_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_int, c_int, c_void_p]),
 }

@@ -13,6 +13,8 @@ namespace nq {
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 // Turn the status of the launch just made into NQ_OK / NQ_ELAUNCH.
 int check_launch(const char *what);
+// Compute units of the current device (cached per device).
+int device_cus();
 
 // ---------------------------------------------------------------- vectors
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

@@ -408,22 +408,6 @@ int launch_decode(const DecodeArgs &a, int batch, hipStream_t s) {
 
 using namespace nq;
 
-namespace nq {
-namespace {
-// Compute units of the current device (cached per device).
-int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-}  // namespace
-}  // namespace nq
 
 // Split size: one split per workgroup should carry enough tokens that the
 // workgroup's fixed costs (Q load, first-step latency, partial write) stay

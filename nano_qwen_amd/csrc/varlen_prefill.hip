@@ -26,9 +26,9 @@
 //    operand reads are bank-conflict free.
 //  * Online softmax in the log2 domain with lazy rescaling: O and l are only
 //    rescaled when a row maximum grows by more than 2^8, so P <= 256.
-//  * Grid order: last query tiles first (most keys), and XCD-aware: the
-//    consecutive tiles of one (sequence, kv head) run on the same XCD and
-//    share its L2.
+//  * Grid order (map_work): the workgroups of one (sequence, kv head) stay on
+//    one XCD and share its L2, every XCD gets a share of every sequence, and
+//    within an XCD the last query tiles (the most keys) start first.
 #include "nq_device.hpp"
 
 namespace nq {
@@ -40,6 +40,7 @@ constexpr int kRows = 32;    // query rows per wave
 constexpr int kKeys = 32;    // keys per LDS tile
 constexpr int kMaxBt = 4096;  // block-table entries staged in LDS (1M tokens at 256)
 constexpr float kRescale = 8.0f;  // log2 growth of a row max that forces a rescale
+constexpr int kQueueWords = 16;   // prefill workspace: 8 per-XCD counters + 1 finish counter (+ pad)
 
 struct PrefillArgs {
   const uint8_t *q;
@@ -60,9 +61,46 @@ struct PrefillArgs {
   float scale_log2;
   const float *k_scale;
   const float *v_scale;
+  uint32_t *queue;  // persistent kernel: kQueueWords work counters (zero between calls)
+  int pin;          // work groups pinned to XCDs (>= 8 groups)
 };
 
 __device__ inline int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1) | (row & 8); }
+
+// Work item of a workgroup: query tile qt of kv-head slot y (kv head x quad)
+// of sequence s.
+struct Work {
+  int qt, y, s;
+};
+
+// Groups u = s * n_y + y -- the workgroups that read the same K/V -- are
+// pinned to XCD u % 8 (the hardware places workgroup L on XCD L % 8), so they
+// share that XCD's L2; y varies fastest in u, so every XCD gets a share of
+// every sequence and the XCDs stay balanced however the lengths vary.  Within
+// an XCD the workgroups run in query-tile order from the last tile (the most
+// keys) down, across all of the XCD's groups, so the longest work starts
+// first and the short tiles fill the tail.  Fewer than 8 groups: no pinning.
+__device__ inline bool map_work(int L, int n_x, int n_y, int num_seqs, Work &w) {
+  const int U = n_y * num_seqs;
+  int u;
+  if (U >= 8) {
+    const int x = L & 7, i = L >> 3;
+    const int cx = (U - x + 7) >> 3;
+    if (i >= cx * n_x) return false;
+    w.qt = n_x - 1 - i / cx;
+    u = x + 8 * (i % cx);
+  } else {
+    if (L >= U * n_x) return false;
+    w.qt = n_x - 1 - L / U;
+    u = L % U;
+  }
+  w.y = u % n_y;
+  w.s = u / n_y;
+  return true;
+}
+
+// Grid size for map_work.
+inline int64_t work_grid(int64_t n_x, int64_t U) { return U >= 8 ? 8 * ((U + 7) / 8) * n_x : U * n_x; }
 
 template <class T, bool FP8, int D>
 struct PTile {
@@ -159,20 +197,9 @@ void varlen_prefill_kernel(const PrefillArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m = lane & 15, g = lane >> 4;
 
-  // ---- XCD-aware, longest-first work mapping.  Hardware places workgroup L
-  // on XCD L % 8; logical index Lg = (L % 8) * per + L / 8 makes consecutive
-  // logical indices -- consecutive query tiles of one (sequence, kv-head
-  // quad) -- run on one XCD.
-  const int n_x = a.n_qtiles, n_y = a.Hkv * a.quads;
-  const int total = n_x * n_y * a.num_seqs;
-  const int L = blockIdx.x;
-  const int per = (total + 7) / 8;
-  const int Lg = (L % 8) * per + L / 8;
-  if (Lg >= total) return;
-  const int xt = Lg % n_x;
-  const int yz = Lg / n_x;
-  const int y = yz % n_y, s = yz / n_y;
-  const int qt = n_x - 1 - xt;  // last tiles first: they have the most keys
+  Work w;
+  if (!map_work(blockIdx.x, a.n_qtiles, a.Hkv * a.quads, a.num_seqs, w)) return;
+  const int qt = w.qt, y = w.y, s = w.s;
   const int kvh = y / a.quads, quad = y % a.quads;
   const int rb = 4 / a.G4;  // row blocks of 32 per workgroup
   const int head = kvh * a.G + quad * 4 + (wave % a.G4);
@@ -337,31 +364,20 @@ struct DTile {
   static constexpr int ROWB = D * 2;
   static constexpr int TILE_B = kKeys * ROWB;   // 8 KiB per K (or V) tile
   static constexpr int SLOT_B = 2 * TILE_B;     // K + V
-  static constexpr int LDS_BYTES = kStages * SLOT_B + kMaxBt * 4;
+  static constexpr int LDS_BYTES = kStages * SLOT_B + kMaxBt * 4 + 16;  // + queue item slots
 };
 
+// One work item of the persistent kernel: query tile qt (64 rows per head,
+// kNW/G4 row blocks of 32) of kv-head slot y of sequence s.
 template <class T, int D>
-__global__ __launch_bounds__(64 * kNW) __attribute__((amdgpu_waves_per_eu(2)))
-void varlen_prefill_dma_kernel(const PrefillArgs a) {
+__device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y, int s, uint8_t *smem) {
   using DT = DTile<T, D>;
   using PT = PTile<T, false, D>;
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   int32_t *lds_bt = reinterpret_cast<int32_t *>(smem + kStages * DT::SLOT_B);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m = lane & 15, g = lane >> 4;
 
-  // XCD-aware, longest-first work mapping (see varlen_prefill_kernel).
-  const int n_x = a.n_qtiles, n_y = a.Hkv * a.quads;
-  const int total = n_x * n_y * a.num_seqs;
-  const int L = blockIdx.x;
-  const int per = (total + 7) / 8;
-  const int Lg = (L % 8) * per + L / 8;
-  if (Lg >= total) return;
-  const int xt = Lg % n_x;
-  const int yz = Lg / n_x;
-  const int y = yz % n_y, s = yz / n_y;
-  const int qt = n_x - 1 - xt;
   const int kvh = y / a.quads, quad = y % a.quads;
   const int rb = kNW / a.G4;  // row blocks of 32 per workgroup
   const int head = kvh * a.G + quad * 4 + (wave % a.G4);
@@ -549,20 +565,75 @@ void varlen_prefill_dma_kernel(const PrefillArgs a) {
   }
 }
 
+// Persistent prefill: one workgroup per CU pulls work items from a queue.
+// The hardware dispatcher keeps only about half of the CUs busy when
+// one-per-CU workgroups of very different lengths are launched as a plain
+// grid; a queue keeps every CU fed until the work runs out.
+//
+// Items are grouped as in map_work: XCD x (workgroups L with L % 8 == x) owns
+// the groups u = x, x + 8, ... and serves them from its own counter
+// queue[x], in query-tile order from the last tile down (longest first).
+// queue[8] counts finished workgroups; the last one to finish puts all nine
+// words back to zero, so the workspace is ready for the next call without a
+// host-side clear.
+template <class T, int D>
+__global__ __launch_bounds__(64 * kNW) __attribute__((amdgpu_waves_per_eu(2)))
+void varlen_prefill_dma_kernel(const PrefillArgs a) {
+  using DT = DTile<T, D>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  int *lds_item = reinterpret_cast<int *>(smem + kStages * DT::SLOT_B + kMaxBt * 4);
+
+  const int n_x = a.n_qtiles, n_y = a.Hkv * a.quads;
+  const int U = n_y * a.num_seqs;
+  const int x = a.pin ? static_cast<int>(blockIdx.x & 7) : 0;
+  const int cx = a.pin ? (U - x + 7) >> 3 : U;
+  const int n_items = cx * n_x;
+  uint32_t *ctr = a.queue + x;
+
+  if (threadIdx.x == 0) lds_item[0] = static_cast<int>(atomicAdd(ctr, 1u));
+  __syncthreads();
+  int item = lds_item[0];
+  for (int it = 1; item < n_items; ++it) {
+    uint32_t next = 0;
+    if (threadIdx.x == 0) next = atomicAdd(ctr, 1u);  // in flight while this item runs
+    const int qt = n_x - 1 - item / cx;
+    const int u = a.pin ? x + 8 * (item % cx) : item % cx;
+    prefill_item<T, D>(a, qt, u % n_y, u / n_y, smem);
+    // Alternate slots: a wave still reading slot it-1 cannot overlap the
+    // write of slot it+1, which comes after the next barrier.
+    if (threadIdx.x == 0) lds_item[it & 1] = static_cast<int>(next);
+    __syncthreads();  // also: LDS ring and block table free for the next item
+    item = lds_item[it & 1];
+  }
+  if (threadIdx.x == 0) {
+    if (atomicAdd(a.queue + 8, 1u) == gridDim.x - 1) {
+      // Every other workgroup has taken its last index and finished.
+#pragma unroll
+      for (int c = 0; c < 9; ++c) atomicExch(a.queue + c, 0u);
+    }
+  }
+}
+
 template <class T, bool FP8, int D>
 int launch_prefill(PrefillArgs a, hipStream_t s) {
   if constexpr (!FP8) {
     using DT = DTile<T, D>;
     a.n_qtiles = a.n_qtiles_dma;
-    const int64_t total = static_cast<int64_t>(a.n_qtiles) * a.Hkv * a.quads * a.num_seqs;
-    if (total > 0x7fffffff) return fail(NQ_EINVAL, "varlen_prefill: grid too large");
-    const int grid = static_cast<int>((total + 7) / 8 * 8);
-    varlen_prefill_dma_kernel<T, D><<<grid, 64 * kNW, DT::LDS_BYTES, s>>>(a);
+    const int64_t U = static_cast<int64_t>(a.Hkv) * a.quads * a.num_seqs;
+    const int64_t total = work_grid(a.n_qtiles, U);
+    if (total > 0x7fffffff) return fail(NQ_EINVAL, "varlen_prefill: too many work items");
+    if (!a.queue) return fail(NQ_EINVAL, "varlen_prefill: null workspace");
+    a.pin = U >= 8;
+    // One resident workgroup per CU (two waves per SIMD), never more than
+    // there are items; a multiple of 8 so every XCD gets the same count.
+    int64_t grid = (device_cus() + 7) / 8 * 8;
+    if (grid > total) grid = total;  // work_grid() is a multiple of 8 when pinned
+    varlen_prefill_dma_kernel<T, D><<<static_cast<int>(grid), 64 * kNW, DT::LDS_BYTES, s>>>(a);
   } else {
     using PT = PTile<T, FP8, D>;
-    const int64_t total = static_cast<int64_t>(a.n_qtiles) * a.Hkv * a.quads * a.num_seqs;
+    const int64_t total = work_grid(a.n_qtiles, static_cast<int64_t>(a.Hkv) * a.quads * a.num_seqs);
     if (total > 0x7fffffff) return fail(NQ_EINVAL, "varlen_prefill: grid too large");
-    const int grid = static_cast<int>((total + 7) / 8 * 8);
+    const int grid = static_cast<int>(total);
     varlen_prefill_kernel<T, FP8, D><<<grid, kPThreads, PT::LDS_BYTES, s>>>(a);
   }
   return check_launch("varlen_prefill");
@@ -573,6 +644,8 @@ int launch_prefill(PrefillArgs a, hipStream_t s) {
 
 using namespace nq;
 
+extern "C" int64_t nq_prefill_workspace_bytes(void) { return kQueueWords * sizeof(uint32_t); }
+
 extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_head_stride, const void *k,
                                  const void *v, int64_t kv_row_stride, const int32_t *cu_seqlens_q,
                                  const int32_t *cu_seqlens_k, int max_seqlen_q, int max_seqlen_k,
@@ -580,7 +653,8 @@ extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_
                                  int64_t num_blocks, void *out, int64_t out_row_stride,
                                  int64_t out_head_stride, int num_seqs, int num_q_heads, int num_kv_heads,
                                  int head_dim, int block_size, float softmax_scale, int causal, int q_dtype,
-                                 int kv_dtype, const float *k_scale, const float *v_scale, void *stream) {
+                                 int kv_dtype, const float *k_scale, const float *v_scale, void *workspace,
+                                 int64_t workspace_bytes, void *stream) {
   if (num_seqs == 0 || max_seqlen_q == 0) return NQ_OK;
   if (num_seqs < 0 || max_seqlen_q < 0 || max_seqlen_k < 0 || num_q_heads <= 0 || num_kv_heads <= 0)
     return fail(NQ_EINVAL, "varlen_prefill: bad sizes");
@@ -615,7 +689,11 @@ extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_
       !aligned(out, 8))
     return fail(NQ_EINVAL, "varlen_prefill: q/k/v/out alignment");
   if (kv_row_stride * ksz > (1 << 20)) return fail(NQ_EINVAL, "varlen_prefill: K/V row stride too large");
+  if ((!workspace || workspace_bytes < nq_prefill_workspace_bytes() || !aligned(workspace, 4)))
+    return fail(NQ_EINVAL, "varlen_prefill: workspace of %lld bytes at %p (need %lld, 4-byte aligned)",
+                (long long)workspace_bytes, workspace, (long long)nq_prefill_workspace_bytes());
   PrefillArgs a{};
+  a.queue = static_cast<uint32_t *>(workspace);
   a.q = static_cast<const uint8_t *>(q);
   a.q_rs = q_row_stride * qsz;
   a.q_hs = q_head_stride * qsz;

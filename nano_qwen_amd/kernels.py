@@ -20,6 +20,7 @@ from . import _lib
 from ._lib import check, dtype_code, lib, ptr, require_cuda, stream_of
 
 _workspaces: dict[int, torch.Tensor] = {}
+_prefill_queues: dict[int, torch.Tensor] = {}
 
 
 def store_kvcache(key, value, k_cache, v_cache, slot_mapping, k_scale=None, v_scale=None):
@@ -69,6 +70,22 @@ def decode_workspace(device, nbytes: int) -> torch.Tensor | None:
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _workspaces[idx] = ws
+    return ws
+
+
+def prefill_workspace(device) -> torch.Tensor:
+    """Persistent work-queue counters of the prefill kernel for ``device``.
+
+    Zeroed once here; every completed prefill call leaves them zero again, so
+    the same tensor serves every later call (and graph replays).  Calls that
+    share it must not overlap (one stream).
+    """
+    idx = torch.device(device).index or 0
+    ws = _prefill_queues.get(idx)
+    if ws is None:
+        nbytes = lib().nq_prefill_workspace_bytes()
+        ws = torch.zeros((nbytes + 3) // 4, dtype=torch.int32, device=device)
+        _prefill_queues[idx] = ws
     return ws
 
 
@@ -143,12 +160,13 @@ def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen
     fp8 = k.dtype == torch.float8_e4m3fn
     if out is None:
         out = torch.empty(tq, hq, d, dtype=q.dtype, device=q.device)
+    ws = prefill_workspace(q.device)
     rc = lib().nq_varlen_prefill(
         ptr(q), q.stride(0), q.stride(1), ptr(k), ptr(v), kv_rs, ptr(cu_seqlens_q), ptr(cu_seqlens_k),
         int(max_seqlen_q), int(max_seqlen_k), ptr(block_table), bt_stride, W, nb, ptr(out),
         out.stride(0), out.stride(1), n, hq, hkv, d, bs, float(softmax_scale), 1 if causal else 0,
         dtype_code(q.dtype), dtype_code(k.dtype), ptr(k_scale) if fp8 else None,
-        ptr(v_scale) if fp8 else None, stream_of(q))
+        ptr(v_scale) if fp8 else None, ptr(ws), ws.numel() * 4, stream_of(q))
     check(rc, "varlen_prefill")
     return out
 
@@ -166,4 +184,4 @@ def prepare_decode(sampled_token_ids, batch_slots, seq_lens, last_block_ids, inp
 
 
 __all__ = ["store_kvcache", "paged_decode", "varlen_prefill", "prepare_decode", "decode_plan",
-           "decode_workspace", "_lib"]
+           "decode_workspace", "prefill_workspace", "_lib"]

@@ -128,3 +128,19 @@ def test_decode_equals_last_prefill_row(cuda):
 def test_prefill_cfg3_full(cuda):
     case = make_prefill_case("cfg3", seed=0, device=cuda)
     check(case, list(range(16)), TOL_BF16, rows_per_seq=24)
+
+
+def test_prefill_queue_resets_between_calls(cuda):
+    """The persistent kernel's work-queue counters come back to zero after
+    every call: repeated calls (different shapes in between) give bitwise
+    identical outputs, and the workspace reads zero afterwards."""
+    big = make_prefill_case("cfg3", seed=8, device=cuda, nseq=6, lq=(100, 900), prefix_blocks=(1, 2))
+    small = make_prefill_case("cfg3", seed=9, device=cuda, nseq=1, lq=(30, 30), prefix_blocks=(0, 0),
+                              hq=8, hkv=2)
+    first = run_step(big).clone()
+    for _ in range(3):
+        run_step(small)
+        again = run_step(big)
+        assert torch.equal(first, again)
+    ws = kernels.prefill_workspace(cuda)
+    assert int(ws.abs().sum()) == 0

@@ -45,8 +45,9 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert rc == -1 and b"null" in lib.nq_last_error()
     assert lib.nq_store_kvcache(None, 0, None, 0, None, None, None, 0, 10, 8, 128, 2, 2, None, None, None) == 0
     rc = lib.nq_varlen_prefill(None, 0, 0, None, None, 0, None, None, 10, 10, None, 0, 0, 0, None, 0, 0, 1, 32, 8,
-                               128, 256, 0.1, 1, 2, 1, None, None, None)
+                               128, 256, 0.1, 1, 2, 1, None, None, None, 0, None)
     assert rc == -2  # bf16 q with f16 kv
+    assert lib.nq_prefill_workspace_bytes() >= 36  # 8 per-XCD counters + 1 finish counter
 
 
 def test_decode_plan_covers_table_and_respects_env(monkeypatch):
