@@ -34,6 +34,7 @@ struct BF16 {
   __device__ static inline float to_float(uint16_t h) {
     return __builtin_bit_cast(float, static_cast<uint32_t>(h) << 16);
   }
+  static constexpr uint32_t kOne2 = 0x3f803f80u;  // two 1.0
   // two fp32 -> packed pair (lo = a), one v_cvt_pk_bf16_f32 (RNE)
   __device__ static inline uint32_t pack2(float a, float b) {
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -59,6 +60,7 @@ struct F16 {
   __device__ static inline float to_float(uint16_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, h));
   }
+  static constexpr uint32_t kOne2 = 0x3c003c00u;  // two 1.0
   __device__ static inline uint32_t pack2(float a, float b) {
     return static_cast<uint32_t>(from_float(a)) | (static_cast<uint32_t>(from_float(b)) << 16);
   }
@@ -78,6 +80,13 @@ __device__ inline T ldg(const T *p) {
   return __builtin_nontemporal_load(p);
 }
 
+// Load of data that no kernel writes while it runs (sequence metadata, block
+// tables), through the constant address space: with a wave-uniform address
+// it becomes a scalar load, which does not wait on the vector-memory counter.
+template <class T>
+__device__ inline T ld_const(const T *p) {
+  return *(const __attribute__((address_space(4))) T *)(reinterpret_cast<uintptr_t>(p));
+}
 __device__ inline u32x4 load16(const void *p) { return *reinterpret_cast<const u32x4 *>(p); }
 __device__ inline void store16(void *p, const u32x4 &v) { *reinterpret_cast<u32x4 *>(p) = v; }
 
@@ -169,6 +178,29 @@ __device__ inline float sum32(float v) {
   return u2f(a) + u2f(b);
 }
 
+// The same maxima with a plain v_max_f32 after the swap: no NaN quieting of
+// the swapped value (the inputs are finite or -inf).
+__device__ inline float vmax_raw(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ inline float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ inline float max16_raw(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(f2u(v), f2u(v), false, false);
+  const uint32_t a = r[0], b = r[1];
+  return vmax_raw(u2f(a), u2f(b));
+}
+__device__ inline float max32_raw(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(f2u(v), f2u(v), false, false);
+  const uint32_t a = r[0], b = r[1];
+  return vmax_raw(u2f(a), u2f(b));
+}
+
 // Transposing LDS read (ds_read_b64_tr_b16).  Within each 16-lane group,
 // lanes 4k..4k+3 address the four 8-byte pieces of "row" k (16 consecutive
 // 16-bit elements); lane i receives element i of rows 0..3, packed in order.
@@ -188,6 +220,16 @@ __device__ inline u32x2 lds_read_tr16_async(const void *p) {
   const uint32_t a = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
       (__attribute__((address_space(3))) const void *)(p)));
   asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(a));
+  return v;
+}
+
+// ds_read_b64_tr_b16 at LDS byte address `addr` + OFF (immediate), issued as
+// an opaque instruction with the same contract as lds_read_tr16_async.
+template <int OFF>
+__device__ inline u32x2 lds_read_tr16_at(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+  u32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
   return v;
 }
 

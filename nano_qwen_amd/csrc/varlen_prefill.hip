@@ -29,6 +29,8 @@
 //  * Grid order (map_work): the workgroups of one (sequence, kv head) stay on
 //    one XCD and share its L2, every XCD gets a share of every sequence, and
 //    within an XCD the last query tiles (the most keys) start first.
+#include <type_traits>
+
 #include "nq_device.hpp"
 
 namespace nq {
@@ -356,7 +358,7 @@ void varlen_prefill_kernel(const PrefillArgs a) {
 // whole tile visible.  The chunk swizzle of the LDS tile is produced by the
 // source address each lane fetches.
 constexpr int kNW = 8;  // waves per workgroup
-constexpr int kStages = 4;
+constexpr int kStages = 5;
 
 template <class T, int D>
 struct DTile {
@@ -364,42 +366,52 @@ struct DTile {
   static constexpr int ROWB = D * 2;
   static constexpr int TILE_B = kKeys * ROWB;   // 8 KiB per K (or V) tile
   static constexpr int SLOT_B = 2 * TILE_B;     // K + V
-  static constexpr int LDS_BYTES = kStages * SLOT_B + kMaxBt * 4 + 16;  // + queue item slots
+  static constexpr int LDS_BYTES = kStages * SLOT_B + 16;  // + queue item slots
 };
 
 // One work item of the persistent kernel: query tile qt (64 rows per head,
 // kNW/G4 row blocks of 32) of kv-head slot y of sequence s.
+//
+// Per key tile, all control is scalar (wave-uniform): the copy of tile
+// jt + kStages - 1 is two buffer-to-LDS loads through descriptors whose range
+// ends at the tile's last valid key (rows past it read as zeros, so no
+// clamping), and the block table is walked one block at a time with scalar
+// loads.  Tiles that every row of the wave sees completely run a mask-free
+// loop; the rest (the causal diagonal, the end of the keys, any tile of a
+// sequence with a missing block) run the masked loop.
 template <class T, int D>
 __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y, int s, uint8_t *smem) {
   using DT = DTile<T, D>;
   using PT = PTile<T, false, D>;
-  int32_t *lds_bt = reinterpret_cast<int32_t *>(smem + kStages * DT::SLOT_B);
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int m = lane & 15, g = lane >> 4;
 
   const int kvh = y / a.quads, quad = y % a.quads;
   const int rb = kNW / a.G4;  // row blocks of 32 per workgroup
   const int head = kvh * a.G + quad * 4 + (wave % a.G4);
-  const int q0 = a.cu_q[s], Lq = a.cu_q[s + 1] - q0;
+  const int q0 = ld_const(a.cu_q + s), Lq = ld_const(a.cu_q + s + 1) - q0;
   const int row_begin = qt * kRows * rb;
   if (row_begin >= Lq) return;
-  const int k0 = a.cu_k[s], Lk = a.cu_k[s + 1] - k0;
+  const int k0 = ld_const(a.cu_k + s), Lk = ld_const(a.cu_k + s + 1) - k0;
   const int P = Lk - Lq;
   const int row_last = min(row_begin + kRows * rb, Lq) - 1;
   const int key_end = a.causal ? max(0, min(Lk, row_last + P + 1)) : Lk;
   const int n_kt = (key_end + kKeys - 1) / kKeys;
   const float sl2 = a.scale_log2;
-
-  if (a.block_tables != nullptr) {
-    const int n_bt = min(min((key_end + a.block_size - 1) / a.block_size, a.max_blocks), kMaxBt);
-    for (int i = threadIdx.x; i < n_bt; i += 64 * kNW) lds_bt[i] = a.block_tables[s * a.bt_stride + i];
-  }
+  const bool paged = a.block_tables != nullptr;
+  const int32_t *bt_row = paged ? a.block_tables + static_cast<int64_t>(s) * a.bt_stride : nullptr;
 
   const int wrow0 = row_begin + kRows * (wave / a.G4);
   const bool wave_live = wrow0 < Lq;
   const int wrow_last = min(wrow0 + kRows - 1, Lq - 1);
   const int wave_key_end = a.causal ? min(Lk, wrow_last + P + 1) : Lk;
+  // Tiles this wave computes (a prefix: a causal wave stops at its own
+  // diagonal) and, among them, the leading tiles that need no mask.
+  const int wave_nkt = wave_live ? min(n_kt, (wave_key_end + kKeys - 1) / kKeys) : 0;
+  int n_plain = min(wave_nkt, Lk / kKeys);
+  if (a.causal) n_plain = min(n_plain, max(0, wrow0 + P + 1) / kKeys);
 
   u32x4 qf[2][PT::NKK];
 #pragma unroll
@@ -411,148 +423,215 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
     for (int kk = 0; kk < PT::NKK; ++kk) qf[qs][kk] = ok ? load16(qp + (8 * g + 32 * kk) * 2) : u32x4{0, 0, 0, 0};
   }
 
-  __syncthreads();  // block table in LDS
-
-  // This lane's DMA row within a tile (wave w copies rows 4w..4w+3) and the
-  // logical chunk it fetches for its fixed LDS position.
+  // ---- K/V copies.  Wave w copies rows 4w..4w+3 of each tile; lane l of
+  // it fetches the logical 16-byte chunk that belongs at LDS byte 16 l of
+  // the wave's 1 KiB (the chunk swizzle is made by the source offset).
   const int drow = 4 * wave + (lane >> 4);
-  const int dchunk = (lane & 15) ^ swz(drow);
-  // Copy tile jt (clamped: a slot past the last tile is refilled with the
-  // last tile, which is never read) into ring slot `slot`.
-  auto issue = [&](int jt, int slot) {
-    jt = min(jt, n_kt - 1);
-    const int kbase = jt * kKeys;
-    const int nvalid = min(kKeys, key_end - kbase);  // >= 1
-    const int r = min(drow, nvalid - 1);              // rows past the end repeat a valid key (masked)
-    int64_t row;
-    if (a.block_tables == nullptr) {
-      row = static_cast<int64_t>(k0) + kbase + r;
-    } else {
-      const int blk = __builtin_amdgcn_readfirstlane(lds_bt[kbase / a.block_size]);
-      const int bb = (blk >= 0 && blk < a.num_blocks) ? blk : 0;  // a missing block reads block 0 (masked below)
-      row = static_cast<int64_t>(bb) * a.block_size + kbase % a.block_size + r;
+  const uint32_t src_off = static_cast<uint32_t>(drow * a.kv_rs + kvh * DT::ROWB + (((lane & 15) ^ swz(drow)) << 4));
+  int iss_jt = 0, iss_slot = 0;    // next tile to copy, its ring slot
+  int iss_bidx = 0, iss_in = 0;    // its block-table index and offset in the block
+  int iss_blk = 0;                 // block of iss_bidx (valid when iss_in > 0)
+  bool any_bad = false;            // a tile of this item lies in a missing block
+  auto issue = [&]() {
+    int nvalid = 0;
+    int64_t row0 = 0;
+    if (iss_jt < n_kt) {
+      nvalid = min(kKeys, key_end - iss_jt * kKeys);
+      if (paged) {
+        if (iss_in == 0) iss_blk = (iss_bidx < a.max_blocks) ? ld_const(bt_row + iss_bidx) : -1;
+        const bool ok = iss_blk >= 0 && iss_blk < a.num_blocks;
+        any_bad |= !ok;
+        row0 = static_cast<int64_t>(ok ? iss_blk : 0) * a.block_size + iss_in;
+        if (!ok) nvalid = 0;
+        iss_in += kKeys;
+        if (iss_in == a.block_size) {
+          iss_in = 0;
+          ++iss_bidx;
+        }
+      } else {
+        row0 = static_cast<int64_t>(k0) + iss_jt * kKeys;
+      }
     }
-    const int64_t off = row * a.kv_rs + static_cast<int64_t>(kvh) * DT::ROWB + dchunk * 16;
-    uint8_t *dst = smem + slot * DT::SLOT_B + wave * 1024;
-    dma16(a.k + off, dst);
-    dma16(a.v + off, dst + DT::TILE_B);
+    const int64_t base = row0 * a.kv_rs;
+    const uint32_t nrec = static_cast<uint32_t>(nvalid * a.kv_rs);
+    uint8_t *dst = smem + iss_slot * DT::SLOT_B + wave * 1024;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.k + base, nrec),
+                                             (__attribute__((address_space(3))) void *)dst, 16, src_off, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.v + base, nrec),
+                                             (__attribute__((address_space(3))) void *)(dst + DT::TILE_B), 16,
+                                             src_off, 0, 0, 0);
+    ++iss_jt;
+    iss_slot = (iss_slot + 1 == kStages) ? 0 : iss_slot + 1;
   };
 
-  float m_use[2] = {kNegInf, kNegInf}, l_run[2] = {0.f, 0.f};
-  f32x4 o[2][PT::NJ];
+  // Per-lane LDS byte offsets inside a K or V tile (fixed for the item).
+  // K^T operand kk: key row m (row m + 16 is +16 rows), dims 32kk + 8g.. ;
+  // V^T operand j: rows r0 and r0 + 16 (same swizzle: swz() ignores bit 4).
+  int koff[PT::NKK], voff[PT::NJ];
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs)
+  for (int kk = 0; kk < PT::NKK; ++kk) koff[kk] = m * DT::ROWB + (((4 * kk + g) ^ swz(m)) << 4);
+  {
+    const int vg = lane >> 4, vk = (lane >> 2) & 3, vq = lane & 3;
+    const int r0 = 4 * vg + vk;
+#pragma unroll
+    for (int j = 0; j < PT::NJ; ++j) voff[j] = r0 * DT::ROWB + (((2 * j + (vq >> 1)) ^ swz(r0)) << 4) + (vq & 1) * 8;
+  }
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) uint8_t *)(smem)));
+
+  // S^T (32 keys x 32 rows, unscaled) of the tile in ring slot `slot`.
+  auto qk = [&](int slot, f32x4 (&sc)[2][2]) {
+    const uint8_t *kt = smem + slot * DT::SLOT_B;
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int kk = 0; kk < PT::NKK; ++kk) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const u32x4 kf = *reinterpret_cast<const u32x4 *>(kt + koff[kk] + ks * 16 * DT::ROWB);
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) sc[qs][ks] = T::mfma16x16x32(kf, qf[qs][kk], sc[qs][ks]);
+      }
+    }
+  };
+
+  float m_use[2] = {kNegInf, kNegInf};  // running row max, scaled (log2) domain
+  f32x4 o[2][PT::NJ], lsum[2];          // O^T accumulators; row sums of P (every element)
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    lsum[qs] = f32x4{0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < PT::NJ; ++j) o[qs][j] = f32x4{0, 0, 0, 0};
-
-  if (n_kt > 0) {
-#pragma unroll
-    for (int st = 0; st < kStages - 1; ++st) issue(st, st);
   }
-  for (int jt = 0; jt < n_kt; ++jt) {
-    wait_vmcnt<2 * (kStages - 2)>();  // this wave's copies of tile jt have landed
-    wait_lgkmcnt0();                   // and its reads of tile jt-1 are done
-    raw_barrier();                     // tile jt complete; slot of tile jt-1 free
-    issue(jt + kStages - 1, (jt + kStages - 1) % kStages);
+  const u32x4 ones = u32x4{T::kOne2, T::kOne2, T::kOne2, T::kOne2};
+
+  // One key tile: softmax of the current S (`sc`, tile jt, in ring slot
+  // `slot`) and O += P V, with the QK products of tile jt + 1 issued
+  // alongside (independent MFMA work for the exp / pack VALU work).
+  f32x4 sc[2][2];
+  auto step = [&](auto mask_tag, int jt, int slot, bool blk_ok) {
+    constexpr bool MASK = decltype(mask_tag)::value;
     const int kbase = jt * kKeys;
-    const uint8_t *kt = smem + (jt % kStages) * DT::SLOT_B;
-    const uint8_t *vt = kt + DT::TILE_B;
-    bool blk_ok = true;
-    if (a.block_tables != nullptr) {
-      const int blk = __builtin_amdgcn_readfirstlane(lds_bt[kbase / a.block_size]);
-      blk_ok = blk >= 0 && blk < a.num_blocks;
+    float x[2][8], mnew[2];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      int lim = 0;
+      if constexpr (MASK) {
+        const int row = wrow0 + 16 * qs + m;
+        lim = a.causal ? min(Lk - 1, row + P) : Lk - 1;  // last visible key
+        if (!blk_ok) lim = -1;
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          float v = sc[qs][ks][rr];
+          if constexpr (MASK) v = (kbase + 16 * ks + 4 * g + rr > lim) ? kNegInf : v;
+          x[qs][4 * ks + rr] = v;
+        }
+      const float ml = max3_raw(max3_raw(x[qs][0], x[qs][1], x[qs][2]), max3_raw(x[qs][3], x[qs][4], x[qs][5]),
+                                vmax_raw(x[qs][6], x[qs][7]));
+      mnew[qs] = max32_raw(max16_raw(ml)) * sl2;
     }
-    if (wave_live && kbase < wave_key_end) {
-      f32x4 sc[2][2];
+    // Lazy rescale: only when a row max grows by more than 2^kRescale.
+    if (__builtin_amdgcn_ballot_w64(mnew[0] > m_use[0] + kRescale || mnew[1] > m_use[1] + kRescale) != 0) {
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) {
+        const float m_new = fmaxf(m_use[qs], mnew[qs]);
+        const float alpha = (m_use[qs] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(m_use[qs] - m_new);
+        lsum[qs] *= alpha;
+#pragma unroll
+        for (int j = 0; j < PT::NJ; ++j) o[qs][j] *= alpha;
+        m_use[qs] = m_new;
+      }
+    }
+    // S of tile jt + 1 (unused past this wave's last tile: the slot then
+    // holds zeros or a later tile, read in bounds and discarded).
+    f32x4 sn[2][2];
+    qk(slot + 1 == kStages ? 0 : slot + 1, sn);
+    u32x4 pb[2];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      const float mref = (m_use[qs] == kNegInf) ? 0.f : m_use[qs];
+      uint32_t pw[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[qs][2 * t], sl2, -mref));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[qs][2 * t + 1], sl2, -mref));
+        pw[t] = T::pack2(p0, p1);
+      }
+      pb[qs] = u32x4{pw[0], pw[1], pw[2], pw[3]};
+    }
+    // O^T += V^T P^T in two halves of head_dim (4 V^T operands live at a
+    // time); the transposing reads are opaque and waited for by a wait that
+    // names their registers, so no MFMA is scheduled above it.
+    const uint32_t vt = lds0 + slot * DT::SLOT_B + DT::TILE_B;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      u32x4 vf[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const u32x2 lo = lds_read_tr16_at<0>(vt + voff[4 * h + jj]);
+        const u32x2 hi = lds_read_tr16_at<16 * DT::ROWB>(vt + voff[4 * h + jj]);
+        vf[jj] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vf[0]), "+v"(vf[1]), "+v"(vf[2]), "+v"(vf[3]) : : "memory");
 #pragma unroll
       for (int qs = 0; qs < 2; ++qs)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = f32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int kk = 0; kk < PT::NKK; ++kk) {
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const u32x4 kf = PT::kfrag(kt, ks, kk, m, g);
-#pragma unroll
-          for (int qs = 0; qs < 2; ++qs) sc[qs][ks] = T::mfma16x16x32(kf, qf[qs][kk], sc[qs][ks]);
-        }
-      }
-      const bool need_mask = !blk_ok || kbase + kKeys - 1 > wrow0 + P || kbase + kKeys > Lk;
-      u32x4 pb[2];
-#pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
-        const int row = wrow0 + 16 * qs + m;
-        int lim = a.causal ? min(Lk - 1, row + P) : Lk - 1;  // last visible key
-        if (!blk_ok) lim = -1;
-        float x[8];
-        float mloc = kNegInf;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const int j = kbase + 16 * ks + 4 * g + rr;
-            float v = sc[qs][ks][rr] * sl2;
-            if (need_mask && j > lim) v = kNegInf;
-            x[4 * ks + rr] = v;
-            mloc = fmaxf(mloc, v);
-          }
-        mloc = max32(max16(mloc));
-        if (__builtin_amdgcn_ballot_w64(mloc > m_use[qs] + kRescale) != 0) {
-          const float m_new = fmaxf(m_use[qs], mloc);
-          const float alpha = (m_use[qs] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(m_use[qs] - m_new);
-          l_run[qs] *= alpha;
-#pragma unroll
-          for (int j = 0; j < PT::NJ; ++j) o[qs][j] *= alpha;
-          m_use[qs] = m_new;
-        }
-        const float mref = (m_use[qs] == kNegInf) ? 0.f : m_use[qs];
-        float psum = 0.f;
-        uint32_t pw[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float p0 = __builtin_amdgcn_exp2f(x[2 * t] - mref);
-          const float p1 = __builtin_amdgcn_exp2f(x[2 * t + 1] - mref);
-          psum += p0 + p1;
-          pw[t] = T::pack2(p0, p1);
-        }
-        l_run[qs] += psum;
-        pb[qs] = u32x4{pw[0], pw[1], pw[2], pw[3]};
-      }
-      // V^T operands: all 16 transposing reads issued back to back (opaque to
-      // the compiler, so it does not drain the DMA ring), one LDS wait.
-      u32x4 vf[PT::NJ];
-      {
-        const int vg = lane >> 4, vk = (lane >> 2) & 3, vq = lane & 3;
-        const int r0 = 4 * vg + vk, r1 = r0 + 16;
-#pragma unroll
-        for (int j = 0; j < PT::NJ; ++j) {
-          const int lc = 2 * j + (vq >> 1), sub = (vq & 1) * 8;
-          const u32x2 lo = lds_read_tr16_async(vt + r0 * PT::ROWB + ((lc ^ swz(r0)) << 4) + sub);
-          const u32x2 hi = lds_read_tr16_async(vt + r1 * PT::ROWB + ((lc ^ swz(r1)) << 4) + sub);
-          vf[j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-        }
-      }
-      // The wait names the fragments as in/out operands, so no consumer can
-      // be scheduled above it.
-      static_assert(PT::NJ == 8, "operand list below");
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(vf[0]), "+v"(vf[1]), "+v"(vf[2]), "+v"(vf[3]), "+v"(vf[4]), "+v"(vf[5]), "+v"(vf[6]),
-                     "+v"(vf[7])
-                   :
-                   : "memory");
-#pragma unroll
-      for (int j = 0; j < PT::NJ; ++j) {
-#pragma unroll
-        for (int qs = 0; qs < 2; ++qs) o[qs][j] = T::mfma16x16x32(vf[j], pb[qs], o[qs][j]);
-      }
+        for (int jj = 0; jj < 4; ++jj) o[qs][4 * h + jj] = T::mfma16x16x32(vf[jj], pb[qs], o[qs][4 * h + jj]);
     }
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) lsum[qs] = T::mfma16x16x32(ones, pb[qs], lsum[qs]);
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = sn[qs][ks];
+  };
+
+  // Once per tile jt and wave, in tile order, in both loops below.
+  auto sync_issue = [&]() {
+    wait_vmcnt<2 * (kStages - 3)>();  // this wave's copies of tile jt + 1 have landed
+    wait_lgkmcnt0();                   // and its reads of tile jt - 1 are done
+    raw_barrier();                     // tile jt + 1 complete; slot of tile jt - 1 free
+    issue();                           // tile jt + kStages - 1
+  };
+  // Whether the block of key tile jt exists (the masked loop of an item with
+  // a missing block only).
+  auto block_ok = [&](int jt) {
+    const int blk = ld_const(bt_row + jt * kKeys / a.block_size);
+    return blk >= 0 && blk < a.num_blocks;
+  };
+
+  if (n_kt > 0) {
+#pragma unroll
+    for (int st = 0; st < kStages - 1; ++st) issue();
+    wait_vmcnt<2 * (kStages - 2)>();  // this wave's copies of tile 0 have landed
+    raw_barrier();                     // everyone's
+    if (wave_nkt > 0) qk(0, sc);
   }
-  wait_vmcnt<0>();  // drain the clamped tail copies before the workgroup can exit
+  // The copies of a tile are issued kStages - 1 tiles ahead, so a missing
+  // block is known (any_bad) before its tile is computed; from then on the
+  // masked loop runs.
+  int jt = 0, slot = 0;
+  for (; jt < n_plain && !any_bad; ++jt) {
+    sync_issue();
+    step(std::false_type{}, jt, slot, true);
+    slot = slot + 1 == kStages ? 0 : slot + 1;
+  }
+  for (; jt < n_kt; ++jt) {
+    sync_issue();
+    if (jt < wave_nkt) step(std::true_type{}, jt, slot, !any_bad || block_ok(jt));
+    slot = slot + 1 == kStages ? 0 : slot + 1;
+  }
+  wait_vmcnt<0>();  // drain the tail copies before the LDS is reused
 
   if (!wave_live) return;
 #pragma unroll
   for (int qs = 0; qs < 2; ++qs) {
-    const float l = sum32(sum16(l_run[qs]));
+    const float l = lsum[qs][0];  // every element holds the row sum of row m
     const int row = wrow0 + 16 * qs + m;
     if (row >= Lq) continue;
     const float inv = l > 0.f ? 1.0f / l : 0.f;
@@ -581,7 +660,7 @@ __global__ __launch_bounds__(64 * kNW) __attribute__((amdgpu_waves_per_eu(2)))
 void varlen_prefill_dma_kernel(const PrefillArgs a) {
   using DT = DTile<T, D>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  int *lds_item = reinterpret_cast<int *>(smem + kStages * DT::SLOT_B + kMaxBt * 4);
+  int *lds_item = reinterpret_cast<int *>(smem + kStages * DT::SLOT_B);
 
   const int n_x = a.n_qtiles, n_y = a.Hkv * a.quads;
   const int U = n_y * a.num_seqs;
@@ -592,7 +671,7 @@ void varlen_prefill_dma_kernel(const PrefillArgs a) {
 
   if (threadIdx.x == 0) lds_item[0] = static_cast<int>(atomicAdd(ctr, 1u));
   __syncthreads();
-  int item = lds_item[0];
+  int item = __builtin_amdgcn_readfirstlane(lds_item[0]);  // uniform from here on
   for (int it = 1; item < n_items; ++it) {
     uint32_t next = 0;
     if (threadIdx.x == 0) next = atomicAdd(ctr, 1u);  // in flight while this item runs
@@ -603,7 +682,7 @@ void varlen_prefill_dma_kernel(const PrefillArgs a) {
     // write of slot it+1, which comes after the next barrier.
     if (threadIdx.x == 0) lds_item[it & 1] = static_cast<int>(next);
     __syncthreads();  // also: LDS ring and block table free for the next item
-    item = lds_item[it & 1];
+    item = __builtin_amdgcn_readfirstlane(lds_item[it & 1]);
   }
   if (threadIdx.x == 0) {
     if (atomicAdd(a.queue + 8, 1u) == gridDim.x - 1) {
