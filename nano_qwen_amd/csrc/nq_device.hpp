@@ -233,6 +233,16 @@ __device__ inline u32x2 lds_read_tr16_at(uint32_t addr) {
   return v;
 }
 
+// ds_read_b128 at LDS byte address `addr` + OFF, opaque like lds_read_tr16_at
+// (issued where it stands; the caller waits with a tied s_waitcnt).
+template <int OFF>
+__device__ inline u32x4 lds_read_b128_at(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 

@@ -425,41 +425,48 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
 
   // ---- K/V copies.  Wave w copies rows 4w..4w+3 of each tile; lane l of
   // it fetches the logical 16-byte chunk that belongs at LDS byte 16 l of
-  // the wave's 1 KiB (the chunk swizzle is made by the source offset).
+  // the wave's 1 KiB (the chunk swizzle is made by the source offset).  The
+  // copy state is scalar: the byte offset of the next tile's first row, the
+  // remaining tiles of its block, and the block-table entry of the next
+  // block, fetched one block ahead.
   const int drow = 4 * wave + (lane >> 4);
   const uint32_t src_off = static_cast<uint32_t>(drow * a.kv_rs + kvh * DT::ROWB + (((lane & 15) ^ swz(drow)) << 4));
-  int iss_jt = 0, iss_slot = 0;    // next tile to copy, its ring slot
-  int iss_bidx = 0, iss_in = 0;    // its block-table index and offset in the block
-  int iss_blk = 0;                 // block of iss_bidx (valid when iss_in > 0)
-  bool any_bad = false;            // a tile of this item lies in a missing block
+  const int64_t tile_bytes = static_cast<int64_t>(kKeys) * a.kv_rs;
+  const int64_t v_minus_k = a.v - a.k;
+  const int tiles_per_blk = paged ? a.block_size / kKeys : 0x7fffffff;
+  int iss_jt = 0, iss_slot = 0;   // next tile to copy, its ring slot
+  int iss_left = 0;               // tiles of the current block still to copy (paged)
+  int iss_bidx = 0;               // block-table index of the next block
+  int64_t iss_off = paged ? 0 : static_cast<int64_t>(k0) * a.kv_rs;  // byte offset of the next tile
+  bool iss_ok = true;             // the current block exists
+  bool any_bad = false;           // a tile of this item lies in a missing block
+  // Block-table entry bidx of this sequence (paged only: bt_row is null otherwise).
+  auto blk_entry = [&](int bidx) { return bidx < a.max_blocks ? ld_const(bt_row + bidx) : -1; };
+  int blk_next = paged ? blk_entry(0) : 0;
   auto issue = [&]() {
-    int nvalid = 0;
-    int64_t row0 = 0;
+    uint32_t nrec = 0;
     if (iss_jt < n_kt) {
-      nvalid = min(kKeys, key_end - iss_jt * kKeys);
-      if (paged) {
-        if (iss_in == 0) iss_blk = (iss_bidx < a.max_blocks) ? ld_const(bt_row + iss_bidx) : -1;
-        const bool ok = iss_blk >= 0 && iss_blk < a.num_blocks;
-        any_bad |= !ok;
-        row0 = static_cast<int64_t>(ok ? iss_blk : 0) * a.block_size + iss_in;
-        if (!ok) nvalid = 0;
-        iss_in += kKeys;
-        if (iss_in == a.block_size) {
-          iss_in = 0;
-          ++iss_bidx;
-        }
-      } else {
-        row0 = static_cast<int64_t>(k0) + iss_jt * kKeys;
+      if (paged && iss_left == 0) {  // entering the next block
+        const int blk = blk_next;
+        blk_next = blk_entry(iss_bidx + 1);  // used a block from now
+        ++iss_bidx;
+        iss_ok = blk >= 0 && blk < a.num_blocks;
+        any_bad |= !iss_ok;
+        iss_off = static_cast<int64_t>(iss_ok ? blk : 0) * a.block_size * a.kv_rs;
+        iss_left = tiles_per_blk;
       }
+      const int nvalid = min(kKeys, key_end - iss_jt * kKeys);
+      nrec = iss_ok ? static_cast<uint32_t>(nvalid * a.kv_rs) : 0u;
     }
-    const int64_t base = row0 * a.kv_rs;
-    const uint32_t nrec = static_cast<uint32_t>(nvalid * a.kv_rs);
     uint8_t *dst = smem + iss_slot * DT::SLOT_B + wave * 1024;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.k + base, nrec),
+    const uint8_t *ksrc = a.k + iss_off;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(ksrc, nrec),
                                              (__attribute__((address_space(3))) void *)dst, 16, src_off, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.v + base, nrec),
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(ksrc + v_minus_k, nrec),
                                              (__attribute__((address_space(3))) void *)(dst + DT::TILE_B), 16,
                                              src_off, 0, 0, 0);
+    iss_off += tile_bytes;
+    if (paged) --iss_left;
     ++iss_jt;
     iss_slot = (iss_slot + 1 == kStages) ? 0 : iss_slot + 1;
   };
@@ -479,22 +486,36 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
       (__attribute__((address_space(3))) uint8_t *)(smem)));
 
-  // S^T (32 keys x 32 rows, unscaled) of the tile in ring slot `slot`.
-  auto qk = [&](int slot, f32x4 (&sc)[2][2]) {
-    const uint8_t *kt = smem + slot * DT::SLOT_B;
+  // K^T operands of the tile in ring slot `slot` (opaque reads: the caller
+  // waits for them with a tied s_waitcnt), then S^T = K Q^T (32 keys x 32
+  // rows, unscaled).
+  auto kread = [&](int slot, u32x4 (&kf)[PT::NKK][2]) {
+    const uint32_t kt = lds0 + slot * DT::SLOT_B;
+#pragma unroll
+    for (int kk = 0; kk < PT::NKK; ++kk) {
+      kf[kk][0] = lds_read_b128_at<0>(kt + koff[kk]);
+      kf[kk][1] = lds_read_b128_at<16 * DT::ROWB>(kt + koff[kk]);
+    }
+  };
+  auto kwait = [&](u32x4 (&kf)[PT::NKK][2]) {
+    static_assert(PT::NKK == 4, "operand list below");
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(kf[0][0]), "+v"(kf[0][1]), "+v"(kf[1][0]), "+v"(kf[1][1]), "+v"(kf[2][0]), "+v"(kf[2][1]),
+                   "+v"(kf[3][0]), "+v"(kf[3][1])
+                 :
+                 : "memory");
+  };
+  auto qk = [&](const u32x4 (&kf)[PT::NKK][2], f32x4 (&sc)[2][2]) {
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = f32x4{0, 0, 0, 0};
 #pragma unroll
-    for (int kk = 0; kk < PT::NKK; ++kk) {
+    for (int kk = 0; kk < PT::NKK; ++kk)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const u32x4 kf = *reinterpret_cast<const u32x4 *>(kt + koff[kk] + ks * 16 * DT::ROWB);
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int qs = 0; qs < 2; ++qs) sc[qs][ks] = T::mfma16x16x32(kf, qf[qs][kk], sc[qs][ks]);
-      }
-    }
+        for (int qs = 0; qs < 2; ++qs) sc[qs][ks] = T::mfma16x16x32(kf[kk][ks], qf[qs][kk], sc[qs][ks]);
   };
 
   float m_use[2] = {kNegInf, kNegInf};  // running row max, scaled (log2) domain
@@ -507,13 +528,17 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
   }
   const u32x4 ones = u32x4{T::kOne2, T::kOne2, T::kOne2, T::kOne2};
 
-  // One key tile: softmax of the current S (`sc`, tile jt, in ring slot
-  // `slot`) and O += P V, with the QK products of tile jt + 1 issued
-  // alongside (independent MFMA work for the exp / pack VALU work).
+  // One key tile, right after the barrier that completes tile jt + 1:
+  // softmax of the current S (`sc`, tile jt in ring slot `slot`) and
+  // O += P V, with the K reads and QK products of tile jt + 1 and the copy
+  // of tile jt + kStages - 1 issued alongside, so the LDS latency hides
+  // under the row-max work and the MFMAs under the exp / pack work.
   f32x4 sc[2][2];
   auto step = [&](auto mask_tag, int jt, int slot, bool blk_ok) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const int kbase = jt * kKeys;
+    u32x4 kf[PT::NKK][2];
+    kread(slot + 1 == kStages ? 0 : slot + 1, kf);  // tile jt + 1 (a discarded repeat past the last)
     float x[2][8], mnew[2];
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
@@ -547,10 +572,10 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
         m_use[qs] = m_new;
       }
     }
-    // S of tile jt + 1 (unused past this wave's last tile: the slot then
-    // holds zeros or a later tile, read in bounds and discarded).
+    issue();
+    kwait(kf);
     f32x4 sn[2][2];
-    qk(slot + 1 == kStages ? 0 : slot + 1, sn);
+    qk(kf, sn);
     u32x4 pb[2];
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
@@ -591,12 +616,12 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
       for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = sn[qs][ks];
   };
 
-  // Once per tile jt and wave, in tile order, in both loops below.
-  auto sync_issue = [&]() {
+  // Once per tile jt and wave, in tile order, in both loops below; waves
+  // with no work on tile jt still copy their share of tile jt + kStages - 1.
+  auto sync = [&]() {
     wait_vmcnt<2 * (kStages - 3)>();  // this wave's copies of tile jt + 1 have landed
     wait_lgkmcnt0();                   // and its reads of tile jt - 1 are done
     raw_barrier();                     // tile jt + 1 complete; slot of tile jt - 1 free
-    issue();                           // tile jt + kStages - 1
   };
   // Whether the block of key tile jt exists (the masked loop of an item with
   // a missing block only).
@@ -610,20 +635,28 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
     for (int st = 0; st < kStages - 1; ++st) issue();
     wait_vmcnt<2 * (kStages - 2)>();  // this wave's copies of tile 0 have landed
     raw_barrier();                     // everyone's
-    if (wave_nkt > 0) qk(0, sc);
+    if (wave_nkt > 0) {
+      u32x4 kf[PT::NKK][2];
+      kread(0, kf);
+      kwait(kf);
+      qk(kf, sc);
+    }
   }
   // The copies of a tile are issued kStages - 1 tiles ahead, so a missing
   // block is known (any_bad) before its tile is computed; from then on the
   // masked loop runs.
   int jt = 0, slot = 0;
   for (; jt < n_plain && !any_bad; ++jt) {
-    sync_issue();
+    sync();
     step(std::false_type{}, jt, slot, true);
     slot = slot + 1 == kStages ? 0 : slot + 1;
   }
   for (; jt < n_kt; ++jt) {
-    sync_issue();
-    if (jt < wave_nkt) step(std::true_type{}, jt, slot, !any_bad || block_ok(jt));
+    sync();
+    if (jt < wave_nkt)
+      step(std::true_type{}, jt, slot, !any_bad || block_ok(jt));
+    else
+      issue();
     slot = slot + 1 == kStages ? 0 : slot + 1;
   }
   wait_vmcnt<0>();  // drain the tail copies before the LDS is reused
