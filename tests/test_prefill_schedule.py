@@ -110,7 +110,10 @@ def test_copy_schedule_edges_and_missing_block():
         bt[i, :k] = perm[off:off + k]
         off += k
     assert_in_bounds(lq, lk, bt, 20, 256, 8, 32)
-    bt[2, 0] = -1  # a missing block is never copied from
-    rows = list(copy_schedule(lq, lk, bt, 20, 256, 8, 32))
-    assert all(not (s == 2 and lo < 256) or True for s, lo, _ in rows)
+    full = [c for c in copy_schedule(lq, lk, bt, 20, 256, 8, 32) if c[0] == 2]
+    first = int(bt[2, 0])
+    bt[2, 0] = -1  # a missing block: its tiles are not copied (they read as zeros)
+    holed = [c for c in copy_schedule(lq, lk, bt, 20, 256, 8, 32) if c[0] == 2]
     assert_in_bounds(lq, lk, bt, 20, 256, 8, 32)
+    assert len(holed) < len(full)
+    assert all(lo // 256 != first for _, lo, _ in holed)
