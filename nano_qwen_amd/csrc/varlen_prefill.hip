@@ -556,15 +556,19 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
           if constexpr (MASK) v = (kbase + 16 * ks + 4 * g + rr > lim) ? kNegInf : v;
           x[qs][4 * ks + rr] = v;
         }
-      const float ml = max3_raw(max3_raw(x[qs][0], x[qs][1], x[qs][2]), max3_raw(x[qs][3], x[qs][4], x[qs][5]),
-                                vmax_raw(x[qs][6], x[qs][7]));
-      mnew[qs] = max32_raw(max16_raw(ml)) * sl2;
+      // this lane's maximum over its 8 keys of row m (scaled)
+      mnew[qs] = max3_raw(max3_raw(x[qs][0], x[qs][1], x[qs][2]), max3_raw(x[qs][3], x[qs][4], x[qs][5]),
+                          vmax_raw(x[qs][6], x[qs][7])) * sl2;
     }
-    // Lazy rescale: only when a row max grows by more than 2^kRescale.
+    // Lazy rescale: the running maximum m_use of a row (the same in the four
+    // lanes that hold the row) only moves when some element exceeds it by
+    // more than kRescale, so P = 2^(s - m_use) <= 2^kRescale.  Each lane
+    // checks its own elements; the cross-lane row maximum is only formed when
+    // a rescale happens.
     if (__builtin_amdgcn_ballot_w64(mnew[0] > m_use[0] + kRescale || mnew[1] > m_use[1] + kRescale) != 0) {
 #pragma unroll
       for (int qs = 0; qs < 2; ++qs) {
-        const float m_new = fmaxf(m_use[qs], mnew[qs]);
+        const float m_new = fmaxf(m_use[qs], max32_raw(max16_raw(mnew[qs])));
         const float alpha = (m_use[qs] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(m_use[qs] - m_new);
         lsum[qs] *= alpha;
 #pragma unroll
