@@ -210,6 +210,34 @@ def cpu_baseline_prefill(case, n_seqs=2, reps=3):
                        f"attention only, median of {reps}", seconds=t)
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "paged_decode_cfg2_traffic.md")
+
+
+def measured_traffic(path=TRAFFIC_FILE):
+    """HBM bytes per launch of the headline kernels, from the committed
+    rocprofv3 counter summary (a line `traffic_bytes_per_launch: N`), or None."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        return None
+    return None
+
+
+def copy_calibration(nbytes, reps=3):
+    """A plain device copy of `nbytes` (reads nbytes, writes nbytes), for
+    scaling rocprofv3's FETCH_SIZE / WRITE_SIZE to bytes."""
+    import torch
+    x = torch.ones(nbytes, dtype=torch.uint8, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(reps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": nbytes, "reps": reps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -217,6 +245,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None, help="run one config (cfg2|cfg3|cfg4|cfg5)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device copy of BYTES (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures the paged attention path on ONE GPU; "
@@ -224,6 +254,9 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from nano_qwen_amd._lib import lib
     lib()
@@ -281,7 +314,7 @@ def main():
         line["roofline"] = {
             "bound": "hbm", "kernel": "paged_decode (main + split-K merge)",
             "achieved": round(head["attn_gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(head["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(head["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
             "attn_ms": round(head["attn_ms"], 5), "algorithmic_bytes": head["attn_bytes"],
         }
     if "cfg3" in extra:
