@@ -9,16 +9,20 @@
 // block table (any prefix hit in the batch, engine/model_runner.py:275-276)
 // K/V are the whole paged cache (layers/attention.py:65-66).
 //
-// Design (one workgroup = 4 waves; each wave = one query head x 32 rows):
+// Two kernels share the tile layout and the softmax:
+//  * varlen_prefill_dma_kernel (16-bit K/V): persistent workgroups of 8 waves
+//    (G4 <= 4 query heads of one kv head x row blocks of 32), one per CU,
+//    pulling work items from per-XCD queues; K/V tiles of 32 keys are copied
+//    HBM -> LDS by the LDS DMA into a 5-slot ring (no VGPRs), the QK
+//    products of tile j+1 overlap the softmax of tile j.
+//  * varlen_prefill_kernel (fp8 K/V): 4-wave workgroups, one per query tile,
+//    K/V staged through registers (global -> convert -> LDS) into a double
+//    buffer.
+// Common to both:
 //  * GQA sharing in LDS: the waves of a workgroup are query heads of the SAME
-//    kv head (G4 = min(G, 4) heads x 4/G4 row blocks), so every K/V tile
-//    staged in LDS serves all of them; heads of one group also share the
-//    causal structure, so the waves run identical trip counts.
-//  * K/V tiles of 32 keys, double-buffered in LDS: the loads of tile j+1 are
-//    in flight while tile j is computed (one barrier per tile).  A tile never
-//    crosses a cache block (block_size % 32 == 0), so one scalar buffer
-//    descriptor covers it and keys past the causal limit read as zeros.  The
-//    sequence's block-table row is copied to LDS once.
+//    kv head, so every K/V tile staged in LDS serves all of them.
+//  * A tile never crosses a cache block (block_size % 32 == 0), so one buffer
+//    descriptor covers it and keys past the causal limit read as zeros.
 //  * S^T = K . Q^T and O^T += V^T . P^T on v_mfma_f32_16x16x32 with Q in
 //    registers; P stays in registers (the S^T accumulator layout is the PV
 //    B-operand layout); V^T comes from the row-major tile through
@@ -26,9 +30,6 @@
 //    operand reads are bank-conflict free.
 //  * Online softmax in the log2 domain with lazy rescaling: O and l are only
 //    rescaled when a row maximum grows by more than 2^8, so P <= 256.
-//  * Grid order (map_work): the workgroups of one (sequence, kv head) stay on
-//    one XCD and share its L2, every XCD gets a share of every sequence, and
-//    within an XCD the last query tiles (the most keys) start first.
 #include <type_traits>
 
 #include "nq_device.hpp"
