@@ -30,6 +30,8 @@
 //    operand reads are bank-conflict free.
 //  * Online softmax in the log2 domain with lazy rescaling: O and l are only
 //    rescaled when a row maximum grows by more than 2^8, so P <= 256.
+#include <stdlib.h>
+
 #include <type_traits>
 
 #include "nq_device.hpp"
@@ -69,6 +71,17 @@ struct PrefillArgs {
 };
 
 __device__ inline int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1) | (row & 8); }
+
+// Chunk swizzles of the 16-bit DMA kernel's LDS tiles (16-byte chunk c of
+// key row r is stored at chunk c ^ swz(r)), one per tile because the two
+// operand reads want different ones.  Measured with SQ_LDS_BANK_CONFLICT on
+// gfx950 over all bit permutations of r: the K operand's ds_read_b128 (16
+// rows x one chunk per 16 lanes) is conflict-free exactly when swizzle bit 0
+// comes from row bit 0 or 1, the V^T operand's ds_read_b64_tr_b16 (rows
+// 4vg..4vg+3 x 32 bytes) exactly when it comes from row bit 3; both halve
+// the LDS throughput (2-way conflicts) otherwise.
+__device__ inline int swz_k(int row) { return row & 15; }
+__device__ inline int swz_v(int row) { return ((row & 7) << 1) | ((row >> 3) & 1); }
 
 // Work item of a workgroup: query tile qt of kv-head slot y (kv head x quad)
 // of sequence s.
@@ -350,16 +363,24 @@ void varlen_prefill_kernel(const PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// 16-bit K/V: 8-wave workgroups fed by an LDS DMA ring.
+// 16-bit K/V: persistent workgroups fed by an LDS DMA ring.
 //
-// K/V tiles of 32 keys go HBM/L2 -> LDS directly (global_load_lds_dwordx4,
-// no VGPRs), into a ring of kStages slots, so kStages-1 tiles are in flight
-// while one is computed.  Each wave copies 4 rows of K and 4 of V per tile;
-// it waits for its own copies (vmcnt) and a raw workgroup barrier makes the
-// whole tile visible.  The chunk swizzle of the LDS tile is produced by the
-// source address each lane fetches.
-constexpr int kNW = 8;  // waves per workgroup
-constexpr int kStages = 5;
+// K/V tiles of 32 keys go HBM/L2 -> LDS directly (buffer loads to LDS, no
+// VGPRs), into a ring of kSlots slots; copies run kAhead tiles ahead of the
+// tile being computed.  Each of the NW waves copies 32/NW rows of K and of V
+// per tile (1 KiB = 4 rows per load); it waits for its own copies (vmcnt)
+// and one raw workgroup barrier per tile makes the whole tile visible.  The
+// chunk swizzle of the LDS tile is produced by the source offset each lane
+// fetches.
+//
+// Shape <NW, QS>: NW waves per workgroup, each wave QS x 16 query rows of one
+// head.  <8, 2> runs two waves per SIMD (up to 256 registers each); <4, 4>
+// one wave per SIMD with 64 rows, so every K/V operand read from LDS and
+// every per-tile step (barrier, copies, checks) serves twice the rows.  Both
+// cover 256 / G4 query rows x G4 heads per work item.
+constexpr int kSlots = 5;  // LDS ring slots
+constexpr int kAhead = 4;  // tiles copied ahead of the tile being computed
+constexpr int kItemRows = 256;  // query rows x heads of one work item (G4 heads x 256/G4 rows)
 
 template <class T, int D>
 struct DTile {
@@ -367,46 +388,50 @@ struct DTile {
   static constexpr int ROWB = D * 2;
   static constexpr int TILE_B = kKeys * ROWB;   // 8 KiB per K (or V) tile
   static constexpr int SLOT_B = 2 * TILE_B;     // K + V
-  static constexpr int LDS_BYTES = kStages * SLOT_B + 16;  // + queue item slots
+  static constexpr int LDS_BYTES = kSlots * SLOT_B + 16;  // + queue item slots
 };
 
-// One work item of the persistent kernel: query tile qt (64 rows per head,
-// kNW/G4 row blocks of 32) of kv-head slot y of sequence s.
+// One work item of the persistent kernel: query tile qt (kItemRows/G4 rows
+// of G4 heads) of kv-head slot y of sequence s.
 //
 // Per key tile, all control is scalar (wave-uniform): the copy of tile
-// jt + kStages - 1 is two buffer-to-LDS loads through descriptors whose range
-// ends at the tile's last valid key (rows past it read as zeros, so no
-// clamping), and the block table is walked one block at a time with scalar
-// loads.  Tiles that every row of the wave sees completely run a mask-free
-// loop; the rest (the causal diagonal, the end of the keys, any tile of a
-// sequence with a missing block) run the masked loop.
-template <class T, int D>
+// jt + kAhead is buffer-to-LDS loads through descriptors whose range ends at
+// the tile's last valid key (rows past it read as zeros, so no clamping),
+// and the block table is walked one block at a time with scalar loads.
+// Tiles that every row of the wave sees completely run a mask-free loop; the
+// rest (the causal diagonal, the end of the keys, any tile of a sequence
+// with a missing block) run the masked loop.
+template <class T, int D, int NW, int QS>
 __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y, int s, uint8_t *smem) {
   using DT = DTile<T, D>;
   using PT = PTile<T, false, D>;
+  constexpr int RW = 16 * QS;        // query rows per wave
+  constexpr int CR = kKeys / NW;     // tile rows each wave copies
+  constexpr int COPS = CR / 4;       // 1 KiB loads per K (or V) per wave and tile
+  static_assert(CR % 4 == 0, "a copy moves whole groups of 4 rows");
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int m = lane & 15, g = lane >> 4;
 
   const int kvh = y / a.quads, quad = y % a.quads;
-  const int rb = kNW / a.G4;  // row blocks of 32 per workgroup
+  const int rb = NW / a.G4;  // row blocks of RW per workgroup
   const int head = kvh * a.G + quad * 4 + (wave % a.G4);
   const int q0 = ld_const(a.cu_q + s), Lq = ld_const(a.cu_q + s + 1) - q0;
-  const int row_begin = qt * kRows * rb;
+  const int row_begin = qt * RW * rb;
   if (row_begin >= Lq) return;
   const int k0 = ld_const(a.cu_k + s), Lk = ld_const(a.cu_k + s + 1) - k0;
   const int P = Lk - Lq;
-  const int row_last = min(row_begin + kRows * rb, Lq) - 1;
+  const int row_last = min(row_begin + RW * rb, Lq) - 1;
   const int key_end = a.causal ? max(0, min(Lk, row_last + P + 1)) : Lk;
   const int n_kt = (key_end + kKeys - 1) / kKeys;
   const float sl2 = a.scale_log2;
   const bool paged = a.block_tables != nullptr;
   const int32_t *bt_row = paged ? a.block_tables + static_cast<int64_t>(s) * a.bt_stride : nullptr;
 
-  const int wrow0 = row_begin + kRows * (wave / a.G4);
+  const int wrow0 = row_begin + RW * (wave / a.G4);
   const bool wave_live = wrow0 < Lq;
-  const int wrow_last = min(wrow0 + kRows - 1, Lq - 1);
+  const int wrow_last = min(wrow0 + RW - 1, Lq - 1);
   const int wave_key_end = a.causal ? min(Lk, wrow_last + P + 1) : Lk;
   // Tiles this wave computes (a prefix: a causal wave stops at its own
   // diagonal) and, among them, the leading tiles that need no mask.
@@ -414,9 +439,9 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
   int n_plain = min(wave_nkt, Lk / kKeys);
   if (a.causal) n_plain = min(n_plain, max(0, wrow0 + P + 1) / kKeys);
 
-  u32x4 qf[2][PT::NKK];
+  u32x4 qf[QS][PT::NKK];
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
+  for (int qs = 0; qs < QS; ++qs) {
     const int r = wrow0 + 16 * qs + m;
     const bool ok = r < Lq;
     const uint8_t *qp = a.q + static_cast<int64_t>(q0 + (ok ? r : 0)) * a.q_rs + static_cast<int64_t>(head) * a.q_hs;
@@ -424,14 +449,20 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
     for (int kk = 0; kk < PT::NKK; ++kk) qf[qs][kk] = ok ? load16(qp + (8 * g + 32 * kk) * 2) : u32x4{0, 0, 0, 0};
   }
 
-  // ---- K/V copies.  Wave w copies rows 4w..4w+3 of each tile; lane l of
-  // it fetches the logical 16-byte chunk that belongs at LDS byte 16 l of
-  // the wave's 1 KiB (the chunk swizzle is made by the source offset).  The
-  // copy state is scalar: the byte offset of the next tile's first row, the
-  // remaining tiles of its block, and the block-table entry of the next
-  // block, fetched one block ahead.
-  const int drow = 4 * wave + (lane >> 4);
-  const uint32_t src_off = static_cast<uint32_t>(drow * a.kv_rs + kvh * DT::ROWB + (((lane & 15) ^ swz(drow)) << 4));
+  // ---- K/V copies.  Wave w copies rows CR*w .. CR*w + CR - 1 of each tile,
+  // 4 rows per load; lane l of load c fetches the logical 16-byte chunk that
+  // belongs at byte 16 l of the load's 1 KiB (the chunk swizzles swz_k /
+  // swz_v are made by the source offsets).  The copy state is scalar: the byte offset of the
+  // next tile's first row, the remaining tiles of its block, and the
+  // block-table entry of the next block, fetched one block ahead.
+  uint32_t src_k[COPS], src_v[COPS];
+#pragma unroll
+  for (int c = 0; c < COPS; ++c) {
+    const int drow = CR * wave + 4 * c + (lane >> 4);
+    const uint32_t row_off = static_cast<uint32_t>(drow * a.kv_rs + kvh * DT::ROWB);
+    src_k[c] = row_off + (((lane & 15) ^ swz_k(drow)) << 4);
+    src_v[c] = row_off + (((lane & 15) ^ swz_v(drow)) << 4);
+  }
   const int64_t tile_bytes = static_cast<int64_t>(kKeys) * a.kv_rs;
   const int64_t v_minus_k = a.v - a.k;
   const int tiles_per_blk = paged ? a.block_size / kKeys : 0x7fffffff;
@@ -459,36 +490,41 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
       const int nvalid = min(kKeys, key_end - iss_jt * kKeys);
       nrec = iss_ok ? static_cast<uint32_t>(nvalid * a.kv_rs) : 0u;
     }
-    uint8_t *dst = smem + iss_slot * DT::SLOT_B + wave * 1024;
+    uint8_t *dst = smem + iss_slot * DT::SLOT_B + wave * (CR * DT::ROWB);
     const uint8_t *ksrc = a.k + iss_off;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(ksrc, nrec),
-                                             (__attribute__((address_space(3))) void *)dst, 16, src_off, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(ksrc + v_minus_k, nrec),
-                                             (__attribute__((address_space(3))) void *)(dst + DT::TILE_B), 16,
-                                             src_off, 0, 0, 0);
+    const auto rk = make_rsrc(ksrc, nrec);
+    const auto rv = make_rsrc(ksrc + v_minus_k, nrec);
+#pragma unroll
+    for (int c = 0; c < COPS; ++c) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void *)(dst + 1024 * c), 16,
+                                               src_k[c], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rv, (__attribute__((address_space(3))) void *)(dst + DT::TILE_B + 1024 * c), 16, src_v[c], 0, 0, 0);
+    }
     iss_off += tile_bytes;
     if (paged) --iss_left;
     ++iss_jt;
-    iss_slot = (iss_slot + 1 == kStages) ? 0 : iss_slot + 1;
+    iss_slot = (iss_slot + 1 == kSlots) ? 0 : iss_slot + 1;
   };
 
   // Per-lane LDS byte offsets inside a K or V tile (fixed for the item).
   // K^T operand kk: key row m (row m + 16 is +16 rows), dims 32kk + 8g.. ;
-  // V^T operand j: rows r0 and r0 + 16 (same swizzle: swz() ignores bit 4).
+  // V^T operand j: rows r0 and r0 + 16 (same swizzle: both swizzles ignore
+  // row bit 4).
   int koff[PT::NKK], voff[PT::NJ];
 #pragma unroll
-  for (int kk = 0; kk < PT::NKK; ++kk) koff[kk] = m * DT::ROWB + (((4 * kk + g) ^ swz(m)) << 4);
+  for (int kk = 0; kk < PT::NKK; ++kk) koff[kk] = m * DT::ROWB + (((4 * kk + g) ^ swz_k(m)) << 4);
   {
     const int vg = lane >> 4, vk = (lane >> 2) & 3, vq = lane & 3;
     const int r0 = 4 * vg + vk;
 #pragma unroll
-    for (int j = 0; j < PT::NJ; ++j) voff[j] = r0 * DT::ROWB + (((2 * j + (vq >> 1)) ^ swz(r0)) << 4) + (vq & 1) * 8;
+    for (int j = 0; j < PT::NJ; ++j) voff[j] = r0 * DT::ROWB + (((2 * j + (vq >> 1)) ^ swz_v(r0)) << 4) + (vq & 1) * 8;
   }
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
       (__attribute__((address_space(3))) uint8_t *)(smem)));
 
   // K^T operands of the tile in ring slot `slot` (opaque reads: the caller
-  // waits for them with a tied s_waitcnt), then S^T = K Q^T (32 keys x 32
+  // waits for them with a tied s_waitcnt), then S^T = K Q^T (32 keys x RW
   // rows, unscaled).
   auto kread = [&](int slot, u32x4 (&kf)[PT::NKK][2]) {
     const uint32_t kt = lds0 + slot * DT::SLOT_B;
@@ -506,9 +542,9 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
                  :
                  : "memory");
   };
-  auto qk = [&](const u32x4 (&kf)[PT::NKK][2], f32x4 (&sc)[2][2]) {
+  auto qk = [&](const u32x4 (&kf)[PT::NKK][2], f32x4 (&sc)[QS][2]) {
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs)
+    for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = f32x4{0, 0, 0, 0};
 #pragma unroll
@@ -516,33 +552,50 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int qs = 0; qs < 2; ++qs) sc[qs][ks] = T::mfma16x16x32(kf[kk][ks], qf[qs][kk], sc[qs][ks]);
+        for (int qs = 0; qs < QS; ++qs) sc[qs][ks] = T::mfma16x16x32(kf[kk][ks], qf[qs][kk], sc[qs][ks]);
   };
 
-  float m_use[2] = {kNegInf, kNegInf};  // running row max, scaled (log2) domain
-  f32x4 o[2][PT::NJ], lsum[2];          // O^T accumulators; row sums of P (every element)
+  // V^T operands of head_dim half h (dims 64h .. 64h+63) of the tile in ring
+  // slot `slot`: 8 opaque transposing reads.
+  auto vread = [&](int slot, int h, u32x4 (&vf)[4]) {
+    const uint32_t vt = lds0 + slot * DT::SLOT_B + DT::TILE_B;
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
+    for (int jj = 0; jj < 4; ++jj) {
+      const u32x2 lo = lds_read_tr16_at<0>(vt + voff[4 * h + jj]);
+      const u32x2 hi = lds_read_tr16_at<16 * DT::ROWB>(vt + voff[4 * h + jj]);
+      vf[jj] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+  };
+
+  float m_use[QS];      // running row max, scaled (log2) domain
+  f32x4 o[QS][PT::NJ];  // O^T accumulators
+  f32x4 lsum[QS];       // row sums of P (every element)
+#pragma unroll
+  for (int qs = 0; qs < QS; ++qs) {
+    m_use[qs] = kNegInf;
     lsum[qs] = f32x4{0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < PT::NJ; ++j) o[qs][j] = f32x4{0, 0, 0, 0};
   }
   const u32x4 ones = u32x4{T::kOne2, T::kOne2, T::kOne2, T::kOne2};
 
-  // One key tile, right after the barrier that completes tile jt + 1:
-  // softmax of the current S (`sc`, tile jt in ring slot `slot`) and
-  // O += P V, with the K reads and QK products of tile jt + 1 and the copy
-  // of tile jt + kStages - 1 issued alongside, so the LDS latency hides
-  // under the row-max work and the MFMAs under the exp / pack work.
-  f32x4 sc[2][2];
-  auto step = [&](auto mask_tag, int jt, int slot, bool blk_ok) {
+  // First half of key tile jt, right after the barrier that completes tile
+  // jt + 1: the lazy-rescale check of the current S (`sc`, tile jt), the K
+  // reads and QK products of tile jt + 1 (into `sc` on return) and P of tile
+  // jt (into `pb`), with the copy of tile jt + kAhead issued in between, so
+  // the LDS latency hides under the check and the MFMAs under the exp / pack
+  // work.  MASK: the tile crosses the causal diagonal, the end of the keys,
+  // or a missing block.
+  f32x4 sc[QS][2];
+  auto front = [&](auto mask_tag, int jt, int slot, bool blk_ok, u32x4 (&pb)[QS], u32x4 (&vf0)[4]) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const int kbase = jt * kKeys;
     u32x4 kf[PT::NKK][2];
-    kread(slot + 1 == kStages ? 0 : slot + 1, kf);  // tile jt + 1 (a discarded repeat past the last)
-    float x[2][8], mnew[2];
+    kread(slot + 1 == kSlots ? 0 : slot + 1, kf);  // tile jt + 1 (a discarded repeat past the last)
+    float x[QS][8], mnew[QS];
+    bool grow = false;
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
+    for (int qs = 0; qs < QS; ++qs) {
       int lim = 0;
       if constexpr (MASK) {
         const int row = wrow0 + 16 * qs + m;
@@ -560,15 +613,16 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
       // this lane's maximum over its 8 keys of row m (scaled)
       mnew[qs] = max3_raw(max3_raw(x[qs][0], x[qs][1], x[qs][2]), max3_raw(x[qs][3], x[qs][4], x[qs][5]),
                           vmax_raw(x[qs][6], x[qs][7])) * sl2;
+      grow |= mnew[qs] > m_use[qs] + kRescale;
     }
     // Lazy rescale: the running maximum m_use of a row (the same in the four
     // lanes that hold the row) only moves when some element exceeds it by
     // more than kRescale, so P = 2^(s - m_use) <= 2^kRescale.  Each lane
     // checks its own elements; the cross-lane row maximum is only formed when
-    // a rescale happens.
-    if (__builtin_amdgcn_ballot_w64(mnew[0] > m_use[0] + kRescale || mnew[1] > m_use[1] + kRescale) != 0) {
+    // a rescale happens.  All earlier tiles' P V products are already in o.
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
+      for (int qs = 0; qs < QS; ++qs) {
         const float m_new = fmaxf(m_use[qs], max32_raw(max16_raw(mnew[qs])));
         const float alpha = (m_use[qs] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(m_use[qs] - m_new);
         lsum[qs] *= alpha;
@@ -579,11 +633,11 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
     }
     issue();
     kwait(kf);
-    f32x4 sn[2][2];
+    vread(slot, 0, vf0);  // first half of tile jt's V^T operands, waited for in back()
+    f32x4 sn[QS][2];
     qk(kf, sn);
-    u32x4 pb[2];
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
+    for (int qs = 0; qs < QS; ++qs) {
       const float mref = (m_use[qs] == kNegInf) ? 0.f : m_use[qs];
       uint32_t pw[4];
 #pragma unroll
@@ -594,39 +648,49 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
       }
       pb[qs] = u32x4{pw[0], pw[1], pw[2], pw[3]};
     }
-    // O^T += V^T P^T in two halves of head_dim (4 V^T operands live at a
-    // time); the transposing reads are opaque and waited for by a wait that
-    // names their registers, so no MFMA is scheduled above it.
-    const uint32_t vt = lds0 + slot * DT::SLOT_B + DT::TILE_B;
+    // Interleave the 8 QS QK products with the ~20 QS exp / scale / pack
+    // instructions (one MFMA, then two VALU), so the VALU work issues while
+    // the matrix core is busy instead of in a run of its own.
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      u32x4 vf[4];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const u32x2 lo = lds_read_tr16_at<0>(vt + voff[4 * h + jj]);
-        const u32x2 hi = lds_read_tr16_at<16 * DT::ROWB>(vt + voff[4 * h + jj]);
-        vf[jj] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-      }
-      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vf[0]), "+v"(vf[1]), "+v"(vf[2]), "+v"(vf[3]) : : "memory");
-#pragma unroll
-      for (int qs = 0; qs < 2; ++qs)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) o[qs][4 * h + jj] = T::mfma16x16x32(vf[jj], pb[qs], o[qs][4 * h + jj]);
+    for (int i = 0; i < 8 * QS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
     }
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) lsum[qs] = T::mfma16x16x32(ones, pb[qs], lsum[qs]);
-#pragma unroll
-    for (int qs = 0; qs < 2; ++qs)
+    for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = sn[qs][ks];
   };
+  // Second half: O^T += V^T P^T for the tile in ring slot `slot`, in two
+  // halves of head_dim (4 V^T operands of 16 dims each per half).  The first
+  // half's transposing reads were issued in front(); the second half's are
+  // issued here before the first half's products.  The reads are opaque and
+  // waited for by waits that name their registers, so no MFMA is scheduled
+  // above them (LDS reads complete in order: lgkmcnt(8) leaves only the
+  // second half outstanding).
+  auto back = [&](int slot, const u32x4 (&pb)[QS], u32x4 (&vf0)[4]) {
+    u32x4 vf1[4];
+    vread(slot, 1, vf1);
+    asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(vf0[0]), "+v"(vf0[1]), "+v"(vf0[2]), "+v"(vf0[3]) : : "memory");
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) o[qs][jj] = T::mfma16x16x32(vf0[jj], pb[qs], o[qs][jj]);
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vf1[0]), "+v"(vf1[1]), "+v"(vf1[2]), "+v"(vf1[3]) : : "memory");
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) o[qs][4 + jj] = T::mfma16x16x32(vf1[jj], pb[qs], o[qs][4 + jj]);
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs) lsum[qs] = T::mfma16x16x32(ones, pb[qs], lsum[qs]);
+  };
 
   // Once per tile jt and wave, in tile order, in both loops below; waves
-  // with no work on tile jt still copy their share of tile jt + kStages - 1.
+  // with no work on tile jt still copy their share of tile jt + kAhead.
   auto sync = [&]() {
-    wait_vmcnt<2 * (kStages - 3)>();  // this wave's copies of tile jt + 1 have landed
-    wait_lgkmcnt0();                   // and its reads of tile jt - 1 are done
-    raw_barrier();                     // tile jt + 1 complete; slot of tile jt - 1 free
+    wait_vmcnt<2 * COPS * (kAhead - 2)>();  // this wave's copies of tile jt + 1 have landed
+    wait_lgkmcnt0();                         // and its reads of tile jt - 1 are done
+    raw_barrier();                           // tile jt + 1 complete; slot of tile jt - 1 free
   };
   // Whether the block of key tile jt exists (the masked loop of an item with
   // a missing block only).
@@ -637,9 +701,9 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
 
   if (n_kt > 0) {
 #pragma unroll
-    for (int st = 0; st < kStages - 1; ++st) issue();
-    wait_vmcnt<2 * (kStages - 2)>();  // this wave's copies of tile 0 have landed
-    raw_barrier();                     // everyone's
+    for (int st = 0; st < kAhead; ++st) issue();
+    wait_vmcnt<2 * COPS * (kAhead - 1)>();  // this wave's copies of tile 0 have landed
+    raw_barrier();                           // everyone's
     if (wave_nkt > 0) {
       u32x4 kf[PT::NKK][2];
       kread(0, kf);
@@ -647,28 +711,33 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
       qk(kf, sc);
     }
   }
-  // The copies of a tile are issued kStages - 1 tiles ahead, so a missing
-  // block is known (any_bad) before its tile is computed; from then on the
-  // masked loop runs.
+  // The copies of a tile are issued kAhead tiles ahead, so a missing block
+  // is known (any_bad) before its tile is computed; from then on the masked
+  // loop runs.
   int jt = 0, slot = 0;
   for (; jt < n_plain && !any_bad; ++jt) {
     sync();
-    step(std::false_type{}, jt, slot, true);
-    slot = slot + 1 == kStages ? 0 : slot + 1;
+    u32x4 pb[QS], vf0[4];
+    front(std::false_type{}, jt, slot, true, pb, vf0);
+    back(slot, pb, vf0);
+    slot = slot + 1 == kSlots ? 0 : slot + 1;
   }
   for (; jt < n_kt; ++jt) {
     sync();
-    if (jt < wave_nkt)
-      step(std::true_type{}, jt, slot, !any_bad || block_ok(jt));
-    else
+    if (jt < wave_nkt) {
+      u32x4 pb[QS], vf0[4];
+      front(std::true_type{}, jt, slot, !any_bad || block_ok(jt), pb, vf0);
+      back(slot, pb, vf0);
+    } else {
       issue();
-    slot = slot + 1 == kStages ? 0 : slot + 1;
+    }
+    slot = slot + 1 == kSlots ? 0 : slot + 1;
   }
   wait_vmcnt<0>();  // drain the tail copies before the LDS is reused
 
   if (!wave_live) return;
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
+  for (int qs = 0; qs < QS; ++qs) {
     const float l = lsum[qs][0];  // every element holds the row sum of row m
     const int row = wrow0 + 16 * qs + m;
     if (row >= Lq) continue;
@@ -693,12 +762,12 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
 // queue[8] counts finished workgroups; the last one to finish puts all nine
 // words back to zero, so the workspace is ready for the next call without a
 // host-side clear.
-template <class T, int D>
-__global__ __launch_bounds__(64 * kNW) __attribute__((amdgpu_waves_per_eu(2)))
+template <class T, int D, int NW, int QS>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)))
 void varlen_prefill_dma_kernel(const PrefillArgs a) {
   using DT = DTile<T, D>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  int *lds_item = reinterpret_cast<int *>(smem + kStages * DT::SLOT_B);
+  int *lds_item = reinterpret_cast<int *>(smem + kSlots * DT::SLOT_B);
 
   const int n_x = a.n_qtiles, n_y = a.Hkv * a.quads;
   const int U = n_y * a.num_seqs;
@@ -715,11 +784,11 @@ void varlen_prefill_dma_kernel(const PrefillArgs a) {
     if (threadIdx.x == 0) next = atomicAdd(ctr, 1u);  // in flight while this item runs
     const int qt = n_x - 1 - item / cx;
     const int u = a.pin ? x + 8 * (item % cx) : item % cx;
-    prefill_item<T, D>(a, qt, u % n_y, u / n_y, smem);
+    prefill_item<T, D, NW, QS>(a, qt, u % n_y, u / n_y, smem);
     // Alternate slots: a wave still reading slot it-1 cannot overlap the
     // write of slot it+1, which comes after the next barrier.
     if (threadIdx.x == 0) lds_item[it & 1] = static_cast<int>(next);
-    __syncthreads();  // also: LDS ring and block table free for the next item
+    __syncthreads();  // also: LDS ring free for the next item
     item = __builtin_amdgcn_readfirstlane(lds_item[it & 1]);
   }
   if (threadIdx.x == 0) {
@@ -729,6 +798,17 @@ void varlen_prefill_dma_kernel(const PrefillArgs a) {
       for (int c = 0; c < 9; ++c) atomicExch(a.queue + c, 0u);
     }
   }
+}
+
+// Waves per workgroup of the 16-bit kernel: 8 (two 32-row waves per SIMD,
+// the faster on MI355X at cfg3) or 4 (one 64-row wave per SIMD);
+// NQ_PREFILL_WAVES=4 selects the latter.
+int prefill_shape() {
+  static int shape = [] {
+    const char *e = getenv("NQ_PREFILL_WAVES");
+    return (e && atoi(e) == 4) ? 4 : 8;
+  }();
+  return shape;
 }
 
 template <class T, bool FP8, int D>
@@ -741,11 +821,14 @@ int launch_prefill(PrefillArgs a, hipStream_t s) {
     if (total > 0x7fffffff) return fail(NQ_EINVAL, "varlen_prefill: too many work items");
     if (!a.queue) return fail(NQ_EINVAL, "varlen_prefill: null workspace");
     a.pin = U >= 8;
-    // One resident workgroup per CU (two waves per SIMD), never more than
-    // there are items; a multiple of 8 so every XCD gets the same count.
+    // One resident workgroup per CU, never more than there are items; a
+    // multiple of 8 so every XCD gets the same count.
     int64_t grid = (device_cus() + 7) / 8 * 8;
     if (grid > total) grid = total;  // work_grid() is a multiple of 8 when pinned
-    varlen_prefill_dma_kernel<T, D><<<static_cast<int>(grid), 64 * kNW, DT::LDS_BYTES, s>>>(a);
+    if (prefill_shape() == 4)
+      varlen_prefill_dma_kernel<T, D, 4, 4><<<static_cast<int>(grid), 64 * 4, DT::LDS_BYTES, s>>>(a);
+    else
+      varlen_prefill_dma_kernel<T, D, 8, 2><<<static_cast<int>(grid), 64 * 8, DT::LDS_BYTES, s>>>(a);
   } else {
     using PT = PTile<T, FP8, D>;
     const int64_t total = work_grid(a.n_qtiles, static_cast<int64_t>(a.Hkv) * a.quads * a.num_seqs);
@@ -835,8 +918,8 @@ extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_
   a.num_seqs = num_seqs;
   const int rows_per_wg = kRows * (4 / a.G4);
   a.n_qtiles = (max_seqlen_q + rows_per_wg - 1) / rows_per_wg;
-  const int rows_per_wg_dma = kRows * (kNW / a.G4);
-  a.n_qtiles_dma = (max_seqlen_q + rows_per_wg_dma - 1) / rows_per_wg_dma;
+  const int rows_per_item = kItemRows / a.G4;
+  a.n_qtiles_dma = (max_seqlen_q + rows_per_item - 1) / rows_per_item;
   a.causal = causal;
   a.scale_log2 = softmax_scale * kLog2e;
   a.k_scale = k_scale;

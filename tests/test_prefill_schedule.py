@@ -15,7 +15,7 @@ import torch
 
 from oracle.inputs import make_prefill_case
 
-KKEYS, KSTAGES, KROWS, KNW = 32, 5, 32, 8
+KKEYS, KAHEAD, KROWS, KNW = 32, 4, 32, 8  # kKeys, kAhead, kRows, kNW
 
 
 def copy_schedule(lq, lk, bt, num_blocks, bs, hkv, hq, causal=True):
@@ -46,7 +46,7 @@ def copy_schedule(lq, lk, bt, num_blocks, bs, hkv, hq, causal=True):
             jt, left, bidx, ok = 0, 0, 0, True
             off = 0 if paged else k0
             blk_next = entry(0) if paged else 0
-            for _ in range(n_kt + KSTAGES - 1):
+            for _ in range(n_kt + KAHEAD):  # kAhead in the prologue, then one per tile
                 rows = 0
                 if jt < n_kt:
                     if paged and left == 0:
