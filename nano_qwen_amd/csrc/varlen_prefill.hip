@@ -10,11 +10,11 @@
 // K/V are the whole paged cache (layers/attention.py:65-66).
 //
 // Two kernels share the tile layout and the softmax:
-//  * varlen_prefill_dma_kernel (16-bit K/V): persistent workgroups of 8 waves
-//    (G4 <= 4 query heads of one kv head x row blocks of 32), one per CU,
+//  * varlen_prefill_dma_kernel (16-bit K/V): persistent workgroups (G4 <= 4
+//    query heads of one kv head x row blocks), resident on every CU and
 //    pulling work items from per-XCD queues; K/V tiles of 32 keys are copied
-//    HBM -> LDS by the LDS DMA into a 5-slot ring (no VGPRs), the QK
-//    products of tile j+1 overlap the softmax of tile j.
+//    HBM -> LDS by the LDS DMA into a ring (no VGPRs), the QK products of
+//    tile j+1 overlap the softmax of tile j.
 //  * varlen_prefill_kernel (fp8 K/V): 4-wave workgroups, one per query tile,
 //    K/V staged through registers (global -> convert -> LDS) into a double
 //    buffer.
@@ -61,7 +61,7 @@ struct PrefillArgs {
   int64_t num_blocks;
   uint8_t *out;
   int64_t o_rs, o_hs;  // bytes
-  int Hq, Hkv, G, G4, quads, block_size, num_seqs, n_qtiles, n_qtiles_dma;
+  int Hq, Hkv, G, G4, quads, block_size, num_seqs, n_qtiles, max_seqlen_q;
   int causal;
   float scale_log2;
   const float *k_scale;
@@ -373,25 +373,36 @@ void varlen_prefill_kernel(const PrefillArgs a) {
 // chunk swizzle of the LDS tile is produced by the source offset each lane
 // fetches.
 //
-// Shape <NW, QS>: NW waves per workgroup, each wave QS x 16 query rows of one
-// head.  <8, 2> runs two waves per SIMD (up to 256 registers each); <4, 4>
-// one wave per SIMD with 64 rows, so every K/V operand read from LDS and
-// every per-tile step (barrier, copies, checks) serves twice the rows.  Both
-// cover 256 / G4 query rows x G4 heads per work item.
-constexpr int kSlots = 5;  // LDS ring slots
-constexpr int kAhead = 4;  // tiles copied ahead of the tile being computed
-constexpr int kItemRows = 256;  // query rows x heads of one work item (G4 heads x 256/G4 rows)
-
+// Shapes (PShape): NW waves per workgroup, each wave QS x 16 query rows of
+// one head, WPE waves per SIMD.  A = one 8-wave workgroup per CU; B = one
+// 4-wave workgroup per CU with 64-row waves (every K/V operand read and
+// per-tile step serves twice the rows); C = two independent 4-wave
+// workgroups per CU, whose barriers, prologues and epilogues do not line up,
+// so one's stalls overlap the other's work.
 template <class T, int D>
 struct DTile {
   static_assert(D == 128, "tile layout assumes head_dim 128");
   static constexpr int ROWB = D * 2;
   static constexpr int TILE_B = kKeys * ROWB;   // 8 KiB per K (or V) tile
   static constexpr int SLOT_B = 2 * TILE_B;     // K + V
-  static constexpr int LDS_BYTES = kSlots * SLOT_B + 16;  // + queue item slots
 };
 
-// One work item of the persistent kernel: query tile qt (kItemRows/G4 rows
+// Launch shape of the 16-bit kernel: NW waves per workgroup, each QS x 16
+// query rows of one head; WPE waves per SIMD (so WPE * 4 / NW resident
+// workgroups per CU); a ring of SLOTS K/V tiles, copies SLOTS - 1 ahead.
+template <int NW_, int QS_, int WPE_, int SLOTS_>
+struct PShape {
+  static constexpr int NW = NW_, QS = QS_, WPE = WPE_, SLOTS = SLOTS_, AHEAD = SLOTS_ - 1;
+  static constexpr int WG_PER_CU = WPE * 4 / NW;
+  static constexpr int ITEM_ROWS = 16 * QS * NW;  // query rows x heads of one work item
+  static constexpr int LDS_BYTES = SLOTS * 2 * kKeys * 256 + 16;  // ring + queue item slots
+  static_assert(WG_PER_CU * LDS_BYTES <= 160 * 1024, "LDS of the resident workgroups");
+};
+using ShapeA = PShape<8, 2, 2, 5>;  // one workgroup per CU, two 32-row waves per SIMD
+using ShapeB = PShape<4, 4, 1, 5>;  // one workgroup per CU, one 64-row wave per SIMD
+using ShapeC = PShape<4, 2, 2, 4>;  // two independent workgroups per CU, 32-row waves
+
+// One work item of the persistent kernel: query tile qt (S::ITEM_ROWS/G4 rows
 // of G4 heads) of kv-head slot y of sequence s.
 //
 // Per key tile, all control is scalar (wave-uniform): the copy of tile
@@ -401,10 +412,11 @@ struct DTile {
 // Tiles that every row of the wave sees completely run a mask-free loop; the
 // rest (the causal diagonal, the end of the keys, any tile of a sequence
 // with a missing block) run the masked loop.
-template <class T, int D, int NW, int QS>
+template <class T, int D, class S>
 __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y, int s, uint8_t *smem) {
   using DT = DTile<T, D>;
   using PT = PTile<T, false, D>;
+  constexpr int NW = S::NW, QS = S::QS, kSlots = S::SLOTS, kAhead = S::AHEAD;
   constexpr int RW = 16 * QS;        // query rows per wave
   constexpr int CR = kKeys / NW;     // tile rows each wave copies
   constexpr int COPS = CR / 4;       // 1 KiB loads per K (or V) per wave and tile
@@ -762,12 +774,12 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
 // queue[8] counts finished workgroups; the last one to finish puts all nine
 // words back to zero, so the workspace is ready for the next call without a
 // host-side clear.
-template <class T, int D, int NW, int QS>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)))
+template <class T, int D, class S>
+__global__ __launch_bounds__(64 * S::NW) __attribute__((amdgpu_waves_per_eu(S::WPE)))
 void varlen_prefill_dma_kernel(const PrefillArgs a) {
   using DT = DTile<T, D>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  int *lds_item = reinterpret_cast<int *>(smem + kSlots * DT::SLOT_B);
+  int *lds_item = reinterpret_cast<int *>(smem + S::SLOTS * DT::SLOT_B);
 
   const int n_x = a.n_qtiles, n_y = a.Hkv * a.quads;
   const int U = n_y * a.num_seqs;
@@ -784,7 +796,7 @@ void varlen_prefill_dma_kernel(const PrefillArgs a) {
     if (threadIdx.x == 0) next = atomicAdd(ctr, 1u);  // in flight while this item runs
     const int qt = n_x - 1 - item / cx;
     const int u = a.pin ? x + 8 * (item % cx) : item % cx;
-    prefill_item<T, D, NW, QS>(a, qt, u % n_y, u / n_y, smem);
+    prefill_item<T, D, S>(a, qt, u % n_y, u / n_y, smem);
     // Alternate slots: a wave still reading slot it-1 cannot overlap the
     // write of slot it+1, which comes after the next barrier.
     if (threadIdx.x == 0) lds_item[it & 1] = static_cast<int>(next);
@@ -800,35 +812,42 @@ void varlen_prefill_dma_kernel(const PrefillArgs a) {
   }
 }
 
-// Waves per workgroup of the 16-bit kernel: 8 (two 32-row waves per SIMD,
-// the faster on MI355X at cfg3) or 4 (one 64-row wave per SIMD);
-// NQ_PREFILL_WAVES=4 selects the latter.
-int prefill_shape() {
-  static int shape = [] {
-    const char *e = getenv("NQ_PREFILL_WAVES");
-    return (e && atoi(e) == 4) ? 4 : 8;
+// Launch shape of the 16-bit kernel: C (two independent 4-wave workgroups
+// per CU) measured fastest at cfg3 on MI355X (480 us against 495 for A and
+// 515 for B); NQ_PREFILL_SHAPE = a | b | c selects one for measurements.
+char prefill_shape() {
+  static char shape = [] {
+    const char *e = getenv("NQ_PREFILL_SHAPE");
+    return (e && (e[0] == 'a' || e[0] == 'b' || e[0] == 'c')) ? e[0] : 'c';
   }();
   return shape;
+}
+
+template <class T, int D, class S>
+int launch_prefill_dma(PrefillArgs a, hipStream_t st) {
+  const int rows_per_item = S::ITEM_ROWS / a.G4;
+  a.n_qtiles = (a.max_seqlen_q + rows_per_item - 1) / rows_per_item;
+  const int64_t U = static_cast<int64_t>(a.Hkv) * a.quads * a.num_seqs;
+  const int64_t total = work_grid(a.n_qtiles, U);
+  if (total > 0x7fffffff) return fail(NQ_EINVAL, "varlen_prefill: too many work items");
+  if (!a.queue) return fail(NQ_EINVAL, "varlen_prefill: null workspace");
+  a.pin = U >= 8;
+  // S::WG_PER_CU resident workgroups per CU, never more than there are
+  // items; a multiple of 8 so every XCD gets the same count.
+  int64_t grid = (static_cast<int64_t>(device_cus()) * S::WG_PER_CU + 7) / 8 * 8;
+  if (grid > total) grid = total;  // work_grid() is a multiple of 8 when pinned
+  varlen_prefill_dma_kernel<T, D, S><<<static_cast<int>(grid), 64 * S::NW, S::LDS_BYTES, st>>>(a);
+  return check_launch("varlen_prefill");
 }
 
 template <class T, bool FP8, int D>
 int launch_prefill(PrefillArgs a, hipStream_t s) {
   if constexpr (!FP8) {
-    using DT = DTile<T, D>;
-    a.n_qtiles = a.n_qtiles_dma;
-    const int64_t U = static_cast<int64_t>(a.Hkv) * a.quads * a.num_seqs;
-    const int64_t total = work_grid(a.n_qtiles, U);
-    if (total > 0x7fffffff) return fail(NQ_EINVAL, "varlen_prefill: too many work items");
-    if (!a.queue) return fail(NQ_EINVAL, "varlen_prefill: null workspace");
-    a.pin = U >= 8;
-    // One resident workgroup per CU, never more than there are items; a
-    // multiple of 8 so every XCD gets the same count.
-    int64_t grid = (device_cus() + 7) / 8 * 8;
-    if (grid > total) grid = total;  // work_grid() is a multiple of 8 when pinned
-    if (prefill_shape() == 4)
-      varlen_prefill_dma_kernel<T, D, 4, 4><<<static_cast<int>(grid), 64 * 4, DT::LDS_BYTES, s>>>(a);
-    else
-      varlen_prefill_dma_kernel<T, D, 8, 2><<<static_cast<int>(grid), 64 * 8, DT::LDS_BYTES, s>>>(a);
+    switch (prefill_shape()) {
+      case 'b': return launch_prefill_dma<T, D, ShapeB>(a, s);
+      case 'c': return launch_prefill_dma<T, D, ShapeC>(a, s);
+      default: return launch_prefill_dma<T, D, ShapeA>(a, s);
+    }
   } else {
     using PT = PTile<T, FP8, D>;
     const int64_t total = work_grid(a.n_qtiles, static_cast<int64_t>(a.Hkv) * a.quads * a.num_seqs);
@@ -916,10 +935,9 @@ extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_
   a.quads = G < 4 ? 1 : G / 4;
   a.block_size = block_size;
   a.num_seqs = num_seqs;
+  a.max_seqlen_q = max_seqlen_q;
   const int rows_per_wg = kRows * (4 / a.G4);
   a.n_qtiles = (max_seqlen_q + rows_per_wg - 1) / rows_per_wg;
-  const int rows_per_item = kItemRows / a.G4;
-  a.n_qtiles_dma = (max_seqlen_q + rows_per_item - 1) / rows_per_item;
   a.causal = causal;
   a.scale_log2 = softmax_scale * kLog2e;
   a.k_scale = k_scale;
