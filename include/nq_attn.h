@@ -130,7 +130,9 @@ int nq_paged_decode(const void *q, int64_t q_batch_stride, int64_t q_head_stride
  * block_tables != NULL: k/v are the paged caches; key j of s is cache row
  *   block_tables[s*bt_stride + j/block_size]*block_size + j%block_size.
  * kv_dtype == q_dtype (F16/BF16), or NQ_FP8_E4M3 with k_scale/v_scale.
- * workspace: >= nq_prefill_workspace_bytes() bytes, 4-byte aligned, all zero
+ * q, k, v and out (base pointers, row and head strides) must be 16-byte
+ * aligned (NQ_EINVAL otherwise); a K/V row stride is at most 1 MiB.
+ * workspace:>= nq_prefill_workspace_bytes() bytes, 4-byte aligned, all zero
  * before its first use; every completed call leaves it zero again, so it is
  * allocated and cleared once and then reused (also under graph replay).
  * Calls that share a workspace must not run concurrently.

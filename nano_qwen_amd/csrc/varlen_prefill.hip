@@ -748,17 +748,34 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
   wait_vmcnt<0>();  // drain the tail copies before the LDS is reused
 
   if (!wave_live) return;
+  // Output: lane (g, m) holds dims 16j + 4g .. +3 of row m for every j.  The
+  // lanes of lane groups g and g^1 (same row) trade one 8-byte piece per
+  // pair of j through permlane16_swap, so each writes 16 contiguous bytes:
+  // even g dims 16j0 + 4g .. +7, odd g dims 16j1 + 4(g-1) .. +7 (j0 = 2p,
+  // j1 = 2p + 1): eight 16-byte stores per 16 rows instead of sixteen 8-byte.
+  const bool odd = (g & 1) != 0;
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) {
     const float l = lsum[qs][0];  // every element holds the row sum of row m
     const int row = wrow0 + 16 * qs + m;
-    if (row >= Lq) continue;
+    if (row >= Lq) continue;      // the same for both lanes of a swap pair
     const float inv = l > 0.f ? 1.0f / l : 0.f;
     uint8_t *op = a.out + static_cast<int64_t>(q0 + row) * a.o_rs + static_cast<int64_t>(head) * a.o_hs;
 #pragma unroll
-    for (int j = 0; j < PT::NJ; ++j) {
-      const f32x4 v = o[qs][j] * inv;
-      *reinterpret_cast<u32x2 *>(op + (16 * j + 4 * g) * 2) = u32x2{T::pack2(v[0], v[1]), T::pack2(v[2], v[3])};
+    for (int p = 0; p < PT::NJ / 2; ++p) {
+      const f32x4 v0 = o[qs][2 * p] * inv, v1 = o[qs][2 * p + 1] * inv;
+      const uint32_t c00 = T::pack2(v0[0], v0[1]), c01 = T::pack2(v0[2], v0[3]);
+      const uint32_t c10 = T::pack2(v1[0], v1[1]), c11 = T::pack2(v1[2], v1[3]);
+      const uint32_t x0 = odd ? c00 : c10, x1 = odd ? c01 : c11;  // the piece the partner needs
+      // After the swap, even lanes find the partner's value in the second
+      // result, odd lanes in the first.
+      const auto r0 = __builtin_amdgcn_permlane16_swap(x0, x0, false, false);
+      const auto r1 = __builtin_amdgcn_permlane16_swap(x1, x1, false, false);
+      const uint32_t y0 = odd ? static_cast<uint32_t>(r0[0]) : static_cast<uint32_t>(r0[1]);
+      const uint32_t y1 = odd ? static_cast<uint32_t>(r1[0]) : static_cast<uint32_t>(r1[1]);
+      const int dim0 = odd ? 16 * (2 * p + 1) + 4 * (g - 1) : 16 * (2 * p) + 4 * g;
+      const u32x4 w = odd ? u32x4{y0, y1, c10, c11} : u32x4{c00, c01, y0, y1};
+      store16(op + dim0 * 2, w);
     }
   }
 }
@@ -904,8 +921,8 @@ extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_
   }
   const int qsz = 2, ksz = fp8 ? 1 : 2;
   if ((q_row_stride * qsz) % 16 || (q_head_stride * qsz) % 16 || !aligned(q, 16) || (kv_row_stride * ksz) % 16 ||
-      !aligned(k, 16) || !aligned(v, 16) || (out_row_stride * qsz) % 8 || (out_head_stride * qsz) % 8 ||
-      !aligned(out, 8))
+      !aligned(k, 16) || !aligned(v, 16) || (out_row_stride * qsz) % 16 || (out_head_stride * qsz) % 16 ||
+      !aligned(out, 16))
     return fail(NQ_EINVAL, "varlen_prefill: q/k/v/out alignment");
   if (kv_row_stride * ksz > (1 << 20)) return fail(NQ_EINVAL, "varlen_prefill: K/V row stride too large");
   if ((!workspace || workspace_bytes < nq_prefill_workspace_bytes() || !aligned(workspace, 4)))
