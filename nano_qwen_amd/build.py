@@ -45,9 +45,12 @@ def _flags():
 
 # Per-source extra flags.  The prefill kernels keep their MFMA accumulators
 # in VGPR form: with the default heuristics the 64-row kernel spends about
-# 175 AGPR<->VGPR moves per key tile.
+# 175 AGPR<->VGPR moves per key tile.  Their work-queue atomics stay plain
+# atomics: the atomic optimizer rewrites one into a wave-wide add whose
+# result is needed at once, so the wave would wait for every K/V copy in
+# flight right after it instead of where the fetched index is used.
 EXTRA_FLAGS = {
-    "varlen_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "varlen_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
 }
 
 

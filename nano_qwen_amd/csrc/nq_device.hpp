@@ -87,6 +87,23 @@ template <class T>
 __device__ inline T ld_const(const T *p) {
   return *(const __attribute__((address_space(4))) T *)(reinterpret_cast<uintptr_t>(p));
 }
+// A wave-uniform value copied into scalar registers of its own.  Kernel
+// arguments arrive through wide scalar loads; the register allocator keeps
+// such a load as one unit, so a loop that needs two of its fields would
+// otherwise spill and reload all sixteen registers together.
+template <class T>
+__device__ inline T own_sgpr(T x) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit values");
+  uint32_t w[sizeof(T) / 4];
+  __builtin_memcpy(w, &x, sizeof(T));
+#pragma unroll
+  for (unsigned i = 0; i < sizeof(T) / 4; ++i) {
+    w[i] = __builtin_amdgcn_readfirstlane(w[i]);
+    asm volatile("" : "+s"(w[i]));
+  }
+  __builtin_memcpy(&x, w, sizeof(T));
+  return x;
+}
 __device__ inline u32x4 load16(const void *p) { return *reinterpret_cast<const u32x4 *>(p); }
 __device__ inline void store16(void *p, const u32x4 &v) { *reinterpret_cast<u32x4 *>(p) = v; }
 

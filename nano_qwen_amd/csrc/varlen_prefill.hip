@@ -45,6 +45,8 @@ constexpr int kRows = 32;    // query rows per wave
 constexpr int kKeys = 32;    // keys per LDS tile
 constexpr int kMaxBt = 4096;  // block-table entries staged in LDS (1M tokens at 256)
 constexpr float kRescale = 8.0f;  // log2 growth of a row max that forces a rescale
+constexpr int kMaxLevels = 1024;  // work-queue cost levels (key tiles per item, coarsened past it)
+constexpr int kMaxSeqs = 1024;    // sequences whose bounds the persistent kernel keeps in LDS
 constexpr int kQueueWords = 16;   // prefill workspace: 8 per-XCD counters + 1 finish counter (+ pad)
 
 struct PrefillArgs {
@@ -58,16 +60,19 @@ struct PrefillArgs {
   const int32_t *block_tables;  // null: packed K/V
   int64_t bt_stride;
   int max_blocks;  // table width: entries past it are never read
-  int64_t num_blocks;
+  int num_blocks;  // clamped to INT32_MAX: block ids are int32
   uint8_t *out;
   int64_t o_rs, o_hs;  // bytes
-  int Hq, Hkv, G, G4, quads, block_size, num_seqs, n_qtiles, max_seqlen_q;
+  int Hq, Hkv, G, G4, quads, block_size, num_seqs, n_qtiles, max_seqlen_q, max_seqlen_k;
   int causal;
   float scale_log2;
   const float *k_scale;
   const float *v_scale;
   uint32_t *queue;  // persistent kernel: kQueueWords work counters (zero between calls)
   int pin;          // work groups pinned to XCDs (>= 8 groups)
+  int by_cost;      // persistent kernel: queue in cost order over live items (num_seqs <= kMaxSeqs)
+  int level_shift;  // cost level of an item: its key tiles >> level_shift (< n_levels)
+  int n_levels;
 };
 
 __device__ inline int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1) | (row & 8); }
@@ -390,122 +395,406 @@ struct DTile {
 // Launch shape of the 16-bit kernel: NW waves per workgroup, each QS x 16
 // query rows of one head; WPE waves per SIMD (so WPE * 4 / NW resident
 // workgroups per CU); a ring of SLOTS K/V tiles, copies SLOTS - 1 ahead.
+// Two waves per SIMD: a wave owns at most 256 VGPRs, and the kernel keeps the
+// last one (v255) out of the compiler's hands for the work-queue fetch.
 template <int NW_, int QS_, int WPE_, int SLOTS_>
 struct PShape {
   static constexpr int NW = NW_, QS = QS_, WPE = WPE_, SLOTS = SLOTS_, AHEAD = SLOTS_ - 1;
   static constexpr int WG_PER_CU = WPE * 4 / NW;
   static constexpr int ITEM_ROWS = 16 * QS * NW;  // query rows x heads of one work item
-  static constexpr int LDS_BYTES = SLOTS * 2 * kKeys * 256 + 16;  // ring + queue item slots
+  static constexpr int RING_BYTES = SLOTS * 2 * kKeys * 256;
+  // ring, queue item slots (4 words), queue size (4 words), cost-level
+  // starts, sequence bounds (cu_q, cu_k)
+  static constexpr int LDS_BYTES = RING_BYTES + 32 + 4 * kMaxLevels + 8 * (kMaxSeqs + 1);
+  static_assert(WPE == 2, "two waves per SIMD");
   static_assert(WG_PER_CU * LDS_BYTES <= 160 * 1024, "LDS of the resident workgroups");
 };
 using ShapeA = PShape<8, 2, 2, 5>;  // one workgroup per CU, two 32-row waves per SIMD
-using ShapeB = PShape<4, 4, 1, 5>;  // one workgroup per CU, one 64-row wave per SIMD
 using ShapeC = PShape<4, 2, 2, 4>;  // two independent workgroups per CU, 32-row waves
 
-// One work item of the persistent kernel: query tile qt (S::ITEM_ROWS/G4 rows
-// of G4 heads) of kv-head slot y of sequence s.
+// Work-queue fetch the compiler does not track.  A compiled atomic's result
+// is waited for by the compiler as soon as it can no longer count the
+// operations issued after it -- here, across the tile loop -- with a wait for
+// every K/V copy in flight.  This one returns into v255, which the kernel's
+// register limit (255) keeps from the compiler, and is read back by
+// queue_fetch_result() once `younger` vector-memory operations of this wave
+// have followed it: vmcnt completes in issue order, so waiting until at most
+// `younger` (rounded down to a step) are outstanding covers the atomic.
+// Issue and read from the same single lane; one fetch in flight at a time.
+__device__ inline void queue_fetch_issue(uint32_t *ctr) {
+  asm volatile("global_atomic_add v255, %0, %1, off sc0" : : "v"(ctr), "v"(1u) : "memory", "v255");
+}
+__device__ inline uint32_t queue_fetch_result(int younger) {
+  uint32_t r;
+  if (younger >= 48)
+    asm volatile("s_waitcnt vmcnt(48)\n\tv_mov_b32 %0, v255" : "=v"(r) : : "memory", "v255");
+  else if (younger >= 32)
+    asm volatile("s_waitcnt vmcnt(32)\n\tv_mov_b32 %0, v255" : "=v"(r) : : "memory", "v255");
+  else if (younger >= 16)
+    asm volatile("s_waitcnt vmcnt(16)\n\tv_mov_b32 %0, v255" : "=v"(r) : : "memory", "v255");
+  else if (younger >= 8)
+    asm volatile("s_waitcnt vmcnt(8)\n\tv_mov_b32 %0, v255" : "=v"(r) : : "memory", "v255");
+  else
+    asm volatile("s_waitcnt vmcnt(0)\n\tv_mov_b32 %0, v255" : "=v"(r) : : "memory", "v255");
+  return r;
+}
+
+// A work item of the persistent kernel: query tile qt (S::ITEM_ROWS/G4 rows
+// of G4 heads) of kv-head slot y of sequence s, described by wave-uniform
+// scalars.  `live` is false past the end of the queue and for query tiles
+// past a sequence's rows.
+struct Item {
+  bool live;
+  int s, kvh, head0, q0, Lq, k0, Lk, P, row_begin, key_end, n_kt;
+};
+
+// Item fields of query tile qt of kv-head slot y of sequence s.
+__device__ __forceinline__ Item fill_item(const PrefillArgs &a, int s, int y, int qt, int rows, int q0, int Lq, int k0,
+                                          int Lk) {
+  Item it{};
+  it.live = false;
+  it.s = s;
+  it.kvh = y / a.quads;
+  it.head0 = it.kvh * a.G + (y % a.quads) * 4;
+  it.q0 = q0;
+  it.Lq = Lq;
+  it.row_begin = qt * rows;
+  if (it.row_begin >= Lq) return it;
+  it.k0 = k0;
+  it.Lk = Lk;
+  it.P = Lk - Lq;
+  const int row_last = min(it.row_begin + rows, Lq) - 1;
+  it.key_end = a.causal ? max(0, min(Lk, row_last + it.P + 1)) : Lk;
+  it.n_kt = (it.key_end + kKeys - 1) / kKeys;
+  it.live = true;
+  return it;
+}
+
+// Queue order by query tile (used when the sequence bounds do not fit in
+// LDS): XCD x's groups u = x, x + 8, ... (every group without pinning), from
+// the last query tile down; items past a sequence's rows are not live.
+template <class S>
+__device__ __forceinline__ Item describe_by_tile(const PrefillArgs &a, int idx, int n_items, int n_x, int n_y, int cx,
+                                                 int x) {
+  Item it{};
+  it.live = false;
+  if (idx >= n_items) return it;
+  const int qt = n_x - 1 - idx / cx;
+  const int u = a.pin ? x + 8 * (idx % cx) : idx % cx;
+  const int s = u / n_y;
+  const int rows = 16 * S::QS * (S::NW / a.G4);
+  const int q0 = ld_const(a.cu_q + s), k0 = ld_const(a.cu_k + s);
+  return fill_item(a, s, u % n_y, qt, rows, q0, ld_const(a.cu_q + s + 1) - q0, k0, ld_const(a.cu_k + s + 1) - k0);
+}
+
+// Queue order by cost: the live items of XCD x's groups (see above), by
+// cost level (key tiles >> level_shift) from the highest down, then by
+// sequence, kv-head slot and query tile -- longest first, so the last items
+// a workgroup takes are short ones, and no index is spent on an item
+// without rows.  Each workgroup derives the order from the sequence bounds
+// (kept in LDS) and a table of level starts it builds at launch.
+struct CostQueue {
+  const int *lev;  // LDS: first queue index of each level
+  const int *cuq;  // LDS: cu_seqlens_q, cu_seqlens_k
+  const int *cuk;
+  int x, n_y, rows, ystep;
+};
+// Kv-head slots of sequence s in the queue: y0, y0 + ystep, ... < n_y.
+__device__ __forceinline__ int first_slot(const CostQueue &cq, int s) {
+  return cq.ystep == 8 ? ((cq.x - s * cq.n_y) & 7) : 0;
+}
+__device__ __forceinline__ int n_slots(const CostQueue &cq, int y0) {
+  return y0 < cq.n_y ? (cq.n_y - 1 - y0) / cq.ystep + 1 : 0;
+}
+// Smallest query tile (of nq) whose item has at least v key tiles.
+__device__ __forceinline__ int first_tile_with(const PrefillArgs &a, const CostQueue &cq, int v, int nq, int Lk,
+                                               int P) {
+  if (v <= 0) return 0;
+  if (!a.causal) return (Lk + kKeys - 1) / kKeys >= v ? 0 : nq;
+  const int64_t t = static_cast<int64_t>(kKeys) * (v - 1);  // the item needs key_end > t
+  if (Lk <= t) return nq;
+  const int64_t need = t - P;  // (qt + 1) * rows > need
+  return need < 0 ? 0 : static_cast<int>(min<int64_t>(need / cq.rows, nq));
+}
+// Cost level of query tile qt of a sequence (as fill_item computes key_end).
+__device__ __forceinline__ int cost_level(const PrefillArgs &a, const CostQueue &cq, int qt, int Lq, int Lk) {
+  const int row_last = min((qt + 1) * cq.rows, Lq) - 1;
+  const int key_end = a.causal ? max(0, min(Lk, row_last + Lk - Lq + 1)) : Lk;
+  return min(((key_end + kKeys - 1) / kKeys) >> a.level_shift, a.n_levels - 1);
+}
+// Wave-wide inclusive prefix sum.
+__device__ __forceinline__ int wave_scan(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(v, d, 64);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+// Item at queue index idx.  Called by whole waves (all 64 lanes).
+__device__ __forceinline__ Item describe_by_cost(const PrefillArgs &a, const CostQueue &cq, int idx, int n_items) {
+  Item it{};
+  it.live = false;
+  if (idx >= n_items) return it;
+  const int lane = threadIdx.x & 63;
+  const int nl = a.n_levels;
+  // Level: the lowest L whose start is <= idx (starts fall as L rises).
+  const int step = (nl + 63) / 64;
+  const int l1 = min(lane * step, nl - 1);
+  const int b = __builtin_amdgcn_readfirstlane(
+      __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane * step < nl && cq.lev[l1] > idx)));
+  int L = 0;
+  if (b > 0) {
+    const int base = (b - 1) * step + 1;
+    const int l2 = min(base + lane, nl - 1);
+    L = base + __builtin_amdgcn_readfirstlane(
+                   __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < step && base + lane < nl && cq.lev[l2] > idx)));
+  }
+  int r = idx - cq.lev[L];
+  const int lo_v = L << a.level_shift;
+  const bool top = L == nl - 1;  // the last level takes every item above it
+  const int hi_v = (L + 1) << a.level_shift;
+  // The sequence: items of level L in sequence order, 64 sequences per step.
+  for (int base = 0; base < a.num_seqs; base += 64) {
+    const int s = base + lane;
+    int cnt = 0, qlo = 0, nqt = 0;
+    if (s < a.num_seqs) {
+      const int Lq = cq.cuq[s + 1] - cq.cuq[s], Lk = cq.cuk[s + 1] - cq.cuk[s];
+      const int nq = Lq > 0 ? (Lq + cq.rows - 1) / cq.rows : 0;
+      qlo = first_tile_with(a, cq, lo_v, nq, Lk, Lk - Lq);
+      const int qhi = top ? nq : first_tile_with(a, cq, hi_v, nq, Lk, Lk - Lq);
+      nqt = max(0, qhi - qlo);
+      cnt = nqt * n_slots(cq, first_slot(cq, s));
+    }
+    const int incl = wave_scan(cnt, lane);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    if (r < total) {
+      const int ls = __builtin_amdgcn_readfirstlane(
+          static_cast<int>(__builtin_ctzll(__builtin_amdgcn_ballot_w64(incl > r))));
+      const int s_it = base + ls;
+      r -= __builtin_amdgcn_readlane(incl - cnt, ls);
+      const int n_t = __builtin_amdgcn_readlane(nqt, ls);
+      const int qt = __builtin_amdgcn_readlane(qlo, ls) + r % n_t;
+      const int y = first_slot(cq, s_it) + cq.ystep * (r / n_t);
+      const int q0 = cq.cuq[s_it], k0 = cq.cuk[s_it];
+      return fill_item(a, s_it, y, qt, cq.rows, q0, cq.cuq[s_it + 1] - q0, k0, cq.cuk[s_it + 1] - k0);
+    }
+    r -= total;
+  }
+  return it;  // not reached for idx < n_items
+}
+
+// Persistent prefill: S::WG_PER_CU workgroups per CU pull work items from
+// per-XCD queues.  The hardware dispatcher keeps only about half of the CUs
+// busy when one-per-CU workgroups of very different lengths are launched as
+// a plain grid; a queue keeps every CU fed until the work runs out.
 //
-// Per key tile, all control is scalar (wave-uniform): the copy of tile
-// jt + kAhead is buffer-to-LDS loads through descriptors whose range ends at
-// the tile's last valid key (rows past it read as zeros, so no clamping),
-// and the block table is walked one block at a time with scalar loads.
-// Tiles that every row of the wave sees completely run a mask-free loop; the
-// rest (the causal diagonal, the end of the keys, any tile of a sequence
-// with a missing block) run the masked loop.
+// Queue: items are grouped as in map_work -- XCD x (workgroups L with
+// L % 8 == x) owns the groups u = x, x + 8, ... and serves them from its own
+// counter queue[x], in query-tile order from the last tile down (longest
+// first).  Thread 0 fetches two items ahead; indices reach the other waves
+// through LDS, and each item is described (sequence bounds, keys, tiles) one
+// item ahead.  queue[8] counts finished workgroups; the last one puts all
+// nine words back to zero, so the workspace is ready for the next call.
+//
+// K/V copies form one stream across items: each stream entry is one 32-key
+// tile (of the item being copied, or an empty load when none is queued)
+// copied into ring slot (entry index mod SLOTS), kAhead entries ahead of the
+// tile being computed.  While an item computes its last tiles, the stream is
+// already copying the next item's first ones.  All copy control is scalar
+// (wave-uniform): descriptors whose range ends at the tile's last valid key
+// (rows past it read as zeros), the block table walked one block at a time
+// with scalar loads, the next item's copy parameters set when it is queued.
+//
+// Per tile, after one barrier: the K reads of tile j+1, the lazy-rescale
+// check of tile j, the next stream entry, the QK products of tile j+1
+// interleaved with the exp / pack work of tile j, then O += P V of tile j.
+// Tiles every row of a wave sees completely run a mask-free loop; the rest
+// (the causal diagonal, the end of the keys, a missing block) the masked one.
+// An item's output is stored at the start of the next one, right after that
+// item's Q loads are issued, so the stores cover the Q latency.
+//
+// vmcnt accounting: each stream entry is 2 * COPS loads per wave, and the
+// waits count only younger stream entries -- except that a new item's first
+// kAhead tiles may precede the Q loads and the previous item's output stores
+// (a fixed count per wave), which the waits then add.
 template <class T, int D, class S>
-__device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y, int s, uint8_t *smem) {
+__device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   using DT = DTile<T, D>;
   using PT = PTile<T, false, D>;
   constexpr int NW = S::NW, QS = S::QS, kSlots = S::SLOTS, kAhead = S::AHEAD;
   constexpr int RW = 16 * QS;        // query rows per wave
   constexpr int CR = kKeys / NW;     // tile rows each wave copies
-  constexpr int COPS = CR / 4;       // 1 KiB loads per K (or V) per wave and tile
+  constexpr int COPS = CR / 4;       // 1 KiB loads per K (or V) per wave and entry
+  constexpr int QOPS = QS * PT::NKK;        // Q loads per wave and item
+  constexpr int SOPS = QS * (PT::NJ / 2);   // output stores per wave and item
+  constexpr int EOPS = QOPS + SOPS;
   static_assert(CR % 4 == 0, "a copy moves whole groups of 4 rows");
+  static_assert(2 * COPS * kAhead + EOPS < 64, "vmcnt range");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  static_assert(S::RING_BYTES == kSlots * DT::SLOT_B, "ring size");
+  int *lds_item = reinterpret_cast<int *>(smem + S::RING_BYTES);  // fetched queue indices
+  int *lds_n = lds_item + 4;                                      // queue size (cost order)
+  int *lds_lev = lds_item + 8;                                    // level starts (cost order)
+  int *lds_cuq = lds_lev + kMaxLevels;
+  int *lds_cuk = lds_cuq + kMaxSeqs + 1;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int m = lane & 15, g = lane >> 4;
-
-  const int kvh = y / a.quads, quad = y % a.quads;
-  const int rb = NW / a.G4;  // row blocks of RW per workgroup
-  const int head = kvh * a.G + quad * 4 + (wave % a.G4);
-  const int q0 = ld_const(a.cu_q + s), Lq = ld_const(a.cu_q + s + 1) - q0;
-  const int row_begin = qt * RW * rb;
-  if (row_begin >= Lq) return;
-  const int k0 = ld_const(a.cu_k + s), Lk = ld_const(a.cu_k + s + 1) - k0;
-  const int P = Lk - Lq;
-  const int row_last = min(row_begin + RW * rb, Lq) - 1;
-  const int key_end = a.causal ? max(0, min(Lk, row_last + P + 1)) : Lk;
-  const int n_kt = (key_end + kKeys - 1) / kKeys;
   const float sl2 = a.scale_log2;
   const bool paged = a.block_tables != nullptr;
-  const int32_t *bt_row = paged ? a.block_tables + static_cast<int64_t>(s) * a.bt_stride : nullptr;
+  const int row_in_item = RW * (wave / a.G4);  // this wave's first row within an item
+  const int head_in_item = wave % a.G4;
 
-  const int wrow0 = row_begin + RW * (wave / a.G4);
-  const bool wave_live = wrow0 < Lq;
-  const int wrow_last = min(wrow0 + RW - 1, Lq - 1);
-  const int wave_key_end = a.causal ? min(Lk, wrow_last + P + 1) : Lk;
-  // Tiles this wave computes (a prefix: a causal wave stops at its own
-  // diagonal) and, among them, the leading tiles that need no mask.
-  const int wave_nkt = wave_live ? min(n_kt, (wave_key_end + kKeys - 1) / kKeys) : 0;
-  int n_plain = min(wave_nkt, Lk / kKeys);
-  if (a.causal) n_plain = min(n_plain, max(0, wrow0 + P + 1) / kKeys);
-
-  u32x4 qf[QS][PT::NKK];
-#pragma unroll
-  for (int qs = 0; qs < QS; ++qs) {
-    const int r = wrow0 + 16 * qs + m;
-    const bool ok = r < Lq;
-    const uint8_t *qp = a.q + static_cast<int64_t>(q0 + (ok ? r : 0)) * a.q_rs + static_cast<int64_t>(head) * a.q_hs;
-#pragma unroll
-    for (int kk = 0; kk < PT::NKK; ++kk) qf[qs][kk] = ok ? load16(qp + (8 * g + 32 * kk) * 2) : u32x4{0, 0, 0, 0};
+  const int n_x = a.n_qtiles, n_y = a.Hkv * a.quads;
+  const int U = n_y * a.num_seqs;
+  const int x = a.pin ? static_cast<int>(blockIdx.x & 7) : 0;
+  const int cx = a.pin ? (U - x + 7) >> 3 : U;
+  uint32_t *ctr = a.queue + x;
+  const CostQueue cq{lds_lev, lds_cuq, lds_cuk, x, n_y, 16 * QS * (NW / a.G4), a.pin ? 8 : 1};
+  if (a.by_cost) {
+    // Sequence bounds into LDS, then the live items of this queue counted
+    // per cost level, then each level's first index (highest level first).
+    for (int i = threadIdx.x; i <= a.num_seqs; i += blockDim.x) {
+      lds_cuq[i] = a.cu_q[i];
+      lds_cuk[i] = a.cu_k[i];
+    }
+    for (int i = threadIdx.x; i < a.n_levels; i += blockDim.x) lds_lev[i] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < a.num_seqs * n_x; i += blockDim.x) {
+      const int sq = i / n_x, qt = i - sq * n_x;
+      const int Lq = lds_cuq[sq + 1] - lds_cuq[sq];
+      const int w = n_slots(cq, first_slot(cq, sq));
+      if (qt * cq.rows < Lq && w > 0)
+        atomicAdd(&lds_lev[cost_level(a, cq, qt, Lq, lds_cuk[sq + 1] - lds_cuk[sq])], w);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      int carry = 0;
+      for (int top = a.n_levels - 1; top >= 0; top -= 64) {
+        const int L = top - lane;
+        const int c = L >= 0 ? lds_lev[L] : 0;
+        const int incl = wave_scan(c, lane);
+        if (L >= 0) lds_lev[L] = carry + incl - c;
+        carry += __builtin_amdgcn_readlane(incl, 63);
+      }
+      if (lane == 0) *lds_n = carry;
+    }
   }
 
-  // ---- K/V copies.  Wave w copies rows CR*w .. CR*w + CR - 1 of each tile,
-  // 4 rows per load; lane l of load c fetches the logical 16-byte chunk that
-  // belongs at byte 16 l of the load's 1 KiB (the chunk swizzles swz_k /
-  // swz_v are made by the source offsets).  The copy state is scalar: the byte offset of the
-  // next tile's first row, the remaining tiles of its block, and the
-  // block-table entry of the next block, fetched one block ahead.
+  // ---------------------------------------------------------------- stream
+  // Copy-stream arguments in registers of their own (the host bounds the
+  // row stride by 1 MiB, so byte counts of a tile fit 32 bits).
+  const uint8_t *const kbase = own_sgpr(a.k);
+  const int64_t v_minus_k = own_sgpr(static_cast<int64_t>(a.v - a.k));
+  const int kv_rs = own_sgpr(static_cast<int>(a.kv_rs));
+  const int tile_bytes = kKeys * kv_rs;
+  const int64_t blk_bytes = own_sgpr(static_cast<int64_t>(a.block_size) * a.kv_rs);
+  const int num_blocks = own_sgpr(a.num_blocks);
+  const int max_blocks = own_sgpr(a.max_blocks);
+  const int tiles_per_blk = paged ? a.block_size / kKeys : 0x40000000;
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) uint8_t *)(smem)));
+  const uint32_t lds_last = lds0 + (kSlots - 1) * DT::SLOT_B;  // the last ring slot
+  // The stream issues runs of entries that share a descriptor shape: a run
+  // ends at a block boundary, before an item's partial last tile, at the end
+  // of an item, or after one empty entry.  Per entry the common path only
+  // counts down, advances the source address and the ring slot, and issues
+  // the copies; the rest happens once per run (next_run).
+  int st_pos = 0;                   // entries issued so far
+  int run_left = 0;                 // entries left in the current run
+  const uint8_t *st_src = kbase;    // K source of the next entry (its row 0, at the item's kv head)
+  uint32_t st_nrec = 0;             // bytes each copy of the run may read (0: rows read as zeros)
+  uint32_t st_dst = lds0;           // ring slot of the next entry
+  int st_rem = 0;                   // keys of the item being copied not yet in a run
+  int st_left = 0, st_bidx = 0, st_blk_next = 0;  // paged: tiles left in the block, next entry and its value
+  int st_head = 0;                  // byte offset of the item's kv head within a row
+  const int32_t *st_bt = nullptr;
+  // The item queued to be copied next, in the form the stream takes over.
+  int nx_rem = 0;       // its keys (0: none queued)
+  int nx_head = 0;      // its kv head's byte offset within a row
+  int64_t nx_base = 0;  // paged: address of its block-table row; packed: byte offset of its first key
+  int nx_blk0 = 0;      // paged: its first block-table entry
+  int nx_first = 0;     // stream index of the queued item's first tile, once started
+  // A copied tile lay in a missing block: from then on every tile takes the
+  // masked path (which checks its block); plain_end bounds the current
+  // item's mask-free loop.
+  int bad_seen = 0, plain_end = 0;
+  // This wave's rows of a tile and its 16-byte pieces (the kv head's offset
+  // is in the source address).
   uint32_t src_k[COPS], src_v[COPS];
 #pragma unroll
   for (int c = 0; c < COPS; ++c) {
     const int drow = CR * wave + 4 * c + (lane >> 4);
-    const uint32_t row_off = static_cast<uint32_t>(drow * a.kv_rs + kvh * DT::ROWB);
+    const uint32_t row_off = static_cast<uint32_t>(drow * kv_rs);
     src_k[c] = row_off + (((lane & 15) ^ swz_k(drow)) << 4);
     src_v[c] = row_off + (((lane & 15) ^ swz_v(drow)) << 4);
   }
-  const int64_t tile_bytes = static_cast<int64_t>(kKeys) * a.kv_rs;
-  const int64_t v_minus_k = a.v - a.k;
-  const int tiles_per_blk = paged ? a.block_size / kKeys : 0x7fffffff;
-  int iss_jt = 0, iss_slot = 0;   // next tile to copy, its ring slot
-  int iss_left = 0;               // tiles of the current block still to copy (paged)
-  int iss_bidx = 0;               // block-table index of the next block
-  int64_t iss_off = paged ? 0 : static_cast<int64_t>(k0) * a.kv_rs;  // byte offset of the next tile
-  bool iss_ok = true;             // the current block exists
-  bool any_bad = false;           // a tile of this item lies in a missing block
-  // Block-table entry bidx of this sequence (paged only: bt_row is null otherwise).
-  auto blk_entry = [&](int bidx) { return bidx < a.max_blocks ? ld_const(bt_row + bidx) : -1; };
-  int blk_next = paged ? blk_entry(0) : 0;
-  auto issue = [&]() {
-    uint32_t nrec = 0;
-    if (iss_jt < n_kt) {
-      if (paged && iss_left == 0) {  // entering the next block
-        const int blk = blk_next;
-        blk_next = blk_entry(iss_bidx + 1);  // used a block from now
-        ++iss_bidx;
-        iss_ok = blk >= 0 && blk < a.num_blocks;
-        any_bad |= !iss_ok;
-        iss_off = static_cast<int64_t>(iss_ok ? blk : 0) * a.block_size * a.kv_rs;
-        iss_left = tiles_per_blk;
-      }
-      const int nvalid = min(kKeys, key_end - iss_jt * kKeys);
-      nrec = iss_ok ? static_cast<uint32_t>(nvalid * a.kv_rs) : 0u;
+  // Block-table entry bidx of a sequence's row (paged only).
+  auto blk_entry = [&](const int32_t *bt, int bidx) { return bidx < max_blocks ? ld_const(bt + bidx) : -1; };
+  auto queue_copy = [&](const Item &it) {
+    nx_rem = (it.live && it.n_kt > 0) ? it.key_end : 0;
+    nx_head = it.kvh * DT::ROWB;
+    if (paged) {
+      const int32_t *bt = a.block_tables + static_cast<int64_t>(it.s) * a.bt_stride;
+      nx_base = static_cast<int64_t>(reinterpret_cast<uintptr_t>(bt));
+      nx_blk0 = nx_rem > 0 ? blk_entry(bt, 0) : 0;
+    } else {
+      nx_base = static_cast<int64_t>(it.k0) * kv_rs + nx_head;
     }
-    uint8_t *dst = smem + iss_slot * DT::SLOT_B + wave * (CR * DT::ROWB);
-    const uint8_t *ksrc = a.k + iss_off;
-    const auto rk = make_rsrc(ksrc, nrec);
-    const auto rv = make_rsrc(ksrc + v_minus_k, nrec);
+  };
+  // Sets up the next run (run_left == 0 on entry).
+  auto next_run = [&]() {
+    if (st_rem <= 0 && nx_rem > 0) {  // start the queued item
+      st_rem = nx_rem;
+      nx_rem = 0;
+      st_head = nx_head;
+      st_bt = paged ? reinterpret_cast<const int32_t *>(static_cast<uintptr_t>(nx_base)) : nullptr;
+      st_src = kbase + (paged ? 0 : nx_base);
+      st_blk_next = nx_blk0;
+      st_bidx = 0;
+      st_left = paged ? 0 : 0x40000000;
+      nx_first = st_pos;
+    }
+    if (st_rem <= 0) {  // nothing to copy: one empty entry
+      st_nrec = 0;
+      run_left = 1;
+      return;
+    }
+    bool ok = true;
+    if (st_left == 0) {  // entering the next block (paged)
+      const int blk = st_blk_next;
+      st_blk_next = blk_entry(st_bt, st_bidx + 1);  // used a block from now
+      ++st_bidx;
+      ok = blk >= 0 && blk < num_blocks;
+      if (!ok) {
+        bad_seen = 1;
+        plain_end = 0;
+      }
+      st_src = kbase + static_cast<int64_t>(ok ? blk : 0) * blk_bytes + st_head;
+      st_left = tiles_per_blk;
+    } else if (paged) {
+      ok = st_nrec != 0;  // the same block as the previous run
+    }
+    const int full = min(st_left, st_rem / kKeys);  // whole tiles left in the block and the item
+    if (full > 0) {
+      run_left = full;
+      st_left -= full;
+      st_rem -= full * kKeys;
+      st_nrec = ok ? static_cast<uint32_t>(tile_bytes) : 0u;
+    } else {  // the item's partial last tile
+      run_left = 1;
+      st_left -= 1;
+      st_nrec = ok ? static_cast<uint32_t>(st_rem * kv_rs) : 0u;
+      st_rem = 0;
+    }
+  };
+  auto issue = [&]() {
+    if (run_left == 0) next_run();
+    uint8_t *dst = smem + (st_dst - lds0) + wave * (CR * DT::ROWB);
+    const auto rk = make_rsrc(st_src, st_nrec);
+    const auto rv = make_rsrc(st_src + v_minus_k, st_nrec);
 #pragma unroll
     for (int c = 0; c < COPS; ++c) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void *)(dst + 1024 * c), 16,
@@ -513,16 +802,15 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rv, (__attribute__((address_space(3))) void *)(dst + DT::TILE_B + 1024 * c), 16, src_v[c], 0, 0, 0);
     }
-    iss_off += tile_bytes;
-    if (paged) --iss_left;
-    ++iss_jt;
-    iss_slot = (iss_slot + 1 == kSlots) ? 0 : iss_slot + 1;
+    st_src += tile_bytes;
+    st_dst = st_dst == lds_last ? lds0 : st_dst + DT::SLOT_B;
+    --run_left;
+    ++st_pos;
   };
 
-  // Per-lane LDS byte offsets inside a K or V tile (fixed for the item).
+  // ------------------------------------------------------- operand offsets
   // K^T operand kk: key row m (row m + 16 is +16 rows), dims 32kk + 8g.. ;
-  // V^T operand j: rows r0 and r0 + 16 (same swizzle: both swizzles ignore
-  // row bit 4).
+  // V^T operand j: rows r0 and r0 + 16 (both swizzles ignore row bit 4).
   int koff[PT::NKK], voff[PT::NJ];
 #pragma unroll
   for (int kk = 0; kk < PT::NKK; ++kk) koff[kk] = m * DT::ROWB + (((4 * kk + g) ^ swz_k(m)) << 4);
@@ -532,294 +820,366 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs &a, int qt, int y
 #pragma unroll
     for (int j = 0; j < PT::NJ; ++j) voff[j] = r0 * DT::ROWB + (((2 * j + (vq >> 1)) ^ swz_v(r0)) << 4) + (vq & 1) * 8;
   }
-  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-      (__attribute__((address_space(3))) uint8_t *)(smem)));
+  const u32x4 ones = u32x4{T::kOne2, T::kOne2, T::kOne2, T::kOne2};
 
-  // K^T operands of the tile in ring slot `slot` (opaque reads: the caller
-  // waits for them with a tied s_waitcnt), then S^T = K Q^T (32 keys x RW
-  // rows, unscaled).
-  auto kread = [&](int slot, u32x4 (&kf)[PT::NKK][2]) {
-    const uint32_t kt = lds0 + slot * DT::SLOT_B;
+  // Q operands of an item for this wave: always QOPS loads, so the count the
+  // waits add is fixed.  A row past the sequence (or of an item past the
+  // queue) loads an existing row instead; its scores and output are computed
+  // but never stored, and nothing selects on the loaded values, which would
+  // make the compiler wait for them -- and for every K/V copy in flight.
+  u32x4 qf[QS][PT::NKK];
+  auto load_q = [&](const Item &it) {
+    const int head = it.live ? it.head0 + head_in_item : 0;
 #pragma unroll
-    for (int kk = 0; kk < PT::NKK; ++kk) {
-      kf[kk][0] = lds_read_b128_at<0>(kt + koff[kk]);
-      kf[kk][1] = lds_read_b128_at<16 * DT::ROWB>(kt + koff[kk]);
-    }
-  };
-  auto kwait = [&](u32x4 (&kf)[PT::NKK][2]) {
-    static_assert(PT::NKK == 4, "operand list below");
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(kf[0][0]), "+v"(kf[0][1]), "+v"(kf[1][0]), "+v"(kf[1][1]), "+v"(kf[2][0]), "+v"(kf[2][1]),
-                   "+v"(kf[3][0]), "+v"(kf[3][1])
-                 :
-                 : "memory");
-  };
-  auto qk = [&](const u32x4 (&kf)[PT::NKK][2], f32x4 (&sc)[QS][2]) {
+    for (int qs = 0; qs < QS; ++qs) {
+      const int r = it.row_begin + row_in_item + 16 * qs + m;
+      const int row = (it.live && r < it.Lq) ? it.q0 + r : it.q0;
+      const uint8_t *qp = a.q + static_cast<int64_t>(row) * a.q_rs + static_cast<int64_t>(head) * a.q_hs;
 #pragma unroll
-    for (int qs = 0; qs < QS; ++qs)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = f32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int kk = 0; kk < PT::NKK; ++kk)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int qs = 0; qs < QS; ++qs) sc[qs][ks] = T::mfma16x16x32(kf[kk][ks], qf[qs][kk], sc[qs][ks]);
-  };
-
-  // V^T operands of head_dim half h (dims 64h .. 64h+63) of the tile in ring
-  // slot `slot`: 8 opaque transposing reads.
-  auto vread = [&](int slot, int h, u32x4 (&vf)[4]) {
-    const uint32_t vt = lds0 + slot * DT::SLOT_B + DT::TILE_B;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const u32x2 lo = lds_read_tr16_at<0>(vt + voff[4 * h + jj]);
-      const u32x2 hi = lds_read_tr16_at<16 * DT::ROWB>(vt + voff[4 * h + jj]);
-      vf[jj] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      for (int kk = 0; kk < PT::NKK; ++kk) qf[qs][kk] = load16(qp + (8 * g + 32 * kk) * 2);
     }
   };
 
-  float m_use[QS];      // running row max, scaled (log2) domain
-  f32x4 o[QS][PT::NJ];  // O^T accumulators
-  f32x4 lsum[QS];       // row sums of P (every element)
+  f32x4 o[QS][PT::NJ];  // O^T accumulators of the item computed last
+  f32x4 lsum[QS];       // its row sums of P (every element)
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) {
-    m_use[qs] = kNegInf;
     lsum[qs] = f32x4{0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < PT::NJ; ++j) o[qs][j] = f32x4{0, 0, 0, 0};
   }
-  const u32x4 ones = u32x4{T::kOne2, T::kOne2, T::kOne2, T::kOne2};
-
-  // First half of key tile jt, right after the barrier that completes tile
-  // jt + 1: the lazy-rescale check of the current S (`sc`, tile jt), the K
-  // reads and QK products of tile jt + 1 (into `sc` on return) and P of tile
-  // jt (into `pb`), with the copy of tile jt + kAhead issued in between, so
-  // the LDS latency hides under the check and the MFMAs under the exp / pack
-  // work.  MASK: the tile crosses the causal diagonal, the end of the keys,
-  // or a missing block.
-  f32x4 sc[QS][2];
-  auto front = [&](auto mask_tag, int jt, int slot, bool blk_ok, u32x4 (&pb)[QS], u32x4 (&vf0)[4]) {
-    constexpr bool MASK = decltype(mask_tag)::value;
-    const int kbase = jt * kKeys;
-    u32x4 kf[PT::NKK][2];
-    kread(slot + 1 == kSlots ? 0 : slot + 1, kf);  // tile jt + 1 (a discarded repeat past the last)
-    float x[QS][8], mnew[QS];
-    bool grow = false;
+  // Output of an item: SOPS stores per wave.  Lane (g, m) holds dims
+  // 16j + 4g .. +3 of row m for every j.  The lanes of lane groups g and g^1
+  // (same row) trade one 8-byte piece per pair of j through permlane16_swap,
+  // so each writes 16 contiguous bytes: even g dims 16j0 + 4g .. +7, odd g
+  // dims 16j1 + 4(g-1) .. +7 (j0 = 2p, j1 = 2p + 1).  The stores go through a
+  // descriptor covering the sequence's rows of this head, so rows past the
+  // end (and a wave with no rows) are dropped by the range check, not skipped.
+  auto store_out = [&](const Item &it) {
+    const bool odd = (g & 1) != 0;
+    const int wrow0 = it.row_begin + row_in_item;
+    const int head = it.head0 + head_in_item;
+    const uint8_t *obase = a.out + static_cast<int64_t>(it.q0) * a.o_rs + static_cast<int64_t>(head) * a.o_hs;
+    const uint32_t orange = wrow0 < it.Lq ? static_cast<uint32_t>((it.Lq - 1) * a.o_rs + D * 2) : 0u;
+    const auto ro = make_rsrc(obase, orange);
 #pragma unroll
     for (int qs = 0; qs < QS; ++qs) {
-      int lim = 0;
-      if constexpr (MASK) {
-        const int row = wrow0 + 16 * qs + m;
-        lim = a.causal ? min(Lk - 1, row + P) : Lk - 1;  // last visible key
-        if (!blk_ok) lim = -1;
+      const float l = lsum[qs][0];  // every element holds the row sum of row m
+      const int row = wrow0 + 16 * qs + m;
+      const float inv = l > 0.f ? 1.0f / l : 0.f;
+      const uint32_t roff = row < it.Lq ? static_cast<uint32_t>(row * a.o_rs) : 0x7fffffffu;
+#pragma unroll
+      for (int p = 0; p < PT::NJ / 2; ++p) {
+        const f32x4 v0 = o[qs][2 * p] * inv, v1 = o[qs][2 * p + 1] * inv;
+        const uint32_t c00 = T::pack2(v0[0], v0[1]), c01 = T::pack2(v0[2], v0[3]);
+        const uint32_t c10 = T::pack2(v1[0], v1[1]), c11 = T::pack2(v1[2], v1[3]);
+        const uint32_t x0 = odd ? c00 : c10, x1 = odd ? c01 : c11;  // the piece the partner needs
+        // After the swap, even lanes find the partner's value in the
+        // second result, odd lanes in the first.
+        const auto r0 = __builtin_amdgcn_permlane16_swap(x0, x0, false, false);
+        const auto r1 = __builtin_amdgcn_permlane16_swap(x1, x1, false, false);
+        const uint32_t y0 = odd ? static_cast<uint32_t>(r0[0]) : static_cast<uint32_t>(r0[1]);
+        const uint32_t y1 = odd ? static_cast<uint32_t>(r1[0]) : static_cast<uint32_t>(r1[1]);
+        const int dim0 = odd ? 16 * (2 * p + 1) + 4 * (g - 1) : 16 * (2 * p) + 4 * g;
+        const u32x4 w = odd ? u32x4{y0, y1, c10, c11} : u32x4{c00, c01, y0, y1};
+        const uint32_t voff_o = roff == 0x7fffffffu ? roff : roff + dim0 * 2;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, w),
+                                               ro, static_cast<int>(voff_o), 0, 0);
       }
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          float v = sc[qs][ks][rr];
-          if constexpr (MASK) v = (kbase + 16 * ks + 4 * g + rr > lim) ? kNegInf : v;
-          x[qs][4 * ks + rr] = v;
-        }
-      // this lane's maximum over its 8 keys of row m (scaled)
-      mnew[qs] = max3_raw(max3_raw(x[qs][0], x[qs][1], x[qs][2]), max3_raw(x[qs][3], x[qs][4], x[qs][5]),
-                          vmax_raw(x[qs][6], x[qs][7])) * sl2;
-      grow |= mnew[qs] > m_use[qs] + kRescale;
     }
-    // Lazy rescale: the running maximum m_use of a row (the same in the four
-    // lanes that hold the row) only moves when some element exceeds it by
-    // more than kRescale, so P = 2^(s - m_use) <= 2^kRescale.  Each lane
-    // checks its own elements; the cross-lane row maximum is only formed when
-    // a rescale happens.  All earlier tiles' P V products are already in o.
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+  };
+
+  // ----------------------------------------------------------------- queue
+  if (threadIdx.x == 0) {
+    lds_item[0] = static_cast<int>(atomicAdd(ctr, 1u));
+    lds_item[1] = static_cast<int>(atomicAdd(ctr, 1u));
+  }
+  __syncthreads();
+  const int n_items = a.by_cost ? __builtin_amdgcn_readfirstlane(*lds_n) : cx * n_x;
+  auto describe = [&](int idx) {
+    return a.by_cost ? describe_by_cost(a, cq, idx, n_items) : describe_by_tile<S>(a, idx, n_items, n_x, n_y, cx, x);
+  };
+  int idx_cur = __builtin_amdgcn_readfirstlane(lds_item[0]);
+  int idx_nxt = __builtin_amdgcn_readfirstlane(lds_item[1]);
+  Item cur = describe(idx_cur);
+  Item nxt = describe(idx_nxt);
+  Item prev{};  // the item whose output is still in o / lsum
+  prev.live = false;
+  queue_copy(cur);
+
+  for (int k = 0;; ++k) {
+    // The item's Q, loaded at one place only: Q is not carried around the
+    // loop, so the compiler never copies (and waits for) loaded registers.
+    load_q(cur);
+    int epi_pos = -1;  // stream entries before this index precede the Q loads and stores just issued
+    if (prev.live) {
+      store_out(prev);
+      epi_pos = st_pos;
+    }
+    if (idx_cur >= n_items) break;
+    int fetch_pos = st_pos;  // stream index at the fetch of item k + 2 (in flight during item k)
+    if (cur.live) {
+      // Stream index of the item's first tile: already in the stream, or
+      // started now (an item without tiles is never queued).
+      int p0 = st_pos;
+      if (cur.n_kt > 0) {
+        if (nx_rem > 0) issue();
+        p0 = nx_first;
+      }
+      queue_copy(nxt);
+      while (st_pos < p0 + kAhead) issue();
+      // Wait for tile 0 (younger: kAhead - 1 stream entries, plus the Q
+      // loads and stores above if tile 0 preceded them).
+      if (p0 < epi_pos)
+        wait_vmcnt<2 * COPS * (kAhead - 1) + EOPS>();
+      else
+        wait_vmcnt<2 * COPS * (kAhead - 1)>();
+      raw_barrier();
+
+      const int Lq = cur.Lq, Lk = cur.Lk, P = cur.P, n_kt = cur.n_kt;
+      const int wrow0 = cur.row_begin + row_in_item;
+      const bool wave_live = wrow0 < Lq;
+      const int wrow_last = min(wrow0 + RW - 1, Lq - 1);
+      const int wave_key_end = a.causal ? min(Lk, wrow_last + P + 1) : Lk;
+      // Tiles this wave computes (a prefix: a causal wave stops at its own
+      // diagonal) and, among them, the leading tiles that need no mask.
+      const int wave_nkt = wave_live ? min(n_kt, (wave_key_end + kKeys - 1) / kKeys) : 0;
+      int n_plain = min(wave_nkt, Lk / kKeys);
+      if (a.causal) n_plain = min(n_plain, max(0, wrow0 + P + 1) / kKeys);
+      const int32_t *bt_row = paged ? a.block_tables + static_cast<int64_t>(cur.s) * a.bt_stride : nullptr;
+
+      auto kread = [&](uint32_t kt, u32x4 (&kf)[PT::NKK][2]) {  // kt: the tile's ring slot
+#pragma unroll
+        for (int kk = 0; kk < PT::NKK; ++kk) {
+          kf[kk][0] = lds_read_b128_at<0>(kt + koff[kk]);
+          kf[kk][1] = lds_read_b128_at<16 * DT::ROWB>(kt + koff[kk]);
+        }
+      };
+      auto kwait = [&](u32x4 (&kf)[PT::NKK][2]) {
+        static_assert(PT::NKK == 4, "operand list below");
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(kf[0][0]), "+v"(kf[0][1]), "+v"(kf[1][0]), "+v"(kf[1][1]), "+v"(kf[2][0]),
+                       "+v"(kf[2][1]), "+v"(kf[3][0]), "+v"(kf[3][1])
+                     :
+                     : "memory");
+      };
+      auto qk = [&](const u32x4 (&kf)[PT::NKK][2], f32x4 (&sc)[QS][2]) {
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int kk = 0; kk < PT::NKK; ++kk)
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int qs = 0; qs < QS; ++qs) sc[qs][ks] = T::mfma16x16x32(kf[kk][ks], qf[qs][kk], sc[qs][ks]);
+      };
+      // V^T operands of head_dim half h (dims 64h .. 64h+63) of the tile in
+      // ring slot `slot`: 8 opaque transposing reads.
+      auto vread = [&](uint32_t slot, int h, u32x4 (&vf)[4]) {
+        const uint32_t vt = slot + DT::TILE_B;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const u32x2 lo = lds_read_tr16_at<0>(vt + voff[4 * h + jj]);
+          const u32x2 hi = lds_read_tr16_at<16 * DT::ROWB>(vt + voff[4 * h + jj]);
+          vf[jj] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+      };
+
+      float m_use[QS];  // running row max, scaled (log2) domain
 #pragma unroll
       for (int qs = 0; qs < QS; ++qs) {
-        const float m_new = fmaxf(m_use[qs], max32_raw(max16_raw(mnew[qs])));
-        const float alpha = (m_use[qs] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(m_use[qs] - m_new);
-        lsum[qs] *= alpha;
+        m_use[qs] = kNegInf;
+        lsum[qs] = f32x4{0, 0, 0, 0};
 #pragma unroll
-        for (int j = 0; j < PT::NJ; ++j) o[qs][j] *= alpha;
-        m_use[qs] = m_new;
+        for (int j = 0; j < PT::NJ; ++j) o[qs][j] = f32x4{0, 0, 0, 0};
       }
-    }
-    issue();
-    kwait(kf);
-    vread(slot, 0, vf0);  // first half of tile jt's V^T operands, waited for in back()
-    f32x4 sn[QS][2];
-    qk(kf, sn);
+      // Q is complete from here on: the compiler waits for it at this point
+      // (behind the prologue's copies at most), not before the QK products
+      // inside the tile loop, where its wait would also cover the K/V copies
+      // issued since.
 #pragma unroll
-    for (int qs = 0; qs < QS; ++qs) {
-      const float mref = (m_use[qs] == kNegInf) ? 0.f : m_use[qs];
-      uint32_t pw[4];
+      for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[qs][2 * t], sl2, -mref));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[qs][2 * t + 1], sl2, -mref));
-        pw[t] = T::pack2(p0, p1);
+        for (int kk = 0; kk < PT::NKK; ++kk) asm volatile("" : "+v"(qf[qs][kk]));
+      // The fetch goes after that wait, which would otherwise include it.
+      if (threadIdx.x == 0) queue_fetch_issue(ctr);
+      fetch_pos = st_pos;
+      f32x4 sc[QS][2];
+      if (wave_nkt > 0) {
+        u32x4 kf[PT::NKK][2];
+        kread(lds0 + (p0 % kSlots) * DT::SLOT_B, kf);
+        kwait(kf);
+        qk(kf, sc);
       }
-      pb[qs] = u32x4{pw[0], pw[1], pw[2], pw[3]};
-    }
-    // Interleave the 8 QS QK products with the ~20 QS exp / scale / pack
-    // instructions (one MFMA, then two VALU), so the VALU work issues while
-    // the matrix core is busy instead of in a run of its own.
-#pragma unroll
-    for (int i = 0; i < 8 * QS; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
-    }
-#pragma unroll
-    for (int qs = 0; qs < QS; ++qs)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = sn[qs][ks];
-  };
-  // Second half: O^T += V^T P^T for the tile in ring slot `slot`, in two
-  // halves of head_dim (4 V^T operands of 16 dims each per half).  The first
-  // half's transposing reads were issued in front(); the second half's are
-  // issued here before the first half's products.  The reads are opaque and
-  // waited for by waits that name their registers, so no MFMA is scheduled
-  // above them (LDS reads complete in order: lgkmcnt(8) leaves only the
-  // second half outstanding).
-  auto back = [&](int slot, const u32x4 (&pb)[QS], u32x4 (&vf0)[4]) {
-    u32x4 vf1[4];
-    vread(slot, 1, vf1);
-    asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(vf0[0]), "+v"(vf0[1]), "+v"(vf0[2]), "+v"(vf0[3]) : : "memory");
-#pragma unroll
-    for (int qs = 0; qs < QS; ++qs)
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) o[qs][jj] = T::mfma16x16x32(vf0[jj], pb[qs], o[qs][jj]);
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vf1[0]), "+v"(vf1[1]), "+v"(vf1[2]), "+v"(vf1[3]) : : "memory");
-#pragma unroll
-    for (int qs = 0; qs < QS; ++qs)
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) o[qs][4 + jj] = T::mfma16x16x32(vf1[jj], pb[qs], o[qs][4 + jj]);
-#pragma unroll
-    for (int qs = 0; qs < QS; ++qs) lsum[qs] = T::mfma16x16x32(ones, pb[qs], lsum[qs]);
-  };
 
-  // Once per tile jt and wave, in tile order, in both loops below; waves
-  // with no work on tile jt still copy their share of tile jt + kAhead.
-  auto sync = [&]() {
-    wait_vmcnt<2 * COPS * (kAhead - 2)>();  // this wave's copies of tile jt + 1 have landed
-    wait_lgkmcnt0();                         // and its reads of tile jt - 1 are done
-    raw_barrier();                           // tile jt + 1 complete; slot of tile jt - 1 free
-  };
-  // Whether the block of key tile jt exists (the masked loop of an item with
-  // a missing block only).
-  auto block_ok = [&](int jt) {
-    const int blk = ld_const(bt_row + jt * kKeys / a.block_size);
-    return blk >= 0 && blk < a.num_blocks;
-  };
-
-  if (n_kt > 0) {
+      // First half of key tile jt (ring slot `slot`), right after the barrier
+      // that completes tile jt + 1: the lazy-rescale check of the current S
+      // (`sc`), the K reads and QK products of tile jt + 1 (into `sc` on
+      // return) and P of tile jt (into `pb`), with the next stream entry in
+      // between; vf0 gets the first half of tile jt's V^T operands.
+      auto front = [&](auto mask_tag, int jt, uint32_t slot, uint32_t slot_next, bool blk_ok, u32x4 (&pb)[QS],
+                       u32x4 (&vf0)[4]) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const int kbase = jt * kKeys;
+        u32x4 kf[PT::NKK][2];
+        kread(slot_next, kf);  // tile jt + 1 (discarded past the last)
+        float xs[QS][8], mnew[QS];
+        bool grow = false;
 #pragma unroll
-    for (int st = 0; st < kAhead; ++st) issue();
-    wait_vmcnt<2 * COPS * (kAhead - 1)>();  // this wave's copies of tile 0 have landed
-    raw_barrier();                           // everyone's
-    if (wave_nkt > 0) {
-      u32x4 kf[PT::NKK][2];
-      kread(0, kf);
-      kwait(kf);
-      qk(kf, sc);
-    }
-  }
-  // The copies of a tile are issued kAhead tiles ahead, so a missing block
-  // is known (any_bad) before its tile is computed; from then on the masked
-  // loop runs.
-  int jt = 0, slot = 0;
-  for (; jt < n_plain && !any_bad; ++jt) {
-    sync();
-    u32x4 pb[QS], vf0[4];
-    front(std::false_type{}, jt, slot, true, pb, vf0);
-    back(slot, pb, vf0);
-    slot = slot + 1 == kSlots ? 0 : slot + 1;
-  }
-  for (; jt < n_kt; ++jt) {
-    sync();
-    if (jt < wave_nkt) {
-      u32x4 pb[QS], vf0[4];
-      front(std::true_type{}, jt, slot, !any_bad || block_ok(jt), pb, vf0);
-      back(slot, pb, vf0);
+        for (int qs = 0; qs < QS; ++qs) {
+          int lim = 0;
+          if constexpr (MASK) {
+            const int row = wrow0 + 16 * qs + m;
+            lim = a.causal ? min(Lk - 1, row + P) : Lk - 1;  // last visible key
+            if (!blk_ok) lim = -1;
+          }
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+              float v = sc[qs][ks][rr];
+              if constexpr (MASK) v = (kbase + 16 * ks + 4 * g + rr > lim) ? kNegInf : v;
+              xs[qs][4 * ks + rr] = v;
+            }
+          // this lane's maximum over its 8 keys of row m (scaled)
+          mnew[qs] = max3_raw(max3_raw(xs[qs][0], xs[qs][1], xs[qs][2]),
+                              max3_raw(xs[qs][3], xs[qs][4], xs[qs][5]), vmax_raw(xs[qs][6], xs[qs][7])) * sl2;
+          grow |= mnew[qs] > m_use[qs] + kRescale;
+        }
+        // Lazy rescale: the running maximum m_use of a row (the same in the
+        // four lanes that hold the row) only moves when some element exceeds
+        // it by more than kRescale, so P = 2^(s - m_use) <= 2^kRescale.  Each
+        // lane checks its own elements; the cross-lane row maximum is only
+        // formed when a rescale happens.  Earlier tiles' P V are already in o.
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+          for (int qs = 0; qs < QS; ++qs) {
+            const float m_new = fmaxf(m_use[qs], max32_raw(max16_raw(mnew[qs])));
+            const float alpha = (m_use[qs] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(m_use[qs] - m_new);
+            lsum[qs] *= alpha;
+#pragma unroll
+            for (int j = 0; j < PT::NJ; ++j) o[qs][j] *= alpha;
+            m_use[qs] = m_new;
+          }
+        }
+        issue();
+        kwait(kf);
+        vread(slot, 0, vf0);  // first half of tile jt's V^T operands, waited for in back()
+        f32x4 sn[QS][2];
+        qk(kf, sn);
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) {
+          const float mref = (m_use[qs] == kNegInf) ? 0.f : m_use[qs];
+          uint32_t pw[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float p0_ = __builtin_amdgcn_exp2f(__builtin_fmaf(xs[qs][2 * t], sl2, -mref));
+            const float p1_ = __builtin_amdgcn_exp2f(__builtin_fmaf(xs[qs][2 * t + 1], sl2, -mref));
+            pw[t] = T::pack2(p0_, p1_);
+          }
+          pb[qs] = u32x4{pw[0], pw[1], pw[2], pw[3]};
+        }
+        // Interleave the 8 QS QK products with the ~20 QS exp / scale / pack
+        // instructions (one MFMA, then two VALU).
+#pragma unroll
+        for (int i = 0; i < 8 * QS; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+        }
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = sn[qs][ks];
+      };
+      // Second half: O^T += V^T P^T for the tile in ring slot `slot`, in two
+      // halves of head_dim; the second half's reads are issued before the
+      // first half's products.  LDS reads complete in order, so lgkmcnt(8)
+      // leaves only the second half outstanding.
+      auto back = [&](uint32_t slot, const u32x4 (&pb)[QS], u32x4 (&vf0)[4]) {
+        u32x4 vf1[4];
+        vread(slot, 1, vf1);
+        asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(vf0[0]), "+v"(vf0[1]), "+v"(vf0[2]), "+v"(vf0[3]) : : "memory");
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) o[qs][jj] = T::mfma16x16x32(vf0[jj], pb[qs], o[qs][jj]);
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vf1[0]), "+v"(vf1[1]), "+v"(vf1[2]), "+v"(vf1[3]) : : "memory");
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) o[qs][4 + jj] = T::mfma16x16x32(vf1[jj], pb[qs], o[qs][4 + jj]);
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) lsum[qs] = T::mfma16x16x32(ones, pb[qs], lsum[qs]);
+      };
+      // Once per tile jt and wave, in tile order, in both loops below: wait
+      // for this wave's copies of tile jt + 1 (younger: kAhead - 2 stream
+      // entries, plus the Q loads and stores of the item's start if tile
+      // jt + 1 preceded them).
+      const int epi_tiles = epi_pos - p0 - 1;  // leading tiles whose wait adds the item's start operations
+      auto sync = [&](int jt) {
+        if (jt < epi_tiles)
+          wait_vmcnt<2 * COPS * (kAhead - 2) + EOPS>();
+        else
+          wait_vmcnt<2 * COPS * (kAhead - 2)>();
+        wait_lgkmcnt0();  // and its reads of tile jt - 1 are done
+        raw_barrier();    // tile jt + 1 complete; slot of tile jt - 1 free
+      };
+      // Whether the block of key tile jt exists (the masked loop once a
+      // missing block has been seen).
+      auto block_ok = [&](int jt) {
+        const int blk = ld_const(bt_row + jt * kKeys / a.block_size);
+        return blk >= 0 && blk < num_blocks;
+      };
+
+      // Ring slots (LDS addresses) of tiles jt and jt + 1.
+      uint32_t slot = lds0 + (p0 % kSlots) * DT::SLOT_B;
+      uint32_t slot_next = slot == lds_last ? lds0 : slot + DT::SLOT_B;
+      int jt = 0;
+      plain_end = bad_seen ? 0 : n_plain;
+      for (; jt < plain_end; ++jt) {
+        sync(jt);
+        u32x4 pb[QS], vf0[4];
+        front(std::false_type{}, jt, slot, slot_next, true, pb, vf0);
+        back(slot, pb, vf0);
+        slot = slot_next;
+        slot_next = slot_next == lds_last ? lds0 : slot_next + DT::SLOT_B;
+      }
+      for (; jt < n_kt; ++jt) {
+        sync(jt);
+        if (jt < wave_nkt) {
+          u32x4 pb[QS], vf0[4];
+          front(std::true_type{}, jt, slot, slot_next, !bad_seen || !paged || block_ok(jt), pb, vf0);
+          back(slot, pb, vf0);
+        } else {
+          issue();
+        }
+        slot = slot_next;
+        slot_next = slot_next == lds_last ? lds0 : slot_next + DT::SLOT_B;
+      }
     } else {
-      issue();
+      if (threadIdx.x == 0) queue_fetch_issue(ctr);
+      queue_copy(nxt);
     }
-    slot = slot + 1 == kSlots ? 0 : slot + 1;
-  }
-  wait_vmcnt<0>();  // drain the tail copies before the LDS is reused
-
-  if (!wave_live) return;
-  // Output: lane (g, m) holds dims 16j + 4g .. +3 of row m for every j.  The
-  // lanes of lane groups g and g^1 (same row) trade one 8-byte piece per
-  // pair of j through permlane16_swap, so each writes 16 contiguous bytes:
-  // even g dims 16j0 + 4g .. +7, odd g dims 16j1 + 4(g-1) .. +7 (j0 = 2p,
-  // j1 = 2p + 1): eight 16-byte stores per 16 rows instead of sixteen 8-byte.
-  const bool odd = (g & 1) != 0;
-#pragma unroll
-  for (int qs = 0; qs < QS; ++qs) {
-    const float l = lsum[qs][0];  // every element holds the row sum of row m
-    const int row = wrow0 + 16 * qs + m;
-    if (row >= Lq) continue;      // the same for both lanes of a swap pair
-    const float inv = l > 0.f ? 1.0f / l : 0.f;
-    uint8_t *op = a.out + static_cast<int64_t>(q0 + row) * a.o_rs + static_cast<int64_t>(head) * a.o_hs;
-#pragma unroll
-    for (int p = 0; p < PT::NJ / 2; ++p) {
-      const f32x4 v0 = o[qs][2 * p] * inv, v1 = o[qs][2 * p + 1] * inv;
-      const uint32_t c00 = T::pack2(v0[0], v0[1]), c01 = T::pack2(v0[2], v0[3]);
-      const uint32_t c10 = T::pack2(v1[0], v1[1]), c11 = T::pack2(v1[2], v1[3]);
-      const uint32_t x0 = odd ? c00 : c10, x1 = odd ? c01 : c11;  // the piece the partner needs
-      // After the swap, even lanes find the partner's value in the second
-      // result, odd lanes in the first.
-      const auto r0 = __builtin_amdgcn_permlane16_swap(x0, x0, false, false);
-      const auto r1 = __builtin_amdgcn_permlane16_swap(x1, x1, false, false);
-      const uint32_t y0 = odd ? static_cast<uint32_t>(r0[0]) : static_cast<uint32_t>(r0[1]);
-      const uint32_t y1 = odd ? static_cast<uint32_t>(r1[0]) : static_cast<uint32_t>(r1[1]);
-      const int dim0 = odd ? 16 * (2 * p + 1) + 4 * (g - 1) : 16 * (2 * p) + 4 * g;
-      const u32x4 w = odd ? u32x4{y0, y1, c10, c11} : u32x4{c00, c01, y0, y1};
-      store16(op + dim0 * 2, w);
+    // Next item: publish the fetched index (slot k + 2 of 4: a wave still
+    // reading slot k + 1 cannot be overtaken, the write comes after the
+    // barrier that follows its read).  A plain barrier: the fence of
+    // __syncthreads() would wait for the K/V copies in flight.
+    if (threadIdx.x == 0) {
+      // Operations issued since the fetch: the stream's copies.
+      lds_item[(k + 2) & 3] = static_cast<int>(queue_fetch_result(2 * COPS * (st_pos - fetch_pos)));
+      wait_lgkmcnt0();
     }
+    raw_barrier();
+    const int idx_new = __builtin_amdgcn_readfirstlane(lds_item[(k + 2) & 3]);
+    prev = cur;
+    cur = nxt;
+    nxt = describe(idx_new);
+    idx_cur = idx_nxt;
+    idx_nxt = idx_new;
   }
-}
-
-// Persistent prefill: one workgroup per CU pulls work items from a queue.
-// The hardware dispatcher keeps only about half of the CUs busy when
-// one-per-CU workgroups of very different lengths are launched as a plain
-// grid; a queue keeps every CU fed until the work runs out.
-//
-// Items are grouped as in map_work: XCD x (workgroups L with L % 8 == x) owns
-// the groups u = x, x + 8, ... and serves them from its own counter
-// queue[x], in query-tile order from the last tile down (longest first).
-// queue[8] counts finished workgroups; the last one to finish puts all nine
-// words back to zero, so the workspace is ready for the next call without a
-// host-side clear.
-template <class T, int D, class S>
-__global__ __launch_bounds__(64 * S::NW) __attribute__((amdgpu_waves_per_eu(S::WPE)))
-void varlen_prefill_dma_kernel(const PrefillArgs a) {
-  using DT = DTile<T, D>;
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  int *lds_item = reinterpret_cast<int *>(smem + S::SLOTS * DT::SLOT_B);
-
-  const int n_x = a.n_qtiles, n_y = a.Hkv * a.quads;
-  const int U = n_y * a.num_seqs;
-  const int x = a.pin ? static_cast<int>(blockIdx.x & 7) : 0;
-  const int cx = a.pin ? (U - x + 7) >> 3 : U;
-  const int n_items = cx * n_x;
-  uint32_t *ctr = a.queue + x;
-
-  if (threadIdx.x == 0) lds_item[0] = static_cast<int>(atomicAdd(ctr, 1u));
-  __syncthreads();
-  int item = __builtin_amdgcn_readfirstlane(lds_item[0]);  // uniform from here on
-  for (int it = 1; item < n_items; ++it) {
-    uint32_t next = 0;
-    if (threadIdx.x == 0) next = atomicAdd(ctr, 1u);  // in flight while this item runs
-    const int qt = n_x - 1 - item / cx;
-    const int u = a.pin ? x + 8 * (item % cx) : item % cx;
-    prefill_item<T, D, S>(a, qt, u % n_y, u / n_y, smem);
-    // Alternate slots: a wave still reading slot it-1 cannot overlap the
-    // write of slot it+1, which comes after the next barrier.
-    if (threadIdx.x == 0) lds_item[it & 1] = static_cast<int>(next);
-    __syncthreads();  // also: LDS ring free for the next item
-    item = __builtin_amdgcn_readfirstlane(lds_item[it & 1]);
-  }
+  wait_vmcnt<0>();  // the stream's last (empty) copies and the last stores complete before the workgroup ends
   if (threadIdx.x == 0) {
     if (atomicAdd(a.queue + 8, 1u) == gridDim.x - 1) {
       // Every other workgroup has taken its last index and finished.
@@ -829,13 +1189,21 @@ void varlen_prefill_dma_kernel(const PrefillArgs a) {
   }
 }
 
+// The body lives in a device function: its inline assembly uses register
+// constraints that only the device compilation accepts.
+template <class T, int D, class S>
+__global__ __launch_bounds__(64 * S::NW) __attribute__((amdgpu_waves_per_eu(S::WPE), amdgpu_num_vgpr(255)))
+void varlen_prefill_dma_kernel(const PrefillArgs a) {
+  prefill_persistent<T, D, S>(a);
+}
+
 // Launch shape of the 16-bit kernel: C (two independent 4-wave workgroups
-// per CU) measured fastest at cfg3 on MI355X (480 us against 495 for A and
-// 515 for B); NQ_PREFILL_SHAPE = a | b | c selects one for measurements.
+// per CU) measured fastest at cfg3 on MI355X; NQ_PREFILL_SHAPE = a | c
+// selects one for measurements.
 char prefill_shape() {
   static char shape = [] {
     const char *e = getenv("NQ_PREFILL_SHAPE");
-    return (e && (e[0] == 'a' || e[0] == 'b' || e[0] == 'c')) ? e[0] : 'c';
+    return (e && (e[0] == 'a' || e[0] == 'c')) ? e[0] : 'c';
   }();
   return shape;
 }
@@ -849,6 +1217,13 @@ int launch_prefill_dma(PrefillArgs a, hipStream_t st) {
   if (total > 0x7fffffff) return fail(NQ_EINVAL, "varlen_prefill: too many work items");
   if (!a.queue) return fail(NQ_EINVAL, "varlen_prefill: null workspace");
   a.pin = U >= 8;
+  // Cost order when the sequence bounds fit in LDS and counting the items
+  // at launch stays short; query-tile order otherwise.
+  a.by_cost = a.num_seqs <= kMaxSeqs && static_cast<int64_t>(a.num_seqs) * a.n_qtiles <= 65536;
+  const int nkt_max = (a.max_seqlen_k + kKeys - 1) / kKeys;  // key tiles of the longest item
+  a.level_shift = 0;
+  while ((nkt_max >> a.level_shift) + 1 > kMaxLevels) ++a.level_shift;
+  a.n_levels = (nkt_max >> a.level_shift) + 1;
   // S::WG_PER_CU resident workgroups per CU, never more than there are
   // items; a multiple of 8 so every XCD gets the same count.
   int64_t grid = (static_cast<int64_t>(device_cus()) * S::WG_PER_CU + 7) / 8 * 8;
@@ -861,7 +1236,6 @@ template <class T, bool FP8, int D>
 int launch_prefill(PrefillArgs a, hipStream_t s) {
   if constexpr (!FP8) {
     switch (prefill_shape()) {
-      case 'b': return launch_prefill_dma<T, D, ShapeB>(a, s);
       case 'c': return launch_prefill_dma<T, D, ShapeC>(a, s);
       default: return launch_prefill_dma<T, D, ShapeA>(a, s);
     }
@@ -925,6 +1299,9 @@ extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_
       !aligned(out, 16))
     return fail(NQ_EINVAL, "varlen_prefill: q/k/v/out alignment");
   if (kv_row_stride * ksz > (1 << 20)) return fail(NQ_EINVAL, "varlen_prefill: K/V row stride too large");
+  // Output stores address a sequence's rows of one head with 32-bit offsets.
+  if ((static_cast<int64_t>(max_seqlen_q) + 256) * out_row_stride * qsz >= (int64_t{1} << 31))
+    return fail(NQ_EINVAL, "varlen_prefill: max_seqlen_q %d x output row stride too large", max_seqlen_q);
   if ((!workspace || workspace_bytes < nq_prefill_workspace_bytes() || !aligned(workspace, 4)))
     return fail(NQ_EINVAL, "varlen_prefill: workspace of %lld bytes at %p (need %lld, 4-byte aligned)",
                 (long long)workspace_bytes, workspace, (long long)nq_prefill_workspace_bytes());
@@ -941,7 +1318,7 @@ extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_
   a.block_tables = block_tables;
   a.bt_stride = bt_stride;
   a.max_blocks = max_blocks_per_seq;
-  a.num_blocks = num_blocks;
+  a.num_blocks = static_cast<int>(num_blocks < 0x7fffffff ? num_blocks : 0x7fffffff);
   a.out = static_cast<uint8_t *>(out);
   a.o_rs = out_row_stride * qsz;
   a.o_hs = out_head_stride * qsz;
@@ -953,6 +1330,7 @@ extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_
   a.block_size = block_size;
   a.num_seqs = num_seqs;
   a.max_seqlen_q = max_seqlen_q;
+  a.max_seqlen_k = max_seqlen_k;
   const int rows_per_wg = kRows * (4 / a.G4);
   a.n_qtiles = (max_seqlen_q + rows_per_wg - 1) / rows_per_wg;
   a.causal = causal;
