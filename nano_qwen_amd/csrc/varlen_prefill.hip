@@ -498,23 +498,24 @@ struct CostQueue {
   const int *cuq;  // LDS: cu_seqlens_q, cu_seqlens_k
   const int *cuk;
   int x, n_y, rows, ystep;
+  int rows_log2, ystep_log2;  // rows and ystep are powers of two
 };
 // Kv-head slots of sequence s in the queue: y0, y0 + ystep, ... < n_y.
 __device__ __forceinline__ int first_slot(const CostQueue &cq, int s) {
   return cq.ystep == 8 ? ((cq.x - s * cq.n_y) & 7) : 0;
 }
 __device__ __forceinline__ int n_slots(const CostQueue &cq, int y0) {
-  return y0 < cq.n_y ? (cq.n_y - 1 - y0) / cq.ystep + 1 : 0;
+  return y0 < cq.n_y ? ((cq.n_y - 1 - y0) >> cq.ystep_log2) + 1 : 0;
 }
 // Smallest query tile (of nq) whose item has at least v key tiles.
 __device__ __forceinline__ int first_tile_with(const PrefillArgs &a, const CostQueue &cq, int v, int nq, int Lk,
                                                int P) {
   if (v <= 0) return 0;
   if (!a.causal) return (Lk + kKeys - 1) / kKeys >= v ? 0 : nq;
-  const int64_t t = static_cast<int64_t>(kKeys) * (v - 1);  // the item needs key_end > t
+  const int t = kKeys * (v - 1);  // the item needs key_end > t (v <= n_levels << level_shift)
   if (Lk <= t) return nq;
-  const int64_t need = t - P;  // (qt + 1) * rows > need
-  return need < 0 ? 0 : static_cast<int>(min<int64_t>(need / cq.rows, nq));
+  const int need = t - P;  // (qt + 1) * rows > need
+  return need < 0 ? 0 : min(need >> cq.rows_log2, nq);
 }
 // Cost level of query tile qt of a sequence (as fill_item computes key_end).
 __device__ __forceinline__ int cost_level(const PrefillArgs &a, const CostQueue &cq, int qt, int Lq, int Lk) {
@@ -522,13 +523,17 @@ __device__ __forceinline__ int cost_level(const PrefillArgs &a, const CostQueue 
   const int key_end = a.causal ? max(0, min(Lk, row_last + Lk - Lq + 1)) : Lk;
   return min(((key_end + kKeys - 1) / kKeys) >> a.level_shift, a.n_levels - 1);
 }
-// Wave-wide inclusive prefix sum.
-__device__ __forceinline__ int wave_scan(int v, int lane) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int t = __shfl_up(v, d, 64);
-    if (lane >= d) v += t;
-  }
+// Wave-wide inclusive prefix sum through DPP: shifts by 1, 2, 4, 8 within
+// each 16-lane row, then each row's running total broadcast into the rows
+// after it (row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3).
+// Lanes whose source is out of range add 0 (the `old` operand).
+__device__ __forceinline__ int wave_scan(int v, int) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
   return v;
 }
 // Item at queue index idx.  Called by whole waves (all 64 lanes).
@@ -560,7 +565,7 @@ __device__ __forceinline__ Item describe_by_cost(const PrefillArgs &a, const Cos
     int cnt = 0, qlo = 0, nqt = 0;
     if (s < a.num_seqs) {
       const int Lq = cq.cuq[s + 1] - cq.cuq[s], Lk = cq.cuk[s + 1] - cq.cuk[s];
-      const int nq = Lq > 0 ? (Lq + cq.rows - 1) / cq.rows : 0;
+      const int nq = Lq > 0 ? (Lq + cq.rows - 1) >> cq.rows_log2 : 0;
       qlo = first_tile_with(a, cq, lo_v, nq, Lk, Lk - Lq);
       const int qhi = top ? nq : first_tile_with(a, cq, hi_v, nq, Lk, Lk - Lq);
       nqt = max(0, qhi - qlo);
@@ -652,7 +657,9 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   const int x = a.pin ? static_cast<int>(blockIdx.x & 7) : 0;
   const int cx = a.pin ? (U - x + 7) >> 3 : U;
   uint32_t *ctr = a.queue + x;
-  const CostQueue cq{lds_lev, lds_cuq, lds_cuk, x, n_y, 16 * QS * (NW / a.G4), a.pin ? 8 : 1};
+  const int item_rows = 16 * QS * (NW / a.G4);
+  const CostQueue cq{lds_lev,   lds_cuq, lds_cuk, x, n_y, item_rows, a.pin ? 8 : 1, 31 - __builtin_clz(item_rows),
+                     a.pin ? 3 : 0};
   if (a.by_cost) {
     // Sequence bounds into LDS, then the live items of this queue counted
     // per cost level, then each level's first index (highest level first).
@@ -1067,31 +1074,47 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         issue();
         kwait(kf);
         vread(slot, 0, vf0);  // first half of tile jt's V^T operands, waited for in back()
+        // The QK products of tile jt + 1 with P of tile jt in between, in a
+        // fixed order: after every second product one unit of P (two
+        // exponentials and a pack), so that the exponentials run while the
+        // matrix core works.  Products that share an accumulator are 2 QS
+        // apart.
         f32x4 sn[QS][2];
-        qk(kf, sn);
-#pragma unroll
-        for (int qs = 0; qs < QS; ++qs) {
-          const float mref = (m_use[qs] == kNegInf) ? 0.f : m_use[qs];
-          uint32_t pw[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const float p0_ = __builtin_amdgcn_exp2f(__builtin_fmaf(xs[qs][2 * t], sl2, -mref));
-            const float p1_ = __builtin_amdgcn_exp2f(__builtin_fmaf(xs[qs][2 * t + 1], sl2, -mref));
-            pw[t] = T::pack2(p0_, p1_);
-          }
-          pb[qs] = u32x4{pw[0], pw[1], pw[2], pw[3]};
-        }
-        // Interleave the 8 QS QK products with the ~20 QS exp / scale / pack
-        // instructions (one MFMA, then two VALU).
-#pragma unroll
-        for (int i = 0; i < 8 * QS; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
-        }
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
+          for (int ks = 0; ks < 2; ++ks) sn[qs][ks] = f32x4{0, 0, 0, 0};
+        float mref[QS];
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) mref[qs] = (m_use[qs] == kNegInf) ? 0.f : m_use[qs];
+        uint32_t pw[QS][4];
+#pragma unroll
+        for (int i = 0; i < PT::NKK * 2 * QS; ++i) {
+          const int kk = i / (2 * QS), ks = (i / QS) % 2, qs = i % QS;
+          sn[qs][ks] = T::mfma16x16x32(kf[kk][ks], qf[qs][kk], sn[qs][ks]);
+          if (i % 2 == 1) {
+            const int u = i / 2, uq = u / 4, t = u % 4;  // unit u: elements 2t, 2t + 1 of rows block uq
+            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(xs[uq][2 * t], sl2, -mref[uq]));
+            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(xs[uq][2 * t + 1], sl2, -mref[uq]));
+            pw[uq][t] = T::pack2(e0, e1);
+          }
+        }
+        // Per unit: a product, the two scale-and-subtract steps, a product,
+        // the two exponentials, the pack.
+#pragma unroll
+        for (int u = 0; u < 4 * QS; ++u) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);  // transcendental
+          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
+        }
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) {
+          pb[qs] = u32x4{pw[qs][0], pw[qs][1], pw[qs][2], pw[qs][3]};
+#pragma unroll
           for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = sn[qs][ks];
+        }
       };
       // Second half: O^T += V^T P^T for the tile in ring slot `slot`, in two
       // halves of head_dim; the second half's reads are issued before the

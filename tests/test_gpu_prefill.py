@@ -144,3 +144,19 @@ def test_prefill_queue_resets_between_calls(cuda):
         assert torch.equal(first, again)
     ws = kernels.prefill_workspace(cuda)
     assert int(ws.abs().sum()) == 0
+
+
+def test_prefill_many_sequences_cost_order(cuda):
+    """70 sequences: the persistent kernel's cost-ordered queue selects items
+    across two 64-sequence steps (and every lane row of the wave scan)."""
+    case = make_prefill_case("cfg3", seed=10, device=cuda, nseq=70, lq=(1, 160), prefix_blocks=(1, 1))
+    check(case, range(70), TOL_BF16)
+
+
+def test_prefill_query_tile_order_past_lds_bounds(cuda):
+    """1100 sequences exceed the sequence bounds the kernel keeps in LDS, so
+    its queue runs in query-tile order (items without rows included)."""
+    case = make_prefill_case("cfg3", seed=11, device=cuda, nseq=1100, lq=(1, 40), prefix_blocks=(0, 0),
+                             hq=8, hkv=2)
+    assert case["block_tables"] is None
+    check(case, range(0, 1100, 7), TOL_BF16)
