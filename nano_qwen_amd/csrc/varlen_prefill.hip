@@ -1021,6 +1021,16 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         qk(kf, sc);
       }
 
+      // Scores of the tile whose P is being formed, and the subtrahend of its
+      // exponents (the running maximum after the tile's rescale check).
+      float xt[QS][8], mref[QS];
+      // One unit of P: elements 2t, 2t + 1 of rows block qs, exponentiated
+      // against the running maximum and packed to 16 bits.
+      auto p_unit = [&](int qs, int t) {
+        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(xt[qs][2 * t], sl2, -mref[qs]));
+        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(xt[qs][2 * t + 1], sl2, -mref[qs]));
+        return T::pack2(e0, e1);
+      };
       // First half of key tile jt (ring slot `slot`), right after the barrier
       // that completes tile jt + 1: the lazy-rescale check of the current S
       // (`sc`), the K reads and QK products of tile jt + 1 (into `sc` on
@@ -1032,7 +1042,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         const int kbase = jt * kKeys;
         u32x4 kf[PT::NKK][2];
         kread(slot_next, kf);  // tile jt + 1 (discarded past the last)
-        float xs[QS][8], mnew[QS];
+        float mnew[QS];
         bool grow = false;
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs) {
@@ -1048,11 +1058,11 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
             for (int rr = 0; rr < 4; ++rr) {
               float v = sc[qs][ks][rr];
               if constexpr (MASK) v = (kbase + 16 * ks + 4 * g + rr > lim) ? kNegInf : v;
-              xs[qs][4 * ks + rr] = v;
+              xt[qs][4 * ks + rr] = v;
             }
           // this lane's maximum over its 8 keys of row m (scaled)
-          mnew[qs] = max3_raw(max3_raw(xs[qs][0], xs[qs][1], xs[qs][2]),
-                              max3_raw(xs[qs][3], xs[qs][4], xs[qs][5]), vmax_raw(xs[qs][6], xs[qs][7])) * sl2;
+          mnew[qs] = max3_raw(max3_raw(xt[qs][0], xt[qs][1], xt[qs][2]),
+                              max3_raw(xt[qs][3], xt[qs][4], xt[qs][5]), vmax_raw(xt[qs][6], xt[qs][7])) * sl2;
           grow |= mnew[qs] > m_use[qs] + kRescale;
         }
         // Lazy rescale: the running maximum m_use of a row (the same in the
@@ -1074,35 +1084,88 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         issue();
         kwait(kf);
         vread(slot, 0, vf0);  // first half of tile jt's V^T operands, waited for in back()
-        // The QK products of tile jt + 1 with P of tile jt in between, in a
-        // fixed order: after every second product one unit of P (two
-        // exponentials and a pack), so that the exponentials run while the
-        // matrix core works.  Products that share an accumulator are 2 QS
+        // The QK products of tile jt + 1 with P of the first QS / 2 row
+        // blocks of tile jt in between (one unit of P -- two exponentials and
+        // a pack -- per 4 products), so that the exponentials run while the
+        // matrix core works; back() does the other row blocks the same way
+        // beside its products.  Products that share an accumulator are 2 QS
         // apart.
         f32x4 sn[QS][2];
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) sn[qs][ks] = f32x4{0, 0, 0, 0};
-        float mref[QS];
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs) mref[qs] = (m_use[qs] == kNegInf) ? 0.f : m_use[qs];
-        uint32_t pw[QS][4];
+        uint32_t pw[QS / 2][4];
 #pragma unroll
         for (int i = 0; i < PT::NKK * 2 * QS; ++i) {
           const int kk = i / (2 * QS), ks = (i / QS) % 2, qs = i % QS;
           sn[qs][ks] = T::mfma16x16x32(kf[kk][ks], qf[qs][kk], sn[qs][ks]);
-          if (i % 2 == 1) {
-            const int u = i / 2, uq = u / 4, t = u % 4;  // unit u: elements 2t, 2t + 1 of rows block uq
-            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(xs[uq][2 * t], sl2, -mref[uq]));
-            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(xs[uq][2 * t + 1], sl2, -mref[uq]));
-            pw[uq][t] = T::pack2(e0, e1);
+          if (i % 4 == 3) {
+            const int u = i / 4, uq = u / 4, t = u % 4;  // unit u: elements 2t, 2t + 1 of rows block uq
+            pw[uq][t] = p_unit(uq, t);
           }
         }
         // Per unit: a product, the two scale-and-subtract steps, a product,
-        // the two exponentials, the pack.
+        // the two exponentials, two products, the pack.
 #pragma unroll
-        for (int u = 0; u < 4 * QS; ++u) {
+        for (int u = 0; u < 2 * QS; ++u) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);  // transcendental
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
+        }
+#pragma unroll
+        for (int qs = 0; qs < QS / 2; ++qs) pb[qs] = u32x4{pw[qs][0], pw[qs][1], pw[qs][2], pw[qs][3]};
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = sn[qs][ks];
+      };
+      // Second half: O^T += V^T P^T for the tile in ring slot `slot`, in two
+      // halves of head_dim (the second half's reads issued before the first
+      // half's products; LDS reads complete in order, so lgkmcnt(8) leaves
+      // only the second half outstanding).  The first QS / 2 row blocks'
+      // products go first, with P of the other row blocks computed between
+      // them (one unit per 2 products); then those blocks' products.
+      auto back = [&](uint32_t slot, u32x4 (&pb)[QS], u32x4 (&vf0)[4]) {
+        constexpr int H = QS / 2;
+        u32x4 vf1[4];
+        vread(slot, 1, vf1);
+        asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(vf0[0]), "+v"(vf0[1]), "+v"(vf0[2]), "+v"(vf0[3]) : : "memory");
+        uint32_t pw[QS - H][4];
+#pragma unroll
+        for (int i = 0; i < 4 * H; ++i) {
+          const int qs = i / 4, jj = i % 4;
+          o[qs][jj] = T::mfma16x16x32(vf0[jj], pb[qs], o[qs][jj]);
+          if (i % 2 == 1) {
+            const int u = i / 2, uq = u / 4, t = u % 4;  // units 0 .. 2H - 1 of the upper blocks
+            pw[uq][t] = p_unit(H + uq, t);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 2 * H; ++u) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);  // transcendental
+          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vf1[0]), "+v"(vf1[1]), "+v"(vf1[2]), "+v"(vf1[3]) : : "memory");
+#pragma unroll
+        for (int i = 0; i < 4 * H; ++i) {
+          const int qs = i / 4, jj = i % 4;
+          o[qs][4 + jj] = T::mfma16x16x32(vf1[jj], pb[qs], o[qs][4 + jj]);
+          if (i % 2 == 1) {
+            const int u = 2 * H + i / 2, uq = u / 4, t = u % 4;  // units 2H .. 4H - 1 of the upper blocks
+            pw[uq][t] = p_unit(H + uq, t);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 2 * H; ++u) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
           __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
@@ -1110,31 +1173,16 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
           __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
         }
 #pragma unroll
-        for (int qs = 0; qs < QS; ++qs) {
-          pb[qs] = u32x4{pw[qs][0], pw[qs][1], pw[qs][2], pw[qs][3]};
+        for (int qs = 0; qs < H; ++qs) lsum[qs] = T::mfma16x16x32(ones, pb[qs], lsum[qs]);
 #pragma unroll
-          for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = sn[qs][ks];
-        }
-      };
-      // Second half: O^T += V^T P^T for the tile in ring slot `slot`, in two
-      // halves of head_dim; the second half's reads are issued before the
-      // first half's products.  LDS reads complete in order, so lgkmcnt(8)
-      // leaves only the second half outstanding.
-      auto back = [&](uint32_t slot, const u32x4 (&pb)[QS], u32x4 (&vf0)[4]) {
-        u32x4 vf1[4];
-        vread(slot, 1, vf1);
-        asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(vf0[0]), "+v"(vf0[1]), "+v"(vf0[2]), "+v"(vf0[3]) : : "memory");
-#pragma unroll
-        for (int qs = 0; qs < QS; ++qs)
+        for (int qs = H; qs < QS; ++qs) {
+          pb[qs] = u32x4{pw[qs - H][0], pw[qs - H][1], pw[qs - H][2], pw[qs - H][3]};
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) o[qs][jj] = T::mfma16x16x32(vf0[jj], pb[qs], o[qs][jj]);
-        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vf1[0]), "+v"(vf1[1]), "+v"(vf1[2]), "+v"(vf1[3]) : : "memory");
-#pragma unroll
-        for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) o[qs][4 + jj] = T::mfma16x16x32(vf1[jj], pb[qs], o[qs][4 + jj]);
-#pragma unroll
-        for (int qs = 0; qs < QS; ++qs) lsum[qs] = T::mfma16x16x32(ones, pb[qs], lsum[qs]);
+          lsum[qs] = T::mfma16x16x32(ones, pb[qs], lsum[qs]);
+        }
       };
       // Once per tile jt and wave, in tile order, in both loops below: wait
       // for this wave's copies of tile jt + 1 (younger: kAhead - 2 stream
