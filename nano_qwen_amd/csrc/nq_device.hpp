@@ -138,6 +138,45 @@ __device__ inline u32x4 buffer_load16_nt(__amdgpu_buffer_rsrc_t r, int voffset) 
 __device__ inline void dma16(const void *src, void *lds) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(lds), 16, 0, 0);
 }
+// The four words of the raw buffer descriptor make_rsrc builds (base, stride
+// 0, num_bytes, raw dword format), for inline assembly.
+__device__ inline u32x4 rsrc_words(const void *base, uint32_t num_bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32));
+  return u32x4{lo, hi & 0xffffu, static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(num_bytes)), 0x00020000u};
+}
+// Global -> LDS copy of 16 bytes per lane (buffer_load_dwordx4 ... lds) as an
+// opaque instruction: lane l's 16 bytes from descriptor `rsrc` at byte offset
+// `voff` land at LDS byte address lds_addr + 16 * l (lds_addr goes into M0).
+// The compiler does not know that the instruction writes LDS, so it never
+// drains the copies in flight before its own LDS reads; callers order them
+// with wait_vmcnt() and a workgroup barrier.  Completion counts in vmcnt.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ inline void dma16_opaque(uint32_t lds_addr, const u32x4 &rsrc, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "m0");
+}
+#pragma clang diagnostic pop
+// LDS reads the compiler schedules and waits for itself, at LDS byte address
+// `addr` + OFF (the constant folds into the instruction's offset).  Only for
+// LDS that no compiler-visible copy writes (the copies above are opaque).
+template <int OFF>
+__device__ inline u32x4 lds_load_b128(uint32_t addr) {
+  static_assert(OFF % 16 == 0 && OFF >= 0 && OFF < 65536, "ds offset");
+  const auto *p = reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(static_cast<uintptr_t>(addr));
+  return p[OFF / 16];
+}
+template <int OFF>
+__device__ inline u32x2 lds_load_tr16(uint32_t addr) {
+  static_assert(OFF % 8 == 0 && OFF >= 0 && OFF < 65536, "ds offset");
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  auto *p = reinterpret_cast<__attribute__((address_space(3))) s16x4 *>(static_cast<uintptr_t>(addr));
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(p + OFF / 8));
+}
 // s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
 template <int N>
 __device__ inline void wait_vmcnt() {

@@ -395,8 +395,7 @@ struct DTile {
 // Launch shape of the 16-bit kernel: NW waves per workgroup, each QS x 16
 // query rows of one head; WPE waves per SIMD (so WPE * 4 / NW resident
 // workgroups per CU); a ring of SLOTS K/V tiles, copies SLOTS - 1 ahead.
-// Two waves per SIMD: a wave owns at most 256 VGPRs, and the kernel keeps the
-// last one (v255) out of the compiler's hands for the work-queue fetch.
+// Two waves per SIMD: a wave owns at most 256 VGPRs.
 template <int NW_, int QS_, int WPE_, int SLOTS_>
 struct PShape {
   static constexpr int NW = NW_, QS = QS_, WPE = WPE_, SLOTS = SLOTS_, AHEAD = SLOTS_ - 1;
@@ -412,33 +411,6 @@ struct PShape {
 using ShapeA = PShape<8, 2, 2, 5>;  // one workgroup per CU, two 32-row waves per SIMD
 using ShapeC = PShape<4, 2, 2, 4>;  // two independent workgroups per CU, 32-row waves
 
-// Work-queue fetch the compiler does not track.  A compiled atomic's result
-// is waited for by the compiler as soon as it can no longer count the
-// operations issued after it -- here, across the tile loop -- with a wait for
-// every K/V copy in flight.  This one returns into v255, which the kernel's
-// register limit (255) keeps from the compiler, and is read back by
-// queue_fetch_result() once `younger` vector-memory operations of this wave
-// have followed it: vmcnt completes in issue order, so waiting until at most
-// `younger` (rounded down to a step) are outstanding covers the atomic.
-// Issue and read from the same single lane; one fetch in flight at a time.
-__device__ inline void queue_fetch_issue(uint32_t *ctr) {
-  asm volatile("global_atomic_add v255, %0, %1, off sc0" : : "v"(ctr), "v"(1u) : "memory", "v255");
-}
-__device__ inline uint32_t queue_fetch_result(int younger) {
-  uint32_t r;
-  if (younger >= 48)
-    asm volatile("s_waitcnt vmcnt(48)\n\tv_mov_b32 %0, v255" : "=v"(r) : : "memory", "v255");
-  else if (younger >= 32)
-    asm volatile("s_waitcnt vmcnt(32)\n\tv_mov_b32 %0, v255" : "=v"(r) : : "memory", "v255");
-  else if (younger >= 16)
-    asm volatile("s_waitcnt vmcnt(16)\n\tv_mov_b32 %0, v255" : "=v"(r) : : "memory", "v255");
-  else if (younger >= 8)
-    asm volatile("s_waitcnt vmcnt(8)\n\tv_mov_b32 %0, v255" : "=v"(r) : : "memory", "v255");
-  else
-    asm volatile("s_waitcnt vmcnt(0)\n\tv_mov_b32 %0, v255" : "=v"(r) : : "memory", "v255");
-  return r;
-}
-
 // A work item of the persistent kernel: query tile qt (S::ITEM_ROWS/G4 rows
 // of G4 heads) of kv-head slot y of sequence s, described by wave-uniform
 // scalars.  `live` is false past the end of the queue and for query tiles
@@ -449,13 +421,24 @@ struct Item {
 };
 
 // Item fields of query tile qt of kv-head slot y of sequence s.
+// floor(n / d) for 0 <= n < 2^22 and 1 <= d < 2^22 without the integer
+// division sequence: the float estimate n * (1/d) is within one of the
+// quotient (relative error below 2^-22), and one step each way corrects it.
+__device__ __forceinline__ int small_div(int n, int d) {
+  int q = static_cast<int>(static_cast<float>(n) * __builtin_amdgcn_rcpf(static_cast<float>(d)));
+  if (q * d > n)
+    --q;
+  else if ((q + 1) * d <= n)
+    ++q;
+  return q;
+}
 __device__ __forceinline__ Item fill_item(const PrefillArgs &a, int s, int y, int qt, int rows, int q0, int Lq, int k0,
                                           int Lk) {
   Item it{};
   it.live = false;
   it.s = s;
-  it.kvh = y / a.quads;
-  it.head0 = it.kvh * a.G + (y % a.quads) * 4;
+  it.kvh = small_div(y, a.quads);
+  it.head0 = it.kvh * a.G + (y - it.kvh * a.quads) * 4;
   it.q0 = q0;
   it.Lq = Lq;
   it.row_begin = qt * rows;
@@ -541,7 +524,11 @@ __device__ __forceinline__ Item describe_by_cost(const PrefillArgs &a, const Cos
   Item it{};
   it.live = false;
   if (idx >= n_items) return it;
-  const int lane = threadIdx.x & 63;
+  // The lane index from an instruction the compiler cannot hoist: addresses
+  // derived from it are recomputed per call instead of being kept (or
+  // spilled) across the tile loops.
+  int lane;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
   const int nl = a.n_levels;
   // Level: the lowest L whose start is <= idx (starts fall as L rises).
   const int step = (nl + 63) / 64;
@@ -579,8 +566,9 @@ __device__ __forceinline__ Item describe_by_cost(const PrefillArgs &a, const Cos
       const int s_it = base + ls;
       r -= __builtin_amdgcn_readlane(incl - cnt, ls);
       const int n_t = __builtin_amdgcn_readlane(nqt, ls);
-      const int qt = __builtin_amdgcn_readlane(qlo, ls) + r % n_t;
-      const int y = first_slot(cq, s_it) + cq.ystep * (r / n_t);
+      const int yi = small_div(r, n_t);
+      const int qt = __builtin_amdgcn_readlane(qlo, ls) + (r - yi * n_t);
+      const int y = first_slot(cq, s_it) + cq.ystep * yi;
       const int q0 = cq.cuq[s_it], k0 = cq.cuk[s_it];
       return fill_item(a, s_it, y, qt, cq.rows, q0, cq.cuq[s_it + 1] - q0, k0, cq.cuk[s_it + 1] - k0);
     }
@@ -633,7 +621,13 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   constexpr int COPS = CR / 4;       // 1 KiB loads per K (or V) per wave and entry
   constexpr int QOPS = QS * PT::NKK;        // Q loads per wave and item
   constexpr int SOPS = QS * (PT::NJ / 2);   // output stores per wave and item
-  constexpr int EOPS = QOPS + SOPS;
+  // Stores that write nothing, after the Q loads: the compiler counts them
+  // (it does not see the K/V copies), so one wait for at most kPad
+  // operations shows it -- as it holds on the hardware, where at least these
+  // kPad follow the Q loads -- that Q and the queue fetch before them are
+  // complete, without a wait for the copies in flight.
+  constexpr int kPad = 2 * COPS * kAhead;
+  constexpr int EOPS = QOPS + SOPS + kPad;
   static_assert(CR % 4 == 0, "a copy moves whole groups of 4 rows");
   static_assert(2 * COPS * kAhead + EOPS < 64, "vmcnt range");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -799,15 +793,13 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   };
   auto issue = [&]() {
     if (run_left == 0) next_run();
-    uint8_t *dst = smem + (st_dst - lds0) + wave * (CR * DT::ROWB);
-    const auto rk = make_rsrc(st_src, st_nrec);
-    const auto rv = make_rsrc(st_src + v_minus_k, st_nrec);
+    const uint32_t dst = st_dst + wave * (CR * DT::ROWB);
+    const u32x4 rk = rsrc_words(st_src, st_nrec);
+    const u32x4 rv = rsrc_words(st_src + v_minus_k, st_nrec);
 #pragma unroll
     for (int c = 0; c < COPS; ++c) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void *)(dst + 1024 * c), 16,
-                                               src_k[c], 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rv, (__attribute__((address_space(3))) void *)(dst + DT::TILE_B + 1024 * c), 16, src_v[c], 0, 0, 0);
+      dma16_opaque(dst + 1024 * c, rk, src_k[c]);
+      dma16_opaque(dst + DT::TILE_B + 1024 * c, rv, src_v[c]);
     }
     st_src += tile_bytes;
     st_dst = st_dst == lds_last ? lds0 : st_dst + DT::SLOT_B;
@@ -818,16 +810,23 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   // ------------------------------------------------------- operand offsets
   // K^T operand kk: key row m (row m + 16 is +16 rows), dims 32kk + 8g.. ;
   // V^T operand j: rows r0 and r0 + 16 (both swizzles ignore row bit 4).
-  int koff[PT::NKK], voff[PT::NJ];
-#pragma unroll
-  for (int kk = 0; kk < PT::NKK; ++kk) koff[kk] = m * DT::ROWB + (((4 * kk + g) ^ swz_k(m)) << 4);
+  // The byte offset of operand kk is m * ROWB + (((4kk + g) ^ swz_k(m)) << 4)
+  // = kbase_l + ((kk << 6) ^ kx_l), and that of operand j is
+  // r0 * ROWB + (((2j + (vq >> 1)) ^ swz_v(r0)) << 4) + 8 (vq & 1)
+  // = vbase_l + ((j << 5) ^ vx_l): the operand index only meets the swizzle's
+  // upper bits, so two registers per lane give every offset (one
+  // xor-and-add per read).  unhoist() keeps the compiler from turning them
+  // back into one loop-invariant register per operand.
+  const uint32_t kbase_l = m * DT::ROWB + ((g ^ (swz_k(m) & 3)) << 4);
+  uint32_t kx_l = (swz_k(m) & 12) << 4;
+  uint32_t vbase_l, vx_l;
   {
     const int vg = lane >> 4, vk = (lane >> 2) & 3, vq = lane & 3;
     const int r0 = 4 * vg + vk;
-#pragma unroll
-    for (int j = 0; j < PT::NJ; ++j) voff[j] = r0 * DT::ROWB + (((2 * j + (vq >> 1)) ^ swz_v(r0)) << 4) + (vq & 1) * 8;
+    vbase_l = r0 * DT::ROWB + (((vq >> 1) ^ (swz_v(r0) & 1)) << 4) + (vq & 1) * 8;
+    vx_l = (swz_v(r0) & 14) << 4;
   }
-  const u32x4 ones = u32x4{T::kOne2, T::kOne2, T::kOne2, T::kOne2};
+  auto unhoist = [&]() { asm volatile("" : "+v"(kx_l), "+v"(vx_l)); };
 
   // Q operands of an item for this wave: always QOPS loads, so the count the
   // waits add is fixed.  A row past the sequence (or of an item past the
@@ -848,10 +847,10 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   };
 
   f32x4 o[QS][PT::NJ];  // O^T accumulators of the item computed last
-  f32x4 lsum[QS];       // its row sums of P (every element)
+  float lsum[QS];       // its row sums of P: this lane's keys (the four lanes of a row add up at the store)
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) {
-    lsum[qs] = f32x4{0, 0, 0, 0};
+    lsum[qs] = 0.f;
 #pragma unroll
     for (int j = 0; j < PT::NJ; ++j) o[qs][j] = f32x4{0, 0, 0, 0};
   }
@@ -871,7 +870,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
     const auto ro = make_rsrc(obase, orange);
 #pragma unroll
     for (int qs = 0; qs < QS; ++qs) {
-      const float l = lsum[qs][0];  // every element holds the row sum of row m
+      const float l = sum32(sum16(lsum[qs]));  // the row sum of row m (lanes m, m + 16, m + 32, m + 48)
       const int row = wrow0 + 16 * qs + m;
       const float inv = l > 0.f ? 1.0f / l : 0.f;
       const uint32_t roff = row < it.Lq ? static_cast<uint32_t>(row * a.o_rs) : 0x7fffffffu;
@@ -915,16 +914,29 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   queue_copy(cur);
 
   for (int k = 0;; ++k) {
-    // The item's Q, loaded at one place only: Q is not carried around the
-    // loop, so the compiler never copies (and waits for) loaded registers.
-    load_q(cur);
+    // The previous item's output, then this item's Q -- loaded at one place
+    // only: Q is not carried around the loop, so the compiler never copies
+    // (and waits for) loaded registers; and the output registers are free
+    // before the Q registers fill.
     int epi_pos = -1;  // stream entries before this index precede the Q loads and stores just issued
     if (prev.live) {
       store_out(prev);
       epi_pos = st_pos;
     }
     if (idx_cur >= n_items) break;
-    int fetch_pos = st_pos;  // stream index at the fetch of item k + 2 (in flight during item k)
+    // Thread 0 fetches item k + 2.  The Q loads issued after it let the
+    // compiler's own wait for the result (at the end of the item) count
+    // them; the copies in flight then need not complete.
+    uint32_t fetched;
+    if (threadIdx.x == 0) fetched = atomicAdd(ctr, 1u);
+    load_q(cur);
+    asm volatile("" ::: "memory");  // the padding stays behind the Q loads
+    {
+      // Every store falls outside `none`; 64 bytes apart, they are not merged.
+      const auto none = make_rsrc(a.queue, 0);
+#pragma unroll
+      for (int i = 0; i < kPad; ++i) __builtin_amdgcn_raw_buffer_store_b32(0u, none, 64 * i, 0, 0);
+    }
     if (cur.live) {
       // Stream index of the item's first tile: already in the stream, or
       // started now (an item without tiles is never queued).
@@ -955,20 +967,14 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
       if (a.causal) n_plain = min(n_plain, max(0, wrow0 + P + 1) / kKeys);
       const int32_t *bt_row = paged ? a.block_tables + static_cast<int64_t>(cur.s) * a.bt_stride : nullptr;
 
-      auto kread = [&](uint32_t kt, u32x4 (&kf)[PT::NKK][2]) {  // kt: the tile's ring slot
+      // K^T operands of the tile in ring slot `kt` (its LDS address).
+      auto kread = [&](uint32_t kt, u32x4 (&kf)[PT::NKK][2]) {
 #pragma unroll
         for (int kk = 0; kk < PT::NKK; ++kk) {
-          kf[kk][0] = lds_read_b128_at<0>(kt + koff[kk]);
-          kf[kk][1] = lds_read_b128_at<16 * DT::ROWB>(kt + koff[kk]);
+          const uint32_t ka = ((kk << 6) ^ kx_l) + (kt + kbase_l);
+          kf[kk][0] = lds_load_b128<0>(ka);
+          kf[kk][1] = lds_load_b128<16 * DT::ROWB>(ka);
         }
-      };
-      auto kwait = [&](u32x4 (&kf)[PT::NKK][2]) {
-        static_assert(PT::NKK == 4, "operand list below");
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(kf[0][0]), "+v"(kf[0][1]), "+v"(kf[1][0]), "+v"(kf[1][1]), "+v"(kf[2][0]),
-                       "+v"(kf[2][1]), "+v"(kf[3][0]), "+v"(kf[3][1])
-                     :
-                     : "memory");
       };
       auto qk = [&](const u32x4 (&kf)[PT::NKK][2], f32x4 (&sc)[QS][2]) {
 #pragma unroll
@@ -982,66 +988,58 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
 #pragma unroll
             for (int qs = 0; qs < QS; ++qs) sc[qs][ks] = T::mfma16x16x32(kf[kk][ks], qf[qs][kk], sc[qs][ks]);
       };
-      // V^T operands of head_dim half h (dims 64h .. 64h+63) of the tile in
-      // ring slot `slot`: 8 opaque transposing reads.
-      auto vread = [&](uint32_t slot, int h, u32x4 (&vf)[4]) {
-        const uint32_t vt = slot + DT::TILE_B;
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const u32x2 lo = lds_read_tr16_at<0>(vt + voff[4 * h + jj]);
-          const u32x2 hi = lds_read_tr16_at<16 * DT::ROWB>(vt + voff[4 * h + jj]);
-          vf[jj] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-        }
-      };
 
       float m_use[QS];  // running row max, scaled (log2) domain
 #pragma unroll
       for (int qs = 0; qs < QS; ++qs) {
         m_use[qs] = kNegInf;
-        lsum[qs] = f32x4{0, 0, 0, 0};
+        lsum[qs] = 0.f;
 #pragma unroll
         for (int j = 0; j < PT::NJ; ++j) o[qs][j] = f32x4{0, 0, 0, 0};
       }
-      // Q is complete from here on: the compiler waits for it at this point
-      // (behind the prologue's copies at most), not before the QK products
-      // inside the tile loop, where its wait would also cover the K/V copies
-      // issued since.
+      // Q is complete from here on: at most kPad operations are younger than
+      // the Q loads' padding, which follows them.
+      wait_vmcnt<kPad>();
 #pragma unroll
       for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
         for (int kk = 0; kk < PT::NKK; ++kk) asm volatile("" : "+v"(qf[qs][kk]));
-      // The fetch goes after that wait, which would otherwise include it.
-      if (threadIdx.x == 0) queue_fetch_issue(ctr);
-      fetch_pos = st_pos;
-      f32x4 sc[QS][2];
+      f32x4 sc[QS][2];  // scores of the tile whose P is formed next
       if (wave_nkt > 0) {
         u32x4 kf[PT::NKK][2];
+        unhoist();
         kread(lds0 + (p0 % kSlots) * DT::SLOT_B, kf);
-        kwait(kf);
         qk(kf, sc);
       }
 
       // Scores of the tile whose P is being formed, and the subtrahend of its
       // exponents (the running maximum after the tile's rescale check).
       float xt[QS][8], mref[QS];
+      float alpha[QS];    // rescale factors of o before the pending products join it
+      bool pend = false;  // whether they differ from 1
       // One unit of P: elements 2t, 2t + 1 of rows block qs, exponentiated
-      // against the running maximum and packed to 16 bits.
+      // against the running maximum, added to the row sums and packed to 16
+      // bits.
       auto p_unit = [&](int qs, int t) {
         const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(xt[qs][2 * t], sl2, -mref[qs]));
         const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(xt[qs][2 * t + 1], sl2, -mref[qs]));
+        lsum[qs] += e0 + e1;
         return T::pack2(e0, e1);
       };
-      // First half of key tile jt (ring slot `slot`), right after the barrier
-      // that completes tile jt + 1: the lazy-rescale check of the current S
-      // (`sc`), the K reads and QK products of tile jt + 1 (into `sc` on
-      // return) and P of tile jt (into `pb`), with the next stream entry in
-      // between; vf0 gets the first half of tile jt's V^T operands.
-      auto front = [&](auto mask_tag, int jt, uint32_t slot, uint32_t slot_next, bool blk_ok, u32x4 (&pb)[QS],
-                       u32x4 (&vf0)[4]) {
+      // Lazy-rescale check of key tile jt (scores sc, masked as the tile
+      // needs): xt takes the scores, m_use the running maxima, mref the
+      // subtrahend of P.  The running maximum m_use of a row (the same in the
+      // four lanes that hold the row) only moves when some element exceeds it
+      // by more than kRescale, so P = 2^(s - m_use) <= 2^kRescale.  Each lane
+      // checks its own elements; the cross-lane row maximum is only formed
+      // when a maximum moves.  The row sums are rescaled at once; the
+      // function returns whether a maximum moved, and alpha then holds the
+      // factors for o, applied before this tile's products (formed with the
+      // new maxima) join it -- at the start of the next tile, once the
+      // previous tile's products are in.
+      auto check = [&](auto mask_tag, int jt, bool blk_ok, float (&alpha)[QS]) {
         constexpr bool MASK = decltype(mask_tag)::value;
         const int kbase = jt * kKeys;
-        u32x4 kf[PT::NKK][2];
-        kread(slot_next, kf);  // tile jt + 1 (discarded past the last)
         float mnew[QS];
         bool grow = false;
 #pragma unroll
@@ -1065,126 +1063,126 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
                               max3_raw(xt[qs][3], xt[qs][4], xt[qs][5]), vmax_raw(xt[qs][6], xt[qs][7])) * sl2;
           grow |= mnew[qs] > m_use[qs] + kRescale;
         }
-        // Lazy rescale: the running maximum m_use of a row (the same in the
-        // four lanes that hold the row) only moves when some element exceeds
-        // it by more than kRescale, so P = 2^(s - m_use) <= 2^kRescale.  Each
-        // lane checks its own elements; the cross-lane row maximum is only
-        // formed when a rescale happens.  Earlier tiles' P V are already in o.
+        bool moved = false;
         if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
           for (int qs = 0; qs < QS; ++qs) {
             const float m_new = fmaxf(m_use[qs], max32_raw(max16_raw(mnew[qs])));
-            const float alpha = (m_use[qs] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(m_use[qs] - m_new);
-            lsum[qs] *= alpha;
-#pragma unroll
-            for (int j = 0; j < PT::NJ; ++j) o[qs][j] *= alpha;
+            alpha[qs] = (m_use[qs] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(m_use[qs] - m_new);
+            lsum[qs] *= alpha[qs];  // the row sums of earlier tiles' P (this tile's join after this)
             m_use[qs] = m_new;
           }
+          moved = true;
         }
-        issue();
-        kwait(kf);
-        vread(slot, 0, vf0);  // first half of tile jt's V^T operands, waited for in back()
-        // The QK products of tile jt + 1 with P of the first QS / 2 row
-        // blocks of tile jt in between (one unit of P -- two exponentials and
-        // a pack -- per 4 products), so that the exponentials run while the
-        // matrix core works; back() does the other row blocks the same way
-        // beside its products.  Products that share an accumulator are 2 QS
-        // apart.
-        f32x4 sn[QS][2];
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) mref[qs] = (m_use[qs] == kNegInf) ? 0.f : m_use[qs];
+        return moved;
+      };
+      auto rescale = [&](const float (&alpha)[QS]) {
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+          for (int j = 0; j < PT::NJ; ++j) o[qs][j] *= alpha[qs];
+      };
+      // V^T operand j of the tile in ring slot `slot`: rows r0 and r0 + 16.
+      auto vread = [&](uint32_t slot, int j) {
+        const uint32_t vt = ((j << 5) ^ vx_l) + (slot + DT::TILE_B + vbase_l);
+        const u32x2 lo = lds_load_tr16<0>(vt), hi = lds_load_tr16<16 * DT::ROWB>(vt);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      };
+      // O^T += V^T P^T of the previous tile (operands vf, pb, read before the
+      // barrier), with P of this tile (units of xt) formed in between -- one
+      // unit, two exponentials and a pack, per two products -- so that the
+      // exponentials run while the matrix core works.  The K reads of tile
+      // jt + 1 (ring slot slot_next) are issued halfway.
+      auto pv_p = [&](const u32x4 (&vf)[PT::NJ], const u32x4 (&pb)[QS], uint32_t (&pw)[QS][4], uint32_t slot_next,
+                      u32x4 (&kf)[PT::NKK][2]) {
+        static_assert(PT::NJ * QS == 16, "two products per unit of P");
+        kread(slot_next, kf);
+#pragma unroll
+        for (int i = 0; i < PT::NJ * QS; ++i) {
+          const int j = i / QS, qs = i % QS;
+          o[qs][j] = T::mfma16x16x32(vf[j], pb[qs], o[qs][j]);
+          if (i % 2 == 1) {
+            const int u = i / 2;
+            pw[u / 4][u % 4] = p_unit(u / 4, u % 4);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4 * QS; ++u) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);  // transcendental
+          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+          if (u == 2 * QS - 1) __builtin_amdgcn_sched_group_barrier(0x100, 2 * PT::NKK, 0);  // DS read (K)
+        }
+      };
+      auto p_only = [&](uint32_t (&pw)[QS][4]) {
+#pragma unroll
+        for (int u = 0; u < 4 * QS; ++u) pw[u / 4][u % 4] = p_unit(u / 4, u % 4);
+      };
+      auto pv_only = [&](const u32x4 (&vf)[PT::NJ], const u32x4 (&pb)[QS]) {
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+          for (int j = 0; j < PT::NJ; ++j) o[qs][j] = T::mfma16x16x32(vf[j], pb[qs], o[qs][j]);
+      };
+      // QK products of tile jt + 1 (kf) into sn, with the V^T operands of
+      // tile jt (ring slot `slot`) read into vf in between: one transposing
+      // read per product.  Products that share an accumulator are 2 QS
+      // apart.
+      auto qk_v = [&](const u32x4 (&kf)[PT::NKK][2], f32x4 (&sn)[QS][2], uint32_t slot, u32x4 (&vf)[PT::NJ]) {
+        constexpr int NP = PT::NKK * 2 * QS;  // products
+        static_assert(NP == 2 * PT::NJ, "one V operand per two products");
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) sn[qs][ks] = f32x4{0, 0, 0, 0};
 #pragma unroll
-        for (int qs = 0; qs < QS; ++qs) mref[qs] = (m_use[qs] == kNegInf) ? 0.f : m_use[qs];
-        uint32_t pw[QS / 2][4];
-#pragma unroll
-        for (int i = 0; i < PT::NKK * 2 * QS; ++i) {
+        for (int i = 0; i < NP; ++i) {
           const int kk = i / (2 * QS), ks = (i / QS) % 2, qs = i % QS;
           sn[qs][ks] = T::mfma16x16x32(kf[kk][ks], qf[qs][kk], sn[qs][ks]);
-          if (i % 4 == 3) {
-            const int u = i / 4, uq = u / 4, t = u % 4;  // unit u: elements 2t, 2t + 1 of rows block uq
-            pw[uq][t] = p_unit(uq, t);
-          }
-        }
-        // Per unit: a product, the two scale-and-subtract steps, a product,
-        // the two exponentials, two products, the pack.
-#pragma unroll
-        for (int u = 0; u < 2 * QS; ++u) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);  // transcendental
-          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
+          if (i % 2 == 0) vf[i / 2] = vread(slot, i / 2);
         }
 #pragma unroll
-        for (int qs = 0; qs < QS / 2; ++qs) pb[qs] = u32x4{pw[qs][0], pw[qs][1], pw[qs][2], pw[qs][3]};
+        for (int i = 0; i < NP; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        }
+      };
+      // One key tile jt (ring slot `slot`; tile jt + 1 in slot_next), after
+      // the barrier that completes tile jt + 1: the pending rescale, the
+      // check of tile jt, the next stream entry, O += P V of tile jt - 1 (vf,
+      // pb; PV) with tile jt's P formed and tile jt + 1's K read in between,
+      // the QK products of tile jt + 1 with tile jt's V^T read in between.
+      // On return vf and pb hold tile jt's operands and sc tile jt + 1's
+      // scores.
+      auto tile = [&](auto pv_tag, auto mask_tag, int jt, uint32_t slot, uint32_t slot_next, bool blk_ok,
+                      u32x4 (&vf)[PT::NJ], u32x4 (&pb)[QS]) {
+        unhoist();
+        if (pend) rescale(alpha);  // tile jt - 1's maxima, before its products join o
+        pend = check(mask_tag, jt, blk_ok, alpha);
+        issue();
+        uint32_t pw[QS][4];
+        u32x4 kf[PT::NKK][2];  // tile jt + 1 (discarded past the last)
+        if constexpr (decltype(pv_tag)::value) {
+          pv_p(vf, pb, pw, slot_next, kf);
+        } else {
+          kread(slot_next, kf);
+          p_only(pw);
+        }
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) pb[qs] = u32x4{pw[qs][0], pw[qs][1], pw[qs][2], pw[qs][3]};
+        __builtin_amdgcn_sched_barrier(0);  // the two sections are scheduled apart
+        f32x4 sn[QS][2];
+        qk_v(kf, sn, slot, vf);
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = sn[qs][ks];
       };
-      // Second half: O^T += V^T P^T for the tile in ring slot `slot`, in two
-      // halves of head_dim (the second half's reads issued before the first
-      // half's products; LDS reads complete in order, so lgkmcnt(8) leaves
-      // only the second half outstanding).  The first QS / 2 row blocks'
-      // products go first, with P of the other row blocks computed between
-      // them (one unit per 2 products); then those blocks' products.
-      auto back = [&](uint32_t slot, u32x4 (&pb)[QS], u32x4 (&vf0)[4]) {
-        constexpr int H = QS / 2;
-        u32x4 vf1[4];
-        vread(slot, 1, vf1);
-        asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(vf0[0]), "+v"(vf0[1]), "+v"(vf0[2]), "+v"(vf0[3]) : : "memory");
-        uint32_t pw[QS - H][4];
-#pragma unroll
-        for (int i = 0; i < 4 * H; ++i) {
-          const int qs = i / 4, jj = i % 4;
-          o[qs][jj] = T::mfma16x16x32(vf0[jj], pb[qs], o[qs][jj]);
-          if (i % 2 == 1) {
-            const int u = i / 2, uq = u / 4, t = u % 4;  // units 0 .. 2H - 1 of the upper blocks
-            pw[uq][t] = p_unit(H + uq, t);
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 2 * H; ++u) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);  // transcendental
-          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vf1[0]), "+v"(vf1[1]), "+v"(vf1[2]), "+v"(vf1[3]) : : "memory");
-#pragma unroll
-        for (int i = 0; i < 4 * H; ++i) {
-          const int qs = i / 4, jj = i % 4;
-          o[qs][4 + jj] = T::mfma16x16x32(vf1[jj], pb[qs], o[qs][4 + jj]);
-          if (i % 2 == 1) {
-            const int u = 2 * H + i / 2, uq = u / 4, t = u % 4;  // units 2H .. 4H - 1 of the upper blocks
-            pw[uq][t] = p_unit(H + uq, t);
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 2 * H; ++u) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);  // transcendental
-          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
-        }
-#pragma unroll
-        for (int qs = 0; qs < H; ++qs) lsum[qs] = T::mfma16x16x32(ones, pb[qs], lsum[qs]);
-#pragma unroll
-        for (int qs = H; qs < QS; ++qs) {
-          pb[qs] = u32x4{pw[qs - H][0], pw[qs - H][1], pw[qs - H][2], pw[qs - H][3]};
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) o[qs][jj] = T::mfma16x16x32(vf0[jj], pb[qs], o[qs][jj]);
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) o[qs][4 + jj] = T::mfma16x16x32(vf1[jj], pb[qs], o[qs][4 + jj]);
-          lsum[qs] = T::mfma16x16x32(ones, pb[qs], lsum[qs]);
-        }
-      };
-      // Once per tile jt and wave, in tile order, in both loops below: wait
+      // Once per tile jt and wave, in tile order, in every loop below: wait
       // for this wave's copies of tile jt + 1 (younger: kAhead - 2 stream
       // entries, plus the Q loads and stores of the item's start if tile
       // jt + 1 preceded them).
@@ -1194,7 +1192,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
           wait_vmcnt<2 * COPS * (kAhead - 2) + EOPS>();
         else
           wait_vmcnt<2 * COPS * (kAhead - 2)>();
-        wait_lgkmcnt0();  // and its reads of tile jt - 1 are done
+        wait_lgkmcnt0();  // and its reads of tiles jt - 1 and jt are done
         raw_barrier();    // tile jt + 1 complete; slot of tile jt - 1 free
       };
       // Whether the block of key tile jt exists (the masked loop once a
@@ -1207,30 +1205,51 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
       // Ring slots (LDS addresses) of tiles jt and jt + 1.
       uint32_t slot = lds0 + (p0 % kSlots) * DT::SLOT_B;
       uint32_t slot_next = slot == lds_last ? lds0 : slot + DT::SLOT_B;
-      int jt = 0;
-      plain_end = bad_seen ? 0 : n_plain;
-      for (; jt < plain_end; ++jt) {
-        sync(jt);
-        u32x4 pb[QS], vf0[4];
-        front(std::false_type{}, jt, slot, slot_next, true, pb, vf0);
-        back(slot, pb, vf0);
+      auto advance = [&]() {
         slot = slot_next;
         slot_next = slot_next == lds_last ? lds0 : slot_next + DT::SLOT_B;
+      };
+      u32x4 vf[PT::NJ], pb[QS];  // V^T operands and P of the tile whose products are pending
+      int jt = 0;
+      plain_end = bad_seen ? 0 : n_plain;
+      if (n_kt > 0) {  // tile 0: no earlier tile's products
+        sync(0);
+        if (wave_nkt > 0) {
+          if (plain_end > 0)
+            tile(std::false_type{}, std::false_type{}, 0, slot, slot_next, true, vf, pb);
+          else
+            tile(std::false_type{}, std::true_type{}, 0, slot, slot_next, !bad_seen || !paged || block_ok(0), vf, pb);
+        } else {
+          issue();
+        }
+        advance();
+        jt = 1;
+      }
+      for (; jt < plain_end; ++jt) {
+        sync(jt);
+        tile(std::true_type{}, std::false_type{}, jt, slot, slot_next, true, vf, pb);
+        advance();
       }
       for (; jt < n_kt; ++jt) {
         sync(jt);
         if (jt < wave_nkt) {
-          u32x4 pb[QS], vf0[4];
-          front(std::true_type{}, jt, slot, slot_next, !bad_seen || !paged || block_ok(jt), pb, vf0);
-          back(slot, pb, vf0);
+          tile(std::true_type{}, std::true_type{}, jt, slot, slot_next, !bad_seen || !paged || block_ok(jt), vf, pb);
         } else {
           issue();
+          if (jt == wave_nkt) {  // the wave's last tile
+            unhoist();
+            if (pend) rescale(alpha);
+            pv_only(vf, pb);
+          }
         }
-        slot = slot_next;
-        slot_next = slot_next == lds_last ? lds0 : slot_next + DT::SLOT_B;
+        advance();
+      }
+      if (n_kt > 0 && wave_nkt == n_kt) {  // the item's last tile
+        unhoist();
+        if (pend) rescale(alpha);
+        pv_only(vf, pb);
       }
     } else {
-      if (threadIdx.x == 0) queue_fetch_issue(ctr);
       queue_copy(nxt);
     }
     // Next item: publish the fetched index (slot k + 2 of 4: a wave still
@@ -1238,8 +1257,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
     // barrier that follows its read).  A plain barrier: the fence of
     // __syncthreads() would wait for the K/V copies in flight.
     if (threadIdx.x == 0) {
-      // Operations issued since the fetch: the stream's copies.
-      lds_item[(k + 2) & 3] = static_cast<int>(queue_fetch_result(2 * COPS * (st_pos - fetch_pos)));
+      lds_item[(k + 2) & 3] = static_cast<int>(fetched);
       wait_lgkmcnt0();
     }
     raw_barrier();
@@ -1263,7 +1281,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
 // The body lives in a device function: its inline assembly uses register
 // constraints that only the device compilation accepts.
 template <class T, int D, class S>
-__global__ __launch_bounds__(64 * S::NW) __attribute__((amdgpu_waves_per_eu(S::WPE), amdgpu_num_vgpr(255)))
+__global__ __launch_bounds__(64 * S::NW) __attribute__((amdgpu_waves_per_eu(S::WPE)))
 void varlen_prefill_dma_kernel(const PrefillArgs a) {
   prefill_persistent<T, D, S>(a);
 }

@@ -19,10 +19,10 @@ mirrored in the other.  For every workgroup of a launch it checks:
 - every `s_waitcnt vmcnt(N)` the kernel issues is safe (at least N of the
   wave's memory operations are younger than the awaited copies) and tight
   (exactly N) -- in the waves that only copy, load and store, and safe in
-  wave 0, whose work-queue fetch (an atomic the compiler does not track) is
-  one more operation;
-- the wait before the fetched index is read counts no more operations after
-  the fetch than the wave issued.
+  wave 0, whose work-queue fetch (an atomic) is one more operation;
+- the wait for Q (vmcnt(PAD) after the prologue) leaves only the padding
+  stores and later operations outstanding, so the Q loads and the fetch
+  before them are complete.
 
 Sizes follow the launch shapes built for 16-bit K/V (waves per workgroup,
 16-row blocks per wave, ring slots).
@@ -64,8 +64,12 @@ class Shape:
         return self.QS * NJ // 2
 
     @property
+    def PAD(self):  # stores that write nothing, after the Q loads
+        return 2 * self.COPS * self.AHEAD
+
+    @property
     def EOPS(self):
-        return self.QOPS + self.SOPS
+        return self.QOPS + self.SOPS + self.PAD
 
 
 SHAPES = {"a": Shape(8, 2, 5, 1), "c": Shape(4, 2, 4, 2)}
@@ -320,16 +324,17 @@ class Workgroup:
         if self.wave0:
             self.ops.append(("a",))
             self.fetch_at = len(self.ops) - 1
-        self.fetch_pos = self.pos
 
-    def fetch_result(self, younger):
-        """queue_fetch_result(younger): waits until at most younger
-        operations (rounded down to a step) are outstanding."""
+    def wait_q(self):
+        """wait_vmcnt<PAD> after the prologue barrier: at most PAD operations
+        outstanding, so everything before the padding -- the Q loads and the
+        fetch -- is complete."""
+        n = self.S.PAD
+        last_q = max(i for i, op in enumerate(self.ops) if op[0] == "q")
+        assert all(op[0] == "p" for op in self.ops[last_q + 1:last_q + 1 + n]), "padding follows the Q loads"
+        assert len(self.ops) - 1 - last_q >= n, "fewer than PAD operations after the Q loads"
         if self.wave0:
-            after = len(self.ops) - 1 - self.fetch_at
-            assert younger <= after, f"fetch read after {younger} operations, only {after} issued"
-            step = max(t for t in (0, 8, 16, 32, 48) if t <= younger)
-            assert step < 64
+            assert self.fetch_at < last_q, "the fetch precedes the Q loads"
 
     def read(self, p, item, jt):
         assert p <= self.landed, f"stream entry {p} read before its copies completed"
@@ -347,13 +352,15 @@ class Workgroup:
         self.queue_copy(cur)
         items = 0
         while True:
-            self.ops += [("q",)] * S.QOPS  # this item's Q
             epi_pos = -1
             if prev is not None:  # the previous item's output
                 self.ops += [("s",)] * S.SOPS
                 epi_pos = self.pos
             if idx_cur >= self.n_items:
                 break
+            self.fetch()
+            self.ops += [("q",)] * S.QOPS  # this item's Q
+            self.ops += [("p",)] * S.PAD  # padding
             if cur is not None:
                 items += 1
                 p0 = self.pos
@@ -367,21 +374,19 @@ class Workgroup:
                 assert self.pos == p0 + S.AHEAD
                 n_kt = cur["n_kt"]
                 self.wait(p0, 2 * S.COPS * (S.AHEAD - 1) + (S.EOPS if p0 < epi_pos else 0))
-                self.fetch()  # after the Q wait of the prologue
+                self.wait_q()
                 if n_kt > 0:
                     self.read(p0, idx_cur, 0)  # K of tile 0
                 for jt in range(n_kt):
                     assert self.pos == p0 + S.AHEAD + jt
                     t = p0 + jt + 1
                     self.wait(t, 2 * S.COPS * (S.AHEAD - 2) + (S.EOPS if t < epi_pos else 0))
+                    self.issue()
                     if jt + 1 < n_kt:
                         self.read(t, idx_cur, jt + 1)  # K of the next tile
-                    self.issue()
                     self.read(p0 + jt, idx_cur, jt)  # V of this tile
             else:
-                self.fetch()
                 self.queue_copy(nxt)
-            self.fetch_result(2 * S.COPS * (self.pos - self.fetch_pos))
             self.barrier()  # end of item
             idx_new = idx[nxt_fetch]
             nxt_fetch += 1
