@@ -10,7 +10,9 @@ between two independent KV pools (each larger than the 256 MB MALL), so no
 step re-reads KV the previous step left in the Infinity Cache.
 
 The headline (``value``) is cfg2's algorithmic HBM bandwidth in GB/s; cfg3's
-TFLOP/s and the other decode configurations are reported under ``extra``.
+TFLOP/s and the other decode configurations are reported under ``extra``, as
+is the fused q/k norm + rotary + KV store call over cfg3's and cfg2's new
+tokens (``cfg3_norm_rope``, ``cfg2_norm_rope``: HBM GB/s).
 ``roofline`` covers the dominant kernel of the headline workload (paged
 decode: main kernel + split-K merge), timed with HIP events on the stream
 the kernels run on.  ``cpu_baseline`` times the CPU restatement of the path
@@ -123,6 +125,40 @@ def bench_prefill(name, steps, warmup, seed=0):
                 attn_tflops=fl / (ms_attn * 1e-3) / 1e12, mfma_frac=fl / (ms_attn * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
                 flops=fl, tokens_per_s=sum(case["lq"]) / (ms * 1e-3), total_q=sum(case["lq"]),
                 gbs=prefill_bytes(case) / (ms * 1e-3) / 1e9), case
+
+
+def bench_norm_rope(name, steps, warmup, seed=0):
+    """The fused q/k norm + rotary + KV store call over the new tokens of a
+    configuration (Qwen3.5 partial rotary factor 0.25: R = 32 of D = 128).
+    The timed loop calls the C ABI directly with the checked arguments."""
+    import torch
+    from nano_qwen_amd import kernels
+    from nano_qwen_amd._lib import lib
+    from oracle.inputs import make_norm_rope_case, norm_rope_bytes
+
+    c = make_norm_rope_case(name, seed=seed, device="cuda")
+    d = c["d"]
+    q_out = torch.empty(c["n"], c["hq"], d, dtype=c["key"].dtype, device="cuda")
+    k_out = torch.empty_like(c["key"])
+    args = kernels.qk_norm_rope_store(
+        c["positions"], c["q_gate"][..., :d], c["key"], c["value"], c["q_weight"], c["k_weight"], c["eps"],
+        c["cos_sin_cache"], c["rotary_dim"], k_cache=c["k_cache"], v_cache=c["v_cache"],
+        slot_mapping=c["slot_mapping"], k_scale=c["k_scale"], v_scale=c["v_scale"], q_out=q_out, k_out=k_out,
+        _return_args=True)
+    fn = lib().nq_qk_norm_rope_store
+
+    def step(i):
+        rc = fn(*args)
+        if rc:
+            raise RuntimeError(f"qk_norm_rope_store failed ({rc})")
+
+    # A call lasts under 0.1 ms: warm up for about 20 ms so the clocks have
+    # ramped before the timed steps.
+    ms = _events_time(step, steps, max(warmup, 200))
+    nb = norm_rope_bytes(c)
+    return dict(ms_per_step=ms, gbs=nb / (ms * 1e-3) / 1e9, hbm_frac=nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                bytes=nb, tokens=c["n"], rotary_dim=c["rotary_dim"],
+                tokens_per_s=c["n"] / (ms * 1e-3)), c
 
 
 def cpu_baseline_decode(case, n_seqs=8, reps=5):
@@ -244,7 +280,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default=None, help="run one config (cfg2|cfg3|cfg4|cfg5)")
+    ap.add_argument("--only", default=None,
+                    help="run one config (cfg2|cfg3|cfg4|cfg5|cfg3_norm_rope|cfg2_norm_rope)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration)")
     args = ap.parse_args()
@@ -264,11 +301,13 @@ def main():
 
     extra = {}
     head = None
-    todo = [args.only] if args.only else ["cfg2", "cfg3", "cfg4", "cfg5"]
+    todo = [args.only] if args.only else ["cfg2", "cfg3", "cfg4", "cfg5", "cfg3_norm_rope", "cfg2_norm_rope"]
     cpu = None
     for name in todo:
         print(f"[bench] {name} ...", file=sys.stderr, flush=True)
-        if name == "cfg3":
+        if name.endswith("_norm_rope"):
+            r, case = bench_norm_rope(name.split("_")[0], args.steps, args.warmup)
+        elif name == "cfg3":
             r, case = bench_prefill(name, args.steps, args.warmup)
             if not args.no_cpu:
                 r["cpu_baseline"] = cpu_baseline_prefill(case)

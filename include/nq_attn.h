@@ -168,6 +168,53 @@ int nq_prepare_decode(const int64_t *sampled_token_ids, const int64_t *batch_slo
                       int32_t *context_lens, int32_t *slot_mapping,
                       int num_seqs, int block_size, void *stream);
 
+/*
+ * Fused q/k Gemma RMS norm + partial rotary embedding + KV-cache store.
+ * Replaces, in Qwen3_5Attention.forward (models/qwen3_5.py:135-137), the
+ * calls q_norm(query), k_norm(key) (GemmaRMSNorm, layers/layernorm.py:81-91)
+ * and rotary_emb(positions, query, key) (InterleavedMRoPE,
+ * layers/rotary_embedding.py:104-123), plus the store that Attention.forward
+ * then makes (layers/attention.py:62-63).
+ *
+ * q [num_tokens, num_q_heads, head_dim] with strides (q_row_stride,
+ * q_head_stride, 1) -- e.g. the query half of q_proj's [N, Hq, 2*D] output;
+ * k and v [num_tokens, num_kv_heads, head_dim] with row strides and head
+ * stride head_dim.  dtype (F32/F16/BF16) is the type of q, k, v, both
+ * weights [head_dim] and both outputs.  For each row x of a head:
+ *   y = rnd(rnd(x / sqrt(mean(x^2) + eps)) * (w + weight_offset))
+ * (fp32 arithmetic, rnd = round to dtype; weight_offset is 1.0 for the
+ * Gemma norm), then the first rotary_dim dims rotate by the table row
+ * cos_sin_cache[positions[i]] (float32 [max_position, rotary_dim]: the
+ * rotary_dim/2 cosines, then the sines):
+ *   e <  R/2: z[e] = rnd(y[e]*cos[e] - y[e+R/2]*sin[e])
+ *   e >= R/2: z[e] = rnd(y[e]*cos[e-R/2] + y[e-R/2]*sin[e-R/2])
+ * rotary_dim is a multiple of 16 in [0, head_dim]; head_dim is 64, 128 or
+ * 256; positions are int64, and a position outside [0, max_position) gives a
+ * NaN row.  q_out (strides q_out_row_stride, q_out_head_stride, 1) receives
+ * the rotated q; k_out (row stride k_out_row_stride, may be NULL) the rotated
+ * k.  Outputs may alias their inputs with equal strides (in place).
+ * k_cache/v_cache == NULL: no store (the reference skips it while the caches
+ * are empty).  Otherwise the rotated k row and the v row of token i go to
+ * cache row slot_mapping[i] exactly as nq_store_kvcache stores them
+ * (cache_dtype == dtype, or NQ_FP8_E4M3 with k_scale/v_scale); slots outside
+ * [0, num_slots) are skipped.  Every pointer and stride must be 16-byte
+ * aligned.
+ */
+int nq_qk_norm_rope_store(const void *q, int64_t q_row_stride, int64_t q_head_stride,
+                          const void *k, int64_t k_row_stride,
+                          const void *v, int64_t v_row_stride,
+                          const int64_t *positions, const float *cos_sin_cache,
+                          int64_t max_position, int rotary_dim,
+                          const void *q_weight, const void *k_weight,
+                          float eps, float weight_offset,
+                          void *q_out, int64_t q_out_row_stride, int64_t q_out_head_stride,
+                          void *k_out, int64_t k_out_row_stride,
+                          void *k_cache, void *v_cache, const int32_t *slot_mapping,
+                          int64_t num_slots, int64_t num_tokens,
+                          int num_q_heads, int num_kv_heads, int head_dim,
+                          int dtype, int cache_dtype,
+                          const float *k_scale, const float *v_scale, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,6 +74,22 @@ struct F16 {
   }
 };
 
+// ---------------------------------------------------------------- fp8 e4m3fn
+// Saturate to +-448 keeping NaN (comparisons with NaN are false).
+__device__ inline float sat448(float y) {
+  y = y > 448.f ? 448.f : y;
+  y = y < -448.f ? -448.f : y;
+  return y;
+}
+// Four values -> four e4m3fn bytes (saturating, round to nearest even), the
+// first value in the lowest byte.
+__device__ inline uint32_t fp8x4(float a, float b, float c, float d) {
+  int w = 0;
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(a), sat448(b), w, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(c), sat448(d), w, true);
+  return static_cast<uint32_t>(w);
+}
+
 // ---------------------------------------------------------------- memory
 template <typename T>
 __device__ inline T ldg(const T *p) {

@@ -45,13 +45,6 @@ __global__ __launch_bounds__(kThreads) void store_copy_kernel(
   }
 }
 
-// Saturate to +-448 keeping NaN (comparisons with NaN are false).
-__device__ inline float sat448(float y) {
-  y = y > 448.f ? 448.f : y;
-  y = y < -448.f ? -448.f : y;
-  return y;
-}
-
 // fp8 quantizing store: each thread produces 16 output bytes (16 elements,
 // all of one kv head because head_dim % 16 == 0).  IN: 0 f32, 1 f16, 2 bf16.
 template <int IN>
@@ -103,12 +96,8 @@ __global__ __launch_bounds__(kThreads) void store_fp8_kernel(
     }
     u32x4 out;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      int w = 0;
-      w = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(x[4 * t] * inv), sat448(x[4 * t + 1] * inv), w, false);
-      w = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(x[4 * t + 2] * inv), sat448(x[4 * t + 3] * inv), w, true);
-      out[t] = static_cast<uint32_t>(w);
-    }
+    for (int t = 0; t < 4; ++t)
+      out[t] = fp8x4(x[4 * t] * inv, x[4 * t + 1] * inv, x[4 * t + 2] * inv, x[4 * t + 3] * inv);
     uint8_t *dst = (is_v ? v_cache : k_cache) + static_cast<int64_t>(slot) * row_elems + e0;
     store16(dst, out);
   }

@@ -9,6 +9,7 @@ and meanings follow the calls the reference makes:
 * ``varlen_prefill``  -- flash_attn_varlen_func at layers/attention.py:67-70
 * ``paged_decode``    -- flash_attn_with_kvcache at layers/attention.py:72-74
 * ``prepare_decode``  -- engine/decode_init.py:39-65
+* ``qk_norm_rope_store`` -- models/qwen3_5.py:135-137 + layers/attention.py:63
 """
 from __future__ import annotations
 
@@ -183,5 +184,73 @@ def prepare_decode(sampled_token_ids, batch_slots, seq_lens, last_block_ids, inp
     check(rc, "prepare_decode")
 
 
-__all__ = ["store_kvcache", "paged_decode", "varlen_prefill", "prepare_decode", "decode_plan",
+def qk_norm_rope_store(positions, query, key, value, q_weight, k_weight, eps, cos_sin_cache, rotary_dim,
+                       k_cache=None, v_cache=None, slot_mapping=None, k_scale=None, v_scale=None,
+                       weight_offset=1.0, q_out=None, k_out=None, _return_args=False):
+    """Gemma RMS norm of ``query [N, Hq, D]`` / ``key [N, Hkv, D]``, rotary
+    embedding of their first ``rotary_dim`` dims, and the KV store.
+
+    One launch replacing ``q_norm``, ``k_norm`` and ``rotary_emb`` of
+    models/qwen3_5.py:135-137 plus ``store_kvcache`` of layers/attention.py:63.
+    ``query`` may be a strided view (the query half of ``q_proj``'s output).
+    ``cos_sin_cache`` is the float32 table ``[max_position, (1,) rotary_dim]``
+    (cosines, then sines); ``positions`` int64 ``[N]``.  Returns
+    ``(q_out, k_out)``, new contiguous tensors unless given (passing the
+    inputs rotates in place).  Without caches nothing is stored.
+    ``_return_args`` returns the checked C-ABI argument tuple instead of
+    launching (for timing loops that call the library directly).
+    """
+    require_cuda(positions, query, key, value, q_weight, k_weight, cos_sin_cache, k_cache, v_cache,
+                 slot_mapping, what="qk_norm_rope_store")
+    n, hq, d = query.shape
+    n2, hkv, d2 = key.shape
+    if n2 != n or d2 != d or query.stride(-1) != 1 or key.stride(-1) != 1 or key.stride(1) != d:
+        raise RuntimeError("qk_norm_rope_store: query [N, Hq, D] and key [N, Hkv, D] with contiguous heads")
+    if key.dtype != query.dtype or q_weight.dtype != query.dtype or k_weight.dtype != query.dtype:
+        raise RuntimeError("qk_norm_rope_store: query, key and both weights must share one dtype")
+    if q_weight.numel() != d or k_weight.numel() != d or not (q_weight.is_contiguous() and k_weight.is_contiguous()):
+        raise RuntimeError("qk_norm_rope_store: weights must be contiguous [head_dim]")
+    if positions.dtype != torch.int64 or positions.numel() != n:
+        raise RuntimeError("qk_norm_rope_store: positions must be int64 [N]")
+    if cos_sin_cache.dtype != torch.float32 or not cos_sin_cache.is_contiguous():
+        raise RuntimeError("qk_norm_rope_store: cos_sin_cache must be contiguous float32")
+    max_pos = cos_sin_cache.shape[0]
+    if cos_sin_cache.numel() != max_pos * rotary_dim:
+        raise RuntimeError("qk_norm_rope_store: cos_sin_cache must be [max_position, rotary_dim]")
+    store = k_cache is not None and k_cache.numel() > 0 and v_cache is not None and v_cache.numel() > 0
+    fp8 = store and k_cache.dtype == torch.float8_e4m3fn
+    if store:
+        if value is None or value.shape != key.shape or value.stride(-1) != 1 or value.stride(1) != d:
+            raise RuntimeError("qk_norm_rope_store: value must be [N, Hkv, D] with contiguous heads")
+        if slot_mapping is None or slot_mapping.dtype != torch.int32 or slot_mapping.numel() != n:
+            raise RuntimeError("qk_norm_rope_store: slot_mapping must be int32 [N]")
+        if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+            raise RuntimeError("qk_norm_rope_store: caches must be contiguous")
+        if fp8 and (k_scale is None or v_scale is None):
+            raise RuntimeError("qk_norm_rope_store: an fp8 cache needs k_scale and v_scale")
+        if not fp8 and k_cache.dtype != key.dtype:
+            raise RuntimeError(f"qk_norm_rope_store: cache dtype {k_cache.dtype} != key dtype {key.dtype}")
+    if q_out is None:
+        q_out = torch.empty(n, hq, d, dtype=query.dtype, device=query.device)
+    if k_out is None:
+        k_out = torch.empty(n, hkv, d, dtype=key.dtype, device=key.device)
+    if q_out.shape != query.shape or k_out.shape != key.shape or q_out.stride(-1) != 1 or k_out.stride(1) != d:
+        raise RuntimeError("qk_norm_rope_store: q_out/k_out shapes must match query/key")
+    num_slots = k_cache.numel() // (hkv * d) if store else 0
+    args = (
+        ptr(query), query.stride(0), query.stride(1), ptr(key), key.stride(0),
+        ptr(value) if store else None, value.stride(0) if store else 0, ptr(positions), ptr(cos_sin_cache),
+        max_pos, int(rotary_dim), ptr(q_weight), ptr(k_weight), float(eps), float(weight_offset),
+        ptr(q_out), q_out.stride(0), q_out.stride(1), ptr(k_out), k_out.stride(0),
+        ptr(k_cache) if store else None, ptr(v_cache) if store else None,
+        ptr(slot_mapping) if store else None, num_slots, n, hq, hkv, d, dtype_code(query.dtype),
+        dtype_code(k_cache.dtype) if store else dtype_code(query.dtype),
+        ptr(k_scale) if fp8 else None, ptr(v_scale) if fp8 else None, stream_of(query))
+    if _return_args:
+        return args
+    check(lib().nq_qk_norm_rope_store(*args), "qk_norm_rope_store")
+    return q_out, k_out
+
+
+__all__ = ["store_kvcache", "paged_decode", "varlen_prefill", "prepare_decode", "decode_plan", "qk_norm_rope_store",
            "decode_workspace", "prefill_workspace", "_lib"]

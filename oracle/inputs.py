@@ -230,3 +230,47 @@ def prefill_bytes(case):
     act = case["q"].element_size()
     kv_item = case["k_cache"].element_size()
     return 2 * tq * hq * d * act + 2 * tk * hkv * d * kv_item + 2 * tq * hkv * d * (act + kv_item)
+
+
+def make_norm_rope_case(name="cfg3", seed=0, device="cpu", rotary_dim=32, max_position=32768):
+    """Inputs of the fused q/k norm + rotary + KV store step for the new tokens
+    of a prefill (cfg3) or decode (cfg2/cfg4/cfg5) configuration.
+
+    The token set, positions (prefix + 0..Lq-1 per prefill sequence; ctx - 1
+    per decode sequence), slots and caches are those of the configuration;
+    ``q_gate [N, Hq, 2D]`` stands for ``q_proj``'s output (query | gate per
+    head, models/qwen3_5.py:125-126).  Norm weights are U(-1, 1) (Gemma
+    weights are centred on 0, layers/layernorm.py docstring) and the table is
+    the rope cache of ``rotary_dim`` dims, base 1e7.
+    """
+    from .qk_norm_rope import rope_cache
+    kind = CONFIGS[name]["kind"]
+    base = (make_prefill_case if kind == "prefill" else make_decode_case)(name, seed=seed, device=device)
+    if kind == "prefill":
+        pos = [p + i for p, lq in zip(base["prefix"], base["lq"]) for i in range(lq)]
+    else:
+        pos = (base["context_lens"].to("cpu").to(torch.int64) - 1).tolist()
+    n, hq, hkv, d = len(pos), base["hq"], base["hkv"], base["d"]
+    act, amp = CONFIGS[name]["dtype"], CONFIGS[name]["amp"]
+    g = torch.Generator(device=device).manual_seed(seed + 2)
+    cpu = torch.Generator().manual_seed(seed + 3)
+    return dict(name=name, hq=hq, hkv=hkv, d=d, rotary_dim=rotary_dim, n=n,
+                q_gate=_randn((n, hq, 2 * d), g, device, amp, act),
+                key=base["k_new"], value=base["v_new"],
+                q_weight=(torch.rand(d, generator=cpu) * 2 - 1).to(act).to(device),
+                k_weight=(torch.rand(d, generator=cpu) * 2 - 1).to(act).to(device),
+                positions=torch.tensor(pos, dtype=torch.int64, device=device),
+                cos_sin_cache=torch.from_numpy(rope_cache(rotary_dim, max_position, 1e7)).to(device),
+                k_cache=base["k_cache"], v_cache=base["v_cache"], slot_mapping=base["slot_mapping"],
+                k_scale=base["k_scale"], v_scale=base["v_scale"], eps=1e-6)
+
+
+def norm_rope_bytes(case):
+    """Algorithmic HBM bytes of one fused norm + rotary + store call: q, k, v
+    read once; q_out, k_out and the two cache rows written once; each token's
+    position, slot and table row; both weights."""
+    n, hq, hkv, d, r = case["n"], case["hq"], case["hkv"], case["d"], case["rotary_dim"]
+    es = case["key"].element_size()
+    ces = case["k_cache"].element_size()
+    per_tok = (hq * d + 2 * hkv * d) * es + (hq * d + hkv * d) * es + 2 * hkv * d * ces + 8 + 4 + 4 * r
+    return n * per_tok + 2 * d * es
