@@ -1,3 +1,4 @@
 from .attention import Attention, store_kvcache
+from .qk_norm_rope import qk_norm_rope_store
 
-__all__ = ["Attention", "store_kvcache"]
+__all__ = ["Attention", "store_kvcache", "qk_norm_rope_store"]

@@ -42,11 +42,16 @@ class Attention(nn.Module):
         self.k_cache = self.v_cache = torch.tensor([])
         self.k_scale = self.v_scale = None
 
-    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
-        """layers/attention.py:59-75: store, then prefill or paged decode."""
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_stored: bool = False):
+        """layers/attention.py:59-75: store, then prefill or paged decode.
+
+        ``kv_stored=True`` skips the store because the caller already made it
+        (``layers.qk_norm_rope_store`` stores in the same launch as the q/k
+        norm and rotation).
+        """
         context = get_context()
         k_cache, v_cache = self.k_cache, self.v_cache
-        if k_cache.numel() and v_cache.numel():
+        if k_cache.numel() and v_cache.numel() and not kv_stored:
             store_kvcache(k, v, k_cache, v_cache, context.slot_mapping, self.k_scale, self.v_scale)
         if context.is_prefill:
             k_scale = v_scale = None

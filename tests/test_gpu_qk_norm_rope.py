@@ -176,3 +176,72 @@ def test_full_prefill_step(cuda):
     rows = g["slot_mapping"].long()
     assert torch.equal(g["k_cache"].view(-1, 8, d)[rows].view(torch.int16), k_out.view(torch.int16))
     assert torch.equal(g["v_cache"].view(-1, 8, d)[rows].view(torch.int16), g["value"].view(torch.int16))
+
+
+class _Norm(torch.nn.Module):
+    """Stand-in with the reference GemmaRMSNorm's parameters (layers/layernorm.py)."""
+
+    def __init__(self, w, eps):
+        super().__init__()
+        self.weight = torch.nn.Parameter(w)
+        self.eps = eps
+
+
+class _Rope(torch.nn.Module):
+    """Stand-in with InterleavedMRoPE's buffer layout [max_position, 1, R]."""
+
+    def __init__(self, table, rot):
+        super().__init__()
+        self.rotary_dim = rot
+        self.register_buffer("cos_sin_cache", table.unsqueeze(1))
+
+
+@pytest.mark.parametrize("mode", ["decode", "prefill_paged"])
+def test_layer_path_equals_unfused(cuda, mode):
+    """layers.qk_norm_rope_store + Attention(kv_stored=True) gives the same bits
+    as the unfused sequence: oracle norm + rotation, then Attention.forward
+    with its own store (models/qwen3_5.py:135-139)."""
+    from nano_qwen_amd.layers import Attention, qk_norm_rope_store
+    from nano_qwen_amd.utils.context import reset_context, set_context
+    from oracle.inputs import make_norm_rope_case
+    name = "cfg2" if mode == "decode" else "cfg3"
+    c = make_norm_rope_case(name, seed=3, device="cpu")
+    d, hq, hkv = c["d"], c["hq"], c["hkv"]
+    if mode == "decode":
+        from oracle.inputs import make_decode_case
+        base = make_decode_case("cfg2", seed=3, device="cpu")
+        ctx = dict(is_prefill=False, slot_mapping=base["slot_mapping"], context_lens=base["context_lens"],
+                   block_tables=base["block_tables"])
+    else:
+        from oracle.inputs import make_prefill_case
+        base = make_prefill_case("cfg3", seed=3, device="cpu")
+        ctx = dict(is_prefill=True, cu_seqlens_q=base["cu_seqlens_q"], cu_seqlens_k=base["cu_seqlens_k"],
+                   max_seqlen_q=base["max_seqlen_q"], max_seqlen_k=base["max_seqlen_k"],
+                   slot_mapping=base["slot_mapping"], block_tables=base["block_tables"])
+    dev = lambda t: t.to(cuda) if torch.is_tensor(t) else t
+    ctx = {k: dev(v) for k, v in ctx.items()}
+    outs = []
+    for fused in (True, False):
+        attn = Attention(hq, d, d ** -0.5, hkv)
+        attn.k_cache, attn.v_cache = c["k_cache"].to(cuda), c["v_cache"].to(cuda)
+        set_context(**ctx)
+        q_gate = c["q_gate"].to(cuda)
+        query, key, value = q_gate[..., :d], c["key"].to(cuda), c["value"].to(cuda)
+        if fused:
+            qn, kn = _Norm(c["q_weight"].to(cuda), c["eps"]), _Norm(c["k_weight"].to(cuda), c["eps"])
+            rope = _Rope(c["cos_sin_cache"].to(cuda), c["rotary_dim"])
+            q2, k2 = qk_norm_rope_store(c["positions"].to(cuda), query, key, value, qn, kn, rope, attn)
+            out = attn(q2, k2, value, kv_stored=True)
+        else:
+            f = lambda t: t.float().numpy()
+            rq, rk = o.qk_norm_rope(f(c["q_gate"])[..., :d], f(c["key"]), c["positions"].numpy(),
+                                    c["cos_sin_cache"].numpy(), c["rotary_dim"], f(c["q_weight"]),
+                                    f(c["k_weight"]), c["eps"], "bf16")
+            q2 = torch.from_numpy(rq).to(torch.bfloat16).to(cuda)
+            k2 = torch.from_numpy(rk).to(torch.bfloat16).to(cuda)
+            out = attn(q2, k2, value)
+        torch.cuda.synchronize()
+        outs.append((out.cpu(), attn.k_cache.cpu(), attn.v_cache.cpu()))
+        reset_context()
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
