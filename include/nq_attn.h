@@ -115,6 +115,44 @@ int nq_paged_decode(const void *q, int64_t q_batch_stride, int64_t q_head_stride
                     const float *k_scale, const float *v_scale, void *stream);
 
 /*
+ * nq_paged_decode with Qwen3.5's attention output gate applied in the output
+ * store.  Replaces the decode call (layers/attention.py:72-74) together with
+ * the gating that follows it in Qwen3_5Attention.forward
+ * (models/qwen3_5.py:140-142):  out = rnd(rnd(o) * rnd(sigmoid(gate))),
+ * sigmoid(g) = 1 / (1 + exp(-g)) in fp32, rnd = round to the q/out type --
+ * eager torch's arithmetic for 16-bit tensors.
+ * gate [batch, num_q_heads, head_dim] has the type of q/out, strides
+ * (gate_batch_stride, gate_head_stride, 1), 8-byte aligned (for example the
+ * gate half of q_proj's [B, Hq, 2*D] output).  Rows with context_len <= 0
+ * stay zero.  Every other argument is as for nq_paged_decode.
+ */
+int nq_paged_decode_gated(const void *q, int64_t q_batch_stride, int64_t q_head_stride,
+                          const void *k_cache, const void *v_cache,
+                          const int32_t *block_tables, int64_t bt_stride,
+                          int max_blocks_per_seq, const int32_t *context_lens,
+                          void *out, int64_t out_batch_stride, int64_t out_head_stride,
+                          int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                          int block_size, int64_t num_blocks, float softmax_scale,
+                          int num_splits, int split_tokens,
+                          void *workspace, int64_t workspace_bytes,
+                          int q_dtype, int kv_dtype,
+                          const float *k_scale, const float *v_scale,
+                          const void *gate, int64_t gate_batch_stride, int64_t gate_head_stride,
+                          void *stream);
+
+/*
+ * Qwen3.5's attention output gate as one in-place pass:
+ *   out[i, h, :] = rnd(out[i, h, :] * rnd(sigmoid(gate[i, h, :])))
+ * Replaces attn_output * torch.sigmoid(gate) (models/qwen3_5.py:140-142)
+ * after the prefill call.  out and gate are [num_tokens, num_heads,
+ * head_dim] of type dtype (F16/BF16) with (row, head) strides; every pointer
+ * and stride 16-byte aligned; head_dim a multiple of 8.
+ */
+int nq_output_gate(void *out, int64_t out_row_stride, int64_t out_head_stride,
+                   const void *gate, int64_t gate_row_stride, int64_t gate_head_stride,
+                   int64_t num_tokens, int num_heads, int head_dim, int dtype, void *stream);
+
+/*
  * Causal varlen prefill attention, optionally over paged K/V.
  * Replaces flash_attn_varlen_func(q, k, v, cu_seqlens_q=..., cu_seqlens_k=...,
  *   max_seqlen_q=..., max_seqlen_k=..., softmax_scale=scale, causal=True,

@@ -90,6 +90,29 @@ __device__ inline uint32_t fp8x4(float a, float b, float c, float d) {
   return static_cast<uint32_t>(w);
 }
 
+// ---------------------------------------------------------------- output gate
+// Qwen3.5's attention output gate (models/qwen3_5.py:141-142) as eager torch
+// computes it on 16-bit tensors: out = rnd(rnd(o) * rnd(sigmoid(g))), with
+// sigmoid(g) = 1 / (1 + exp(-g)) in fp32 and rnd = round to T.  The empty
+// asm statements keep each rounding separate (the compiler would otherwise
+// fold a product and its narrowing into one mixed-precision instruction).
+template <class T>
+__device__ inline float gate_one(float o, uint32_t g16) {
+  const float gf = T::to_float(static_cast<uint16_t>(g16));
+  float sg = 1.0f / (1.0f + expf(-gf));
+  asm("" : "+v"(sg));
+  asm("" : "+v"(o));
+  const float sr = T::to_float(T::from_float(sg));
+  const float orr = T::to_float(T::from_float(o));
+  return orr * sr;  // exact in fp32: two 16-bit significands
+}
+// Four outputs of one row (fp32) with their four gate values (packed 16-bit).
+template <class T>
+__device__ inline u32x2 gate4(const f32x4 &v, const u32x2 &g) {
+  return u32x2{T::pack2(gate_one<T>(v[0], g[0] & 0xffffu), gate_one<T>(v[1], g[0] >> 16)),
+               T::pack2(gate_one<T>(v[2], g[1] & 0xffffu), gate_one<T>(v[3], g[1] >> 16))};
+}
+
 // ---------------------------------------------------------------- memory
 template <typename T>
 __device__ inline T ldg(const T *p) {

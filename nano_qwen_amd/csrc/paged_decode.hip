@@ -50,6 +50,8 @@ struct DecodeArgs {
   const int32_t *context_lens;
   uint8_t *out;
   int64_t o_bs, o_hs;  // bytes
+  const uint8_t *gate;  // null, or the output gate [B, Hq, D] (same type as out)
+  int64_t g_bs, g_hs;   // bytes
   float *ws_o;         // [B, Hq, S, D]
   float *ws_lse;       // [B, Hq, S]
   int Hq, Hkv, G, block_size;
@@ -317,10 +319,20 @@ void paged_decode_kernel(const DecodeArgs a) {
   const float inv = (L > 0.f) ? vscale / L : 0.f;
   if (single) {
     uint8_t *op = a.out + b * a.o_bs + head * a.o_hs;
+    if (a.gate) {
+      const uint8_t *gp = a.gate + b * a.g_bs + head * a.g_hs;
+      u32x2 gr[Gm::NJ];
 #pragma unroll
-    for (int j = 0; j < Gm::NJ; ++j) {
-      const f32x4 v = o[j] * inv;
-      *reinterpret_cast<u32x2 *>(op + (16 * j + 4 * g) * 2) = u32x2{T::pack2(v[0], v[1]), T::pack2(v[2], v[3])};
+      for (int j = 0; j < Gm::NJ; ++j) gr[j] = *reinterpret_cast<const u32x2 *>(gp + (16 * j + 4 * g) * 2);
+#pragma unroll
+      for (int j = 0; j < Gm::NJ; ++j)
+        *reinterpret_cast<u32x2 *>(op + (16 * j + 4 * g) * 2) = gate4<T>(o[j] * inv, gr[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < Gm::NJ; ++j) {
+        const f32x4 v = o[j] * inv;
+        *reinterpret_cast<u32x2 *>(op + (16 * j + 4 * g) * 2) = u32x2{T::pack2(v[0], v[1]), T::pack2(v[2], v[3])};
+      }
     }
   } else {
     const int64_t idx = (static_cast<int64_t>(b) * a.Hq + head) * a.num_splits + split;
@@ -364,7 +376,11 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeArgs a, 
   const float inv = W > 0.f ? 1.0f / W : 0.f;
   acc *= inv;
   uint8_t *op = a.out + b * a.o_bs + head * a.o_hs + d4 * 8;
-  *reinterpret_cast<u32x2 *>(op) = u32x2{T::pack2(acc[0], acc[1]), T::pack2(acc[2], acc[3])};
+  if (a.gate)
+    *reinterpret_cast<u32x2 *>(op) =
+        gate4<T>(acc, *reinterpret_cast<const u32x2 *>(a.gate + b * a.g_bs + head * a.g_hs + d4 * 8));
+  else
+    *reinterpret_cast<u32x2 *>(op) = u32x2{T::pack2(acc[0], acc[1]), T::pack2(acc[2], acc[3])};
 }
 
 // kv heads (= waves) per workgroup: 4 for 16-bit caches, 8 for fp8
@@ -453,14 +469,15 @@ extern "C" int64_t nq_decode_workspace_bytes(int batch, int num_q_heads, int hea
   return bytes + (n * 4 + 255) / 256 * 256;
 }
 
-extern "C" int nq_paged_decode(const void *q, int64_t q_batch_stride, int64_t q_head_stride,
-                               const void *k_cache, const void *v_cache, const int32_t *block_tables,
-                               int64_t bt_stride, int max_blocks_per_seq, const int32_t *context_lens,
-                               void *out, int64_t out_batch_stride, int64_t out_head_stride, int batch,
-                               int num_q_heads, int num_kv_heads, int head_dim, int block_size,
-                               int64_t num_blocks, float softmax_scale, int num_splits, int split_tokens,
-                               void *workspace, int64_t workspace_bytes, int q_dtype, int kv_dtype,
-                               const float *k_scale, const float *v_scale, void *stream) {
+static int paged_decode_impl(const void *q, int64_t q_batch_stride, int64_t q_head_stride,
+                             const void *k_cache, const void *v_cache, const int32_t *block_tables,
+                             int64_t bt_stride, int max_blocks_per_seq, const int32_t *context_lens,
+                             void *out, int64_t out_batch_stride, int64_t out_head_stride, int batch,
+                             int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                             int64_t num_blocks, float softmax_scale, int num_splits, int split_tokens,
+                             void *workspace, int64_t workspace_bytes, int q_dtype, int kv_dtype,
+                             const float *k_scale, const float *v_scale, const void *gate,
+                             int64_t gate_batch_stride, int64_t gate_head_stride, void *stream) {
   if (batch == 0) return NQ_OK;
   if (batch < 0 || batch > 65535 || num_q_heads <= 0 || num_kv_heads <= 0 || num_kv_heads > 65535)
     return fail(NQ_EINVAL, "paged_decode: bad batch/head counts");
@@ -503,6 +520,11 @@ extern "C" int nq_paged_decode(const void *q, int64_t q_batch_stride, int64_t q_
   a.out = static_cast<uint8_t *>(out);
   a.o_bs = out_batch_stride * 2;
   a.o_hs = out_head_stride * 2;
+  if (gate && ((gate_batch_stride * 2) % 8 || (gate_head_stride * 2) % 8 || !aligned(gate, 8)))
+    return fail(NQ_EINVAL, "paged_decode: gate must be 8-byte aligned with strides that are multiples of 4");
+  a.gate = static_cast<const uint8_t *>(gate);
+  a.g_bs = gate_batch_stride * 2;
+  a.g_hs = gate_head_stride * 2;
   a.Hq = num_q_heads;
   a.Hkv = num_kv_heads;
   a.G = G;
@@ -526,4 +548,37 @@ extern "C" int nq_paged_decode(const void *q, int64_t q_batch_stride, int64_t q_
   if (q_dtype == NQ_BF16)
     return fp8 ? launch_decode<BF16, true, 128>(a, batch, s) : launch_decode<BF16, false, 128>(a, batch, s);
   return fp8 ? launch_decode<F16, true, 128>(a, batch, s) : launch_decode<F16, false, 128>(a, batch, s);
+}
+
+extern "C" int nq_paged_decode(const void *q, int64_t q_batch_stride, int64_t q_head_stride,
+                               const void *k_cache, const void *v_cache, const int32_t *block_tables,
+                               int64_t bt_stride, int max_blocks_per_seq, const int32_t *context_lens,
+                               void *out, int64_t out_batch_stride, int64_t out_head_stride, int batch,
+                               int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                               int64_t num_blocks, float softmax_scale, int num_splits, int split_tokens,
+                               void *workspace, int64_t workspace_bytes, int q_dtype, int kv_dtype,
+                               const float *k_scale, const float *v_scale, void *stream) {
+  return paged_decode_impl(q, q_batch_stride, q_head_stride, k_cache, v_cache, block_tables, bt_stride,
+                           max_blocks_per_seq, context_lens, out, out_batch_stride, out_head_stride, batch,
+                           num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, softmax_scale,
+                           num_splits, split_tokens, workspace, workspace_bytes, q_dtype, kv_dtype, k_scale,
+                           v_scale, nullptr, 0, 0, stream);
+}
+
+extern "C" int nq_paged_decode_gated(const void *q, int64_t q_batch_stride, int64_t q_head_stride,
+                                     const void *k_cache, const void *v_cache, const int32_t *block_tables,
+                                     int64_t bt_stride, int max_blocks_per_seq, const int32_t *context_lens,
+                                     void *out, int64_t out_batch_stride, int64_t out_head_stride, int batch,
+                                     int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                                     int64_t num_blocks, float softmax_scale, int num_splits,
+                                     int split_tokens, void *workspace, int64_t workspace_bytes, int q_dtype,
+                                     int kv_dtype, const float *k_scale, const float *v_scale,
+                                     const void *gate, int64_t gate_batch_stride, int64_t gate_head_stride,
+                                     void *stream) {
+  if (!gate) return fail(NQ_EINVAL, "paged_decode_gated: null gate");
+  return paged_decode_impl(q, q_batch_stride, q_head_stride, k_cache, v_cache, block_tables, bt_stride,
+                           max_blocks_per_seq, context_lens, out, out_batch_stride, out_head_stride, batch,
+                           num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, softmax_scale,
+                           num_splits, split_tokens, workspace, workspace_bytes, q_dtype, kv_dtype, k_scale,
+                           v_scale, gate, gate_batch_stride, gate_head_stride, stream);
 }

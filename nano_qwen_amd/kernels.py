@@ -90,13 +90,22 @@ def prefill_workspace(device) -> torch.Tensor:
     return ws
 
 
+def _gate3(gate, n, hq, d, what):
+    g3 = gate.squeeze(1) if gate.dim() == 4 else gate
+    if g3.shape != (n, hq, d) or g3.stride(-1) != 1:
+        raise RuntimeError(f"{what}: gate must be [N, Hq, D] with a contiguous last dim")
+    return g3
+
+
 def paged_decode(q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale,
-                 k_scale=None, v_scale=None, out=None):
+                 k_scale=None, v_scale=None, out=None, gate=None):
     """Paged decode attention: ``q [B, 1, Hq, D]`` (or ``[B, Hq, D]``).
 
     Returns ``out`` shaped like ``q`` (``[B, 1, Hq, D]`` as
     flash_attn_with_kvcache does).  ``cache_seqlens [B] int32`` counts the
     cached tokens including the new one; ``block_table [B, W] int32``.
+    With ``gate [B, Hq, D]`` (Qwen3.5's output gate, models/qwen3_5.py:142)
+    the output is ``out * sigmoid(gate)``, applied in the kernel's store.
     """
     require_cuda(q, k_cache, v_cache, cache_seqlens, block_table, what="paged_decode")
     q3 = q.squeeze(1) if q.dim() == 4 else q
@@ -120,22 +129,44 @@ def paged_decode(q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale,
     ns, st = decode_plan(B, hq, hkv, W, bs, k_cache.dtype)
     wsb = lib().nq_decode_workspace_bytes(B, hq, d, ns)
     ws = decode_workspace(q.device, wsb)
-    rc = lib().nq_paged_decode(
-        ptr(q3), q3.stride(0), q3.stride(1), ptr(k_cache), ptr(v_cache), ptr(block_table),
-        block_table.stride(0), W, ptr(cache_seqlens), ptr(o3), o3.stride(0), o3.stride(1),
-        B, hq, hkv, d, bs, nb, float(softmax_scale), ns, st, ptr(ws), 0 if ws is None else ws.numel(),
-        dtype_code(q.dtype), dtype_code(k_cache.dtype), ptr(k_scale) if fp8 else None,
-        ptr(v_scale) if fp8 else None, stream_of(q))
+    args = (ptr(q3), q3.stride(0), q3.stride(1), ptr(k_cache), ptr(v_cache), ptr(block_table),
+            block_table.stride(0), W, ptr(cache_seqlens), ptr(o3), o3.stride(0), o3.stride(1),
+            B, hq, hkv, d, bs, nb, float(softmax_scale), ns, st, ptr(ws), 0 if ws is None else ws.numel(),
+            dtype_code(q.dtype), dtype_code(k_cache.dtype), ptr(k_scale) if fp8 else None,
+            ptr(v_scale) if fp8 else None)
+    if gate is None:
+        rc = lib().nq_paged_decode(*args, stream_of(q))
+    else:
+        require_cuda(gate, what="paged_decode")
+        if gate.dtype != q.dtype:
+            raise RuntimeError("paged_decode: gate dtype must match q")
+        g3 = _gate3(gate, B, hq, d, "paged_decode")
+        rc = lib().nq_paged_decode_gated(*args, ptr(g3), g3.stride(0), g3.stride(1), stream_of(q))
     check(rc, "paged_decode")
     return out
 
 
+def output_gate(out, gate):
+    """In place: ``out [N, H, D] *= sigmoid(gate [N, H, D])`` with eager
+    torch's 16-bit rounding (models/qwen3_5.py:140-142), one launch."""
+    require_cuda(out, gate, what="output_gate")
+    n, h, d = out.shape
+    g3 = _gate3(gate, n, h, d, "output_gate")
+    if out.stride(-1) != 1 or gate.dtype != out.dtype:
+        raise RuntimeError("output_gate: out needs a contiguous last dim and the gate's dtype")
+    check(lib().nq_output_gate(ptr(out), out.stride(0), out.stride(1), ptr(g3), g3.stride(0), g3.stride(1),
+                               n, h, d, dtype_code(out.dtype), stream_of(out)), "output_gate")
+    return out
+
+
 def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
-                   causal=True, block_table=None, k_scale=None, v_scale=None, out=None):
+                   causal=True, block_table=None, k_scale=None, v_scale=None, out=None, gate=None):
     """Causal varlen attention; ``q [Tq, Hq, D]`` -> ``[Tq, Hq, D]``.
 
     Without ``block_table``: ``k, v [Tk, Hkv, D]`` packed by ``cu_seqlens_k``.
     With it: ``k, v`` are the paged caches ``[num_blocks, block_size, Hkv, D]``.
+    With ``gate [Tq, Hq, D]`` the output is ``out * sigmoid(gate)``
+    (models/qwen3_5.py:142), applied by one extra in-place pass.
     """
     require_cuda(q, k, v, cu_seqlens_q, cu_seqlens_k, block_table, what="varlen_prefill")
     tq, hq, d = q.shape
@@ -169,6 +200,8 @@ def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen
         dtype_code(q.dtype), dtype_code(k.dtype), ptr(k_scale) if fp8 else None,
         ptr(v_scale) if fp8 else None, ptr(ws), ws.numel() * 4, stream_of(q))
     check(rc, "varlen_prefill")
+    if gate is not None:
+        output_gate(out, gate)
     return out
 
 
@@ -253,4 +286,5 @@ def qk_norm_rope_store(positions, query, key, value, q_weight, k_weight, eps, co
 
 
 __all__ = ["store_kvcache", "paged_decode", "varlen_prefill", "prepare_decode", "decode_plan", "qk_norm_rope_store",
+           "output_gate",
            "decode_workspace", "prefill_workspace", "_lib"]

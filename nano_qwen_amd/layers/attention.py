@@ -42,12 +42,15 @@ class Attention(nn.Module):
         self.k_cache = self.v_cache = torch.tensor([])
         self.k_scale = self.v_scale = None
 
-    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_stored: bool = False):
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_stored: bool = False,
+                gate: torch.Tensor | None = None):
         """layers/attention.py:59-75: store, then prefill or paged decode.
 
         ``kv_stored=True`` skips the store because the caller already made it
         (``layers.qk_norm_rope_store`` stores in the same launch as the q/k
-        norm and rotation).
+        norm and rotation).  ``gate [N, Hq, D]`` returns
+        ``o * sigmoid(gate)``, Qwen3.5's output gate (models/qwen3_5.py:140-142):
+        inside the decode kernel's store, or one in-place pass after prefill.
         """
         context = get_context()
         k_cache, v_cache = self.k_cache, self.v_cache
@@ -62,10 +65,11 @@ class Attention(nn.Module):
                                        context.max_seqlen_q, context.max_seqlen_k,
                                        softmax_scale=self.scale, causal=True,
                                        block_table=context.block_tables,
-                                       k_scale=k_scale, v_scale=v_scale)
+                                       k_scale=k_scale, v_scale=v_scale, gate=gate)
         else:    # decode
             o = kernels.paged_decode(q.unsqueeze(1), k_cache, v_cache,
                                      cache_seqlens=context.context_lens,
                                      block_table=context.block_tables, softmax_scale=self.scale,
-                                     k_scale=self.k_scale, v_scale=self.v_scale)
+                                     k_scale=self.k_scale, v_scale=self.v_scale,
+                                     gate=None if gate is None else gate.unsqueeze(1))
         return o

@@ -199,3 +199,25 @@ def test_sum_squares_order_is_a_sum():
         np.testing.assert_allclose(s, ref, rtol=d * 6e-8)
         xi = rng.integers(-50, 50, (10, d)).astype(F32)
         assert np.array_equal(o.sum_squares(xi)[:, 0], (xi.astype(np.int64) ** 2).sum(-1).astype(F32))
+
+
+def test_output_gate_oracle():
+    """sigmoid32 against the float64 logistic function (scipy's expit, a library
+    routine) within float32 error; sigmoid(0) = 1/2 exactly; a gate of +30 is
+    the identity in bf16, -200 (exp overflows) gives exact zeros, -30 scales by
+    about 9.4e-14; and against the reference's eager torch ops on bf16 tensors."""
+    from scipy.special import expit
+    from oracle.output_gate import output_gate, sigmoid32
+    rng = np.random.default_rng(10)
+    g = (rng.standard_normal(100_000) * 6).astype(F32)
+    np.testing.assert_allclose(sigmoid32(g), expit(g.astype(np.float64)), rtol=4e-7, atol=1e-30)
+    assert sigmoid32(np.zeros(3, F32))[0] == 0.5
+    ob = o.round_to(rng.standard_normal(1000).astype(F32), "bf16")
+    assert np.array_equal(output_gate(ob, np.full(1000, 30, F32), "bf16"), ob)
+    assert np.all(output_gate(ob, np.full(1000, -200, F32), "bf16") == 0)
+    np.testing.assert_allclose(output_gate(ob, np.full(1000, -30, F32), "bf16"), ob * expit(-30.0), rtol=8e-3)
+    assert np.array_equal(output_gate(ob, np.zeros(1000, F32), "bf16"), ob * F32(0.5))
+    gb = o.round_to(g[:1000], "bf16")
+    ref = torch.from_numpy(ob).to(torch.bfloat16) * torch.sigmoid(torch.from_numpy(gb).to(torch.bfloat16))
+    u = _bf16_ulps(output_gate(ob, gb, "bf16"), ref.float().numpy())
+    assert u.max() <= 1 and (u > 0).mean() < 5e-3
