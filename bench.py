@@ -12,7 +12,9 @@ step re-reads KV the previous step left in the Infinity Cache.
 The headline (``value``) is cfg2's algorithmic HBM bandwidth in GB/s; cfg3's
 TFLOP/s and the other decode configurations are reported under ``extra``, as
 is the fused q/k norm + rotary + KV store call over cfg3's and cfg2's new
-tokens (``cfg3_norm_rope``, ``cfg2_norm_rope``: HBM GB/s).
+tokens (``cfg3_norm_rope``, ``cfg2_norm_rope``: HBM GB/s), and Qwen3.5's output
+gate (``cfg2_gate``: gated vs plain decode; ``cfg3_gate``: gated vs plain
+prefill, and the stand-alone in-place gate pass for comparison).
 ``roofline`` covers the dominant kernel of the headline workload (paged
 decode: main kernel + split-K merge), timed with HIP events on the stream
 the kernels run on.  ``cpu_baseline`` times the CPU restatement of the path
@@ -161,6 +163,42 @@ def bench_norm_rope(name, steps, warmup, seed=0):
                 tokens_per_s=c["n"] / (ms * 1e-3)), c
 
 
+def bench_gate(name, steps, warmup, seed=0):
+    """Qwen3.5's output gate: for decode (cfg2) the gated decode step against
+    the plain one (the gate rides in the kernel's store); for prefill (cfg3)
+    the in-place gate pass over the whole output [sum Lq, Hq, D]."""
+    import torch
+    from nano_qwen_amd import kernels
+    from oracle.inputs import make_decode_case, make_prefill_case
+
+    g = torch.Generator(device="cuda").manual_seed(seed + 9)
+    if name == "cfg2":
+        c = make_decode_case(name, seed=seed, device="cuda")
+        B, hq, d = c["q"].shape
+        gate = torch.randn(B, hq, 2 * d, device="cuda", generator=g).to(torch.bfloat16)[..., d:]
+        q4, out = c["q"].unsqueeze(1), torch.empty(B, 1, hq, d, dtype=torch.bfloat16, device="cuda")
+        args = (q4, c["k_cache"], c["v_cache"], c["context_lens"], c["block_tables"], c["scale"])
+        ms_plain = _events_time(lambda i: kernels.paged_decode(*args, out=out), steps, max(warmup, 50))
+        ms_gated = _events_time(lambda i: kernels.paged_decode(*args, out=out, gate=gate), steps, max(warmup, 50))
+        return dict(ms_per_step=ms_gated, decode_ms=ms_plain, gated_decode_ms=ms_gated,
+                    overhead_frac=ms_gated / ms_plain - 1), c
+    c = make_prefill_case(name, seed=seed, device="cuda")
+    tq, hq, d = c["q"].shape
+    out = torch.empty(tq, hq, d, device="cuda", dtype=torch.bfloat16)
+    gate = torch.randn(tq, hq, 2 * d, device="cuda", generator=g).to(torch.bfloat16)[..., d:]
+    kernels.store_kvcache(c["k_new"], c["v_new"], c["k_cache"], c["v_cache"], c["slot_mapping"])
+    args = (c["q"], c["k_cache"], c["v_cache"], c["cu_seqlens_q"], c["cu_seqlens_k"], c["max_seqlen_q"],
+            c["max_seqlen_k"], c["scale"])
+    kw = dict(block_table=c["block_tables"], out=out)
+    ms_plain = _events_time(lambda i: kernels.varlen_prefill(*args, **kw), steps, max(warmup, 10))
+    ms_gated = _events_time(lambda i: kernels.varlen_prefill(*args, gate=gate, **kw), steps, max(warmup, 10))
+    ms_pass = _events_time(lambda i: kernels.output_gate(out, gate), steps, max(warmup, 200))
+    nb = 3 * out.numel() * 2
+    return dict(ms_per_step=ms_gated, prefill_ms=ms_plain, gated_prefill_ms=ms_gated,
+                fused_overhead_frac=ms_gated / ms_plain - 1, gate_pass_ms=ms_pass,
+                gate_pass_gbs=nb / (ms_pass * 1e-3) / 1e9, gate_pass_overhead_frac=ms_pass / ms_plain), c
+
+
 def cpu_baseline_decode(case, n_seqs=8, reps=5):
     """Median wall time of the CPU path on the first n_seqs sequences."""
     import torch
@@ -281,7 +319,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None,
-                    help="run one config (cfg2|cfg3|cfg4|cfg5|cfg3_norm_rope|cfg2_norm_rope)")
+                    help="run one config (cfg2|cfg3|cfg4|cfg5|cfg3_norm_rope|cfg2_norm_rope|cfg2_gate|cfg3_gate)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration)")
     args = ap.parse_args()
@@ -301,12 +339,15 @@ def main():
 
     extra = {}
     head = None
-    todo = [args.only] if args.only else ["cfg2", "cfg3", "cfg4", "cfg5", "cfg3_norm_rope", "cfg2_norm_rope"]
+    todo = [args.only] if args.only else ["cfg2", "cfg3", "cfg4", "cfg5", "cfg3_norm_rope", "cfg2_norm_rope",
+                                                   "cfg2_gate", "cfg3_gate"]
     cpu = None
     for name in todo:
         print(f"[bench] {name} ...", file=sys.stderr, flush=True)
         if name.endswith("_norm_rope"):
             r, case = bench_norm_rope(name.split("_")[0], args.steps, args.warmup)
+        elif name.endswith("_gate"):
+            r, case = bench_gate(name.split("_")[0], args.steps, args.warmup)
         elif name == "cfg3":
             r, case = bench_prefill(name, args.steps, args.warmup)
             if not args.no_cpu:
@@ -326,7 +367,7 @@ def main():
         name = todo[0]
         r = extra[name]
         head_ms = r["ms_per_step"]
-        value = r.get("gbs") if name != "cfg3" else r["tflops"]
+        value = (r.get("gbs") or 0.0) if name != "cfg3" else r["tflops"]
         unit = "GB/s" if name != "cfg3" else "TFLOP/s"
     else:
         head_ms, value, unit = head["ms_per_step"], head["gbs"], "GB/s"

@@ -188,6 +188,30 @@ int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_head_stride
                       const float *k_scale, const float *v_scale,
                       void *workspace, int64_t workspace_bytes, void *stream);
 
+/*
+ * nq_varlen_prefill with Qwen3.5's attention output gate (models/qwen3_5.py:
+ * 140-142): out = rnd(rnd(o) * rnd(sigmoid(gate))) as for
+ * nq_paged_decode_gated.  gate [total_q, num_q_heads, head_dim] has the type
+ * of q/out, strides (gate_row_stride, gate_head_stride, 1), 16-byte aligned
+ * (e.g. the gate half of q_proj's output); total_q = cu_seqlens_q[num_seqs].
+ * The default 16-bit kernel applies the gate in its own output store; the
+ * fp8-K/V kernel is followed by one nq_output_gate pass on the same stream.
+ */
+int nq_varlen_prefill_gated(const void *q, int64_t q_row_stride, int64_t q_head_stride,
+                            const void *k, const void *v, int64_t kv_row_stride,
+                            const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k,
+                            int max_seqlen_q, int max_seqlen_k,
+                            const int32_t *block_tables, int64_t bt_stride,
+                            int max_blocks_per_seq, int64_t num_blocks,
+                            void *out, int64_t out_row_stride, int64_t out_head_stride,
+                            int num_seqs, int num_q_heads, int num_kv_heads,
+                            int head_dim, int block_size, float softmax_scale,
+                            int causal, int q_dtype, int kv_dtype,
+                            const float *k_scale, const float *v_scale,
+                            void *workspace, int64_t workspace_bytes,
+                            const void *gate, int64_t gate_row_stride, int64_t gate_head_stride,
+                            int64_t total_q, void *stream);
+
 /* Bytes of device workspace nq_varlen_prefill needs (work-queue counters). */
 int64_t nq_prefill_workspace_bytes(void);
 

@@ -46,6 +46,11 @@ _SIGS = {
                                   c_void_p, c_int, c_int, c_void_p, c_int64, c_int, c_int64, c_void_p,
                                   c_int64, c_int64, c_int, c_int, c_int, c_int, c_int, c_float, c_int,
                                   c_int, c_int, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+    "nq_varlen_prefill_gated": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p,
+                                        c_void_p, c_int, c_int, c_void_p, c_int64, c_int, c_int64, c_void_p,
+                                        c_int64, c_int64, c_int, c_int, c_int, c_int, c_int, c_float, c_int,
+                                        c_int, c_int, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
+                                        c_int64, c_int64, c_void_p]),
     "nq_prefill_workspace_bytes": (c_int64, []),
     "nq_prepare_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_int, c_int, c_void_p]),

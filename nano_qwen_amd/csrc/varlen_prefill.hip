@@ -73,6 +73,8 @@ struct PrefillArgs {
   int by_cost;      // persistent kernel: queue in cost order over live items (num_seqs <= kMaxSeqs)
   int level_shift;  // cost level of an item: its key tiles >> level_shift (< n_levels)
   int n_levels;
+  const uint8_t *gate;  // null, or Qwen3.5's output gate [total_q, Hq, D] (type of out)
+  int64_t g_rs, g_hs;   // bytes
 };
 
 __device__ inline int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1) | (row & 8); }
@@ -410,6 +412,9 @@ struct PShape {
 };
 using ShapeA = PShape<8, 2, 2, 5>;  // one workgroup per CU, two 32-row waves per SIMD
 using ShapeC = PShape<4, 2, 2, 4>;  // two independent workgroups per CU, 32-row waves
+// Launch shapes built with the output gate in their store (the default one).
+template <class S>
+constexpr bool GATED_OK = std::is_same<S, ShapeC>::value;
 
 // A work item of the persistent kernel: query tile qt (S::ITEM_ROWS/G4 rows
 // of G4 heads) of kv-head slot y of sequence s, described by wave-uniform
@@ -611,7 +616,7 @@ __device__ __forceinline__ Item describe_by_cost(const PrefillArgs &a, const Cos
 // waits count only younger stream entries -- except that a new item's first
 // kAhead tiles may precede the Q loads and the previous item's output stores
 // (a fixed count per wave), which the waits then add.
-template <class T, int D, class S>
+template <class T, int D, class S, bool GATED>
 __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   using DT = DTile<T, D>;
   using PT = PTile<T, false, D>;
@@ -861,7 +866,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   // dims 16j1 + 4(g-1) .. +7 (j0 = 2p, j1 = 2p + 1).  The stores go through a
   // descriptor covering the sequence's rows of this head, so rows past the
   // end (and a wave with no rows) are dropped by the range check, not skipped.
-  auto store_out = [&](const Item &it) {
+  auto store_out_plain = [&](const Item &it) {
     const bool odd = (g & 1) != 0;
     const int wrow0 = it.row_begin + row_in_item;
     const int head = it.head0 + head_in_item;
@@ -893,6 +898,71 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
                                                ro, static_cast<int>(voff_o), 0, 0);
       }
     }
+  };
+
+  auto store_out_gated = [&](const Item &it) {
+    const bool odd = (g & 1) != 0;
+    const int wrow0 = it.row_begin + row_in_item;
+    const int head = it.head0 + head_in_item;
+    const uint8_t *obase = a.out + static_cast<int64_t>(it.q0) * a.o_rs + static_cast<int64_t>(head) * a.o_hs;
+    const uint32_t orange = wrow0 < it.Lq ? static_cast<uint32_t>((it.Lq - 1) * a.o_rs + D * 2) : 0u;
+    const auto ro = make_rsrc(obase, orange);
+    // Output dims [dim0, dim0 + 8) of a lane for store p (after the swap below).
+    auto dim0_of = [&](int p) { return odd ? 16 * (2 * p + 1) + 4 * (g - 1) : 16 * (2 * p) + 4 * g; };
+    // Gated output (models/qwen3_5.py:140-142): the gate's 16 bytes at each
+    // store's address, loaded for one 16-row block before its products.
+    const uint8_t *gbase = nullptr;
+    uint32_t grange = 0;
+    if constexpr (GATED) {
+      gbase = a.gate + static_cast<int64_t>(it.q0) * a.g_rs + static_cast<int64_t>(head) * a.g_hs;
+      grange = wrow0 < it.Lq ? static_cast<uint32_t>((it.Lq - 1) * a.g_rs + D * 2) : 0u;
+    }
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs) {
+      const float l = sum32(sum16(lsum[qs]));  // the row sum of row m (lanes m, m + 16, m + 32, m + 48)
+      const int row = wrow0 + 16 * qs + m;
+      u32x4 gv[PT::NJ / 2];
+      if constexpr (GATED) {
+        const auto rg = make_rsrc(gbase, grange);
+#pragma unroll
+        for (int p = 0; p < PT::NJ / 2; ++p) {
+          const uint32_t goff = row < it.Lq ? static_cast<uint32_t>(row * a.g_rs + dim0_of(p) * 2) : 0x7fffffffu;
+          gv[p] = buffer_load16_nt(rg, static_cast<int>(goff));
+        }
+      }
+      const float inv = l > 0.f ? 1.0f / l : 0.f;
+      const uint32_t roff = row < it.Lq ? static_cast<uint32_t>(row * a.o_rs) : 0x7fffffffu;
+#pragma unroll
+      for (int p = 0; p < PT::NJ / 2; ++p) {
+        const f32x4 v0 = o[qs][2 * p] * inv, v1 = o[qs][2 * p + 1] * inv;
+        const uint32_t c00 = T::pack2(v0[0], v0[1]), c01 = T::pack2(v0[2], v0[3]);
+        const uint32_t c10 = T::pack2(v1[0], v1[1]), c11 = T::pack2(v1[2], v1[3]);
+        const uint32_t x0 = odd ? c00 : c10, x1 = odd ? c01 : c11;  // the piece the partner needs
+        // After the swap, even lanes find the partner's value in the
+        // second result, odd lanes in the first.
+        const auto r0 = __builtin_amdgcn_permlane16_swap(x0, x0, false, false);
+        const auto r1 = __builtin_amdgcn_permlane16_swap(x1, x1, false, false);
+        const uint32_t y0 = odd ? static_cast<uint32_t>(r0[0]) : static_cast<uint32_t>(r0[1]);
+        const uint32_t y1 = odd ? static_cast<uint32_t>(r1[0]) : static_cast<uint32_t>(r1[1]);
+        u32x4 w = odd ? u32x4{y0, y1, c10, c11} : u32x4{c00, c01, y0, y1};
+        if constexpr (GATED) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float o0 = T::to_float(static_cast<uint16_t>(w[t] & 0xffffu));
+            const float o1 = T::to_float(static_cast<uint16_t>(w[t] >> 16));
+            w[t] = T::pack2(gate_one<T>(o0, gv[p][t] & 0xffffu), gate_one<T>(o1, gv[p][t] >> 16));
+          }
+        }
+        const uint32_t voff_o = roff == 0x7fffffffu ? roff : roff + dim0_of(p) * 2;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, w),
+                                               ro, static_cast<int>(voff_o), 0, 0);
+      }
+    }
+  };
+
+  auto store_out = [&](const Item &it) {
+    if constexpr (GATED) store_out_gated(it);
+    else store_out_plain(it);
   };
 
   // ----------------------------------------------------------------- queue
@@ -1280,10 +1350,10 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
 
 // The body lives in a device function: its inline assembly uses register
 // constraints that only the device compilation accepts.
-template <class T, int D, class S>
+template <class T, int D, class S, bool GATED>
 __global__ __launch_bounds__(64 * S::NW) __attribute__((amdgpu_waves_per_eu(S::WPE)))
 void varlen_prefill_dma_kernel(const PrefillArgs a) {
-  prefill_persistent<T, D, S>(a);
+  prefill_persistent<T, D, S, GATED>(a);
 }
 
 // Launch shape of the 16-bit kernel: C (two independent 4-wave workgroups
@@ -1317,7 +1387,13 @@ int launch_prefill_dma(PrefillArgs a, hipStream_t st) {
   // items; a multiple of 8 so every XCD gets the same count.
   int64_t grid = (static_cast<int64_t>(device_cus()) * S::WG_PER_CU + 7) / 8 * 8;
   if (grid > total) grid = total;  // work_grid() is a multiple of 8 when pinned
-  varlen_prefill_dma_kernel<T, D, S><<<static_cast<int>(grid), 64 * S::NW, S::LDS_BYTES, st>>>(a);
+  if constexpr (GATED_OK<S>) {
+    if (a.gate) {
+      varlen_prefill_dma_kernel<T, D, S, true><<<static_cast<int>(grid), 64 * S::NW, S::LDS_BYTES, st>>>(a);
+      return check_launch("varlen_prefill(gated)");
+    }
+  }
+  varlen_prefill_dma_kernel<T, D, S, false><<<static_cast<int>(grid), 64 * S::NW, S::LDS_BYTES, st>>>(a);
   return check_launch("varlen_prefill");
 }
 
@@ -1345,15 +1421,16 @@ using namespace nq;
 
 extern "C" int64_t nq_prefill_workspace_bytes(void) { return kQueueWords * sizeof(uint32_t); }
 
-extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_head_stride, const void *k,
-                                 const void *v, int64_t kv_row_stride, const int32_t *cu_seqlens_q,
-                                 const int32_t *cu_seqlens_k, int max_seqlen_q, int max_seqlen_k,
-                                 const int32_t *block_tables, int64_t bt_stride, int max_blocks_per_seq,
-                                 int64_t num_blocks, void *out, int64_t out_row_stride,
-                                 int64_t out_head_stride, int num_seqs, int num_q_heads, int num_kv_heads,
-                                 int head_dim, int block_size, float softmax_scale, int causal, int q_dtype,
-                                 int kv_dtype, const float *k_scale, const float *v_scale, void *workspace,
-                                 int64_t workspace_bytes, void *stream) {
+static int varlen_prefill_impl(const void *q, int64_t q_row_stride, int64_t q_head_stride, const void *k,
+                               const void *v, int64_t kv_row_stride, const int32_t *cu_seqlens_q,
+                               const int32_t *cu_seqlens_k, int max_seqlen_q, int max_seqlen_k,
+                               const int32_t *block_tables, int64_t bt_stride, int max_blocks_per_seq,
+                               int64_t num_blocks, void *out, int64_t out_row_stride, int64_t out_head_stride,
+                               int num_seqs, int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                               float softmax_scale, int causal, int q_dtype, int kv_dtype, const float *k_scale,
+                               const float *v_scale, void *workspace, int64_t workspace_bytes, const void *gate,
+                               int64_t gate_row_stride, int64_t gate_head_stride, int64_t total_q,
+                               void *stream) {
   if (num_seqs == 0 || max_seqlen_q == 0) return NQ_OK;
   if (num_seqs < 0 || max_seqlen_q < 0 || max_seqlen_k < 0 || num_q_heads <= 0 || num_kv_heads <= 0)
     return fail(NQ_EINVAL, "varlen_prefill: bad sizes");
@@ -1411,6 +1488,21 @@ extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_
   a.out = static_cast<uint8_t *>(out);
   a.o_rs = out_row_stride * qsz;
   a.o_hs = out_head_stride * qsz;
+  // The gate rides in the output store of the default 16-bit launch shape;
+  // other launches get the same arithmetic from one in-place pass afterwards.
+  const bool fused_gate = gate && !fp8 && prefill_shape() == 'c';
+  if (gate) {
+    if ((gate_row_stride * qsz) % 16 || (gate_head_stride * qsz) % 16 || !aligned(gate, 16))
+      return fail(NQ_EINVAL, "varlen_prefill_gated: gate alignment");
+    if ((static_cast<int64_t>(max_seqlen_q) + 256) * gate_row_stride * qsz >= (int64_t{1} << 31))
+      return fail(NQ_EINVAL, "varlen_prefill_gated: max_seqlen_q x gate row stride too large");
+    if (total_q < 0) return fail(NQ_EINVAL, "varlen_prefill_gated: total_q < 0");
+  }
+  if (fused_gate) {
+    a.gate = static_cast<const uint8_t *>(gate);
+    a.g_rs = gate_row_stride * qsz;
+    a.g_hs = gate_head_stride * qsz;
+  }
   a.Hq = num_q_heads;
   a.Hkv = num_kv_heads;
   a.G = G;
@@ -1427,7 +1519,44 @@ extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_
   a.k_scale = k_scale;
   a.v_scale = v_scale;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc;
   if (q_dtype == NQ_BF16)
-    return fp8 ? launch_prefill<BF16, true, 128>(a, st) : launch_prefill<BF16, false, 128>(a, st);
-  return fp8 ? launch_prefill<F16, true, 128>(a, st) : launch_prefill<F16, false, 128>(a, st);
+    rc = fp8 ? launch_prefill<BF16, true, 128>(a, st) : launch_prefill<BF16, false, 128>(a, st);
+  else
+    rc = fp8 ? launch_prefill<F16, true, 128>(a, st) : launch_prefill<F16, false, 128>(a, st);
+  if (rc != NQ_OK || !gate || fused_gate) return rc;
+  return nq_output_gate(out, out_row_stride, out_head_stride, gate, gate_row_stride, gate_head_stride, total_q,
+                        num_q_heads, head_dim, q_dtype, stream);
+}
+
+extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_head_stride, const void *k,
+                                 const void *v, int64_t kv_row_stride, const int32_t *cu_seqlens_q,
+                                 const int32_t *cu_seqlens_k, int max_seqlen_q, int max_seqlen_k,
+                                 const int32_t *block_tables, int64_t bt_stride, int max_blocks_per_seq,
+                                 int64_t num_blocks, void *out, int64_t out_row_stride,
+                                 int64_t out_head_stride, int num_seqs, int num_q_heads, int num_kv_heads,
+                                 int head_dim, int block_size, float softmax_scale, int causal, int q_dtype,
+                                 int kv_dtype, const float *k_scale, const float *v_scale, void *workspace,
+                                 int64_t workspace_bytes, void *stream) {
+  return varlen_prefill_impl(q, q_row_stride, q_head_stride, k, v, kv_row_stride, cu_seqlens_q, cu_seqlens_k,
+                             max_seqlen_q, max_seqlen_k, block_tables, bt_stride, max_blocks_per_seq, num_blocks,
+                             out, out_row_stride, out_head_stride, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                             block_size, softmax_scale, causal, q_dtype, kv_dtype, k_scale, v_scale, workspace,
+                             workspace_bytes, nullptr, 0, 0, 0, stream);
+}
+
+extern "C" int nq_varlen_prefill_gated(
+    const void *q, int64_t q_row_stride, int64_t q_head_stride, const void *k, const void *v,
+    int64_t kv_row_stride, const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k, int max_seqlen_q,
+    int max_seqlen_k, const int32_t *block_tables, int64_t bt_stride, int max_blocks_per_seq, int64_t num_blocks,
+    void *out, int64_t out_row_stride, int64_t out_head_stride, int num_seqs, int num_q_heads, int num_kv_heads,
+    int head_dim, int block_size, float softmax_scale, int causal, int q_dtype, int kv_dtype, const float *k_scale,
+    const float *v_scale, void *workspace, int64_t workspace_bytes, const void *gate, int64_t gate_row_stride,
+    int64_t gate_head_stride, int64_t total_q, void *stream) {
+  if (!gate) return fail(NQ_EINVAL, "varlen_prefill_gated: null gate");
+  return varlen_prefill_impl(q, q_row_stride, q_head_stride, k, v, kv_row_stride, cu_seqlens_q, cu_seqlens_k,
+                             max_seqlen_q, max_seqlen_k, block_tables, bt_stride, max_blocks_per_seq, num_blocks,
+                             out, out_row_stride, out_head_stride, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                             block_size, softmax_scale, causal, q_dtype, kv_dtype, k_scale, v_scale, workspace,
+                             workspace_bytes, gate, gate_row_stride, gate_head_stride, total_q, stream);
 }

@@ -166,7 +166,8 @@ def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen
     Without ``block_table``: ``k, v [Tk, Hkv, D]`` packed by ``cu_seqlens_k``.
     With it: ``k, v`` are the paged caches ``[num_blocks, block_size, Hkv, D]``.
     With ``gate [Tq, Hq, D]`` the output is ``out * sigmoid(gate)``
-    (models/qwen3_5.py:142), applied by one extra in-place pass.
+    (models/qwen3_5.py:142), applied in the kernel's output store (16-bit
+    K/V) or by one in-place pass after it (fp8 K/V).
     """
     require_cuda(q, k, v, cu_seqlens_q, cu_seqlens_k, block_table, what="varlen_prefill")
     tq, hq, d = q.shape
@@ -193,15 +194,20 @@ def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen
     if out is None:
         out = torch.empty(tq, hq, d, dtype=q.dtype, device=q.device)
     ws = prefill_workspace(q.device)
-    rc = lib().nq_varlen_prefill(
-        ptr(q), q.stride(0), q.stride(1), ptr(k), ptr(v), kv_rs, ptr(cu_seqlens_q), ptr(cu_seqlens_k),
-        int(max_seqlen_q), int(max_seqlen_k), ptr(block_table), bt_stride, W, nb, ptr(out),
-        out.stride(0), out.stride(1), n, hq, hkv, d, bs, float(softmax_scale), 1 if causal else 0,
-        dtype_code(q.dtype), dtype_code(k.dtype), ptr(k_scale) if fp8 else None,
-        ptr(v_scale) if fp8 else None, ptr(ws), ws.numel() * 4, stream_of(q))
+    args = (ptr(q), q.stride(0), q.stride(1), ptr(k), ptr(v), kv_rs, ptr(cu_seqlens_q), ptr(cu_seqlens_k),
+            int(max_seqlen_q), int(max_seqlen_k), ptr(block_table), bt_stride, W, nb, ptr(out),
+            out.stride(0), out.stride(1), n, hq, hkv, d, bs, float(softmax_scale), 1 if causal else 0,
+            dtype_code(q.dtype), dtype_code(k.dtype), ptr(k_scale) if fp8 else None,
+            ptr(v_scale) if fp8 else None, ptr(ws), ws.numel() * 4)
+    if gate is None:
+        rc = lib().nq_varlen_prefill(*args, stream_of(q))
+    else:
+        require_cuda(gate, what="varlen_prefill")
+        if gate.dtype != q.dtype:
+            raise RuntimeError("varlen_prefill: gate dtype must match q")
+        g3 = _gate3(gate, tq, hq, d, "varlen_prefill")
+        rc = lib().nq_varlen_prefill_gated(*args, ptr(g3), g3.stride(0), g3.stride(1), tq, stream_of(q))
     check(rc, "varlen_prefill")
-    if gate is not None:
-        output_gate(out, gate)
     return out
 
 

@@ -91,3 +91,47 @@ def test_output_gate_f16_and_errors(cuda):
     assert float(d.max()) <= float(ref.float().abs().max()) * 2 ** -10
     with pytest.raises(RuntimeError, match="dtype"):
         kernels.output_gate(out.float(), gate.float())
+
+
+@pytest.mark.parametrize("kind", ["packed", "fp8"])
+def test_prefill_gated_other_paths(cuda, kind):
+    """Packed K/V (no block table) on the fused store, and fp8 K/V, whose
+    kernel is followed by the in-place gate pass: gated == gate(ungated)."""
+    from oracle.inputs import make_prefill_case
+    if kind == "packed":
+        c = make_prefill_case("cfg3", seed=8, device="cuda", prefix_blocks=(0, 0), lq=(100, 700))
+        k, v, bt, ks, vs = c["k_new"], c["v_new"], None, None, None
+    else:
+        c = make_prefill_case("cfg3", seed=9, device="cuda", kv="fp8", lq=(100, 700))
+        kernels.store_kvcache(c["k_new"], c["v_new"], c["k_cache"], c["v_cache"], c["slot_mapping"],
+                              c["k_scale"], c["v_scale"])
+        k, v, bt, ks, vs = c["k_cache"], c["v_cache"], c["block_tables"], c["k_scale"], c["v_scale"]
+    tq, hq, d = c["q"].shape
+    gate = _gate_of(tq, hq, d, 10, cuda)
+    args = (c["q"], k, v, c["cu_seqlens_q"], c["cu_seqlens_k"], c["max_seqlen_q"], c["max_seqlen_k"], c["scale"])
+    plain = kernels.varlen_prefill(*args, block_table=bt, k_scale=ks, v_scale=vs)
+    gated = kernels.varlen_prefill(*args, block_table=bt, k_scale=ks, v_scale=vs, gate=gate)
+    torch.cuda.synchronize()
+    ref = gate_ref(plain.float().cpu().numpy(), gate.float().cpu().numpy(), "bf16")
+    _check(gated, torch.from_numpy(ref).to(torch.bfloat16), f"prefill {kind} gated vs oracle")
+
+
+def test_attention_layer_gate(cuda):
+    """Attention.forward(q, k, v, gate=...) on a decode step equals the
+    kernel-level gated decode."""
+    from nano_qwen_amd.layers import Attention
+    from nano_qwen_amd.utils.context import reset_context, set_context
+    from oracle.inputs import make_decode_case
+    c = make_decode_case("cfg2", seed=11, device="cuda")
+    B, hq, d = c["q"].shape
+    gate = _gate_of(B, hq, d, 12, cuda)
+    attn = Attention(hq, d, c["scale"], c["hkv"])
+    attn.k_cache, attn.v_cache = c["k_cache"], c["v_cache"]
+    set_context(False, slot_mapping=c["slot_mapping"], context_lens=c["context_lens"],
+                block_tables=c["block_tables"])
+    out = attn(c["q"], c["k_new"], c["v_new"], gate=gate).squeeze(1)
+    reset_context()
+    ref = kernels.paged_decode(c["q"].unsqueeze(1), c["k_cache"], c["v_cache"], c["context_lens"],
+                               c["block_tables"], c["scale"], gate=gate).squeeze(1)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
