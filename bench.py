@@ -58,13 +58,13 @@ def _second_pool(case):
     return k2, v2
 
 
-def bench_decode(name, steps, warmup, seed=0):
+def bench_decode(name, steps, warmup, seed=0, **override):
     import torch
     from nano_qwen_amd import kernels
     from oracle.inputs import decode_bytes, decode_flops, make_decode_case
 
     dev = torch.device("cuda:0")
-    case = make_decode_case(name, seed=seed, device=dev)
+    case = make_decode_case(name, seed=seed, device=dev, **override)
     pools = [(case["k_cache"], case["v_cache"]), _second_pool(case)]
     out = torch.empty(case["batch"], 1, case["hq"], case["d"], dtype=case["q"].dtype, device=dev)
     q = case["q"].unsqueeze(1)
@@ -319,7 +319,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None,
-                    help="run one config (cfg2|cfg3|cfg4|cfg5|cfg3_norm_rope|cfg2_norm_rope|cfg2_gate|cfg3_gate)")
+                    help="run one config (cfg2|cfg3|cfg4|cfg5|cfg3_norm_rope|cfg2_norm_rope|cfg2_gate|cfg3_gate|"
+                         "cfg2_d256|cfg5_d256)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration)")
     args = ap.parse_args()
@@ -340,7 +341,7 @@ def main():
     extra = {}
     head = None
     todo = [args.only] if args.only else ["cfg2", "cfg3", "cfg4", "cfg5", "cfg3_norm_rope", "cfg2_norm_rope",
-                                                   "cfg2_gate", "cfg3_gate"]
+                                                   "cfg2_gate", "cfg3_gate", "cfg2_d256", "cfg5_d256"]
     cpu = None
     for name in todo:
         print(f"[bench] {name} ...", file=sys.stderr, flush=True)
@@ -348,6 +349,10 @@ def main():
             r, case = bench_norm_rope(name.split("_")[0], args.steps, args.warmup)
         elif name.endswith("_gate"):
             r, case = bench_gate(name.split("_")[0], args.steps, args.warmup)
+        elif name.endswith("_d256"):
+            # head_dim 256 (Qwen3.5's full-attention layers) with cfg2's / cfg5's
+            # KV bytes per token: Hkv * D = 4 * 256
+            r, case = bench_decode(name.split("_")[0], args.steps, args.warmup, d=256, hq=16, hkv=4)
         elif name == "cfg3":
             r, case = bench_prefill(name, args.steps, args.warmup)
             if not args.no_cpu:

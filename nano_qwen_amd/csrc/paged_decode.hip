@@ -80,7 +80,10 @@ struct Geo {
   static constexpr int TOK_PER_LOAD = 64 / SRC_CHUNKS;   // tokens covered by one load instruction
   static constexpr int RAW = kStep / TOK_PER_LOAD;       // load instructions per 32-token step
   static constexpr int TILE_B = kStep * ROWB;            // LDS bytes per wave
-  static_assert(CHUNKS == 16, "swizzle below assumes 16 chunks per row (D = 128)");
+  // The swizzle below permutes chunks within aligned groups of 16; rows are a
+  // multiple of 256 bytes apart, so a group's 16 chunks hit 16 distinct bank
+  // quads for D = 128 and D = 256 alike.
+  static_assert(CHUNKS % 16 == 0, "rows of whole 16-chunk groups");
 };
 
 // XOR swizzle of 16-byte chunks within an LDS row (row index mod 16).  It is
@@ -394,7 +397,8 @@ int decode_heads_per_wg(int hkv, bool fp8) {
 template <class T, bool FP8, int D>
 int launch_decode(const DecodeArgs &a, int batch, hipStream_t s) {
   using W = DecodeWave<T, FP8, D>;
-  const int hpw = decode_heads_per_wg(a.Hkv, FP8);
+  int hpw = decode_heads_per_wg(a.Hkv, FP8);
+  if constexpr (D == 256 && !FP8) hpw = 4;  // eight waves of ~360 registers do not fit a CU
   dim3 grid(a.num_splits, (a.Hkv + hpw - 1) / hpw, batch);
   const size_t lds = static_cast<size_t>(hpw) * W::LDS_PER_WAVE_B;
   // Register budget per wave = in-flight K/V (DEPTH steps) + state: two
@@ -403,7 +407,15 @@ int launch_decode(const DecodeArgs &a, int batch, hipStream_t s) {
   const int depth_env = env_int("NQ_DECODE_DEPTH", 0);
   const int depth = depth_env == 1 || depth_env == 2 ? depth_env : 2;
 #define NQ_DECODE_LAUNCH(H, DP, WP) paged_decode_kernel<T, FP8, D, H, DP, WP><<<grid, 64 * H, lds, s>>>(a)
-  if (hpw == 8) {
+  if constexpr (D == 256) {
+    // Twice the raw K/V per step: one step in flight, one wave per SIMD.
+    if constexpr (FP8) {
+      if (hpw == 8) NQ_DECODE_LAUNCH(8, 1, 1);
+      else NQ_DECODE_LAUNCH(4, 1, 1);
+    } else {
+      NQ_DECODE_LAUNCH(4, 1, 1);
+    }
+  } else if (hpw == 8) {
     if (depth == 2) NQ_DECODE_LAUNCH(8, 2, FP8 ? 3 : 2);
     else NQ_DECODE_LAUNCH(8, 1, FP8 ? 4 : 3);
   } else {
@@ -486,7 +498,8 @@ static int paged_decode_impl(const void *q, int64_t q_batch_stride, int64_t q_he
                 num_kv_heads);
   const int G = num_q_heads / num_kv_heads;
   if (G > 16) return fail(NQ_EUNSUPPORTED, "paged_decode: GQA group %d > 16", G);
-  if (head_dim != 128) return fail(NQ_EUNSUPPORTED, "paged_decode: head_dim %d (built: 128)", head_dim);
+  if (head_dim != 128 && head_dim != 256)
+    return fail(NQ_EUNSUPPORTED, "paged_decode: head_dim %d (built: 128, 256)", head_dim);
   if (block_size <= 0 || block_size % 32 != 0)
     return fail(NQ_EUNSUPPORTED, "paged_decode: block_size %d must be a multiple of 32", block_size);
   if (q_dtype != NQ_BF16 && q_dtype != NQ_F16)
@@ -546,8 +559,12 @@ static int paged_decode_impl(const void *q, int64_t q_batch_stride, int64_t q_he
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (q_dtype == NQ_BF16)
-    return fp8 ? launch_decode<BF16, true, 128>(a, batch, s) : launch_decode<BF16, false, 128>(a, batch, s);
-  return fp8 ? launch_decode<F16, true, 128>(a, batch, s) : launch_decode<F16, false, 128>(a, batch, s);
+    return head_dim == 256
+               ? (fp8 ? launch_decode<BF16, true, 256>(a, batch, s) : launch_decode<BF16, false, 256>(a, batch, s))
+               : (fp8 ? launch_decode<BF16, true, 128>(a, batch, s) : launch_decode<BF16, false, 128>(a, batch, s));
+  return head_dim == 256
+             ? (fp8 ? launch_decode<F16, true, 256>(a, batch, s) : launch_decode<F16, false, 256>(a, batch, s))
+             : (fp8 ? launch_decode<F16, true, 128>(a, batch, s) : launch_decode<F16, false, 128>(a, batch, s));
 }
 
 extern "C" int nq_paged_decode(const void *q, int64_t q_batch_stride, int64_t q_head_stride,

@@ -205,3 +205,22 @@ def test_decode_fp8_vs_bf16_dequantized_reference(cuda):
     ref = P.paged_decode(f64(case["q"]).astype(np.float32), f64(ks).astype(np.float32),
                          f64(vs).astype(np.float32), table, case["context_lens"].cpu().numpy(), case["scale"])
     assert_close(f64(out[ids, 0]), ref, **TOL_FP8, what="fp8 vs bf16-dequantized fp32 reference")
+
+
+@pytest.mark.parametrize("kv", ["same", "fp8"])
+@pytest.mark.parametrize("split", [0, 512])
+def test_decode_head_dim_256(cuda, kv, split, monkeypatch):
+    """head_dim 256, the reference model's own full-attention layers
+    (models/qwen3_5.py:69-72 with the transformers default), one- and
+    multi-split plans, 16-bit and fp8 caches."""
+    if split:
+        monkeypatch.setenv("NQ_DECODE_SPLIT_TOKENS", str(split))
+    name = "cfg5" if kv == "fp8" else "cfg2"
+    case = make_decode_case(name, seed=7 + split, device=cuda, batch=6, ctx=(1, 1500), d=256, hq=16, hkv=2)
+    check(case, range(6), TOL_FP8 if kv == "fp8" else TOL_BF16)
+
+
+def test_decode_head_dim_256_f16_groups(cuda):
+    case = make_decode_case("cfg2", seed=9, device=cuda, batch=4, ctx=(300, 900), d=256, hq=8, hkv=8,
+                            dtype=torch.float16)
+    check(case, range(4), TOL_BF16)
