@@ -101,13 +101,13 @@ def bench_decode(name, steps, warmup, seed=0, **override):
     return res, case
 
 
-def bench_prefill(name, steps, warmup, seed=0):
+def bench_prefill(name, steps, warmup, seed=0, **override):
     import torch
     from nano_qwen_amd import kernels
     from oracle.inputs import make_prefill_case, prefill_bytes, prefill_flops
 
     dev = torch.device("cuda:0")
-    case = make_prefill_case(name, seed=seed, device=dev)
+    case = make_prefill_case(name, seed=seed, device=dev, **override)
     out = torch.empty_like(case["q"])
 
     def attn(i):
@@ -320,7 +320,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None,
                     help="run one config (cfg2|cfg3|cfg4|cfg5|cfg3_norm_rope|cfg2_norm_rope|cfg2_gate|cfg3_gate|"
-                         "cfg2_d256|cfg5_d256)")
+                         "cfg2_d256|cfg5_d256|cfg3_d256)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration)")
     args = ap.parse_args()
@@ -341,7 +341,8 @@ def main():
     extra = {}
     head = None
     todo = [args.only] if args.only else ["cfg2", "cfg3", "cfg4", "cfg5", "cfg3_norm_rope", "cfg2_norm_rope",
-                                                   "cfg2_gate", "cfg3_gate", "cfg2_d256", "cfg5_d256"]
+                                                   "cfg2_gate", "cfg3_gate", "cfg2_d256", "cfg5_d256",
+                                                   "cfg3_d256"]
     cpu = None
     for name in todo:
         print(f"[bench] {name} ...", file=sys.stderr, flush=True)
@@ -349,6 +350,8 @@ def main():
             r, case = bench_norm_rope(name.split("_")[0], args.steps, args.warmup)
         elif name.endswith("_gate"):
             r, case = bench_gate(name.split("_")[0], args.steps, args.warmup)
+        elif name == "cfg3_d256":
+            r, case = bench_prefill("cfg3", args.steps, args.warmup, d=256, hq=16, hkv=4)
         elif name.endswith("_d256"):
             # head_dim 256 (Qwen3.5's full-attention layers) with cfg2's / cfg5's
             # KV bytes per token: Hkv * D = 4 * 256

@@ -127,7 +127,9 @@ inline int64_t work_grid(int64_t n_x, int64_t U) { return U >= 8 ? 8 * ((U + 7) 
 
 template <class T, bool FP8, int D>
 struct PTile {
-  static_assert(D == 128, "tile layout assumes head_dim 128");
+  // swz() permutes chunks within aligned groups of 16 and rows are a multiple
+  // of 256 bytes apart, so the reads stay conflict-free at D = 256 too.
+  static_assert(D == 128 || D == 256, "head_dim 128 or 256");
   static constexpr int ROWB = D * 2;            // LDS row: one key, 16-bit elements
   static constexpr int TILE_B = kKeys * ROWB;   // one K (or V) tile
   static constexpr int SRC_ROWB = FP8 ? D : D * 2;
@@ -210,8 +212,10 @@ struct PTile {
   }
 };
 
+// Two waves per SIMD at D = 128; at D = 256 the accumulators and Q operands
+// double, and one wave per SIMD holds them without spilling.
 template <class T, bool FP8, int D>
-__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2)))
 void varlen_prefill_kernel(const PrefillArgs a) {
   using PT = PTile<T, FP8, D>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -1399,7 +1403,7 @@ int launch_prefill_dma(PrefillArgs a, hipStream_t st) {
 
 template <class T, bool FP8, int D>
 int launch_prefill(PrefillArgs a, hipStream_t s) {
-  if constexpr (!FP8) {
+  if constexpr (!FP8 && D == 128) {
     switch (prefill_shape()) {
       case 'c': return launch_prefill_dma<T, D, ShapeC>(a, s);
       default: return launch_prefill_dma<T, D, ShapeA>(a, s);
@@ -1440,7 +1444,8 @@ static int varlen_prefill_impl(const void *q, int64_t q_row_stride, int64_t q_he
   const int G = num_q_heads / num_kv_heads;
   if (G > 4 && G % 4 != 0) return fail(NQ_EUNSUPPORTED, "varlen_prefill: GQA group %d (need <= 4 or a multiple of 4)", G);
   if (G == 3) return fail(NQ_EUNSUPPORTED, "varlen_prefill: GQA group 3");
-  if (head_dim != 128) return fail(NQ_EUNSUPPORTED, "varlen_prefill: head_dim %d (built: 128)", head_dim);
+  if (head_dim != 128 && head_dim != 256)
+    return fail(NQ_EUNSUPPORTED, "varlen_prefill: head_dim %d (built: 128, 256)", head_dim);
   if (q_dtype != NQ_BF16 && q_dtype != NQ_F16)
     return fail(NQ_EUNSUPPORTED, "varlen_prefill: q dtype %d (need f16/bf16)", q_dtype);
   const bool fp8 = kv_dtype == NQ_FP8_E4M3;
@@ -1490,7 +1495,7 @@ static int varlen_prefill_impl(const void *q, int64_t q_row_stride, int64_t q_he
   a.o_hs = out_head_stride * qsz;
   // The gate rides in the output store of the default 16-bit launch shape;
   // other launches get the same arithmetic from one in-place pass afterwards.
-  const bool fused_gate = gate && !fp8 && prefill_shape() == 'c';
+  const bool fused_gate = gate && !fp8 && head_dim == 128 && prefill_shape() == 'c';
   if (gate) {
     if ((gate_row_stride * qsz) % 16 || (gate_head_stride * qsz) % 16 || !aligned(gate, 16))
       return fail(NQ_EINVAL, "varlen_prefill_gated: gate alignment");
@@ -1520,10 +1525,16 @@ static int varlen_prefill_impl(const void *q, int64_t q_row_stride, int64_t q_he
   a.v_scale = v_scale;
   hipStream_t st = static_cast<hipStream_t>(stream);
   int rc;
-  if (q_dtype == NQ_BF16)
+  if (head_dim == 256) {
+    if (q_dtype == NQ_BF16)
+      rc = fp8 ? launch_prefill<BF16, true, 256>(a, st) : launch_prefill<BF16, false, 256>(a, st);
+    else
+      rc = fp8 ? launch_prefill<F16, true, 256>(a, st) : launch_prefill<F16, false, 256>(a, st);
+  } else if (q_dtype == NQ_BF16) {
     rc = fp8 ? launch_prefill<BF16, true, 128>(a, st) : launch_prefill<BF16, false, 128>(a, st);
-  else
+  } else {
     rc = fp8 ? launch_prefill<F16, true, 128>(a, st) : launch_prefill<F16, false, 128>(a, st);
+  }
   if (rc != NQ_OK || !gate || fused_gate) return rc;
   return nq_output_gate(out, out_row_stride, out_head_stride, gate, gate_row_stride, gate_head_stride, total_q,
                         num_q_heads, head_dim, q_dtype, stream);

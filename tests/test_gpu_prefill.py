@@ -160,3 +160,40 @@ def test_prefill_query_tile_order_past_lds_bounds(cuda):
                              hq=8, hkv=2)
     assert case["block_tables"] is None
     check(case, range(0, 1100, 7), TOL_BF16)
+
+
+@pytest.mark.parametrize("kind", ["packed", "paged", "fp8", "f16_group8"])
+def test_prefill_head_dim_256(cuda, kind):
+    """head_dim 256, the reference model's own full-attention layers
+    (models/qwen3_5.py:69-72 with the transformers default): packed and paged
+    K/V, fp8 K/V, and f16 with a GQA group of 8."""
+    kw = dict(nseq=4, lq=(1, 600), d=256, hq=16, hkv=4)
+    if kind == "packed":
+        case = make_prefill_case("cfg3", seed=20, device=cuda, prefix_blocks=(0, 0), **kw)
+    elif kind == "paged":
+        case = make_prefill_case("cfg3", seed=21, device=cuda, prefix_blocks=(1, 3), **kw)
+    elif kind == "fp8":
+        case = make_prefill_case("cfg3", seed=22, device=cuda, prefix_blocks=(1, 2), kv="fp8", **kw)
+    else:
+        kw.update(hq=16, hkv=2)
+        case = make_prefill_case("cfg3", seed=23, device=cuda, prefix_blocks=(1, 2), dtype=torch.float16, **kw)
+    check(case, range(4), TOL_FP8 if kind == "fp8" else TOL_BF16)
+
+
+def test_prefill_head_dim_256_gated(cuda):
+    """The output gate at head_dim 256 (the in-place pass follows the kernel)."""
+    from oracle.output_gate import output_gate as gate_ref
+    case = make_prefill_case("cfg3", seed=24, device=cuda, nseq=3, lq=(50, 500), prefix_blocks=(1, 2),
+                             d=256, hq=16, hkv=4)
+    run_step(case)
+    tq, hq, d = case["q"].shape
+    g = torch.Generator().manual_seed(5)
+    gate = (torch.randn(tq, hq, 2 * d, generator=g) * 3).to(torch.bfloat16).to(cuda)[..., d:]
+    args = (case["q"], case["k_cache"], case["v_cache"], case["cu_seqlens_q"], case["cu_seqlens_k"],
+            case["max_seqlen_q"], case["max_seqlen_k"], case["scale"])
+    plain = kernels.varlen_prefill(*args, block_table=case["block_tables"])
+    gated = kernels.varlen_prefill(*args, block_table=case["block_tables"], gate=gate)
+    torch.cuda.synchronize()
+    ref = torch.from_numpy(gate_ref(plain.float().cpu().numpy(), gate.float().cpu().numpy(), "bf16"))
+    diff = (gated.cpu().view(torch.int16).int() - ref.to(torch.bfloat16).view(torch.int16).int()).abs()
+    assert int(diff.max()) <= 1 and float((diff > 0).float().mean()) <= 1e-3
