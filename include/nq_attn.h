@@ -90,6 +90,7 @@ int64_t nq_decode_workspace_bytes(int batch, int num_q_heads, int head_dim,
  *   cache_seqlens=context_lens, block_table=block_tables,
  *   softmax_scale=scale, causal=True)   (layers/attention.py:71-74).
  *
+ * head_dim is 128 or 256 (NQ_EUNSUPPORTED otherwise).
  * q   [batch, num_q_heads, head_dim] with strides (q_batch_stride,
  *     q_head_stride, 1); out likewise.  q and out have type q_dtype
  *     (F16/BF16).  k_cache/v_cache have type kv_dtype (== q_dtype, or
@@ -158,6 +159,7 @@ int nq_output_gate(void *out, int64_t out_row_stride, int64_t out_head_stride,
  *   max_seqlen_q=..., max_seqlen_k=..., softmax_scale=scale, causal=True,
  *   block_table=block_tables)   (layers/attention.py:64-70).
  *
+ * head_dim is 128 or 256 (NQ_EUNSUPPORTED otherwise).
  * q [total_q, num_q_heads, head_dim] (strides q_row_stride, q_head_stride, 1),
  * out likewise.  Sequence s owns query rows [cu_q[s], cu_q[s+1]) and
  * Lk = cu_k[s+1]-cu_k[s] keys; query row i (0-based in s) sees keys
