@@ -41,7 +41,6 @@ namespace {
 
 constexpr int kPWaves = 4;
 constexpr int kPThreads = 64 * kPWaves;
-constexpr int kRows = 32;    // query rows per wave
 constexpr int kKeys = 32;    // keys per LDS tile
 constexpr int kMaxBt = 4096;  // block-table entries staged in LDS (1M tokens at 256)
 constexpr float kRescale = 8.0f;  // log2 growth of a row max that forces a rescale
@@ -212,11 +211,17 @@ struct PTile {
   }
 };
 
-// Two waves per SIMD at D = 128; at D = 256 the accumulators and Q operands
-// double, and one wave per SIMD holds them without spilling.
+// Query rows per wave of the register-staged kernel: 32 at D = 128; 16 at
+// D = 256, where the accumulators and Q operands of each row double, so that
+// two waves per SIMD still fit.
+template <int D>
+constexpr int kRegQS = D == 256 ? 1 : 2;
+
 template <class T, bool FP8, int D>
-__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2)))
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void varlen_prefill_kernel(const PrefillArgs a) {
+  constexpr int QS = kRegQS<D>;       // 16-row sub-tiles per wave
+  constexpr int RW = 16 * QS;         // query rows per wave
   using PT = PTile<T, FP8, D>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   int32_t *lds_bt = reinterpret_cast<int32_t *>(smem + 4 * PT::TILE_B);
@@ -231,11 +236,11 @@ void varlen_prefill_kernel(const PrefillArgs a) {
   const int rb = 4 / a.G4;  // row blocks of 32 per workgroup
   const int head = kvh * a.G + quad * 4 + (wave % a.G4);
   const int q0 = a.cu_q[s], Lq = a.cu_q[s + 1] - q0;
-  const int row_begin = qt * kRows * rb;
+  const int row_begin = qt * RW * rb;
   if (row_begin >= Lq) return;
   const int k0 = a.cu_k[s], Lk = a.cu_k[s + 1] - k0;
   const int P = Lk - Lq;
-  const int row_last = min(row_begin + kRows * rb, Lq) - 1;
+  const int row_last = min(row_begin + RW * rb, Lq) - 1;
   const int key_end = a.causal ? max(0, min(Lk, row_last + P + 1)) : Lk;
   const int n_kt = (key_end + kKeys - 1) / kKeys;
 
@@ -249,15 +254,15 @@ void varlen_prefill_kernel(const PrefillArgs a) {
     for (int i = threadIdx.x; i < n_bt; i += kPThreads) lds_bt[i] = a.block_tables[s * a.bt_stride + i];
   }
 
-  // This wave's rows: wrow0 .. wrow0+31 (two 16-row sub-tiles).
-  const int wrow0 = row_begin + kRows * (wave / a.G4);
+  // This wave's rows: wrow0 .. wrow0 + RW - 1 (QS 16-row sub-tiles).
+  const int wrow0 = row_begin + RW * (wave / a.G4);
   const bool wave_live = wrow0 < Lq;
-  const int wrow_last = min(wrow0 + kRows - 1, Lq - 1);
+  const int wrow_last = min(wrow0 + RW - 1, Lq - 1);
   const int wave_key_end = a.causal ? min(Lk, wrow_last + P + 1) : Lk;
 
-  u32x4 qf[2][PT::NKK];
+  u32x4 qf[QS][PT::NKK];
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
+  for (int qs = 0; qs < QS; ++qs) {
     const int r = wrow0 + 16 * qs + m;
     const bool ok = r < Lq;
     const uint8_t *qp = a.q + static_cast<int64_t>(q0 + (ok ? r : 0)) * a.q_rs + static_cast<int64_t>(head) * a.q_hs;
@@ -265,10 +270,15 @@ void varlen_prefill_kernel(const PrefillArgs a) {
     for (int kk = 0; kk < PT::NKK; ++kk) qf[qs][kk] = ok ? load16(qp + (8 * g + 32 * kk) * 2) : u32x4{0, 0, 0, 0};
   }
 
-  float m_use[2] = {kNegInf, kNegInf}, l_run[2] = {0.f, 0.f};
-  f32x4 o[2][PT::NJ];
+  float m_use[QS], l_run[QS];
+  f32x4 o[QS][PT::NJ];
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs)
+  for (int qs = 0; qs < QS; ++qs) {
+    m_use[qs] = kNegInf;
+    l_run[qs] = 0.f;
+  }
+#pragma unroll
+  for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
     for (int j = 0; j < PT::NJ; ++j) o[qs][j] = f32x4{0, 0, 0, 0};
 
@@ -287,9 +297,9 @@ void varlen_prefill_kernel(const PrefillArgs a) {
     const bool more = jt + 1 < n_kt;
     if (more) PT::load(a, lds_bt, k0, kvh, kbase + kKeys, key_end, kr, vr);
     if (wave_live && kbase < wave_key_end) {
-      f32x4 sc[2][2];
+      f32x4 sc[QS][2];
 #pragma unroll
-      for (int qs = 0; qs < 2; ++qs)
+      for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = f32x4{0, 0, 0, 0};
 #pragma unroll
@@ -298,14 +308,14 @@ void varlen_prefill_kernel(const PrefillArgs a) {
         for (int ks = 0; ks < 2; ++ks) {
           const u32x4 kf = PT::kfrag(kt, ks, kk, m, g);
 #pragma unroll
-          for (int qs = 0; qs < 2; ++qs) sc[qs][ks] = T::mfma16x16x32(kf, qf[qs][kk], sc[qs][ks]);
+          for (int qs = 0; qs < QS; ++qs) sc[qs][ks] = T::mfma16x16x32(kf, qf[qs][kk], sc[qs][ks]);
         }
       }
       // mask only where the tile crosses the causal diagonal or the key end
       const bool need_mask = kbase + kKeys - 1 > wrow0 + P || kbase + kKeys > Lk;
-      u32x4 pb[2];
+      u32x4 pb[QS];
 #pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
+      for (int qs = 0; qs < QS; ++qs) {
         const int row = wrow0 + 16 * qs + m;
         const int lim = a.causal ? min(Lk - 1, row + P) : Lk - 1;  // last visible key
         float x[8];
@@ -347,7 +357,7 @@ void varlen_prefill_kernel(const PrefillArgs a) {
       for (int j = 0; j < PT::NJ; ++j) {
         const u32x4 vf = PT::vfrag(vt, j, lane);
 #pragma unroll
-        for (int qs = 0; qs < 2; ++qs) o[qs][j] = T::mfma16x16x32(vf, pb[qs], o[qs][j]);
+        for (int qs = 0; qs < QS; ++qs) o[qs][j] = T::mfma16x16x32(vf, pb[qs], o[qs][j]);
       }
     }
     if (more) {
@@ -359,7 +369,7 @@ void varlen_prefill_kernel(const PrefillArgs a) {
 
   if (!wave_live) return;
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
+  for (int qs = 0; qs < QS; ++qs) {
     const float l = sum32(sum16(l_run[qs]));
     const int row = wrow0 + 16 * qs + m;
     if (row >= Lq) continue;
@@ -1517,7 +1527,9 @@ static int varlen_prefill_impl(const void *q, int64_t q_row_stride, int64_t q_he
   a.num_seqs = num_seqs;
   a.max_seqlen_q = max_seqlen_q;
   a.max_seqlen_k = max_seqlen_k;
-  const int rows_per_wg = kRows * (4 / a.G4);
+  // Query rows per workgroup of the register-staged kernel (the persistent
+  // kernel sets its own tiling at launch).
+  const int rows_per_wg = 16 * (head_dim == 256 ? kRegQS<256> : kRegQS<128>) * (4 / a.G4);
   a.n_qtiles = (max_seqlen_q + rows_per_wg - 1) / rows_per_wg;
   a.causal = causal;
   a.scale_log2 = softmax_scale * kLog2e;
