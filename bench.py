@@ -14,7 +14,9 @@ TFLOP/s and the other decode configurations are reported under ``extra``, as
 is the fused q/k norm + rotary + KV store call over cfg3's and cfg2's new
 tokens (``cfg3_norm_rope``, ``cfg2_norm_rope``: HBM GB/s), and Qwen3.5's output
 gate (``cfg2_gate``: gated vs plain decode; ``cfg3_gate``: gated vs plain
-prefill, and the stand-alone in-place gate pass for comparison).
+prefill, and the stand-alone in-place gate pass for comparison), head_dim 256
+(``cfg2_d256``, ``cfg5_d256``, ``cfg3_d256``) and the Gated DeltaNet decode
+step (``gdn_decode``: HBM GB/s over the state pool).
 ``roofline`` covers the dominant kernel of the headline workload (paged
 decode: main kernel + split-K merge), timed with HIP events on the stream
 the kernels run on.  ``cpu_baseline`` times the CPU restatement of the path
@@ -199,6 +201,29 @@ def bench_gate(name, steps, warmup, seed=0):
                 gate_pass_gbs=nb / (ms_pass * 1e-3) / 1e9, gate_pass_overhead_frac=ms_pass / ms_plain), c
 
 
+def bench_gdn(steps, warmup, seed=0, B=64, H=16, HV=32):
+    """Gated DeltaNet decode step for a batch of B sequences (Qwen3.5-style
+    linear-attention heads: H key heads, HV value heads, K = V = 128, float32
+    state pool).  HBM-bound: each (sequence, value head) state is read and
+    written once."""
+    import torch
+    from nano_qwen_amd import kernels
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    r = lambda *sh: torch.randn(*sh, device="cuda", generator=g)
+    q, k = r(B, H, 128).bfloat16(), r(B, H, 128).bfloat16()
+    v, a, b = r(B, HV, 128).bfloat16(), r(B, HV).bfloat16(), r(B, HV).bfloat16()
+    A_log, dt = r(HV) * 0.5, r(HV) * 0.5
+    state = r(2 * B, HV, 128, 128) * 0.05
+    idx = [torch.randperm(2 * B, device="cuda", generator=g)[:B].to(torch.int32) for _ in range(2)]
+    out = torch.empty(B, HV, 128, dtype=torch.bfloat16, device="cuda")
+    ms = _events_time(lambda i: kernels.gdn_decode(q, k, v, a, b, A_log, dt, state, idx[i % 2], out=out),
+                      steps, max(warmup, 50))
+    nb = 2 * B * HV * 128 * 128 * 4 + (2 * B * H * 128 + 2 * B * HV * 128 + 2 * B * HV) * 2 + B * 4
+    return dict(ms_per_step=ms, gbs=nb / (ms * 1e-3) / 1e9, hbm_frac=nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                bytes=nb, batch=B, k_heads=H, v_heads=HV), None
+
+
 def cpu_baseline_decode(case, n_seqs=8, reps=5):
     """Median wall time of the CPU path on the first n_seqs sequences."""
     import torch
@@ -320,7 +345,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None,
                     help="run one config (cfg2|cfg3|cfg4|cfg5|cfg3_norm_rope|cfg2_norm_rope|cfg2_gate|cfg3_gate|"
-                         "cfg2_d256|cfg5_d256|cfg3_d256)")
+                         "cfg2_d256|cfg5_d256|cfg3_d256|gdn_decode)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration)")
     args = ap.parse_args()
@@ -342,7 +367,7 @@ def main():
     head = None
     todo = [args.only] if args.only else ["cfg2", "cfg3", "cfg4", "cfg5", "cfg3_norm_rope", "cfg2_norm_rope",
                                                    "cfg2_gate", "cfg3_gate", "cfg2_d256", "cfg5_d256",
-                                                   "cfg3_d256"]
+                                                   "cfg3_d256", "gdn_decode"]
     cpu = None
     for name in todo:
         print(f"[bench] {name} ...", file=sys.stderr, flush=True)
@@ -350,6 +375,8 @@ def main():
             r, case = bench_norm_rope(name.split("_")[0], args.steps, args.warmup)
         elif name.endswith("_gate"):
             r, case = bench_gate(name.split("_")[0], args.steps, args.warmup)
+        elif name == "gdn_decode":
+            r, case = bench_gdn(args.steps, args.warmup)
         elif name == "cfg3_d256":
             r, case = bench_prefill("cfg3", args.steps, args.warmup, d=256, hq=16, hkv=4)
         elif name.endswith("_d256"):

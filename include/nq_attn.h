@@ -279,6 +279,38 @@ int nq_qk_norm_rope_store(const void *q, int64_t q_row_stride, int64_t q_head_st
                           int dtype, int cache_dtype,
                           const float *k_scale, const float *v_scale, void *stream);
 
+/*
+ * Gated DeltaNet decode step for a whole batch, on a pool of recurrent
+ * states updated in place.  Replaces decode_gated_delta_rule
+ * (layers/gated_delta_net.py:85-122, FlashInfer's
+ * gated_delta_rule_decode_pretranspose with use_qk_l2norm=True, called once
+ * per sequence by models/qwen3_5.py:226-240) together with the state slot's
+ * read and write around it (layers/gated_delta_net.py:168-173, 250-262).
+ *
+ * For sequence b < batch with slot = state_indices[b] in [0, num_slots)
+ * (other slots: the sequence is skipped, out untouched) and value head hv
+ * (key head h = hv / (num_v_heads / num_k_heads)), S = state[slot, hv]
+ * ([head_v_dim, head_k_dim] fp32, K-last), in fp32:
+ *   q, k = x / sqrt(sum(x^2) + 1e-6) of q[b, h], k[b, h]
+ *   g    = -exp(A_log[hv]) * softplus(a[b, hv] + dt_bias[hv])
+ *          (softplus(x) = x for x > 20, else log1p(exp(x)))
+ *   beta = sigmoid(b[b, hv])
+ *   S    = exp(g) * S;  u = beta * (v[b, hv] - S k);  S = S + u k^T
+ *   out[b, hv] = S q / sqrt(head_k_dim)       (rounded to dtype)
+ * q, k [batch, num_k_heads, 128] and v, out [batch, num_v_heads, 128] are
+ * contiguous over (head, dim) with the given row strides; a, b [batch,
+ * num_v_heads]; all of type dtype (F16/BF16).  A_log, dt_bias float
+ * [num_v_heads]; state float [num_slots, num_v_heads, 128, 128], 16-byte
+ * aligned; q and k rows 8-byte aligned.  head_k_dim = head_v_dim = 128 (NQ_EUNSUPPORTED otherwise).
+ * Sequences of one call must use distinct slots.
+ */
+int nq_gdn_decode(const void *q, int64_t q_row_stride, const void *k, int64_t k_row_stride,
+                  const void *v, int64_t v_row_stride, const void *a, int64_t a_row_stride,
+                  const void *b, int64_t b_row_stride, const float *A_log, const float *dt_bias,
+                  float *state, const int32_t *state_indices, int64_t num_slots,
+                  void *out, int64_t out_row_stride, int batch, int num_k_heads, int num_v_heads,
+                  int head_k_dim, int head_v_dim, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

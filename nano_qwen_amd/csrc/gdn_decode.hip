@@ -1,0 +1,205 @@
+// Gated DeltaNet decode step over a pool of recurrent states (gfx950).
+//
+// Reference: decode_gated_delta_rule (layers/gated_delta_net.py:85-122),
+// which calls FlashInfer's gated_delta_rule_decode_pretranspose once per
+// sequence (models/qwen3_5.py:226-240 loops over the batch), after reading
+// and before writing the sequence's state slot (layers/gated_delta_net.py:
+// 168-173, 250-262).  Per sequence b and value head hv (key head
+// h = hv / (HV / H)), with the state S [V, K] ("K-last") of slot
+// state_indices[b]:
+//   q, k  <- x / sqrt(sum(x^2) + 1e-6)            (fp32, use_qk_l2norm)
+//   g      = -exp(A_log[hv]) * softplus(a + dt_bias[hv])
+//   beta   = sigmoid(b)
+//   S     <- exp(g) * S
+//   u      = beta * (v - S k)
+//   S     <- S + u k^T
+//   o      = S (q * K^-1/2)
+// Here one launch covers the whole batch and updates the pool in place.
+//
+// One one-wave workgroup per (sequence, value head, 16-row slice of the
+// state), K = V = 128: no workgroup barrier, many small workgroups, and few
+// enough registers for five waves per SIMD.  The wave owning rows
+// 16w .. 16w + 15 reads with load i of lane l the 16 bytes at row
+// 16w + 2i + l/32, columns 4(l%32) .. +3: every load instruction covers
+// 1 KiB of contiguous state, so the 64 KiB state is read and written once,
+// fully coalesced.  Each wave normalizes q and k itself from its lanes' 4
+// columns (a 32-lane reduction).  A row's dot products (S k, S q) are spread
+// over the 32 lanes of a half-wave and summed by a reduce-scatter
+// (reduce_rows); the per-row update factor goes back to the lanes through
+// LDS.
+#include "nq_device.hpp"
+
+namespace nq {
+namespace {
+
+constexpr int kThreads = 64;
+constexpr int kDim = 128;   // K = V
+
+struct GdnArgs {
+  const uint8_t *q, *k, *v;  // [B, H, K], [B, H, K], [B, HV, V] (rows of heads, dtype T)
+  int64_t q_rs, k_rs, v_rs;  // bytes per token row
+  const uint8_t *a, *b;      // [B, HV] (dtype T)
+  int64_t a_rs, b_rs;        // bytes per token row
+  const float *A_log;        // [HV]
+  const float *dt_bias;      // [HV]
+  float *state;              // [num_slots, HV, V, K]
+  const int32_t *idx;        // [B]
+  int64_t num_slots;
+  uint8_t *out;              // [B, HV, V]
+  int64_t o_rs;              // bytes per token row
+  int H, HV;
+  float eps, scale;
+};
+
+template <class T>
+__device__ inline float elem(const uint8_t *p, int i) {
+  return T::to_float(reinterpret_cast<const uint16_t *>(p)[i]);
+}
+
+__device__ inline float softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+
+// Sum of p[i] over the 32 lanes of a half-wave, for N values i per lane
+// (N = 8 or 16): a reduce-scatter over lane bits 4, 3, ... (N/2 + N/4 + ... + 1
+// exchanges) leaves value i = (l >> (5 - log2 N)) & (N - 1) in lane l, and
+// exchanges over the remaining low bits complete the sum in those lanes.
+template <int N>
+__device__ inline float reduce_rows(float (&p)[N], int lane) {
+#pragma unroll
+  for (int m = 16, c = N; c >= 2; m >>= 1, c >>= 1) {
+    const bool hi = (lane & m) != 0;
+#pragma unroll
+    for (int j = 0; j < c / 2; ++j) {
+      const float keep = hi ? p[j + c / 2] : p[j];
+      const float send = hi ? p[j] : p[j + c / 2];
+      p[j] = keep + __shfl_xor(send, m, 64);
+    }
+  }
+  float r = p[0];
+#pragma unroll
+  for (int m = 16 / N; m >= 1; m >>= 1) r += __shfl_xor(r, m, 64);
+  return r;
+}
+
+// Rows of the state per wave: 2 * kLoads (16 -> five waves per SIMD fit).
+constexpr int kLoads = 8;
+constexpr int kRowsW = 2 * kLoads;
+constexpr int kSh = kLoads == 16 ? 1 : 2;  // lane bits below the row index after reduce_rows
+
+template <class T>
+__global__ __launch_bounds__(kThreads) void gdn_decode_kernel(const GdnArgs a) {
+  const int hv = blockIdx.x, bi = blockIdx.y, w = blockIdx.z;
+  const int lane = threadIdx.x;
+  const int32_t slot = a.idx[bi];
+  if (slot < 0 || slot >= a.num_slots) return;  // padded row: no state to advance
+  const int h = hv / (a.HV / a.H);
+  const int r0 = kRowsW * w + (lane >> 5);  // row of load 0; load i adds 2i
+  const int c0 = 4 * (lane & 31);       // this lane's 4 columns
+
+  // 16 coalesced loads of the state, issued first.
+  float *sp = a.state + ((static_cast<int64_t>(slot) * a.HV + hv) * kDim + r0) * kDim + c0;
+  f32x4 s[kLoads];
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i)
+    s[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(sp + 2 * i * kDim));
+
+  // This lane's 4 columns of q and k, l2-normalized over the 32 lanes that
+  // cover all 128 columns; q also carries the scale.
+  const u32x2 qr = *reinterpret_cast<const u32x2 *>(a.q + bi * a.q_rs + (h * kDim + c0) * 2);
+  const u32x2 kr = *reinterpret_cast<const u32x2 *>(a.k + bi * a.k_rs + (h * kDim + c0) * 2);
+  f32x4 qc{T::to_float(qr[0] & 0xffffu), T::to_float(qr[0] >> 16), T::to_float(qr[1] & 0xffffu),
+           T::to_float(qr[1] >> 16)};
+  f32x4 kc{T::to_float(kr[0] & 0xffffu), T::to_float(kr[0] >> 16), T::to_float(kr[1] & 0xffffu),
+           T::to_float(kr[1] >> 16)};
+  float sq = qc[0] * qc[0] + qc[1] * qc[1] + qc[2] * qc[2] + qc[3] * qc[3];
+  float sk = kc[0] * kc[0] + kc[1] * kc[1] + kc[2] * kc[2] + kc[3] * kc[3];
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1) {
+    sq += __shfl_xor(sq, off, 64);
+    sk += __shfl_xor(sk, off, 64);
+  }
+  qc *= a.scale / sqrtf(sq + a.eps);
+  kc *= 1.0f / sqrtf(sk + a.eps);
+
+  // Row (within the wave's rows) whose sums this lane ends with.
+  const int my_row = 2 * ((lane >> kSh) & (kLoads - 1)) + (lane >> 5);
+  const float vv = elem<T>(a.v + bi * a.v_rs + hv * kDim * 2, kRowsW * w + my_row);
+  const float g = -expf(a.A_log[hv]) * softplus(elem<T>(a.a + bi * a.a_rs, hv) + a.dt_bias[hv]);
+  const float decay = expf(g);
+  const float beta = 1.0f / (1.0f + expf(-elem<T>(a.b + bi * a.b_rs, hv)));
+
+  // u = beta * (v - (exp(g) S) k) for every row of the wave.
+  float p[kLoads];
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    s[i] *= decay;
+    p[i] = s[i][0] * kc[0] + s[i][1] * kc[1] + s[i][2] * kc[2] + s[i][3] * kc[3];
+  }
+  const float u = beta * (vv - reduce_rows(p, lane));
+  __shared__ float urow[kRowsW];
+  const bool writer = (lane & ((1 << kSh) - 1)) == 0;
+  if (writer) urow[my_row] = u;  // one wave: LDS accesses stay in order
+  // S += u k^T, then o = S q.
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    const float ui = urow[2 * i + (lane >> 5)];
+    s[i] += ui * kc;
+    p[i] = s[i][0] * qc[0] + s[i][1] * qc[1] + s[i][2] * qc[2] + s[i][3] * qc[3];
+    __builtin_nontemporal_store(s[i], reinterpret_cast<f32x4 *>(sp + 2 * i * kDim));
+  }
+  const float o = reduce_rows(p, lane);
+  if (writer) reinterpret_cast<uint16_t *>(a.out + bi * a.o_rs + hv * kDim * 2)[kRowsW * w + my_row] = T::from_float(o);
+}
+
+}  // namespace
+}  // namespace nq
+
+using namespace nq;
+
+extern "C" int nq_gdn_decode(const void *q, int64_t q_row_stride, const void *k, int64_t k_row_stride,
+                             const void *v, int64_t v_row_stride, const void *a, int64_t a_row_stride,
+                             const void *b, int64_t b_row_stride, const float *A_log, const float *dt_bias,
+                             float *state, const int32_t *state_indices, int64_t num_slots, void *out,
+                             int64_t out_row_stride, int batch, int num_k_heads, int num_v_heads,
+                             int head_k_dim, int head_v_dim, int dtype, void *stream) {
+  if (batch < 0 || num_k_heads <= 0 || num_v_heads <= 0 || num_slots < 0)
+    return fail(NQ_EINVAL, "gdn_decode: bad sizes (batch=%d heads=%d/%d)", batch, num_k_heads, num_v_heads);
+  if (num_v_heads % num_k_heads != 0)
+    return fail(NQ_EINVAL, "gdn_decode: value heads %d not a multiple of key heads %d", num_v_heads, num_k_heads);
+  if (head_k_dim != kDim || head_v_dim != kDim)
+    return fail(NQ_EUNSUPPORTED, "gdn_decode: head dims %d/%d (built: 128/128)", head_k_dim, head_v_dim);
+  if (dtype != NQ_BF16 && dtype != NQ_F16) return fail(NQ_EUNSUPPORTED, "gdn_decode: dtype %d (f16/bf16)", dtype);
+  if (batch == 0) return NQ_OK;
+  if (!q || !k || !v || !a || !b || !A_log || !dt_bias || !state || !state_indices || !out)
+    return fail(NQ_EINVAL, "gdn_decode: null pointer");
+  if (!aligned(state, 16)) return fail(NQ_EINVAL, "gdn_decode: state must be 16-byte aligned");
+  if (!aligned(q, 8) || !aligned(k, 8) || (q_row_stride * 2) % 8 || (k_row_stride * 2) % 8)
+    return fail(NQ_EINVAL, "gdn_decode: q and k rows must be 8-byte aligned");
+  if (batch > 65535 || num_v_heads > 65535) return fail(NQ_EINVAL, "gdn_decode: grid too large");
+  GdnArgs g{};
+  g.q = static_cast<const uint8_t *>(q);
+  g.k = static_cast<const uint8_t *>(k);
+  g.v = static_cast<const uint8_t *>(v);
+  g.q_rs = q_row_stride * 2;
+  g.k_rs = k_row_stride * 2;
+  g.v_rs = v_row_stride * 2;
+  g.a = static_cast<const uint8_t *>(a);
+  g.b = static_cast<const uint8_t *>(b);
+  g.a_rs = a_row_stride * 2;
+  g.b_rs = b_row_stride * 2;
+  g.A_log = A_log;
+  g.dt_bias = dt_bias;
+  g.state = state;
+  g.idx = state_indices;
+  g.num_slots = num_slots;
+  g.out = static_cast<uint8_t *>(out);
+  g.o_rs = out_row_stride * 2;
+  g.H = num_k_heads;
+  g.HV = num_v_heads;
+  g.eps = 1e-6f;
+  g.scale = 1.0f / sqrtf(static_cast<float>(head_k_dim));
+  dim3 grid(num_v_heads, batch, kDim / kRowsW);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == NQ_BF16) gdn_decode_kernel<BF16><<<grid, kThreads, 0, s>>>(g);
+  else gdn_decode_kernel<F16><<<grid, kThreads, 0, s>>>(g);
+  return check_launch("gdn_decode");
+}

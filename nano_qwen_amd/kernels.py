@@ -291,6 +291,46 @@ def qk_norm_rope_store(positions, query, key, value, q_weight, k_weight, eps, co
     return q_out, k_out
 
 
+def gdn_decode(query, key, value, a, b, A_log, dt_bias, state, state_indices, out=None):
+    """Gated DeltaNet decode step for a batch; ``state`` is updated in place.
+
+    Replaces ``decode_gated_delta_rule`` (layers/gated_delta_net.py:85-122)
+    and the state slot's read/write around it, for all sequences at once:
+    ``query/key [B, H, K]`` (or ``[B, 1, H, K]``), ``value [B, HV, V]``,
+    ``a/b [B, HV]``, ``A_log/dt_bias [HV]`` (float32), ``state`` the float32
+    pool ``[num_slots, HV, V, K]`` and ``state_indices [B]`` int32 (slots
+    outside the pool skip their sequence).  Key heads map to value heads as
+    ``h = hv // (HV // H)`` (the reference's repeat_interleave).  Returns
+    ``out [B, HV, V]``.
+    """
+    require_cuda(query, key, value, a, b, A_log, dt_bias, state, state_indices, what="gdn_decode")
+    q3 = query.reshape(query.shape[0], -1, query.shape[-1]) if query.dim() == 4 else query
+    k3 = key.reshape(key.shape[0], -1, key.shape[-1]) if key.dim() == 4 else key
+    v3 = value.reshape(value.shape[0], -1, value.shape[-1]) if value.dim() == 4 else value
+    B, H, K = q3.shape
+    _, HV, V = v3.shape
+    for t, what in ((q3, "query"), (k3, "key"), (v3, "value")):
+        if t.stride(-1) != 1 or t.stride(1) != t.shape[-1] or t.dtype != q3.dtype:
+            raise RuntimeError(f"gdn_decode: {what} must be [B, heads, dim] contiguous over (head, dim)")
+    a2, b2 = a.reshape(B, HV), b.reshape(B, HV)
+    if a2.stride(-1) != 1 or b2.stride(-1) != 1 or a2.dtype != q3.dtype or b2.dtype != q3.dtype:
+        raise RuntimeError("gdn_decode: a and b must be [B, HV] rows of the query's dtype")
+    if A_log.dtype != torch.float32 or dt_bias.dtype != torch.float32:
+        raise RuntimeError("gdn_decode: A_log and dt_bias must be float32")
+    if state.dtype != torch.float32 or not state.is_contiguous() or state.shape[1:] != (HV, V, K):
+        raise RuntimeError("gdn_decode: state must be a contiguous float32 pool [slots, HV, V, K]")
+    if state_indices.dtype != torch.int32 or state_indices.numel() != B:
+        raise RuntimeError("gdn_decode: state_indices must be int32 [B]")
+    if out is None:
+        out = torch.empty(B, HV, V, dtype=q3.dtype, device=q3.device)
+    rc = lib().nq_gdn_decode(ptr(q3), q3.stride(0), ptr(k3), k3.stride(0), ptr(v3), v3.stride(0), ptr(a2),
+                             a2.stride(0), ptr(b2), b2.stride(0), ptr(A_log.contiguous()),
+                             ptr(dt_bias.contiguous()), ptr(state), ptr(state_indices), state.shape[0],
+                             ptr(out), out.stride(0), B, H, HV, K, V, dtype_code(q3.dtype), stream_of(q3))
+    check(rc, "gdn_decode")
+    return out
+
+
 __all__ = ["store_kvcache", "paged_decode", "varlen_prefill", "prepare_decode", "decode_plan", "qk_norm_rope_store",
-           "output_gate",
+           "output_gate", "gdn_decode",
            "decode_workspace", "prefill_workspace", "_lib"]

@@ -1,0 +1,63 @@
+"""Gated DeltaNet recurrent step, restated in numpy float64.
+
+TEST INFRASTRUCTURE ONLY (see the package docstring): the checker for the
+HIP entry point ``nq_gdn_decode``.
+
+What it restates: decode_gated_delta_rule (layers/gated_delta_net.py:85-122)
+-- FlashInfer's gated_delta_rule_decode_pretranspose with in-kernel gating
+and ``use_qk_l2norm=True``, a third-party library absent here and unpinned
+(its bit-level rounding is not pinned; the restatement is the gated delta
+rule in exact arithmetic) -- with the inputs the layer prepares
+(layers/gated_delta_net.py:178-248): the gating of ``_forward_prefill``
+(g = -exp(A_log) * softplus(a + dt_bias), beta = sigmoid(b), :197-198), the
+q/k l2 norm of layers/fla/l2norm.py (x / sqrt(sum(x^2) + 1e-6)), the
+default scale K^-1/2 (layers/fla/chunk.py:106-107), the key-head
+repeat_interleave for GQA (:199-201), and the state pool slot read and
+written around the call (:168-173, 250-262).  State layout [V, K] (K-last).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def softplus(x):
+    """torch.nn.functional.softplus (beta 1, threshold 20)."""
+    x = np.asarray(x, dtype=np.float64)
+    return np.where(x > 20.0, x, np.log1p(np.exp(np.minimum(x, 20.0))))
+
+
+def l2norm(x, eps=1e-6):
+    x = np.asarray(x, dtype=np.float64)
+    return x / np.sqrt((x * x).sum(-1, keepdims=True) + eps)
+
+
+def gdn_step(S, q, k, v, a, b, A_log, dt_bias):
+    """One token of one value head: returns (o [V], S_new [V, K])."""
+    K = S.shape[1]
+    qn, kn = l2norm(q), l2norm(k)
+    g = -np.exp(np.float64(A_log)) * softplus(np.float64(a) + np.float64(dt_bias))
+    beta = 1.0 / (1.0 + np.exp(-np.float64(b)))
+    S = np.exp(g) * np.asarray(S, dtype=np.float64)
+    u = beta * (np.asarray(v, dtype=np.float64) - S @ kn)
+    S = S + np.outer(u, kn)
+    return S @ (qn * K ** -0.5), S
+
+
+def gdn_decode(q, k, v, a, b, A_log, dt_bias, state, state_indices):
+    """Batch decode step: q, k [B, H, K]; v [B, HV, V]; a, b [B, HV];
+    state [slots, HV, V, K] (updated in place, float64 copy semantics);
+    returns out [B, HV, V] (NaN rows for skipped sequences)."""
+    B, H, _ = q.shape
+    HV, V = v.shape[1], v.shape[2]
+    out = np.full((B, HV, V), np.nan)
+    for bi in range(B):
+        slot = int(state_indices[bi])
+        if slot < 0 or slot >= state.shape[0]:
+            continue
+        for hv in range(HV):
+            h = hv // (HV // H)
+            o, S = gdn_step(state[slot, hv], q[bi, h], k[bi, h], v[bi, hv], a[bi, hv], b[bi, hv],
+                            A_log[hv], dt_bias[hv])
+            out[bi, hv] = o
+            state[slot, hv] = S
+    return out
