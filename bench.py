@@ -16,7 +16,8 @@ tokens (``cfg3_norm_rope``, ``cfg2_norm_rope``: HBM GB/s), and Qwen3.5's output
 gate (``cfg2_gate``: gated vs plain decode; ``cfg3_gate``: gated vs plain
 prefill, and the stand-alone in-place gate pass for comparison), head_dim 256
 (``cfg2_d256``, ``cfg5_d256``, ``cfg3_d256``) and the Gated DeltaNet decode
-step (``gdn_decode``: HBM GB/s over the state pool).
+step (``gdn_decode``: HBM GB/s over the state pool) and prefill
+(``gdn_prefill``: recurrent form over cfg3's sequence lengths).
 ``roofline`` covers the dominant kernel of the headline workload (paged
 decode: main kernel + split-K merge), timed with HIP events on the stream
 the kernels run on.  ``cpu_baseline`` times the CPU restatement of the path
@@ -224,6 +225,35 @@ def bench_gdn(steps, warmup, seed=0, B=64, H=16, HV=32):
                 bytes=nb, batch=B, k_heads=H, v_heads=HV), None
 
 
+def bench_gdn_prefill(steps, warmup, seed=0, H=16, HV=32):
+    """Gated DeltaNet prefill (recurrent form) over cfg3's sequence lengths
+    (16 sequences, Lq ~ U[256, 2048]): each (sequence, value head, 16-row
+    slice) is one wave that carries its state through the tokens in
+    registers.  Reported: tokens/s and the fp32 VALU rate of the recurrence
+    (8 V K flops per token and value head)."""
+    import torch
+    from nano_qwen_amd import kernels
+    from oracle.inputs import make_prefill_case
+
+    lq = make_prefill_case("cfg3", seed=seed, device="cpu")["lq"]
+    cu = torch.tensor([0] + list(torch.tensor(lq).cumsum(0).tolist()), dtype=torch.int32, device="cuda")
+    T = int(cu[-1])
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    r = lambda *sh: torch.randn(*sh, device="cuda", generator=g)
+    q, k = r(T, H, 128).bfloat16(), r(T, H, 128).bfloat16()
+    v, a, b = r(T, HV, 128).bfloat16(), r(T, HV).bfloat16(), r(T, HV).bfloat16()
+    A_log, dt = r(HV) * 0.5, r(HV) * 0.5
+    n = len(lq)
+    state = torch.zeros(n, HV, 128, 128, device="cuda")
+    idx = torch.arange(n, dtype=torch.int32, device="cuda")
+    out = torch.empty(T, HV, 128, dtype=torch.bfloat16, device="cuda")
+    ms = _events_time(lambda i: kernels.gdn_prefill(q, k, v, a, b, A_log, dt, cu, state, idx, out=out),
+                      steps, max(warmup, 3))
+    fl = 8 * 128 * 128 * HV * T
+    return dict(ms_per_step=ms, tokens=T, tokens_per_s=T / (ms * 1e-3), valu_tflops=fl / (ms * 1e-3) / 1e12,
+                valu_frac=fl / (ms * 1e-3) / 1e12 / 157.3, k_heads=H, v_heads=HV), None
+
+
 def cpu_baseline_decode(case, n_seqs=8, reps=5):
     """Median wall time of the CPU path on the first n_seqs sequences."""
     import torch
@@ -345,7 +375,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None,
                     help="run one config (cfg2|cfg3|cfg4|cfg5|cfg3_norm_rope|cfg2_norm_rope|cfg2_gate|cfg3_gate|"
-                         "cfg2_d256|cfg5_d256|cfg3_d256|gdn_decode)")
+                         "cfg2_d256|cfg5_d256|cfg3_d256|gdn_decode|gdn_prefill)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration)")
     args = ap.parse_args()
@@ -367,7 +397,7 @@ def main():
     head = None
     todo = [args.only] if args.only else ["cfg2", "cfg3", "cfg4", "cfg5", "cfg3_norm_rope", "cfg2_norm_rope",
                                                    "cfg2_gate", "cfg3_gate", "cfg2_d256", "cfg5_d256",
-                                                   "cfg3_d256", "gdn_decode"]
+                                                   "cfg3_d256", "gdn_decode", "gdn_prefill"]
     cpu = None
     for name in todo:
         print(f"[bench] {name} ...", file=sys.stderr, flush=True)
@@ -377,6 +407,8 @@ def main():
             r, case = bench_gate(name.split("_")[0], args.steps, args.warmup)
         elif name == "gdn_decode":
             r, case = bench_gdn(args.steps, args.warmup)
+        elif name == "gdn_prefill":
+            r, case = bench_gdn_prefill(args.steps, args.warmup)
         elif name == "cfg3_d256":
             r, case = bench_prefill("cfg3", args.steps, args.warmup, d=256, hq=16, hkv=4)
         elif name.endswith("_d256"):

@@ -311,6 +311,30 @@ int nq_gdn_decode(const void *q, int64_t q_row_stride, const void *k, int64_t k_
                   void *out, int64_t out_row_stride, int batch, int num_k_heads, int num_v_heads,
                   int head_k_dim, int head_v_dim, int dtype, void *stream);
 
+/*
+ * Gated DeltaNet prefill (recurrent form) for a batch of sequences.
+ * Replaces chunk_gated_delta_rule (layers/gated_delta_net.py:44-82, the
+ * Triton chunk kernel of layers/fla/ with use_qk_l2norm_in_kernel=True and
+ * initial_state=None), the gating computed before it (:197-198) and the
+ * final-state write to the pool after it (:210-214), called per sequence by
+ * models/qwen3_5.py:215-224.
+ * Sequence n < num_seqs owns token rows [cu_seqlens[n], cu_seqlens[n+1]) of
+ * q, k [T, num_k_heads, 128], v, out [T, num_v_heads, 128] and a, b
+ * [T, num_v_heads].  Its state starts at zero (initial_state_from_slot == 0,
+ * as in the reference) or at state[state_indices[n]], runs the step of
+ * nq_gdn_decode over the tokens in order, writing out for every token, and
+ * is stored to state[state_indices[n]] (a slot outside [0, num_slots) keeps
+ * nothing and starts from zero).  Types, layouts and alignment as for
+ * nq_gdn_decode; cu_seqlens int32 [num_seqs + 1].
+ */
+int nq_gdn_prefill(const void *q, int64_t q_row_stride, const void *k, int64_t k_row_stride,
+                   const void *v, int64_t v_row_stride, const void *a, int64_t a_row_stride,
+                   const void *b, int64_t b_row_stride, const float *A_log, const float *dt_bias,
+                   const int32_t *cu_seqlens, int num_seqs, float *state,
+                   const int32_t *state_indices, int64_t num_slots, int initial_state_from_slot,
+                   void *out, int64_t out_row_stride, int num_k_heads, int num_v_heads,
+                   int head_k_dim, int head_v_dim, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -69,8 +69,13 @@ __device__ inline float reduce_rows(float (&p)[N], int lane) {
     const bool hi = (lane & m) != 0;
 #pragma unroll
     for (int j = 0; j < c / 2; ++j) {
-      const float keep = hi ? p[j + c / 2] : p[j];
-      const float send = hi ? p[j] : p[j + c / 2];
+      // Both elements are first fixed in registers: otherwise the compiler
+      // turns the selects into an indexed read of p, a compare-and-select
+      // chain over the whole array.
+      float lo = p[j], up = p[j + c / 2];
+      asm volatile("" : "+v"(lo), "+v"(up));
+      const float keep = hi ? up : lo;
+      const float send = hi ? lo : up;
       p[j] = keep + __shfl_xor(send, m, 64);
     }
   }
@@ -85,6 +90,70 @@ constexpr int kLoads = 8;
 constexpr int kRowsW = 2 * kLoads;
 constexpr int kSh = kLoads == 16 ? 1 : 2;  // lane bits below the row index after reduce_rows
 
+// One token's inputs for one lane: its 4 columns of q and k, its row's v, and
+// the two gate inputs (16-bit values).
+struct TokIn {
+  u32x2 q, k;
+  uint32_t v, ga, gb;
+};
+
+template <class T>
+__device__ inline TokIn load_tok(const GdnArgs &a, int64_t t, int h, int hv, int vrow, int c0) {
+  TokIn in;
+  in.q = *reinterpret_cast<const u32x2 *>(a.q + t * a.q_rs + (h * kDim + c0) * 2);
+  in.k = *reinterpret_cast<const u32x2 *>(a.k + t * a.k_rs + (h * kDim + c0) * 2);
+  in.v = reinterpret_cast<const uint16_t *>(a.v + t * a.v_rs + hv * kDim * 2)[vrow];
+  in.ga = reinterpret_cast<const uint16_t *>(a.a + t * a.a_rs)[hv];
+  in.gb = reinterpret_cast<const uint16_t *>(a.b + t * a.b_rs)[hv];
+  return in;
+}
+
+template <class T>
+__device__ inline f32x4 unpack4(const u32x2 &w) {
+  return f32x4{T::to_float(w[0] & 0xffffu), T::to_float(w[0] >> 16), T::to_float(w[1] & 0xffffu),
+               T::to_float(w[1] >> 16)};
+}
+
+// One token of the gated delta rule on the wave's kRowsW state rows (held in
+// s), writing the token's output for those rows.  neg_a = -exp(A_log[hv]).
+template <class T>
+__device__ inline void gdn_token(f32x4 (&s)[kLoads], const TokIn &in, float neg_a, float dt_bias, float eps,
+                                 float scale, int lane, float *urow, int my_row, bool writer, uint16_t *orow) {
+  // q and k: this lane's 4 columns, l2-normalized over the 32 lanes that
+  // cover all 128 columns; q also carries the scale.
+  f32x4 qc = unpack4<T>(in.q), kc = unpack4<T>(in.k);
+  float sq = qc[0] * qc[0] + qc[1] * qc[1] + qc[2] * qc[2] + qc[3] * qc[3];
+  float sk = kc[0] * kc[0] + kc[1] * kc[1] + kc[2] * kc[2] + kc[3] * kc[3];
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1) {
+    sq += __shfl_xor(sq, off, 64);
+    sk += __shfl_xor(sk, off, 64);
+  }
+  qc *= scale / sqrtf(sq + eps);
+  kc *= 1.0f / sqrtf(sk + eps);
+  const float decay = expf(neg_a * softplus(T::to_float(static_cast<uint16_t>(in.ga)) + dt_bias));
+  const float beta = 1.0f / (1.0f + expf(-T::to_float(static_cast<uint16_t>(in.gb))));
+  // u = beta * (v - (exp(g) S) k) for every row of the wave.
+  float p[kLoads];
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    s[i] *= decay;
+    p[i] = s[i][0] * kc[0] + s[i][1] * kc[1] + s[i][2] * kc[2] + s[i][3] * kc[3];
+  }
+  const float u = beta * (T::to_float(static_cast<uint16_t>(in.v)) - reduce_rows(p, lane));
+  if (writer) urow[my_row] = u;  // one wave: LDS accesses stay in order
+  // S += u k^T, then o = S q.
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    const float ui = urow[2 * i + (lane >> 5)];
+    s[i] += ui * kc;
+    p[i] = s[i][0] * qc[0] + s[i][1] * qc[1] + s[i][2] * qc[2] + s[i][3] * qc[3];
+  }
+  const float o = reduce_rows(p, lane);
+  if (writer) orow[my_row] = T::from_float(o);
+}
+
+// Decode: one token per sequence b (row b of q, k, v, a, b and out).
 template <class T>
 __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(const GdnArgs a) {
   const int hv = blockIdx.x, bi = blockIdx.y, w = blockIdx.z;
@@ -93,61 +162,78 @@ __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(const GdnArgs a) {
   if (slot < 0 || slot >= a.num_slots) return;  // padded row: no state to advance
   const int h = hv / (a.HV / a.H);
   const int r0 = kRowsW * w + (lane >> 5);  // row of load 0; load i adds 2i
-  const int c0 = 4 * (lane & 31);       // this lane's 4 columns
+  const int c0 = 4 * (lane & 31);           // this lane's 4 columns
+  const int my_row = 2 * ((lane >> kSh) & (kLoads - 1)) + (lane >> 5);  // row whose sums this lane ends with
+  const bool writer = (lane & ((1 << kSh) - 1)) == 0;
 
-  // 16 coalesced loads of the state, issued first.
+  // The state loads first (coalesced), then the token's inputs.
   float *sp = a.state + ((static_cast<int64_t>(slot) * a.HV + hv) * kDim + r0) * kDim + c0;
   f32x4 s[kLoads];
 #pragma unroll
   for (int i = 0; i < kLoads; ++i)
     s[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(sp + 2 * i * kDim));
-
-  // This lane's 4 columns of q and k, l2-normalized over the 32 lanes that
-  // cover all 128 columns; q also carries the scale.
-  const u32x2 qr = *reinterpret_cast<const u32x2 *>(a.q + bi * a.q_rs + (h * kDim + c0) * 2);
-  const u32x2 kr = *reinterpret_cast<const u32x2 *>(a.k + bi * a.k_rs + (h * kDim + c0) * 2);
-  f32x4 qc{T::to_float(qr[0] & 0xffffu), T::to_float(qr[0] >> 16), T::to_float(qr[1] & 0xffffu),
-           T::to_float(qr[1] >> 16)};
-  f32x4 kc{T::to_float(kr[0] & 0xffffu), T::to_float(kr[0] >> 16), T::to_float(kr[1] & 0xffffu),
-           T::to_float(kr[1] >> 16)};
-  float sq = qc[0] * qc[0] + qc[1] * qc[1] + qc[2] * qc[2] + qc[3] * qc[3];
-  float sk = kc[0] * kc[0] + kc[1] * kc[1] + kc[2] * kc[2] + kc[3] * kc[3];
-#pragma unroll
-  for (int off = 16; off >= 1; off >>= 1) {
-    sq += __shfl_xor(sq, off, 64);
-    sk += __shfl_xor(sk, off, 64);
-  }
-  qc *= a.scale / sqrtf(sq + a.eps);
-  kc *= 1.0f / sqrtf(sk + a.eps);
-
-  // Row (within the wave's rows) whose sums this lane ends with.
-  const int my_row = 2 * ((lane >> kSh) & (kLoads - 1)) + (lane >> 5);
-  const float vv = elem<T>(a.v + bi * a.v_rs + hv * kDim * 2, kRowsW * w + my_row);
-  const float g = -expf(a.A_log[hv]) * softplus(elem<T>(a.a + bi * a.a_rs, hv) + a.dt_bias[hv]);
-  const float decay = expf(g);
-  const float beta = 1.0f / (1.0f + expf(-elem<T>(a.b + bi * a.b_rs, hv)));
-
-  // u = beta * (v - (exp(g) S) k) for every row of the wave.
-  float p[kLoads];
-#pragma unroll
-  for (int i = 0; i < kLoads; ++i) {
-    s[i] *= decay;
-    p[i] = s[i][0] * kc[0] + s[i][1] * kc[1] + s[i][2] * kc[2] + s[i][3] * kc[3];
-  }
-  const float u = beta * (vv - reduce_rows(p, lane));
+  const TokIn in = load_tok<T>(a, bi, h, hv, kRowsW * w + my_row, c0);
   __shared__ float urow[kRowsW];
-  const bool writer = (lane & ((1 << kSh) - 1)) == 0;
-  if (writer) urow[my_row] = u;  // one wave: LDS accesses stay in order
-  // S += u k^T, then o = S q.
+  uint16_t *orow = reinterpret_cast<uint16_t *>(a.out + bi * a.o_rs + hv * kDim * 2) + kRowsW * w;
+  gdn_token<T>(s, in, -expf(a.A_log[hv]), a.dt_bias[hv], a.eps, a.scale, lane, urow, my_row, writer, orow);
 #pragma unroll
-  for (int i = 0; i < kLoads; ++i) {
-    const float ui = urow[2 * i + (lane >> 5)];
-    s[i] += ui * kc;
-    p[i] = s[i][0] * qc[0] + s[i][1] * qc[1] + s[i][2] * qc[2] + s[i][3] * qc[3];
-    __builtin_nontemporal_store(s[i], reinterpret_cast<f32x4 *>(sp + 2 * i * kDim));
+  for (int i = 0; i < kLoads; ++i) __builtin_nontemporal_store(s[i], reinterpret_cast<f32x4 *>(sp + 2 * i * kDim));
+}
+
+// Prefill: sequence n owns token rows [cu[n], cu[n+1]); the state starts from
+// zero (or the slot's contents) and stays in registers across the tokens;
+// each token's inputs are loaded kAheadTok tokens before it is processed.
+constexpr int kAheadTok = 4;
+
+template <class T>
+__global__ __launch_bounds__(kThreads) void gdn_prefill_kernel(const GdnArgs a, const int32_t *cu, int from_slot) {
+  const int hv = blockIdx.x, n = blockIdx.y, w = blockIdx.z;
+  const int lane = threadIdx.x;
+  const int32_t slot = a.idx[n];
+  const bool has_slot = slot >= 0 && slot < a.num_slots;
+  const int h = hv / (a.HV / a.H);
+  const int r0 = kRowsW * w + (lane >> 5);
+  const int c0 = 4 * (lane & 31);
+  const int my_row = 2 * ((lane >> kSh) & (kLoads - 1)) + (lane >> 5);
+  const bool writer = (lane & ((1 << kSh) - 1)) == 0;
+  const int64_t t0 = cu[n], t1 = cu[n + 1];
+
+  float *sp = a.state + ((static_cast<int64_t>(has_slot ? slot : 0) * a.HV + hv) * kDim + r0) * kDim + c0;
+  f32x4 s[kLoads];
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i)
+    s[i] = (from_slot && has_slot) ? __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(sp + 2 * i * kDim))
+                                   : f32x4{0, 0, 0, 0};
+  const float neg_a = -expf(a.A_log[hv]), dtb = a.dt_bias[hv];
+  __shared__ float urow[kRowsW];
+  const int vrow = kRowsW * w + my_row;
+  // Prefetch ring: token indices past the end are clamped to the last token
+  // (loaded, never used), so the steady-state loop has no branches and the
+  // compiler's waits count exactly the loads each token needs.
+  const int64_t last = t1 > t0 ? t1 - 1 : t0;
+  TokIn ring[kAheadTok];
+#pragma unroll
+  for (int j = 0; j < kAheadTok; ++j) ring[j] = load_tok<T>(a, min(t0 + j, last), h, hv, vrow, c0);
+  int64_t t = t0;
+  for (; t + kAheadTok <= t1; t += kAheadTok) {
+#pragma unroll
+    for (int j = 0; j < kAheadTok; ++j) {
+      const TokIn in = ring[j];
+      ring[j] = load_tok<T>(a, min(t + j + kAheadTok, last), h, hv, vrow, c0);
+      uint16_t *orow = reinterpret_cast<uint16_t *>(a.out + (t + j) * a.o_rs + hv * kDim * 2) + kRowsW * w;
+      gdn_token<T>(s, in, neg_a, dtb, a.eps, a.scale, lane, urow, my_row, writer, orow);
+    }
   }
-  const float o = reduce_rows(p, lane);
-  if (writer) reinterpret_cast<uint16_t *>(a.out + bi * a.o_rs + hv * kDim * 2)[kRowsW * w + my_row] = T::from_float(o);
+#pragma unroll
+  for (int j = 0; j < kAheadTok - 1; ++j) {  // the tail: fewer than kAheadTok tokens
+    if (t + j >= t1) break;
+    uint16_t *orow = reinterpret_cast<uint16_t *>(a.out + (t + j) * a.o_rs + hv * kDim * 2) + kRowsW * w;
+    gdn_token<T>(s, ring[j], neg_a, dtb, a.eps, a.scale, lane, urow, my_row, writer, orow);
+  }
+  if (has_slot) {
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) __builtin_nontemporal_store(s[i], reinterpret_cast<f32x4 *>(sp + 2 * i * kDim));
+  }
 }
 
 }  // namespace
@@ -202,4 +288,53 @@ extern "C" int nq_gdn_decode(const void *q, int64_t q_row_stride, const void *k,
   if (dtype == NQ_BF16) gdn_decode_kernel<BF16><<<grid, kThreads, 0, s>>>(g);
   else gdn_decode_kernel<F16><<<grid, kThreads, 0, s>>>(g);
   return check_launch("gdn_decode");
+}
+
+extern "C" int nq_gdn_prefill(const void *q, int64_t q_row_stride, const void *k, int64_t k_row_stride,
+                              const void *v, int64_t v_row_stride, const void *a, int64_t a_row_stride,
+                              const void *b, int64_t b_row_stride, const float *A_log, const float *dt_bias,
+                              const int32_t *cu_seqlens, int num_seqs, float *state, const int32_t *state_indices,
+                              int64_t num_slots, int initial_state_from_slot, void *out, int64_t out_row_stride,
+                              int num_k_heads, int num_v_heads, int head_k_dim, int head_v_dim, int dtype,
+                              void *stream) {
+  if (num_seqs < 0 || num_k_heads <= 0 || num_v_heads <= 0 || num_slots < 0)
+    return fail(NQ_EINVAL, "gdn_prefill: bad sizes (seqs=%d heads=%d/%d)", num_seqs, num_k_heads, num_v_heads);
+  if (num_v_heads % num_k_heads != 0)
+    return fail(NQ_EINVAL, "gdn_prefill: value heads %d not a multiple of key heads %d", num_v_heads, num_k_heads);
+  if (head_k_dim != kDim || head_v_dim != kDim)
+    return fail(NQ_EUNSUPPORTED, "gdn_prefill: head dims %d/%d (built: 128/128)", head_k_dim, head_v_dim);
+  if (dtype != NQ_BF16 && dtype != NQ_F16) return fail(NQ_EUNSUPPORTED, "gdn_prefill: dtype %d (f16/bf16)", dtype);
+  if (num_seqs == 0) return NQ_OK;
+  if (!q || !k || !v || !a || !b || !A_log || !dt_bias || !cu_seqlens || !state || !state_indices || !out)
+    return fail(NQ_EINVAL, "gdn_prefill: null pointer");
+  if (!aligned(state, 16) || !aligned(q, 8) || !aligned(k, 8) || (q_row_stride * 2) % 8 || (k_row_stride * 2) % 8)
+    return fail(NQ_EINVAL, "gdn_prefill: state 16-byte, q/k rows 8-byte alignment");
+  if (num_seqs > 65535 || num_v_heads > 65535) return fail(NQ_EINVAL, "gdn_prefill: grid too large");
+  GdnArgs g{};
+  g.q = static_cast<const uint8_t *>(q);
+  g.k = static_cast<const uint8_t *>(k);
+  g.v = static_cast<const uint8_t *>(v);
+  g.q_rs = q_row_stride * 2;
+  g.k_rs = k_row_stride * 2;
+  g.v_rs = v_row_stride * 2;
+  g.a = static_cast<const uint8_t *>(a);
+  g.b = static_cast<const uint8_t *>(b);
+  g.a_rs = a_row_stride * 2;
+  g.b_rs = b_row_stride * 2;
+  g.A_log = A_log;
+  g.dt_bias = dt_bias;
+  g.state = state;
+  g.idx = state_indices;
+  g.num_slots = num_slots;
+  g.out = static_cast<uint8_t *>(out);
+  g.o_rs = out_row_stride * 2;
+  g.H = num_k_heads;
+  g.HV = num_v_heads;
+  g.eps = 1e-6f;
+  g.scale = 1.0f / sqrtf(static_cast<float>(head_k_dim));
+  dim3 grid(num_v_heads, num_seqs, kDim / kRowsW);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == NQ_BF16) gdn_prefill_kernel<BF16><<<grid, kThreads, 0, s>>>(g, cu_seqlens, initial_state_from_slot);
+  else gdn_prefill_kernel<F16><<<grid, kThreads, 0, s>>>(g, cu_seqlens, initial_state_from_slot);
+  return check_launch("gdn_prefill");
 }

@@ -331,6 +331,43 @@ def gdn_decode(query, key, value, a, b, A_log, dt_bias, state, state_indices, ou
     return out
 
 
+def gdn_prefill(query, key, value, a, b, A_log, dt_bias, cu_seqlens, state, state_indices,
+                initial_state_from_slot=False, out=None):
+    """Gated DeltaNet prefill for packed sequences; final states go to the pool.
+
+    Replaces ``chunk_gated_delta_rule`` (layers/gated_delta_net.py:44-82) with
+    the gating before it and the pool write after it, for every sequence of
+    the batch at once: ``query/key [T, H, K]``, ``value [T, HV, V]``,
+    ``a/b [T, HV]`` packed by ``cu_seqlens [N + 1]`` int32; ``state`` the
+    float32 pool and ``state_indices [N]`` int32.  Returns ``out [T, HV, V]``.
+    """
+    require_cuda(query, key, value, a, b, A_log, dt_bias, cu_seqlens, state, state_indices, what="gdn_prefill")
+    T_, H, K = query.shape
+    HV, V = value.shape[1], value.shape[2]
+    for t, what in ((query, "query"), (key, "key"), (value, "value")):
+        if t.stride(-1) != 1 or t.stride(1) != t.shape[-1] or t.dtype != query.dtype or t.shape[0] != T_:
+            raise RuntimeError(f"gdn_prefill: {what} must be [T, heads, dim] contiguous over (head, dim)")
+    a2, b2 = a.reshape(T_, HV), b.reshape(T_, HV)
+    if a2.stride(-1) != 1 or b2.stride(-1) != 1 or a2.dtype != query.dtype or b2.dtype != query.dtype:
+        raise RuntimeError("gdn_prefill: a and b must be [T, HV] rows of the query's dtype")
+    if A_log.dtype != torch.float32 or dt_bias.dtype != torch.float32:
+        raise RuntimeError("gdn_prefill: A_log and dt_bias must be float32")
+    if state.dtype != torch.float32 or not state.is_contiguous() or state.shape[1:] != (HV, V, K):
+        raise RuntimeError("gdn_prefill: state must be a contiguous float32 pool [slots, HV, V, K]")
+    n = cu_seqlens.numel() - 1
+    if cu_seqlens.dtype != torch.int32 or state_indices.dtype != torch.int32 or state_indices.numel() != n:
+        raise RuntimeError("gdn_prefill: cu_seqlens [N+1] and state_indices [N] must be int32")
+    if out is None:
+        out = torch.empty(T_, HV, V, dtype=query.dtype, device=query.device)
+    rc = lib().nq_gdn_prefill(ptr(query), query.stride(0), ptr(key), key.stride(0), ptr(value), value.stride(0),
+                              ptr(a2), a2.stride(0), ptr(b2), b2.stride(0), ptr(A_log.contiguous()),
+                              ptr(dt_bias.contiguous()), ptr(cu_seqlens), n, ptr(state), ptr(state_indices),
+                              state.shape[0], 1 if initial_state_from_slot else 0, ptr(out), out.stride(0),
+                              H, HV, K, V, dtype_code(query.dtype), stream_of(query))
+    check(rc, "gdn_prefill")
+    return out
+
+
 __all__ = ["store_kvcache", "paged_decode", "varlen_prefill", "prepare_decode", "decode_plan", "qk_norm_rope_store",
-           "output_gate", "gdn_decode",
+           "output_gate", "gdn_decode", "gdn_prefill",
            "decode_workspace", "prefill_workspace", "_lib"]

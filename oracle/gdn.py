@@ -61,3 +61,26 @@ def gdn_decode(q, k, v, a, b, A_log, dt_bias, state, state_indices):
             out[bi, hv] = o
             state[slot, hv] = S
     return out
+
+
+def gdn_prefill(q, k, v, a, b, A_log, dt_bias, cu_seqlens, state, state_indices, from_slot=False):
+    """Packed sequences: q, k [T, H, K]; v [T, HV, V]; a, b [T, HV].  Each
+    sequence's state starts at zero (or the slot's contents), runs gdn_step
+    over its tokens in order, and is stored to its slot (chunk_gated_delta_rule
+    with initial_state=None, then the pool write; the chunked form computes
+    the same recurrence)."""
+    T, H, _ = q.shape
+    HV, V = v.shape[1], v.shape[2]
+    out = np.zeros((T, HV, V))
+    for n in range(len(cu_seqlens) - 1):
+        t0, t1 = int(cu_seqlens[n]), int(cu_seqlens[n + 1])
+        slot = int(state_indices[n])
+        has = 0 <= slot < state.shape[0]
+        for hv in range(HV):
+            h = hv // (HV // H)
+            S = np.array(state[slot, hv], dtype=np.float64) if (from_slot and has) else np.zeros((V, q.shape[2]))
+            for t in range(t0, t1):
+                out[t, hv], S = gdn_step(S, q[t, h], k[t, h], v[t, hv], a[t, hv], b[t, hv], A_log[hv], dt_bias[hv])
+            if has:
+                state[slot, hv] = S
+    return out

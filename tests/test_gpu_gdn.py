@@ -104,3 +104,55 @@ def test_gdn_decode_rejects(cuda):
     with pytest.raises(RuntimeError):
         kernels.gdn_decode(c["q"].to(cuda), c["k"].to(cuda), c["v"].to(cuda), c["a"].to(cuda), c["b"].to(cuda),
                            c["A_log"].to(cuda), c["dt"].to(cuda), state_dev.double(), c["idx"].to(cuda))
+
+
+@pytest.mark.parametrize("from_slot", [False, True])
+def test_gdn_prefill_matches_oracle(cuda, from_slot):
+    """Packed sequences of lengths 1 .. 300 (incl. a tail not a multiple of the
+    prefetch depth), zero or pooled initial state, one skipped slot."""
+    g = torch.Generator().manual_seed(6)
+    lens = [1, 5, 37, 300, 4]
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32)
+    T, H, HV = int(cu[-1]), 2, 4
+    bf = torch.bfloat16
+    q, k = torch.randn(T, H, 128, generator=g).to(bf), torch.randn(T, H, 128, generator=g).to(bf)
+    v = torch.randn(T, HV, 128, generator=g).to(bf)
+    a, b = torch.randn(T, HV, generator=g).to(bf), torch.randn(T, HV, generator=g).to(bf)
+    A_log, dt = torch.randn(HV, generator=g) * 0.5, torch.randn(HV, generator=g) * 0.5
+    state = torch.randn(8, HV, 128, 128, generator=g) * 0.05
+    idx = torch.tensor([6, 0, -1, 3, 5], dtype=torch.int32)
+    state_dev = state.clone().to(cuda)
+    out = kernels.gdn_prefill(q.to(cuda), k.to(cuda), v.to(cuda), a.to(cuda), b.to(cuda), A_log.to(cuda),
+                              dt.to(cuda), cu.to(cuda), state_dev, idx.to(cuda), initial_state_from_slot=from_slot)
+    torch.cuda.synchronize()
+    f = lambda t: t.double().numpy()
+    ref_state = state.double().numpy()
+    ref = gdn.gdn_prefill(f(q), f(k), f(v), f(a), f(b), f(A_log), f(dt), cu.numpy(), ref_state, idx.numpy(),
+                          from_slot=from_slot)
+    o = out.float().cpu().numpy()
+    assert np.all(np.abs(o - ref) <= 2 ** -8 * np.abs(ref) + 1e-3 * np.abs(ref).max()), float(np.abs(o - ref).max())
+    s = state_dev.cpu().double().numpy()
+    assert np.abs(s - ref_state).max() <= 2e-5 * np.abs(ref_state).max()
+
+
+def test_gdn_prefill_then_decode_equals_longer_prefill(cuda):
+    """Prefill of L tokens then one decode step == prefill of L + 1 tokens
+    (same final state, same last output)."""
+    g = torch.Generator().manual_seed(7)
+    L, H, HV, bf = 50, 1, 2, torch.bfloat16
+    q, k = torch.randn(L + 1, H, 128, generator=g).to(bf), torch.randn(L + 1, H, 128, generator=g).to(bf)
+    v = torch.randn(L + 1, HV, 128, generator=g).to(bf)
+    a, b = torch.randn(L + 1, HV, generator=g).to(bf), torch.randn(L + 1, HV, generator=g).to(bf)
+    A_log, dt = (torch.randn(HV, generator=g) * 0.5).to(cuda), (torch.randn(HV, generator=g) * 0.5).to(cuda)
+    q, k, v, a, b = (x.to(cuda) for x in (q, k, v, a, b))
+    st1 = torch.zeros(1, HV, 128, 128, device=cuda)
+    st2 = torch.zeros(1, HV, 128, 128, device=cuda)
+    idx = torch.zeros(1, dtype=torch.int32, device=cuda)
+    kernels.gdn_prefill(q[:L], k[:L], v[:L], a[:L], b[:L], A_log, dt,
+                        torch.tensor([0, L], dtype=torch.int32, device=cuda), st1, idx)
+    o_dec = kernels.gdn_decode(q[L:], k[L:], v[L:], a[L:], b[L:], A_log, dt, st1, idx)
+    o_all = kernels.gdn_prefill(q, k, v, a, b, A_log, dt,
+                                torch.tensor([0, L + 1], dtype=torch.int32, device=cuda), st2, idx)
+    torch.cuda.synchronize()
+    assert torch.equal(st1, st2)
+    assert torch.equal(o_dec[0].view(torch.int16), o_all[L].view(torch.int16))
