@@ -17,7 +17,8 @@ gate (``cfg2_gate``: gated vs plain decode; ``cfg3_gate``: gated vs plain
 prefill, and the stand-alone in-place gate pass for comparison), head_dim 256
 (``cfg2_d256``, ``cfg5_d256``, ``cfg3_d256``) and the Gated DeltaNet decode
 step (``gdn_decode``: HBM GB/s over the state pool) and prefill
-(``gdn_prefill``: recurrent form over cfg3's sequence lengths).
+(``gdn_prefill``: recurrent form over cfg3's sequence lengths), and the gated
+RMS norm of its output (``gdn_norm``, HBM GB/s).
 ``roofline`` covers the dominant kernel of the headline workload (paged
 decode: main kernel + split-K merge), timed with HIP events on the stream
 the kernels run on.  ``cpu_baseline`` times the CPU restatement of the path
@@ -254,6 +255,24 @@ def bench_gdn_prefill(steps, warmup, seed=0, H=16, HV=32):
                 valu_frac=fl / (ms * 1e-3) / 1e12 / 157.3, k_heads=H, v_heads=HV), None
 
 
+def bench_gated_norm(steps, warmup, seed=0, HV=32):
+    """GDN output gated RMS norm over cfg3's token count x HV value heads
+    (rows of 128), in place: reads x and the gate, writes x."""
+    import torch
+    from nano_qwen_amd import kernels
+    from oracle.inputs import make_prefill_case
+
+    T = sum(make_prefill_case("cfg3", seed=seed, device="cpu")["lq"])
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(T, HV, 128, device="cuda", generator=g).bfloat16()
+    z = torch.randn(T, HV, 128, device="cuda", generator=g).bfloat16()
+    w = torch.rand(128, device="cuda", generator=g) + 0.5
+    ms = _events_time(lambda i: kernels.gated_rmsnorm(x, z, w, 1e-6, out=x), steps, max(warmup, 200))
+    nb = 3 * x.numel() * 2 + 128 * 4
+    return dict(ms_per_step=ms, gbs=nb / (ms * 1e-3) / 1e9, hbm_frac=nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                bytes=nb, rows=T * HV), None
+
+
 def cpu_baseline_decode(case, n_seqs=8, reps=5):
     """Median wall time of the CPU path on the first n_seqs sequences."""
     import torch
@@ -375,7 +394,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None,
                     help="run one config (cfg2|cfg3|cfg4|cfg5|cfg3_norm_rope|cfg2_norm_rope|cfg2_gate|cfg3_gate|"
-                         "cfg2_d256|cfg5_d256|cfg3_d256|gdn_decode|gdn_prefill)")
+                         "cfg2_d256|cfg5_d256|cfg3_d256|gdn_decode|gdn_prefill|gdn_norm)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration)")
     args = ap.parse_args()
@@ -397,7 +416,7 @@ def main():
     head = None
     todo = [args.only] if args.only else ["cfg2", "cfg3", "cfg4", "cfg5", "cfg3_norm_rope", "cfg2_norm_rope",
                                                    "cfg2_gate", "cfg3_gate", "cfg2_d256", "cfg5_d256",
-                                                   "cfg3_d256", "gdn_decode", "gdn_prefill"]
+                                                   "cfg3_d256", "gdn_decode", "gdn_prefill", "gdn_norm"]
     cpu = None
     for name in todo:
         print(f"[bench] {name} ...", file=sys.stderr, flush=True)
@@ -407,6 +426,8 @@ def main():
             r, case = bench_gate(name.split("_")[0], args.steps, args.warmup)
         elif name == "gdn_decode":
             r, case = bench_gdn(args.steps, args.warmup)
+        elif name == "gdn_norm":
+            r, case = bench_gated_norm(args.steps, args.warmup)
         elif name == "gdn_prefill":
             r, case = bench_gdn_prefill(args.steps, args.warmup)
         elif name == "cfg3_d256":

@@ -335,6 +335,21 @@ int nq_gdn_prefill(const void *q, int64_t q_row_stride, const void *k, int64_t k
                    void *out, int64_t out_row_stride, int num_k_heads, int num_v_heads,
                    int head_k_dim, int head_v_dim, int dtype, void *stream);
 
+/*
+ * Gated RMS norm of the Gated DeltaNet output, one pass.
+ * Replaces RMSNormGated.forward (layers/layernorm.py:143-157) as applied by
+ * GatedDeltaNet (self.norm(out, z), layers/gated_delta_net.py:205-207,
+ * 268-270).  For each of `rows` rows of dim elements (x and gate of type
+ * dtype, F16/BF16; weight float [dim]), in fp32, rnd = round to dtype:
+ *   n = rnd(x / sqrt(mean(x^2) + eps))
+ *   out = rnd(rnd(n * rnd(weight)) * gate / (1 + exp(-gate)))
+ * dim is 64, 128 or 256; pointers and row strides 16-byte aligned; out may
+ * alias x.
+ */
+int nq_gated_rmsnorm(const void *x, int64_t x_row_stride, const void *gate, int64_t gate_row_stride,
+                     const float *weight, float eps, void *out, int64_t out_row_stride,
+                     int64_t rows, int dim, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -368,6 +368,25 @@ def gdn_prefill(query, key, value, a, b, A_log, dt_bias, cu_seqlens, state, stat
     return out
 
 
+def gated_rmsnorm(x, gate, weight, eps, out=None):
+    """``RMSNormGated(x, gate)`` (layers/layernorm.py:143-157) in one pass over
+    rows of the last dimension: ``x, gate [..., D]`` (16-bit, same dtype),
+    ``weight [D]`` float32.  ``out=x`` normalizes in place."""
+    require_cuda(x, gate, weight, out, what="gated_rmsnorm")
+    d = x.shape[-1]
+    x2, g2 = x.reshape(-1, d), gate.reshape(-1, d)
+    if x2.stride(-1) != 1 or g2.stride(-1) != 1 or gate.dtype != x.dtype or g2.shape[0] != x2.shape[0]:
+        raise RuntimeError("gated_rmsnorm: x and gate must be [..., D] rows of one dtype")
+    if weight.dtype != torch.float32 or weight.numel() != d or not weight.is_contiguous():
+        raise RuntimeError("gated_rmsnorm: weight must be contiguous float32 [D]")
+    if out is None:
+        out = torch.empty_like(x)
+    o2 = out.reshape(-1, d)
+    check(lib().nq_gated_rmsnorm(ptr(x2), x2.stride(0), ptr(g2), g2.stride(0), ptr(weight), float(eps), ptr(o2),
+                                 o2.stride(0), x2.shape[0], d, dtype_code(x.dtype), stream_of(x)), "gated_rmsnorm")
+    return out
+
+
 __all__ = ["store_kvcache", "paged_decode", "varlen_prefill", "prepare_decode", "decode_plan", "qk_norm_rope_store",
-           "output_gate", "gdn_decode", "gdn_prefill",
+           "output_gate", "gdn_decode", "gdn_prefill", "gated_rmsnorm",
            "decode_workspace", "prefill_workspace", "_lib"]

@@ -84,3 +84,22 @@ def gdn_prefill(q, k, v, a, b, A_log, dt_bias, cu_seqlens, state, state_indices,
             if has:
                 state[slot, hv] = S
     return out
+
+
+def gated_rmsnorm(x, gate, weight, eps, dtype):
+    """RMSNormGated.forward (layers/layernorm.py:143-157), eager, over the last
+    axis: n = rnd(x / sqrt(mean(x^2) + eps)); rnd(rnd(n * rnd(w)) * silu(g)),
+    silu(g) = g / (1 + exp(-g)) in float32 operations, rnd = round to dtype.
+    The float32 sum of squares uses qk_norm_rope.sum_squares's order (one
+    valid order for the reference's mean)."""
+    from .qk_norm_rope import round_to, sum_squares
+    F32 = np.float32
+    xf = np.asarray(x, dtype=F32)
+    var = sum_squares(xf) * F32(1.0 / xf.shape[-1])
+    r = (F32(1.0) / np.sqrt((var + F32(eps)).astype(F32))).astype(F32)
+    n = round_to(xf * r, dtype)
+    nw = round_to(n * round_to(np.asarray(weight, dtype=F32), dtype), dtype)
+    g = np.asarray(gate, dtype=F32)
+    with np.errstate(over="ignore"):
+        silu = (g / (F32(1.0) + np.exp(-g).astype(F32))).astype(F32)
+    return round_to(nw * silu, dtype)

@@ -156,3 +156,25 @@ def test_gdn_prefill_then_decode_equals_longer_prefill(cuda):
     torch.cuda.synchronize()
     assert torch.equal(st1, st2)
     assert torch.equal(o_dec[0].view(torch.int16), o_all[L].view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float16, 128), (torch.bfloat16, 256),
+                                     (torch.bfloat16, 64)])
+def test_gated_rmsnorm_matches_oracle(cuda, dtype, d):
+    """Against the oracle (same sum order, every operation rounded on its
+    own): within one ulp on at most 0.5% of elements -- the last float32 bit
+    of exp() in the silu is free; in place on the GDN output layout [T, HV, D]."""
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(37, 4, d, generator=g).to(dtype)
+    z = (torch.randn(37, 4, d, generator=g) * 2).to(dtype)
+    w = 0.5 + torch.rand(d, generator=g)
+    name = "bf16" if dtype == torch.bfloat16 else "f16"
+    ref = gdn.gated_rmsnorm(x.float().numpy(), z.float().numpy(), w.numpy(), 1e-6, name)
+    xd = x.to(cuda)
+    out = kernels.gated_rmsnorm(xd, z.to(cuda), w.to(cuda), 1e-6, out=xd)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == xd.data_ptr()
+    it = torch.int16
+    key = lambda t: (lambda b: torch.where(b < 0, -(b + 32768), b))(t.contiguous().view(it).int())
+    ulps = (key(out.cpu()) - key(torch.from_numpy(ref).to(dtype))).abs()
+    assert int(ulps.max()) <= 1 and float((ulps > 0).float().mean()) <= 5e-3

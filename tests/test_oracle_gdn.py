@@ -64,3 +64,28 @@ def test_decay_composes_and_gqa_map():
     np.testing.assert_allclose(out[0, 3], o)
     np.testing.assert_allclose(pool[2, 3], S)
     assert np.isnan(out[1]).all() and np.array_equal(pool[:2], ref_pool[:2])
+
+
+def test_gated_rmsnorm_oracle():
+    """Against the reference's formula as eager torch CPU ops on bf16 tensors
+    (≤ 1 ulp, almost always exact: the sum order and rsqrt are free); gate 0
+    gives 0; weight 0 gives 0; scaling x by 2^k with eps = 0 changes nothing."""
+    from oracle.qk_norm_rope import round_to
+    F32 = np.float32
+    x = round_to(rng.standard_normal((300, 128)).astype(F32), "bf16")
+    z = round_to(rng.standard_normal((300, 128)).astype(F32) * 2, "bf16")
+    w = (0.5 + rng.random(128)).astype(F32)
+    got = gdn.gated_rmsnorm(x, z, w, 1e-6, "bf16")
+    xt, zt = torch.from_numpy(x).bfloat16(), torch.from_numpy(z).bfloat16()
+    xf = xt.float()
+    ref = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16) * torch.from_numpy(w).to(torch.bfloat16)
+    ref = (ref * torch.nn.functional.silu(zt.float())).to(torch.bfloat16).float().numpy()
+    gu = (got.view(np.uint32) >> 16).astype(np.int64)
+    ru = (ref.view(np.uint32) >> 16).astype(np.int64)
+    key = lambda u: np.where(u & 0x8000, 0x8000 - u, u)
+    ulps = np.abs(key(gu) - key(ru))
+    assert ulps.max() <= 1 and (ulps > 0).mean() < 5e-3
+    assert np.all(gdn.gated_rmsnorm(x, np.zeros_like(z), w, 1e-6, "bf16") == 0)
+    assert np.all(gdn.gated_rmsnorm(x, z, np.zeros_like(w), 1e-6, "bf16") == 0)
+    y0 = gdn.gated_rmsnorm(x, z, w, 0.0, "bf16")
+    assert np.array_equal(gdn.gated_rmsnorm(x * F32(8), z, w, 0.0, "bf16"), y0)
