@@ -18,6 +18,11 @@ Modules
 ``sdpa_path``  the CPU baseline: torch block gather + repeat_interleave +
                ``scaled_dot_product_attention`` (the path ``bench.py`` times
                on the host cores).
+``qk_norm_rope`` q/k Gemma RMS norm + partial rotary embedding + KV store
+               (float32 operations in the reference's rounding order).
+``output_gate`` the ``attn_output * sigmoid(gate)`` gate of Qwen3.5.
+``gdn``        the gated delta rule (decode step, packed prefill) in float64
+               and the gated RMS norm of its output.
 
 Parity pinning (what checks each function; see ``tests/test_oracle.py``):
 
@@ -33,6 +38,9 @@ Parity pinning (what checks each function; see ``tests/test_oracle.py``):
   the causal prefill, padding of block tables).
 * ``metadata``             -- restated closed forms, checked against a
   token-by-token simulation of the reference's block bookkeeping.
+
+Each of the later modules states in its docstring what pins it; the tests
+are ``tests/test_oracle_qk_norm_rope.py`` and ``tests/test_oracle_gdn.py``.
 
 flash_attn's own bit-level rounding (the third-party library the reference
 calls, unpinned version, not installed here) is NOT pinned: the attention
