@@ -18,7 +18,8 @@ prefill, and the stand-alone in-place gate pass for comparison), head_dim 256
 (``cfg2_d256``, ``cfg5_d256``, ``cfg3_d256``) and the Gated DeltaNet decode
 step (``gdn_decode``: HBM GB/s over the state pool) and prefill
 (``gdn_prefill``: recurrent form over cfg3's sequence lengths), and the gated
-RMS norm of its output (``gdn_norm``, HBM GB/s).
+RMS norm of its output (``gdn_norm``) and the causal conv1d before it
+(``gdn_conv``), HBM GB/s.
 ``roofline`` covers the dominant kernel of the headline workload (paged
 decode: main kernel + split-K merge), timed with HIP events on the stream
 the kernels run on.  ``cpu_baseline`` times the CPU restatement of the path
@@ -273,6 +274,30 @@ def bench_gated_norm(steps, warmup, seed=0, HV=32):
                 bytes=nb, rows=T * HV), None
 
 
+def bench_gdn_conv(steps, warmup, seed=0, C=8192, K=4):
+    """GDN causal conv1d + silu over cfg3's packed sequences (prefill) with
+    Qwen3.5-style channels C = 2 * 16 * 128 + 32 * 128: reads x once, writes
+    the output and each sequence's last K - 1 inputs."""
+    import torch
+    from nano_qwen_amd import kernels
+    from oracle.inputs import make_prefill_case
+
+    lq = make_prefill_case("cfg3", seed=seed, device="cpu")["lq"]
+    cu = torch.tensor([0] + list(torch.tensor(lq).cumsum(0).tolist()), dtype=torch.int32, device="cuda")
+    T = int(cu[-1])
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(T, C, device="cuda", generator=g).bfloat16()
+    w = torch.randn(C, K, device="cuda", generator=g).bfloat16()
+    state = torch.zeros(len(lq), C, K - 1, device="cuda", dtype=torch.bfloat16)
+    idx = torch.arange(len(lq), dtype=torch.int32, device="cuda")
+    out = torch.empty_like(x)
+    ms = _events_time(lambda i: kernels.gdn_conv1d(x, w, state, idx, cu_seqlens=cu, out=out), steps,
+                      max(warmup, 100))
+    nb = 2 * x.numel() * 2 + w.numel() * 2 + state.numel() * 2
+    return dict(ms_per_step=ms, gbs=nb / (ms * 1e-3) / 1e9, hbm_frac=nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                bytes=nb, tokens=T, channels=C), None
+
+
 def cpu_baseline_decode(case, n_seqs=8, reps=5):
     """Median wall time of the CPU path on the first n_seqs sequences."""
     import torch
@@ -394,7 +419,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None,
                     help="run one config (cfg2|cfg3|cfg4|cfg5|cfg3_norm_rope|cfg2_norm_rope|cfg2_gate|cfg3_gate|"
-                         "cfg2_d256|cfg5_d256|cfg3_d256|gdn_decode|gdn_prefill|gdn_norm)")
+                         "cfg2_d256|cfg5_d256|cfg3_d256|gdn_decode|gdn_prefill|gdn_norm|gdn_conv)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration)")
     args = ap.parse_args()
@@ -416,7 +441,8 @@ def main():
     head = None
     todo = [args.only] if args.only else ["cfg2", "cfg3", "cfg4", "cfg5", "cfg3_norm_rope", "cfg2_norm_rope",
                                                    "cfg2_gate", "cfg3_gate", "cfg2_d256", "cfg5_d256",
-                                                   "cfg3_d256", "gdn_decode", "gdn_prefill", "gdn_norm"]
+                                                   "cfg3_d256", "gdn_decode", "gdn_prefill", "gdn_norm",
+                                                   "gdn_conv"]
     cpu = None
     for name in todo:
         print(f"[bench] {name} ...", file=sys.stderr, flush=True)
@@ -426,6 +452,8 @@ def main():
             r, case = bench_gate(name.split("_")[0], args.steps, args.warmup)
         elif name == "gdn_decode":
             r, case = bench_gdn(args.steps, args.warmup)
+        elif name == "gdn_conv":
+            r, case = bench_gdn_conv(args.steps, args.warmup)
         elif name == "gdn_norm":
             r, case = bench_gated_norm(args.steps, args.warmup)
         elif name == "gdn_prefill":

@@ -350,6 +350,28 @@ int nq_gated_rmsnorm(const void *x, int64_t x_row_stride, const void *gate, int6
                      const float *weight, float eps, void *out, int64_t out_row_stride,
                      int64_t rows, int dim, int dtype, void *stream);
 
+/*
+ * Causal depthwise conv1d + silu in front of the Gated DeltaNet, with the
+ * conv state pool.  Replaces, in GatedDeltaNet (layers/gated_delta_net.py),
+ * silu(conv1d(qkv)[:, :, :S]) and the state kept for decode (prefill,
+ * :178-180, 207-213) and x = cat(conv_state, qkv); silu(conv1d(x)); the new
+ * state x[:, 1:] (decode, :218-227).
+ * x, out [rows, channels] (16-bit dtype), weight [channels, kernel_size]
+ * (dtype; the reference's conv1d.weight [C, 1, K]), conv_state
+ * [num_slots, channels, kernel_size - 1] (dtype, oldest input first).
+ * cu_seqlens == NULL (decode): sequence b is row b, its window is the slot's
+ *   state then x[b]; the slot then holds the last K - 1 inputs.
+ * cu_seqlens != NULL (prefill): sequence n owns rows [cu[n], cu[n+1]), its
+ *   window starts from zeros (initial_state_from_slot must be 0, as in the
+ *   reference); its slot receives its last K - 1 inputs.
+ * out = rnd(y / (1 + exp(-y))), y = rnd(sum_j w[c][j] x[t-K+1+j]) in fp32.
+ * Slots outside [0, num_slots) skip the state.  kernel_size in [2, 8].
+ */
+int nq_gdn_conv1d(const void *x, int64_t x_row_stride, const void *weight, int kernel_size,
+                  const int32_t *cu_seqlens, int num_seqs, void *conv_state,
+                  const int32_t *state_indices, int64_t num_slots, int initial_state_from_slot,
+                  void *out, int64_t out_row_stride, int channels, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

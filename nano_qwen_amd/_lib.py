@@ -62,6 +62,8 @@ _SIGS = {
                                c_int64, c_int, c_void_p, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p]),
     "nq_gated_rmsnorm": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_float, c_void_p, c_int64,
                                  c_int64, c_int, c_int, c_void_p]),
+    "nq_gdn_conv1d": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p, c_int64,
+                              c_int, c_void_p, c_int64, c_int, c_int, c_void_p]),
     "nq_qk_norm_rope_store": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                       c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_float,
                                       c_float, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p,

@@ -1,0 +1,162 @@
+// Causal depthwise conv1d + silu in front of the Gated DeltaNet (gfx950).
+//
+// Reference: GatedDeltaNet (layers/gated_delta_net.py)
+//   prefill (:178-180, 207-213):  silu(conv1d(qkv)[:, :, :S]) with padding
+//     K - 1 (a causal conv from zeros); the state kept for decode is the
+//     last K - 1 raw inputs;
+//   decode  (:218-227):  x = cat(conv_state, qkv); silu(conv1d(x)); the new
+//     state is x[:, 1:].
+// Per channel c and token t (window of the K inputs ending at t, earlier
+// positions from the sequence's initial state or zero):
+//   y = rnd(sum_j w[c][j] * x[t - K + 1 + j])    (fp32, j = 0 .. K-1 in order)
+//   out = rnd(y / (1 + exp(-y)))
+// with rnd = round to the 16-bit type, as torch computes the bf16 conv and the
+// silu on its bf16 result.  One lane per (token, 2 channels): every output
+// is independent, so prefill runs in parallel over tokens.
+#include "nq_device.hpp"
+
+namespace nq {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxK = 8;
+
+struct ConvArgs {
+  const uint8_t *x;  // [T, C] rows (16-bit)
+  int64_t x_rs;      // bytes
+  const uint8_t *w;  // [C, K] (16-bit)
+  const int32_t *cu;  // [N + 1], or null: one token per sequence (decode)
+  uint8_t *state;     // [slots, C, K - 1] (16-bit)
+  const int32_t *idx;  // [N]
+  int64_t num_slots;
+  int from_state;
+  uint8_t *out;  // [T, C]
+  int64_t o_rs;
+  int C, K, N;
+};
+
+template <class T>
+__device__ inline float ld16(const uint8_t *p, int64_t i) {
+  return T::to_float(reinterpret_cast<const uint16_t *>(p)[i]);
+}
+template <class T>
+__device__ inline float rnd16(float f) {
+  asm("" : "+v"(f));
+  return T::to_float(T::from_float(f));
+}
+
+// grid.x covers channel pairs, grid.y = sequence (decode: the token), and
+// grid.z splits a prefill sequence's tokens (token t0 + z, t0 + z + gridDim.z, ...).
+template <class T>
+__global__ __launch_bounds__(kThreads) void conv_kernel(const ConvArgs a) {
+#pragma clang fp contract(off)
+  const int c = 2 * (blockIdx.x * kThreads + threadIdx.x);
+  const int n = blockIdx.y;
+  if (c >= a.C) return;
+  const int K = a.K;
+  int64_t t0 = n, t1 = n + 1;
+  if (a.cu) {
+    t0 = a.cu[n];
+    t1 = a.cu[n + 1];
+  }
+  const int32_t slot = a.idx[n];
+  const bool has_slot = slot >= 0 && slot < a.num_slots;
+  const int64_t sbase = (static_cast<int64_t>(has_slot ? slot : 0) * a.C) * (K - 1);
+  float w0[kMaxK], w1[kMaxK];
+#pragma unroll
+  for (int j = 0; j < kMaxK; ++j)
+    if (j < K) {
+      w0[j] = ld16<T>(a.w, static_cast<int64_t>(c) * K + j);
+      w1[j] = c + 1 < a.C ? ld16<T>(a.w, static_cast<int64_t>(c + 1) * K + j) : 0.f;
+    }
+  // Input at position p of this sequence (p < t0: the initial state or zero).
+  auto in = [&](int64_t p, int ch) -> float {
+    if (ch >= a.C) return 0.f;
+    if (p >= t0) return ld16<T>(a.x + p * a.x_rs, ch);
+    const int64_t back = t0 - p;  // 1 .. K-1
+    if (!(a.from_state && has_slot) || back > K - 1) return 0.f;
+    return ld16<T>(a.state, sbase + static_cast<int64_t>(ch) * (K - 1) + (K - 1 - back));
+  };
+  for (int64_t t = t0 + blockIdx.z; t < t1; t += gridDim.z) {
+    float y0 = 0.f, y1 = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j)
+      if (j < K) {
+        const int64_t p = t - K + 1 + j;
+        y0 += w0[j] * in(p, c);
+        y1 += w1[j] * in(p, c + 1);
+      }
+    y0 = rnd16<T>(y0);
+    y1 = rnd16<T>(y1);
+    const float s0 = y0 / (1.0f + expf(-y0)), s1 = y1 / (1.0f + expf(-y1));
+    uint16_t *op = reinterpret_cast<uint16_t *>(a.out + t * a.o_rs) + c;
+    if (c + 1 < a.C) {
+      float r0 = s0, r1 = s1;
+      asm("" : "+v"(r0), "+v"(r1));
+      *reinterpret_cast<uint32_t *>(op) = T::pack2(r0, r1);
+    } else {
+      op[0] = T::from_float(rnd16<T>(s0));
+    }
+  }
+  // The state after the sequence: its last K - 1 inputs, written by the
+  // z = 0 workgroups.  Decode (grid.z = 1): the same lane read the old state
+  // above.  Prefill never reads the state (it starts from zero, as the
+  // reference does), so other token blocks cannot race with this write.
+  if (!has_slot || blockIdx.z != 0) return;
+  float keep0[kMaxK], keep1[kMaxK];
+#pragma unroll
+  for (int j = 0; j < kMaxK - 1; ++j)
+    if (j < K - 1) {
+      keep0[j] = in(t1 - (K - 1) + j, c);
+      keep1[j] = in(t1 - (K - 1) + j, c + 1);
+    }
+#pragma unroll
+  for (int j = 0; j < kMaxK - 1; ++j)
+    if (j < K - 1) {
+      uint16_t *sp = reinterpret_cast<uint16_t *>(a.state) + sbase;
+      sp[static_cast<int64_t>(c) * (K - 1) + j] = T::from_float(keep0[j]);
+      if (c + 1 < a.C) sp[static_cast<int64_t>(c + 1) * (K - 1) + j] = T::from_float(keep1[j]);
+    }
+}
+
+}  // namespace
+}  // namespace nq
+
+using namespace nq;
+
+extern "C" int nq_gdn_conv1d(const void *x, int64_t x_row_stride, const void *weight, int kernel_size,
+                             const int32_t *cu_seqlens, int num_seqs, void *conv_state,
+                             const int32_t *state_indices, int64_t num_slots, int initial_state_from_slot,
+                             void *out, int64_t out_row_stride, int channels, int dtype, void *stream) {
+  if (num_seqs < 0 || channels <= 0 || kernel_size < 2 || kernel_size > kMaxK || num_slots < 0)
+    return fail(NQ_EINVAL, "gdn_conv1d: bad sizes (seqs=%d channels=%d kernel=%d, kernel in [2, %d])", num_seqs,
+                channels, kernel_size, kMaxK);
+  if (dtype != NQ_BF16 && dtype != NQ_F16) return fail(NQ_EUNSUPPORTED, "gdn_conv1d: dtype %d (f16/bf16)", dtype);
+  if (cu_seqlens && initial_state_from_slot)
+    return fail(NQ_EUNSUPPORTED, "gdn_conv1d: prefill starts from a zero state (as the reference's does)");
+  if (num_seqs == 0) return NQ_OK;
+  if (!x || !weight || !conv_state || !state_indices || !out) return fail(NQ_EINVAL, "gdn_conv1d: null pointer");
+  if (!aligned(out, 4) || (out_row_stride * 2) % 4) return fail(NQ_EINVAL, "gdn_conv1d: out rows 4-byte aligned");
+  if (num_seqs > 65535) return fail(NQ_EINVAL, "gdn_conv1d: too many sequences for one launch");
+  ConvArgs g{};
+  g.x = static_cast<const uint8_t *>(x);
+  g.x_rs = x_row_stride * 2;
+  g.w = static_cast<const uint8_t *>(weight);
+  g.cu = cu_seqlens;
+  g.state = static_cast<uint8_t *>(conv_state);
+  g.idx = state_indices;
+  g.num_slots = num_slots;
+  g.from_state = cu_seqlens ? 0 : 1;
+  g.out = static_cast<uint8_t *>(out);
+  g.o_rs = out_row_stride * 2;
+  g.C = channels;
+  g.K = kernel_size;
+  g.N = num_seqs;
+  // Channel pairs over grid.x; the tokens of a prefill sequence over grid.z.
+  const int pairs = (channels + 1) / 2;
+  dim3 grid((pairs + kThreads - 1) / kThreads, num_seqs, cu_seqlens ? 64 : 1);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == NQ_BF16) conv_kernel<BF16><<<grid, kThreads, 0, s>>>(g);
+  else conv_kernel<F16><<<grid, kThreads, 0, s>>>(g);
+  return check_launch("gdn_conv1d");
+}

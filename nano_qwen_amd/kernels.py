@@ -387,6 +387,37 @@ def gated_rmsnorm(x, gate, weight, eps, out=None):
     return out
 
 
+def gdn_conv1d(x, weight, conv_state, state_indices, cu_seqlens=None, out=None):
+    """Causal depthwise conv1d + silu with the conv state pool (GatedDeltaNet,
+    layers/gated_delta_net.py:178-180, 207-213, 218-227).
+
+    ``x [rows, C]`` 16-bit; ``weight [C, K]`` (or ``[C, 1, K]``);
+    ``conv_state [slots, C, K - 1]`` of x's dtype; ``state_indices [N]``
+    int32.  Without ``cu_seqlens`` (decode) row b is sequence b's new token;
+    with it (prefill) the rows are packed sequences starting from zero.
+    Returns ``out [rows, C]``; the slots are updated in place.
+    """
+    require_cuda(x, weight, conv_state, state_indices, cu_seqlens, what="gdn_conv1d")
+    rows, C = x.shape
+    w2 = weight.reshape(C, -1)
+    K = w2.shape[1]
+    if x.stride(-1) != 1 or not w2.is_contiguous() or w2.dtype != x.dtype:
+        raise RuntimeError("gdn_conv1d: x rows contiguous; weight contiguous [C, K] of x's dtype")
+    if conv_state.dtype != x.dtype or not conv_state.is_contiguous() or conv_state.shape[1:] != (C, K - 1):
+        raise RuntimeError("gdn_conv1d: conv_state must be contiguous [slots, C, K - 1] of x's dtype")
+    n = rows if cu_seqlens is None else cu_seqlens.numel() - 1
+    if state_indices.dtype != torch.int32 or state_indices.numel() != n:
+        raise RuntimeError("gdn_conv1d: state_indices must be int32 [N]")
+    if cu_seqlens is not None and cu_seqlens.dtype != torch.int32:
+        raise RuntimeError("gdn_conv1d: cu_seqlens must be int32")
+    if out is None:
+        out = torch.empty_like(x)
+    check(lib().nq_gdn_conv1d(ptr(x), x.stride(0), ptr(w2), K, ptr(cu_seqlens), n, ptr(conv_state),
+                              ptr(state_indices), conv_state.shape[0], 0, ptr(out), out.stride(0), C,
+                              dtype_code(x.dtype), stream_of(x)), "gdn_conv1d")
+    return out
+
+
 __all__ = ["store_kvcache", "paged_decode", "varlen_prefill", "prepare_decode", "decode_plan", "qk_norm_rope_store",
-           "output_gate", "gdn_decode", "gdn_prefill", "gated_rmsnorm",
+           "output_gate", "gdn_decode", "gdn_prefill", "gated_rmsnorm", "gdn_conv1d",
            "decode_workspace", "prefill_workspace", "_lib"]

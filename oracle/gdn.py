@@ -103,3 +103,39 @@ def gated_rmsnorm(x, gate, weight, eps, dtype):
     with np.errstate(over="ignore"):
         silu = (g / (F32(1.0) + np.exp(-g).astype(F32))).astype(F32)
     return round_to(nw * silu, dtype)
+
+
+def conv1d_silu(x, weight, conv_state, state_indices, cu_seqlens=None, dtype="bf16"):
+    """Causal depthwise conv1d + silu (layers/gated_delta_net.py:178-180,
+    207-213, 218-227).  x [rows, C], weight [C, K], conv_state [slots, C, K-1]
+    (updated in place).  Per output: y = rnd(sum_j w[j] x[t-K+1+j]) (float32,
+    j in order), out = rnd(y / (1 + exp(-y))).  Decode (no cu_seqlens): row b
+    continues the slot's state; prefill: each sequence starts from zeros and
+    its slot keeps its last K - 1 inputs."""
+    from .qk_norm_rope import round_to
+    F32 = np.float32
+    x = np.asarray(x, dtype=F32)
+    w = np.asarray(weight, dtype=F32)
+    rows, C = x.shape
+    K = w.shape[1]
+    out = np.zeros((rows, C), dtype=F32)
+    seqs = [(b, b + 1) for b in range(rows)] if cu_seqlens is None else \
+        [(int(cu_seqlens[i]), int(cu_seqlens[i + 1])) for i in range(len(cu_seqlens) - 1)]
+    for n, (t0, t1) in enumerate(seqs):
+        slot = int(state_indices[n])
+        has = 0 <= slot < conv_state.shape[0]
+        hist = (np.asarray(conv_state[slot], dtype=F32) if (has and cu_seqlens is None)
+                else np.zeros((C, K - 1), dtype=F32))
+        seq = np.concatenate([hist, x[t0:t1].T], axis=1)  # [C, K-1 + L]
+        for i in range(t1 - t0):
+            win = seq[:, i:i + K]
+            y = np.zeros(C, dtype=F32)
+            for j in range(K):
+                y = (y + (w[:, j] * win[:, j]).astype(F32)).astype(F32)
+            y = round_to(y, dtype)
+            with np.errstate(over="ignore"):
+                s = (y / (F32(1.0) + np.exp(-y).astype(F32))).astype(F32)
+            out[t0 + i] = round_to(s, dtype)
+        if has:
+            conv_state[slot] = seq[:, -(K - 1):]
+    return out
