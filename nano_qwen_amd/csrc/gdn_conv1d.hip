@@ -11,8 +11,11 @@
 //   y = rnd(sum_j w[c][j] * x[t - K + 1 + j])    (fp32, j = 0 .. K-1 in order)
 //   out = rnd(y / (1 + exp(-y)))
 // with rnd = round to the 16-bit type, as torch computes the bf16 conv and the
-// silu on its bf16 result.  One lane per (token, 2 channels): every output
-// is independent, so prefill runs in parallel over tokens.
+// silu on its bf16 result.  One lane per pair of channels and run of kRun
+// consecutive tokens: the last K - 1 inputs stay in registers (a sliding
+// window), so each token costs one coalesced 4-byte load and one store per
+// lane; the runs of a sequence are independent, so prefill is parallel over
+// tokens too.
 #include "nq_device.hpp"
 
 namespace nq {
@@ -20,6 +23,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxK = 8;
+constexpr int kRun = 32;  // tokens per lane and run
 
 struct ConvArgs {
   const uint8_t *x;  // [T, C] rows (16-bit)
@@ -46,7 +50,7 @@ __device__ inline float rnd16(float f) {
 }
 
 // grid.x covers channel pairs, grid.y = sequence (decode: the token), and
-// grid.z splits a prefill sequence's tokens (token t0 + z, t0 + z + gridDim.z, ...).
+// grid.z walks a prefill sequence's runs (run z, z + gridDim.z, ...).
 template <class T>
 __global__ __launch_bounds__(kThreads) void conv_kernel(const ConvArgs a) {
 #pragma clang fp contract(off)
@@ -77,27 +81,56 @@ __global__ __launch_bounds__(kThreads) void conv_kernel(const ConvArgs a) {
     if (!(a.from_state && has_slot) || back > K - 1) return 0.f;
     return ld16<T>(a.state, sbase + static_cast<int64_t>(ch) * (K - 1) + (K - 1 - back));
   };
-  for (int64_t t = t0 + blockIdx.z; t < t1; t += gridDim.z) {
-    float y0 = 0.f, y1 = 0.f;
-#pragma unroll
-    for (int j = 0; j < kMaxK; ++j)
-      if (j < K) {
-        const int64_t p = t - K + 1 + j;
-        y0 += w0[j] * in(p, c);
-        y1 += w1[j] * in(p, c + 1);
-      }
-    y0 = rnd16<T>(y0);
-    y1 = rnd16<T>(y1);
-    const float s0 = y0 / (1.0f + expf(-y0)), s1 = y1 / (1.0f + expf(-y1));
-    uint16_t *op = reinterpret_cast<uint16_t *>(a.out + t * a.o_rs) + c;
-    if (c + 1 < a.C) {
-      float r0 = s0, r1 = s1;
-      asm("" : "+v"(r0), "+v"(r1));
-      *reinterpret_cast<uint32_t *>(op) = T::pack2(r0, r1);
+  // Both channels of input position p as one 4-byte load (p >= t0), else
+  // from the state or zero.
+  auto in2 = [&](int64_t p, float &v0, float &v1) {
+    if (p >= t0 && c + 1 < a.C) {
+      const uint32_t w2 = *reinterpret_cast<const uint32_t *>(a.x + p * a.x_rs + 2 * c);
+      v0 = T::to_float(static_cast<uint16_t>(w2 & 0xffffu));
+      v1 = T::to_float(static_cast<uint16_t>(w2 >> 16));
     } else {
-      op[0] = T::from_float(rnd16<T>(s0));
+      v0 = in(p, c);
+      v1 = in(p, c + 1);
+    }
+  };
+  const int64_t nrun = (t1 - t0 + kRun - 1) / kRun;
+  for (int64_t run = blockIdx.z; run < nrun; run += gridDim.z) {
+    const int64_t ts = t0 + run * kRun, te = min(ts + kRun, t1);
+    float h0[kMaxK], h1[kMaxK];  // window: inputs ts - K + 1 + j, j < K - 1
+#pragma unroll
+    for (int j = 0; j < kMaxK - 1; ++j)
+      if (j < K - 1) in2(ts - K + 1 + j, h0[j], h1[j]);
+    for (int64_t t = ts; t < te; ++t) {
+      float x0, x1;
+      in2(t, x0, x1);
+      float y0 = 0.f, y1 = 0.f;
+#pragma unroll
+      for (int j = 0; j < kMaxK; ++j)
+        if (j < K) {
+          const float v0 = j < K - 1 ? h0[j] : x0, v1 = j < K - 1 ? h1[j] : x1;
+          y0 += w0[j] * v0;
+          y1 += w1[j] * v1;
+        }
+#pragma unroll
+      for (int j = 0; j < kMaxK - 1; ++j)
+        if (j < K - 1) {
+          h0[j] = j + 1 < K - 1 ? h0[j + 1] : x0;
+          h1[j] = j + 1 < K - 1 ? h1[j + 1] : x1;
+        }
+      y0 = rnd16<T>(y0);
+      y1 = rnd16<T>(y1);
+      const float s0 = y0 / (1.0f + expf(-y0)), s1 = y1 / (1.0f + expf(-y1));
+      uint16_t *op = reinterpret_cast<uint16_t *>(a.out + t * a.o_rs) + c;
+      if (c + 1 < a.C) {
+        float r0 = s0, r1 = s1;
+        asm("" : "+v"(r0), "+v"(r1));
+        __builtin_nontemporal_store(T::pack2(r0, r1), reinterpret_cast<uint32_t *>(op));
+      } else {
+        op[0] = T::from_float(rnd16<T>(s0));
+      }
     }
   }
+
   // The state after the sequence: its last K - 1 inputs, written by the
   // z = 0 workgroups.  Decode (grid.z = 1): the same lane read the old state
   // above.  Prefill never reads the state (it starts from zero, as the
@@ -136,7 +169,8 @@ extern "C" int nq_gdn_conv1d(const void *x, int64_t x_row_stride, const void *we
     return fail(NQ_EUNSUPPORTED, "gdn_conv1d: prefill starts from a zero state (as the reference's does)");
   if (num_seqs == 0) return NQ_OK;
   if (!x || !weight || !conv_state || !state_indices || !out) return fail(NQ_EINVAL, "gdn_conv1d: null pointer");
-  if (!aligned(out, 4) || (out_row_stride * 2) % 4) return fail(NQ_EINVAL, "gdn_conv1d: out rows 4-byte aligned");
+  if (!aligned(out, 4) || (out_row_stride * 2) % 4 || !aligned(x, 4) || (x_row_stride * 2) % 4)
+    return fail(NQ_EINVAL, "gdn_conv1d: x and out rows 4-byte aligned");
   if (num_seqs > 65535) return fail(NQ_EINVAL, "gdn_conv1d: too many sequences for one launch");
   ConvArgs g{};
   g.x = static_cast<const uint8_t *>(x);
@@ -154,7 +188,7 @@ extern "C" int nq_gdn_conv1d(const void *x, int64_t x_row_stride, const void *we
   g.N = num_seqs;
   // Channel pairs over grid.x; the tokens of a prefill sequence over grid.z.
   const int pairs = (channels + 1) / 2;
-  dim3 grid((pairs + kThreads - 1) / kThreads, num_seqs, cu_seqlens ? 64 : 1);
+  dim3 grid((pairs + kThreads - 1) / kThreads, num_seqs, cu_seqlens ? 64 : 1);  // 64 runs at a time
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == NQ_BF16) conv_kernel<BF16><<<grid, kThreads, 0, s>>>(g);
   else conv_kernel<F16><<<grid, kThreads, 0, s>>>(g);
