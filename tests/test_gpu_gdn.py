@@ -212,3 +212,57 @@ def test_conv1d_decode_and_prefill(cuda):
     ulps = (key(od.cpu()[live]) - key(torch.from_numpy(refd).to(bf)[live])).abs()
     assert int(ulps.max()) <= 1 and float((ulps > 0).float().mean()) <= 5e-3
     assert torch.equal(st_dev.cpu().float(), torch.from_numpy(ref_state))
+
+
+def test_gdn_core_layer_path(cuda):
+    """layers.gdn_core (conv1d -> delta rule -> gated norm on the pools, with a
+    module carrying the reference GatedDeltaNet's parameters): a prefill of
+    three packed sequences, then two decode steps, against the oracle chain."""
+    from types import SimpleNamespace
+    from nano_qwen_amd.layers import gdn_core
+    g = torch.Generator().manual_seed(10)
+    H, HV, D, K, bf = 2, 4, 128, 4, torch.bfloat16
+    C = 2 * H * D + HV * D
+    layer = SimpleNamespace(
+        num_k_heads=H, num_v_heads=HV, head_k_dim=D, head_v_dim=D,
+        conv1d=SimpleNamespace(weight=(torch.randn(C, 1, K, generator=g) * 0.4).to(bf).to(cuda)),
+        A_log=(torch.randn(HV, generator=g) * 0.5).to(cuda), dt_bias=(torch.randn(HV, generator=g) * 0.5).to(bf).to(cuda),
+        norm=SimpleNamespace(weight=(0.5 + torch.rand(D, generator=g)).to(cuda), eps=1e-6),
+        conv_states=torch.zeros(5, C, K - 1, dtype=bf, device=cuda),
+        recurrent_states=torch.zeros(5, HV, D, D, device=cuda))
+    lens = [3, 40, 17]
+    idx = torch.tensor([4, 1, 2], dtype=torch.int32)
+    ref_conv = np.zeros((5, C, K - 1), np.float32)
+    ref_rec = np.zeros((5, HV, D, D))
+    w = layer.conv1d.weight.reshape(C, K).float().cpu().numpy()
+    A, dt = layer.A_log.float().cpu().numpy(), layer.dt_bias.float().cpu().numpy()
+    nw = layer.norm.weight.cpu().numpy()
+
+    def run(T, cu):
+        x = (torch.randn(T, C, generator=g) * 2).to(bf)
+        z = torch.randn(T, HV * D, generator=g).to(bf)
+        a = torch.randn(T, HV, generator=g).to(bf)
+        b = torch.randn(T, HV, generator=g).to(bf)
+        out = gdn_core(layer, x.to(cuda), z.to(cuda), a.to(cuda), b.to(cuda), idx.to(cuda),
+                       None if cu is None else cu.to(cuda))
+        torch.cuda.synchronize()
+        mixed = gdn.conv1d_silu(x.float().numpy(), w, ref_conv, idx.numpy(), None if cu is None else cu.numpy())
+        q = mixed[:, :H * D].reshape(T, H, D)
+        k = mixed[:, H * D:2 * H * D].reshape(T, H, D)
+        v = mixed[:, 2 * H * D:].reshape(T, HV, D)
+        f = lambda t: t.double().numpy()
+        if cu is None:
+            y = gdn.gdn_decode(q, k, v, f(a), f(b), A, dt, ref_rec, idx.numpy())
+        else:
+            y = gdn.gdn_prefill(q, k, v, f(a), f(b), A, dt, cu.numpy(), ref_rec, idx.numpy())
+        from oracle.qk_norm_rope import round_to
+        yb = round_to(y.astype(np.float32), "bf16").reshape(-1, D)
+        ref = gdn.gated_rmsnorm(yb, z.float().numpy().reshape(-1, D), nw, 1e-6, "bf16").reshape(T, HV * D)
+        o = out.float().cpu().numpy()
+        assert np.all(np.abs(o - ref) <= 2 ** -6 * np.abs(ref) + 2e-2 * np.abs(ref).max()), float(np.abs(o - ref).max())
+        assert np.abs(layer.recurrent_states.cpu().double().numpy() - ref_rec).max() <= 1e-4 * max(1.0, np.abs(ref_rec).max())
+        assert torch.equal(layer.conv_states.cpu().float(), torch.from_numpy(ref_conv))
+
+    run(sum(lens), torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32))
+    run(3, None)
+    run(3, None)
