@@ -196,8 +196,9 @@ int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_head_stride
  * nq_paged_decode_gated.  gate [total_q, num_q_heads, head_dim] has the type
  * of q/out, strides (gate_row_stride, gate_head_stride, 1), 16-byte aligned
  * (e.g. the gate half of q_proj's output); total_q = cu_seqlens_q[num_seqs].
- * The default 16-bit kernel applies the gate in its own output store; the
- * fp8-K/V kernel is followed by one nq_output_gate pass on the same stream.
+ * The kernels apply the gate in their own output stores (a non-default
+ * launch shape, NQ_PREFILL_SHAPE=a, is followed by one nq_output_gate pass on
+ * the same stream instead).
  */
 int nq_varlen_prefill_gated(const void *q, int64_t q_row_stride, int64_t q_head_stride,
                             const void *k, const void *v, int64_t kv_row_stride,

@@ -375,10 +375,18 @@ void varlen_prefill_kernel(const PrefillArgs a) {
     if (row >= Lq) continue;
     const float inv = l > 0.f ? vscale / l : 0.f;
     uint8_t *op = a.out + static_cast<int64_t>(q0 + row) * a.o_rs + static_cast<int64_t>(head) * a.o_hs;
+    if (a.gate) {  // Qwen3.5's output gate (models/qwen3_5.py:140-142) in the store
+      const uint8_t *gp = a.gate + static_cast<int64_t>(q0 + row) * a.g_rs + static_cast<int64_t>(head) * a.g_hs;
 #pragma unroll
-    for (int j = 0; j < PT::NJ; ++j) {
-      const f32x4 v = o[qs][j] * inv;
-      *reinterpret_cast<u32x2 *>(op + (16 * j + 4 * g) * 2) = u32x2{T::pack2(v[0], v[1]), T::pack2(v[2], v[3])};
+      for (int j = 0; j < PT::NJ; ++j)
+        *reinterpret_cast<u32x2 *>(op + (16 * j + 4 * g) * 2) =
+            gate4<T>(o[qs][j] * inv, *reinterpret_cast<const u32x2 *>(gp + (16 * j + 4 * g) * 2));
+    } else {
+#pragma unroll
+      for (int j = 0; j < PT::NJ; ++j) {
+        const f32x4 v = o[qs][j] * inv;
+        *reinterpret_cast<u32x2 *>(op + (16 * j + 4 * g) * 2) = u32x2{T::pack2(v[0], v[1]), T::pack2(v[2], v[3])};
+      }
     }
   }
 }
@@ -1503,9 +1511,10 @@ static int varlen_prefill_impl(const void *q, int64_t q_row_stride, int64_t q_he
   a.out = static_cast<uint8_t *>(out);
   a.o_rs = out_row_stride * qsz;
   a.o_hs = out_head_stride * qsz;
-  // The gate rides in the output store of the default 16-bit launch shape;
-  // other launches get the same arithmetic from one in-place pass afterwards.
-  const bool fused_gate = gate && !fp8 && head_dim == 128 && prefill_shape() == 'c';
+  // The gate rides in the output store of the register-staged kernel (fp8
+  // K/V, head_dim 256) and of the default persistent shape; the other
+  // persistent shape gets the same arithmetic from one in-place pass.
+  const bool fused_gate = gate && (fp8 || head_dim == 256 || prefill_shape() == 'c');
   if (gate) {
     if ((gate_row_stride * qsz) % 16 || (gate_head_stride * qsz) % 16 || !aligned(gate, 16))
       return fail(NQ_EINVAL, "varlen_prefill_gated: gate alignment");
