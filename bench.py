@@ -19,7 +19,7 @@ prefill, and the stand-alone in-place gate pass for comparison), head_dim 256
 step (``gdn_decode``: HBM GB/s over the state pool) and prefill
 (``gdn_prefill``: recurrent form over cfg3's sequence lengths), and the gated
 RMS norm of its output (``gdn_norm``) and the causal conv1d before it
-(``gdn_conv``), HBM GB/s.
+(``gdn_conv``), HBM GB/s; and cfg3 with an fp8 KV cache (``cfg3_fp8``).
 ``roofline`` covers the dominant kernel of the headline workload (paged
 decode: main kernel + split-K merge), timed with HIP events on the stream
 the kernels run on.  ``cpu_baseline`` times the CPU restatement of the path
@@ -118,11 +118,12 @@ def bench_prefill(name, steps, warmup, seed=0, **override):
     def attn(i):
         kernels.varlen_prefill(case["q"], case["k_cache"], case["v_cache"], case["cu_seqlens_q"],
                                case["cu_seqlens_k"], case["max_seqlen_q"], case["max_seqlen_k"], case["scale"],
-                               causal=True, block_table=case["block_tables"], out=out)
+                               causal=True, block_table=case["block_tables"], k_scale=case["k_scale"],
+                               v_scale=case["v_scale"], out=out)
 
     def step(i):
         kernels.store_kvcache(case["k_new"], case["v_new"], case["k_cache"], case["v_cache"],
-                              case["slot_mapping"])
+                              case["slot_mapping"], case["k_scale"], case["v_scale"])
         attn(i)
 
     ms = _events_time(step, steps, warmup)
@@ -419,7 +420,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None,
                     help="run one config (cfg2|cfg3|cfg4|cfg5|cfg3_norm_rope|cfg2_norm_rope|cfg2_gate|cfg3_gate|"
-                         "cfg2_d256|cfg5_d256|cfg3_d256|gdn_decode|gdn_prefill|gdn_norm|gdn_conv)")
+                         "cfg2_d256|cfg5_d256|cfg3_d256|gdn_decode|gdn_prefill|gdn_norm|gdn_conv|cfg3_fp8)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration)")
     args = ap.parse_args()
@@ -442,7 +443,7 @@ def main():
     todo = [args.only] if args.only else ["cfg2", "cfg3", "cfg4", "cfg5", "cfg3_norm_rope", "cfg2_norm_rope",
                                                    "cfg2_gate", "cfg3_gate", "cfg2_d256", "cfg5_d256",
                                                    "cfg3_d256", "gdn_decode", "gdn_prefill", "gdn_norm",
-                                                   "gdn_conv"]
+                                                   "gdn_conv", "cfg3_fp8"]
     cpu = None
     for name in todo:
         print(f"[bench] {name} ...", file=sys.stderr, flush=True)
@@ -458,6 +459,8 @@ def main():
             r, case = bench_gated_norm(args.steps, args.warmup)
         elif name == "gdn_prefill":
             r, case = bench_gdn_prefill(args.steps, args.warmup)
+        elif name == "cfg3_fp8":
+            r, case = bench_prefill("cfg3", args.steps, args.warmup, kv="fp8")
         elif name == "cfg3_d256":
             r, case = bench_prefill("cfg3", args.steps, args.warmup, d=256, hq=16, hkv=4)
         elif name.endswith("_d256"):
