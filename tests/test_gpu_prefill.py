@@ -197,3 +197,26 @@ def test_prefill_head_dim_256_gated(cuda):
     ref = torch.from_numpy(gate_ref(plain.float().cpu().numpy(), gate.float().cpu().numpy(), "bf16"))
     diff = (gated.cpu().view(torch.int16).int() - ref.to(torch.bfloat16).view(torch.int16).int()).abs()
     assert int(diff.max()) <= 1 and float((diff > 0).float().mean()) <= 1e-3
+
+
+def test_kv_gather_dequant_bit_exact(cuda):
+    """The fp8 -> packed 16-bit gather that feeds fp8 prefill: row cu_k[s] + j
+    is rnd(code * scale[h]) of cache row bt[s][j / bs] * bs + j % bs (fp32
+    product, nearest even), bit for bit."""
+    from oracle import fp8 as F
+    from oracle.qk_norm_rope import round_to
+    case = make_prefill_case("cfg3", seed=31, device=cuda, nseq=3, lq=(1, 300), prefix_blocks=(1, 2), kv="fp8")
+    kb, vb = kernels.kv_gather_dequant(case["k_cache"], case["v_cache"], case["block_tables"], case["cu_seqlens_k"],
+                                       case["max_seqlen_k"], case["k_scale"], case["v_scale"], torch.bfloat16)
+    torch.cuda.synchronize()
+    kc = case["k_cache"].view(torch.uint8).cpu().numpy()
+    ks = case["k_scale"].cpu().numpy()
+    bt = case["block_tables"].cpu().numpy()
+    cu = case["cu_seqlens_k"].cpu().numpy()
+    bs = kc.shape[1]
+    for s in range(3):
+        for j in range(0, int(cu[s + 1] - cu[s]), 37):
+            row = kc[bt[s, j // bs], j % bs]                      # [Hkv, D] codes
+            ref = round_to((F.decode_e4m3fn(row).astype(np.float32) * ks[:, None]).astype(np.float32), "bf16")
+            got = kb[int(cu[s]) + j].float().cpu().numpy()
+            assert np.array_equal(got, ref), (s, j)
