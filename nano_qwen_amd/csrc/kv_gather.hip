@@ -20,10 +20,15 @@ template <class T>
 __global__ __launch_bounds__(kThreads) void gather_dequant_kernel(
     const uint8_t *kc, const uint8_t *vc, const int32_t *bt, int64_t bt_stride, int max_blocks,
     int64_t num_blocks, const int32_t *cu_k, int block_size, int row_b, int head_dim, const float *ks,
-    const float *vs, uint8_t *ok, uint8_t *ov) {
+    const float *vs, uint8_t *ok, uint8_t *ov, int max_seqlen_k) {
   const int s = blockIdx.y;
   const int chunks = row_b / 16;  // 16-byte chunks per fp8 row
-  const int64_t k0 = ld_const(cu_k + s), Lk = ld_const(cu_k + s + 1) - k0;
+  // Rows written stay below num_seqs * max_seqlen_k (the output's size) even
+  // if cu_seqlens_k disagrees with max_seqlen_k.
+  const int64_t cap = static_cast<int64_t>(gridDim.y) * max_seqlen_k;
+  const int64_t k0 = ld_const(cu_k + s);
+  int64_t Lk = ld_const(cu_k + s + 1) - k0;
+  Lk = k0 < 0 ? 0 : max<int64_t>(0, min<int64_t>(min<int64_t>(Lk, max_seqlen_k), cap - k0));
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < Lk * chunks; i += stride) {
     const int64_t j = i / chunks;
@@ -93,10 +98,10 @@ extern "C" int nq_kv_gather_dequant(const void *k_cache, const void *v_cache, co
   if (out_dtype == NQ_BF16)
     gather_dequant_kernel<BF16><<<grid, kThreads, 0, s>>>(kc, vc, block_tables, bt_stride, max_blocks_per_seq,
                                                           num_blocks, cu_seqlens_k, block_size, row_b, head_dim,
-                                                          k_scale, v_scale, ko, vo);
+                                                          k_scale, v_scale, ko, vo, max_seqlen_k);
   else
     gather_dequant_kernel<F16><<<grid, kThreads, 0, s>>>(kc, vc, block_tables, bt_stride, max_blocks_per_seq,
                                                          num_blocks, cu_seqlens_k, block_size, row_b, head_dim,
-                                                         k_scale, v_scale, ko, vo);
+                                                         k_scale, v_scale, ko, vo, max_seqlen_k);
   return check_launch("kv_gather_dequant");
 }
