@@ -6,9 +6,9 @@
 // packed row cu_k[s] + j as rnd(code * scale[h]) for every element of kv
 // head h (rnd = round to the 16-bit type, nearest even; missing blocks give
 // zeros).  That is exactly the "attention over the dequantized K/V" the fp8
-// path is specified against.  One lane per 16 fp8 bytes of a row (16
-// elements of one head, since head_dim % 16 == 0), 16-byte loads and two
-// 16-byte stores per lane.
+// path is specified against.  One wave per key row, one lane per 16 fp8 bytes
+// of it (16 elements of one head, since head_dim % 16 == 0): 16-byte loads
+// and two 16-byte stores per lane.
 #include "nq_device.hpp"
 
 namespace nq {
@@ -29,38 +29,42 @@ __global__ __launch_bounds__(kThreads) void gather_dequant_kernel(
   const int64_t k0 = ld_const(cu_k + s);
   int64_t Lk = ld_const(cu_k + s + 1) - k0;
   Lk = k0 < 0 ? 0 : max<int64_t>(0, min<int64_t>(min<int64_t>(Lk, max_seqlen_k), cap - k0));
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < Lk * chunks; i += stride) {
-    const int64_t j = i / chunks;
-    const int c = static_cast<int>(i - j * chunks);
-    const int bi = static_cast<int>(j / block_size);
-    const int blk = bi < max_blocks ? bt[static_cast<int64_t>(s) * bt_stride + bi] : -1;
+  // One wave per key row: the block-table entry is wave-uniform (a scalar
+  // load); lane l moves chunks l, l + 64, ... of the row.
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int64_t j = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave; j < Lk;
+       j += static_cast<int64_t>(gridDim.x) * (kThreads / 64)) {
+    const int bi = __builtin_amdgcn_readfirstlane(static_cast<int>(j / block_size));
+    const int blk = bi < max_blocks ? ld_const(bt + static_cast<int64_t>(s) * bt_stride + bi) : -1;
     const bool ok_blk = blk >= 0 && blk < num_blocks;
-    const int64_t src = (static_cast<int64_t>(blk) * block_size + j % block_size) * row_b + c * 16;
-    const int h = (c * 16) / head_dim;
-    const u32x4 kw = ok_blk ? load16(kc + src) : u32x4{0, 0, 0, 0};
-    const u32x4 vw = ok_blk ? load16(vc + src) : u32x4{0, 0, 0, 0};
-    const float ksc = ks[h], vsc = vs[h];
-    uint8_t *kd = ok + ((k0 + j) * row_b + c * 16) * 2;
-    uint8_t *vd = ov + ((k0 + j) * row_b + c * 16) * 2;
+    const int64_t row = static_cast<int64_t>(blk) * block_size + j % block_size;
+    for (int c = lane; c < chunks; c += 64) {
+      const int64_t src = row * row_b + c * 16;
+      const int h = (c * 16) / head_dim;
+      const u32x4 kw = ok_blk ? load16_stream(kc + src) : u32x4{0, 0, 0, 0};
+      const u32x4 vw = ok_blk ? load16_stream(vc + src) : u32x4{0, 0, 0, 0};
+      const float ksc = ks[h], vsc = vs[h];
+      uint8_t *kd = ok + ((k0 + j) * row_b + c * 16) * 2;
+      uint8_t *vd = ov + ((k0 + j) * row_b + c * 16) * 2;
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      u32x4 ko, vo;
+      for (int half = 0; half < 2; ++half) {
+        u32x4 ko, vo;
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const uint32_t kx = kw[2 * half + q], vx = vw[2 * half + q];
-        const uint32_t kp[2] = {T::template fp8x2<false>(kx), T::template fp8x2<true>(kx)};
-        const uint32_t vp[2] = {T::template fp8x2<false>(vx), T::template fp8x2<true>(vx)};
+        for (int q = 0; q < 2; ++q) {
+          const uint32_t kx = kw[2 * half + q], vx = vw[2 * half + q];
+          const uint32_t kp[2] = {T::template fp8x2<false>(kx), T::template fp8x2<true>(kx)};
+          const uint32_t vp[2] = {T::template fp8x2<false>(vx), T::template fp8x2<true>(vx)};
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          ko[2 * q + e] = T::pack2(T::to_float(static_cast<uint16_t>(kp[e] & 0xffffu)) * ksc,
-                                   T::to_float(static_cast<uint16_t>(kp[e] >> 16)) * ksc);
-          vo[2 * q + e] = T::pack2(T::to_float(static_cast<uint16_t>(vp[e] & 0xffffu)) * vsc,
-                                   T::to_float(static_cast<uint16_t>(vp[e] >> 16)) * vsc);
+          for (int e = 0; e < 2; ++e) {
+            ko[2 * q + e] = T::pack2(T::to_float(static_cast<uint16_t>(kp[e] & 0xffffu)) * ksc,
+                                     T::to_float(static_cast<uint16_t>(kp[e] >> 16)) * ksc);
+            vo[2 * q + e] = T::pack2(T::to_float(static_cast<uint16_t>(vp[e] & 0xffffu)) * vsc,
+                                     T::to_float(static_cast<uint16_t>(vp[e] >> 16)) * vsc);
+          }
         }
+        __builtin_nontemporal_store(ko, reinterpret_cast<u32x4 *>(kd) + half);
+        __builtin_nontemporal_store(vo, reinterpret_cast<u32x4 *>(vd) + half);
       }
-      __builtin_nontemporal_store(ko, reinterpret_cast<u32x4 *>(kd) + half);
-      __builtin_nontemporal_store(vo, reinterpret_cast<u32x4 *>(vd) + half);
     }
   }
 }
@@ -87,9 +91,8 @@ extern "C" int nq_kv_gather_dequant(const void *k_cache, const void *v_cache, co
     return fail(NQ_EINVAL, "kv_gather_dequant: 16-byte alignment");
   if (num_seqs > 65535) return fail(NQ_EINVAL, "kv_gather_dequant: too many sequences");
   const int row_b = num_kv_heads * head_dim;
-  const int64_t per_seq = static_cast<int64_t>(max_seqlen_k) * (row_b / 16);
-  const int64_t bx = (per_seq + kThreads - 1) / kThreads;
-  dim3 grid(static_cast<unsigned>(bx < 1024 ? bx : 1024), num_seqs);
+  const int64_t bx = (static_cast<int64_t>(max_seqlen_k) + kThreads / 64 - 1) / (kThreads / 64);  // rows / 4
+  dim3 grid(static_cast<unsigned>(bx < 4096 ? bx : 4096), num_seqs);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const auto *kc = static_cast<const uint8_t *>(k_cache);
   const auto *vc = static_cast<const uint8_t *>(v_cache);
