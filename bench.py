@@ -426,7 +426,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures the paged attention path on ONE GPU; "
-              "multi-GPU runs are not part of it (see DESIGN.md for how the path shards)", file=sys.stderr)
+              "multi-GPU runs are not part of it (the kernels shard by kv head or by sequence with no communication)", file=sys.stderr)
         sys.exit(2)
 
     import torch
