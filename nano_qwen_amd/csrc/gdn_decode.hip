@@ -16,11 +16,11 @@
 //   o      = S (q * K^-1/2)
 // Here one launch covers the whole batch and updates the pool in place.
 //
-// One one-wave workgroup per (sequence, value head, 16-row slice of the
-// state), K = V = 128: no workgroup barrier, many small workgroups, and few
-// enough registers for five waves per SIMD.  The wave owning rows
-// 16w .. 16w + 15 reads with load i of lane l the 16 bytes at row
-// 16w + 2i + l/32, columns 4(l%32) .. +3: every load instruction covers
+// One one-wave workgroup per (sequence, value head, slice of 2 NL state
+// rows; NL = 4 in decode, 8 in prefill), K = V = 128: no workgroup barrier,
+// many small workgroups, few registers.  The wave owning rows
+// 2NL w .. 2NL w + 2NL - 1 reads with load i of lane l the 16 bytes at row
+// 2NL w + 2i + l/32, columns 4(l%32) .. +3: every load instruction covers
 // 1 KiB of contiguous state, so the 64 KiB state is read and written once,
 // fully coalesced.  Each wave normalizes q and k itself from its lanes' 4
 // columns (a 32-lane reduction).  A row's dot products (S k, S q) are spread
@@ -85,10 +85,15 @@ __device__ inline float reduce_rows(float (&p)[N], int lane) {
   return r;
 }
 
-// Rows of the state per wave: 2 * kLoads (16 -> five waves per SIMD fit).
-constexpr int kLoads = 8;
-constexpr int kRowsW = 2 * kLoads;
-constexpr int kSh = kLoads == 16 ? 1 : 2;  // lane bits below the row index after reduce_rows
+// A wave owns 2 * NL state rows (NL loads per lane).  Decode uses NL = 4:
+// more, smaller waves hide the HBM latency better.  Prefill uses NL = 8: its
+// waves are latency-bound chains whose fixed per-token work (norms, gates,
+// reductions) does not shrink with fewer rows.
+constexpr int kDecodeLoads = 4;
+constexpr int kPrefillLoads = 8;
+// Lane bits below the row index after reduce_rows<NL>.
+template <int NL>
+constexpr int kShOf = NL == 16 ? 1 : (NL == 8 ? 2 : 3);
 
 // One token's inputs for one lane: its 4 columns of q and k, its row's v, and
 // the two gate inputs (16-bit values).
@@ -116,8 +121,8 @@ __device__ inline f32x4 unpack4(const u32x2 &w) {
 
 // One token of the gated delta rule on the wave's kRowsW state rows (held in
 // s), writing the token's output for those rows.  neg_a = -exp(A_log[hv]).
-template <class T>
-__device__ inline void gdn_token(f32x4 (&s)[kLoads], const TokIn &in, float neg_a, float dt_bias, float eps,
+template <class T, int NL>
+__device__ inline void gdn_token(f32x4 (&s)[NL], const TokIn &in, float neg_a, float dt_bias, float eps,
                                  float scale, int lane, float *urow, int my_row, bool writer, uint16_t *orow) {
   // q and k: this lane's 4 columns, l2-normalized over the 32 lanes that
   // cover all 128 columns; q also carries the scale.
@@ -134,9 +139,9 @@ __device__ inline void gdn_token(f32x4 (&s)[kLoads], const TokIn &in, float neg_
   const float decay = expf(neg_a * softplus(T::to_float(static_cast<uint16_t>(in.ga)) + dt_bias));
   const float beta = 1.0f / (1.0f + expf(-T::to_float(static_cast<uint16_t>(in.gb))));
   // u = beta * (v - (exp(g) S) k) for every row of the wave.
-  float p[kLoads];
+  float p[NL];
 #pragma unroll
-  for (int i = 0; i < kLoads; ++i) {
+  for (int i = 0; i < NL; ++i) {
     s[i] *= decay;
     p[i] = s[i][0] * kc[0] + s[i][1] * kc[1] + s[i][2] * kc[2] + s[i][3] * kc[3];
   }
@@ -144,7 +149,7 @@ __device__ inline void gdn_token(f32x4 (&s)[kLoads], const TokIn &in, float neg_
   if (writer) urow[my_row] = u;  // one wave: LDS accesses stay in order
   // S += u k^T, then o = S q.
 #pragma unroll
-  for (int i = 0; i < kLoads; ++i) {
+  for (int i = 0; i < NL; ++i) {
     const float ui = urow[2 * i + (lane >> 5)];
     s[i] += ui * kc;
     p[i] = s[i][0] * qc[0] + s[i][1] * qc[1] + s[i][2] * qc[2] + s[i][3] * qc[3];
@@ -156,6 +161,7 @@ __device__ inline void gdn_token(f32x4 (&s)[kLoads], const TokIn &in, float neg_
 // Decode: one token per sequence b (row b of q, k, v, a, b and out).
 template <class T>
 __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(const GdnArgs a) {
+  constexpr int NL = kDecodeLoads, kRowsW = 2 * NL, kSh = kShOf<NL>;
   const int hv = blockIdx.x, bi = blockIdx.y, w = blockIdx.z;
   const int lane = threadIdx.x;
   const int32_t slot = a.idx[bi];
@@ -163,21 +169,21 @@ __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(const GdnArgs a) {
   const int h = hv / (a.HV / a.H);
   const int r0 = kRowsW * w + (lane >> 5);  // row of load 0; load i adds 2i
   const int c0 = 4 * (lane & 31);           // this lane's 4 columns
-  const int my_row = 2 * ((lane >> kSh) & (kLoads - 1)) + (lane >> 5);  // row whose sums this lane ends with
+  const int my_row = 2 * ((lane >> kSh) & (NL - 1)) + (lane >> 5);  // row whose sums this lane ends with
   const bool writer = (lane & ((1 << kSh) - 1)) == 0;
 
   // The state loads first (coalesced), then the token's inputs.
   float *sp = a.state + ((static_cast<int64_t>(slot) * a.HV + hv) * kDim + r0) * kDim + c0;
-  f32x4 s[kLoads];
+  f32x4 s[NL];
 #pragma unroll
-  for (int i = 0; i < kLoads; ++i)
+  for (int i = 0; i < NL; ++i)
     s[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(sp + 2 * i * kDim));
   const TokIn in = load_tok<T>(a, bi, h, hv, kRowsW * w + my_row, c0);
   __shared__ float urow[kRowsW];
   uint16_t *orow = reinterpret_cast<uint16_t *>(a.out + bi * a.o_rs + hv * kDim * 2) + kRowsW * w;
-  gdn_token<T>(s, in, -expf(a.A_log[hv]), a.dt_bias[hv], a.eps, a.scale, lane, urow, my_row, writer, orow);
+  gdn_token<T, NL>(s, in, -expf(a.A_log[hv]), a.dt_bias[hv], a.eps, a.scale, lane, urow, my_row, writer, orow);
 #pragma unroll
-  for (int i = 0; i < kLoads; ++i) __builtin_nontemporal_store(s[i], reinterpret_cast<f32x4 *>(sp + 2 * i * kDim));
+  for (int i = 0; i < NL; ++i) __builtin_nontemporal_store(s[i], reinterpret_cast<f32x4 *>(sp + 2 * i * kDim));
 }
 
 // Prefill: sequence n owns token rows [cu[n], cu[n+1]); the state starts from
@@ -187,6 +193,7 @@ constexpr int kAheadTok = 4;
 
 template <class T>
 __global__ __launch_bounds__(kThreads) void gdn_prefill_kernel(const GdnArgs a, const int32_t *cu, int from_slot) {
+  constexpr int NL = kPrefillLoads, kRowsW = 2 * NL, kSh = kShOf<NL>;
   const int hv = blockIdx.x, n = blockIdx.y, w = blockIdx.z;
   const int lane = threadIdx.x;
   const int32_t slot = a.idx[n];
@@ -194,14 +201,14 @@ __global__ __launch_bounds__(kThreads) void gdn_prefill_kernel(const GdnArgs a, 
   const int h = hv / (a.HV / a.H);
   const int r0 = kRowsW * w + (lane >> 5);
   const int c0 = 4 * (lane & 31);
-  const int my_row = 2 * ((lane >> kSh) & (kLoads - 1)) + (lane >> 5);
+  const int my_row = 2 * ((lane >> kSh) & (NL - 1)) + (lane >> 5);
   const bool writer = (lane & ((1 << kSh) - 1)) == 0;
   const int64_t t0 = cu[n], t1 = cu[n + 1];
 
   float *sp = a.state + ((static_cast<int64_t>(has_slot ? slot : 0) * a.HV + hv) * kDim + r0) * kDim + c0;
-  f32x4 s[kLoads];
+  f32x4 s[NL];
 #pragma unroll
-  for (int i = 0; i < kLoads; ++i)
+  for (int i = 0; i < NL; ++i)
     s[i] = (from_slot && has_slot) ? __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(sp + 2 * i * kDim))
                                    : f32x4{0, 0, 0, 0};
   const float neg_a = -expf(a.A_log[hv]), dtb = a.dt_bias[hv];
@@ -221,18 +228,18 @@ __global__ __launch_bounds__(kThreads) void gdn_prefill_kernel(const GdnArgs a, 
       const TokIn in = ring[j];
       ring[j] = load_tok<T>(a, min(t + j + kAheadTok, last), h, hv, vrow, c0);
       uint16_t *orow = reinterpret_cast<uint16_t *>(a.out + (t + j) * a.o_rs + hv * kDim * 2) + kRowsW * w;
-      gdn_token<T>(s, in, neg_a, dtb, a.eps, a.scale, lane, urow, my_row, writer, orow);
+      gdn_token<T, NL>(s, in, neg_a, dtb, a.eps, a.scale, lane, urow, my_row, writer, orow);
     }
   }
 #pragma unroll
   for (int j = 0; j < kAheadTok - 1; ++j) {  // the tail: fewer than kAheadTok tokens
     if (t + j >= t1) break;
     uint16_t *orow = reinterpret_cast<uint16_t *>(a.out + (t + j) * a.o_rs + hv * kDim * 2) + kRowsW * w;
-    gdn_token<T>(s, ring[j], neg_a, dtb, a.eps, a.scale, lane, urow, my_row, writer, orow);
+    gdn_token<T, NL>(s, ring[j], neg_a, dtb, a.eps, a.scale, lane, urow, my_row, writer, orow);
   }
   if (has_slot) {
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) __builtin_nontemporal_store(s[i], reinterpret_cast<f32x4 *>(sp + 2 * i * kDim));
+    for (int i = 0; i < NL; ++i) __builtin_nontemporal_store(s[i], reinterpret_cast<f32x4 *>(sp + 2 * i * kDim));
   }
 }
 
@@ -283,7 +290,7 @@ extern "C" int nq_gdn_decode(const void *q, int64_t q_row_stride, const void *k,
   g.HV = num_v_heads;
   g.eps = 1e-6f;
   g.scale = 1.0f / sqrtf(static_cast<float>(head_k_dim));
-  dim3 grid(num_v_heads, batch, kDim / kRowsW);
+  dim3 grid(num_v_heads, batch, kDim / (2 * kDecodeLoads));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == NQ_BF16) gdn_decode_kernel<BF16><<<grid, kThreads, 0, s>>>(g);
   else gdn_decode_kernel<F16><<<grid, kThreads, 0, s>>>(g);
@@ -332,7 +339,7 @@ extern "C" int nq_gdn_prefill(const void *q, int64_t q_row_stride, const void *k
   g.HV = num_v_heads;
   g.eps = 1e-6f;
   g.scale = 1.0f / sqrtf(static_cast<float>(head_k_dim));
-  dim3 grid(num_v_heads, num_seqs, kDim / kRowsW);
+  dim3 grid(num_v_heads, num_seqs, kDim / (2 * kPrefillLoads));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == NQ_BF16) gdn_prefill_kernel<BF16><<<grid, kThreads, 0, s>>>(g, cu_seqlens, initial_state_from_slot);
   else gdn_prefill_kernel<F16><<<grid, kThreads, 0, s>>>(g, cu_seqlens, initial_state_from_slot);
