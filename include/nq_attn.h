@@ -225,14 +225,15 @@ int nq_varlen_prefill_gated(const void *q, int64_t q_row_stride, int64_t q_head_
  * round to nearest even); missing blocks give zeros.  This is the K/V the fp8
  * attention contract is stated against, so nq_varlen_prefill on the packed
  * result (block_tables == NULL) computes fp8 prefill on the 16-bit kernel.
- * max_seqlen_k bounds every Lk_s (rows past num_seqs * max_seqlen_k, and keys
- * past max_seqlen_k, are never written); head_dim % 16 == 0; 16-byte aligned.
+ * k_out/v_out hold out_rows rows (normally cu_seqlens_k[num_seqs]): rows at or
+ * past out_rows, and keys past max_seqlen_k, are never written, whatever
+ * cu_seqlens_k holds; head_dim % 16 == 0; 16-byte aligned.
  */
 int nq_kv_gather_dequant(const void *k_cache, const void *v_cache, const int32_t *block_tables,
                          int64_t bt_stride, int max_blocks_per_seq, int64_t num_blocks,
                          const int32_t *cu_seqlens_k, int num_seqs, int max_seqlen_k, int block_size,
                          int num_kv_heads, int head_dim, const float *k_scale, const float *v_scale,
-                         void *k_out, void *v_out, int out_dtype, void *stream);
+                         void *k_out, void *v_out, int64_t out_rows, int out_dtype, void *stream);
 
 /* Bytes of device workspace nq_varlen_prefill needs (work-queue counters). */
 int64_t nq_prefill_workspace_bytes(void);

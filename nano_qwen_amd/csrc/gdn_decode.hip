@@ -217,25 +217,29 @@ __global__ __launch_bounds__(kThreads) void gdn_prefill_kernel(const GdnArgs a, 
   // Prefetch ring: token indices past the end are clamped to the last token
   // (loaded, never used), so the steady-state loop has no branches and the
   // compiler's waits count exactly the loads each token needs.
-  const int64_t last = t1 > t0 ? t1 - 1 : t0;
-  TokIn ring[kAheadTok];
+  // An empty sequence loads no token (its t0 may be one past the last row):
+  // its final state is the initial one.
+  if (t1 > t0) {
+    const int64_t last = t1 - 1;
+    TokIn ring[kAheadTok];
 #pragma unroll
-  for (int j = 0; j < kAheadTok; ++j) ring[j] = load_tok<T>(a, min(t0 + j, last), h, hv, vrow, c0);
-  int64_t t = t0;
-  for (; t + kAheadTok <= t1; t += kAheadTok) {
+    for (int j = 0; j < kAheadTok; ++j) ring[j] = load_tok<T>(a, min(t0 + j, last), h, hv, vrow, c0);
+    int64_t t = t0;
+    for (; t + kAheadTok <= t1; t += kAheadTok) {
 #pragma unroll
-    for (int j = 0; j < kAheadTok; ++j) {
-      const TokIn in = ring[j];
-      ring[j] = load_tok<T>(a, min(t + j + kAheadTok, last), h, hv, vrow, c0);
-      uint16_t *orow = reinterpret_cast<uint16_t *>(a.out + (t + j) * a.o_rs + hv * kDim * 2) + kRowsW * w;
-      gdn_token<T, NL>(s, in, neg_a, dtb, a.eps, a.scale, lane, urow, my_row, writer, orow);
+      for (int j = 0; j < kAheadTok; ++j) {
+        const TokIn in = ring[j];
+        ring[j] = load_tok<T>(a, min(t + j + kAheadTok, last), h, hv, vrow, c0);
+        uint16_t *orow = reinterpret_cast<uint16_t *>(a.out + (t + j) * a.o_rs + hv * kDim * 2) + kRowsW * w;
+        gdn_token<T, NL>(s, in, neg_a, dtb, a.eps, a.scale, lane, urow, my_row, writer, orow);
+      }
     }
-  }
 #pragma unroll
-  for (int j = 0; j < kAheadTok - 1; ++j) {  // the tail: fewer than kAheadTok tokens
-    if (t + j >= t1) break;
-    uint16_t *orow = reinterpret_cast<uint16_t *>(a.out + (t + j) * a.o_rs + hv * kDim * 2) + kRowsW * w;
-    gdn_token<T, NL>(s, ring[j], neg_a, dtb, a.eps, a.scale, lane, urow, my_row, writer, orow);
+    for (int j = 0; j < kAheadTok - 1; ++j) {  // the tail: fewer than kAheadTok tokens
+      if (t + j >= t1) break;
+      uint16_t *orow = reinterpret_cast<uint16_t *>(a.out + (t + j) * a.o_rs + hv * kDim * 2) + kRowsW * w;
+      gdn_token<T, NL>(s, ring[j], neg_a, dtb, a.eps, a.scale, lane, urow, my_row, writer, orow);
+    }
   }
   if (has_slot) {
 #pragma unroll

@@ -20,12 +20,11 @@ template <class T>
 __global__ __launch_bounds__(kThreads) void gather_dequant_kernel(
     const uint8_t *kc, const uint8_t *vc, const int32_t *bt, int64_t bt_stride, int max_blocks,
     int64_t num_blocks, const int32_t *cu_k, int block_size, int row_b, int head_dim, const float *ks,
-    const float *vs, uint8_t *ok, uint8_t *ov, int max_seqlen_k) {
+    const float *vs, uint8_t *ok, uint8_t *ov, int max_seqlen_k, int64_t cap) {
   const int s = blockIdx.y;
   const int chunks = row_b / 16;  // 16-byte chunks per fp8 row
-  // Rows written stay below num_seqs * max_seqlen_k (the output's size) even
-  // if cu_seqlens_k disagrees with max_seqlen_k.
-  const int64_t cap = static_cast<int64_t>(gridDim.y) * max_seqlen_k;
+  // Rows written stay below `cap` (the output's rows) even if cu_seqlens_k
+  // disagrees with it or with max_seqlen_k.
   const int64_t k0 = ld_const(cu_k + s);
   int64_t Lk = ld_const(cu_k + s + 1) - k0;
   Lk = k0 < 0 ? 0 : max<int64_t>(0, min<int64_t>(min<int64_t>(Lk, max_seqlen_k), cap - k0));
@@ -78,13 +77,13 @@ extern "C" int nq_kv_gather_dequant(const void *k_cache, const void *v_cache, co
                                     int64_t bt_stride, int max_blocks_per_seq, int64_t num_blocks,
                                     const int32_t *cu_seqlens_k, int num_seqs, int max_seqlen_k, int block_size,
                                     int num_kv_heads, int head_dim, const float *k_scale, const float *v_scale,
-                                    void *k_out, void *v_out, int out_dtype, void *stream) {
-  if (num_seqs < 0 || max_seqlen_k < 0 || block_size <= 0 || num_kv_heads <= 0 || head_dim <= 0)
+                                    void *k_out, void *v_out, int64_t out_rows, int out_dtype, void *stream) {
+  if (num_seqs < 0 || max_seqlen_k < 0 || out_rows < 0 || block_size <= 0 || num_kv_heads <= 0 || head_dim <= 0)
     return fail(NQ_EINVAL, "kv_gather_dequant: bad sizes");
   if (head_dim % 16) return fail(NQ_EUNSUPPORTED, "kv_gather_dequant: head_dim %% 16 != 0");
   if (out_dtype != NQ_BF16 && out_dtype != NQ_F16)
     return fail(NQ_EUNSUPPORTED, "kv_gather_dequant: out dtype %d (f16/bf16)", out_dtype);
-  if (num_seqs == 0 || max_seqlen_k == 0) return NQ_OK;
+  if (num_seqs == 0 || max_seqlen_k == 0 || out_rows == 0) return NQ_OK;
   if (!k_cache || !v_cache || !block_tables || !cu_seqlens_k || !k_scale || !v_scale || !k_out || !v_out)
     return fail(NQ_EINVAL, "kv_gather_dequant: null pointer");
   if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(k_out, 16) || !aligned(v_out, 16))
@@ -101,10 +100,10 @@ extern "C" int nq_kv_gather_dequant(const void *k_cache, const void *v_cache, co
   if (out_dtype == NQ_BF16)
     gather_dequant_kernel<BF16><<<grid, kThreads, 0, s>>>(kc, vc, block_tables, bt_stride, max_blocks_per_seq,
                                                           num_blocks, cu_seqlens_k, block_size, row_b, head_dim,
-                                                          k_scale, v_scale, ko, vo, max_seqlen_k);
+                                                          k_scale, v_scale, ko, vo, max_seqlen_k, out_rows);
   else
     gather_dequant_kernel<F16><<<grid, kThreads, 0, s>>>(kc, vc, block_tables, bt_stride, max_blocks_per_seq,
                                                          num_blocks, cu_seqlens_k, block_size, row_b, head_dim,
-                                                         k_scale, v_scale, ko, vo, max_seqlen_k);
+                                                         k_scale, v_scale, ko, vo, max_seqlen_k, out_rows);
   return check_launch("kv_gather_dequant");
 }

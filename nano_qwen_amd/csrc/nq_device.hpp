@@ -114,11 +114,6 @@ __device__ inline u32x2 gate4(const f32x4 &v, const u32x2 &g) {
 }
 
 // ---------------------------------------------------------------- memory
-template <typename T>
-__device__ inline T ldg(const T *p) {
-  return __builtin_nontemporal_load(p);
-}
-
 // Load of data that no kernel writes while it runs (sequence metadata, block
 // tables), through the constant address space: with a wave-uniform address
 // it becomes a scalar load, which does not wait on the vector-memory counter.
@@ -170,13 +165,6 @@ __device__ inline u32x4 buffer_load16_nt(__amdgpu_buffer_rsrc_t r, int voffset) 
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 2));
 }
 
-// Direct global -> LDS copy (gfx950 LDS DMA, 16 bytes per lane): lane l's 16
-// bytes land at lds + 16 * l.  Completion is tracked by the vector-memory
-// counter only -- the compiler inserts no wait for it -- so callers pair it
-// with wait_vmcnt() and a workgroup barrier before reading the LDS.
-__device__ inline void dma16(const void *src, void *lds) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(lds), 16, 0, 0);
-}
 // The four words of the raw buffer descriptor make_rsrc builds (base, stride
 // 0, num_bytes, raw dword format), for inline assembly.
 __device__ inline u32x4 rsrc_words(const void *base, uint32_t num_bytes) {
@@ -242,11 +230,6 @@ __device__ inline void wave_lds_sync() {
   asm volatile("" ::: "memory");
 }
 
-__device__ inline float xor_max(float v, int mask) {
-  return fmaxf(v, __shfl_xor(v, mask, 64));
-}
-__device__ inline float xor_sum(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
-
 // Butterflies across lane l and l^16 / l^32 with gfx950 permlane swaps (one
 // VALU op each, no LDS round trip).  With both operands = v, the swap returns
 // {v, partner} in some order on every lane.
@@ -305,39 +288,6 @@ __device__ inline u32x2 lds_read_tr16(const uint16_t *p) {
       (__attribute__((address_space(3))) s16x4 *)(p));
   return __builtin_bit_cast(u32x2, v);
 }
-// The same read issued as an opaque instruction: the compiler neither waits
-// for it nor for in-flight LDS DMA before it (the builtin carries no alias
-// information, so the backend would drain every outstanding DMA copy first).
-// The caller must wait for it with an s_waitcnt lgkmcnt(0) that names the
-// result registers as operands (so no consumer is scheduled above the wait).
-__device__ inline u32x2 lds_read_tr16_async(const void *p) {
-  u32x2 v;
-  const uint32_t a = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-      (__attribute__((address_space(3))) const void *)(p)));
-  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(a));
-  return v;
-}
-
-// ds_read_b64_tr_b16 at LDS byte address `addr` + OFF (immediate), issued as
-// an opaque instruction with the same contract as lds_read_tr16_async.
-template <int OFF>
-__device__ inline u32x2 lds_read_tr16_at(uint32_t addr) {
-  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
-  u32x2 v;
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
-  return v;
-}
-
-// ds_read_b128 at LDS byte address `addr` + OFF, opaque like lds_read_tr16_at
-// (issued where it stands; the caller waits with a tied s_waitcnt).
-template <int OFF>
-__device__ inline u32x4 lds_read_b128_at(uint32_t addr) {
-  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
-  u32x4 v;
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
-  return v;
-}
-
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 

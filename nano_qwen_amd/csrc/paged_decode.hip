@@ -436,6 +436,9 @@ int launch_decode(const DecodeArgs &a, int batch, hipStream_t s) {
 
 using namespace nq;
 
+// Largest split the decode kernel accepts: a split's block-table entries are
+// held one per lane (64 per wave, one spare for the block after the split).
+static int max_split_tokens(int block_size) { return static_cast<int>((63LL * block_size) / 128 * 128); }
 
 // Split size: one split per workgroup should carry enough tokens that the
 // workgroup's fixed costs (Q load, first-step latency, partial write) stay
@@ -461,7 +464,7 @@ extern "C" int nq_decode_plan(int batch, int num_q_heads, int num_kv_heads, int 
   split = (split + 127) / 128 * 128;
   if (split < 128) split = 128;
   // a split's block-table entries are held one per lane: at most 63 blocks
-  const int64_t max_split = (63LL * block_size) / 128 * 128;
+  const int64_t max_split = max_split_tokens(block_size);
   if (split > max_split) split = max_split;
   if (max_tokens <= split) {
     *num_splits = 1;
@@ -514,6 +517,11 @@ static int paged_decode_impl(const void *q, int64_t q_batch_stride, int64_t q_he
     return fail(NQ_EINVAL, "paged_decode: block table width");
   if (num_splits <= 0 || split_tokens <= 0 || split_tokens % 128 != 0)
     return fail(NQ_EINVAL, "paged_decode: bad split plan (%d x %d)", num_splits, split_tokens);
+  // A split's block-table entries are held one per lane of a wave: a split
+  // may span at most 63 blocks (the cap nq_decode_plan applies).
+  if (split_tokens > max_split_tokens(block_size))
+    return fail(NQ_EINVAL, "paged_decode: split_tokens %d > %d (63 blocks of %d)", split_tokens,
+                max_split_tokens(block_size), block_size);
   if (static_cast<int64_t>(num_splits) * split_tokens < static_cast<int64_t>(max_blocks_per_seq) * block_size)
     return fail(NQ_EINVAL, "paged_decode: split plan covers %lld < %lld tokens",
                 (long long)num_splits * split_tokens, (long long)max_blocks_per_seq * block_size);

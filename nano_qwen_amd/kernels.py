@@ -14,14 +14,46 @@ and meanings follow the calls the reference makes:
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
 from . import _lib
 from ._lib import check, dtype_code, lib, ptr, require_cuda, stream_of
 
-_workspaces: dict[int, torch.Tensor] = {}
-_prefill_queues: dict[int, torch.Tensor] = {}
+# Persistent device buffers of the kernels, one per (device, stream): calls
+# on one stream are ordered, so they may share a buffer; calls on different
+# streams get their own.  A buffer that has to grow is replaced, but the old
+# one is kept alive (``_retired``): a HIP graph captured earlier may still
+# hold its address, and replays must keep writing into valid memory.
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+_prefill_queues: dict[tuple[int, int], torch.Tensor] = {}
+_gather_ws: dict[tuple[int, int], torch.Tensor] = {}
+_retired: list[torch.Tensor] = []
+_DEBUG_QUEUE = os.environ.get("NQ_DEBUG_PREFILL_QUEUE", "0") not in ("", "0")
+
+
+def _key(device) -> tuple[int, int]:
+    dev = torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    return idx, torch.cuda.current_stream(idx).cuda_stream
+
+
+def _grow(table, key, nbytes, dtype, device, zero=False):
+    """The buffer of ``key`` in ``table`` with at least ``nbytes`` bytes;
+    grows geometrically, retiring (never freeing) the buffer it replaces."""
+    cur = table.get(key)
+    if cur is not None and cur.numel() * cur.element_size() >= nbytes:
+        return cur
+    have = 0 if cur is None else cur.numel() * cur.element_size()
+    size = max(nbytes, 2 * have, 1 << 20)
+    item = torch.empty((), dtype=dtype).element_size()
+    n = (size + item - 1) // item
+    buf = torch.zeros(n, dtype=dtype, device=device) if zero else torch.empty(n, dtype=dtype, device=device)
+    if cur is not None:
+        _retired.append(cur)
+    table[key] = buf
+    return buf
 
 
 def store_kvcache(key, value, k_cache, v_cache, slot_mapping, k_scale=None, v_scale=None):
@@ -58,36 +90,54 @@ def decode_plan(batch, num_q_heads, num_kv_heads, max_blocks_per_seq, block_size
 
 
 def decode_workspace(device, nbytes: int) -> torch.Tensor | None:
-    """Persistent, grow-only split-K workspace for ``device``.
+    """Persistent split-K workspace of at least ``nbytes`` for the current
+    stream of ``device``.
 
-    Kept across calls so a captured HIP graph keeps a fixed pointer; growing
-    it inside a capture allocates from the capture's pool, which torch keeps
-    alive with the graph.  Calls that share it must not overlap (one stream).
+    Kept across calls so a captured HIP graph keeps a fixed pointer.  Growing
+    it never frees the old buffer (a graph may hold it); growing it inside a
+    capture allocates from the capture's pool, which torch keeps alive with
+    the graph.  ``reserve_decode_workspace`` sizes it once up front.
     """
     if nbytes <= 0:
         return None
-    idx = torch.device(device).index or 0
-    ws = _workspaces.get(idx)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _workspaces[idx] = ws
-    return ws
+    return _grow(_workspaces, _key(device), nbytes, torch.uint8, device)
+
+
+def reserve_decode_workspace(device, max_batch, num_q_heads, num_kv_heads, max_blocks_per_seq, block_size,
+                             head_dim, kv_dtype) -> int:
+    """Size the current stream's split-K workspace for the largest decode
+    the caller will run (batch ``max_batch``, tables ``max_blocks_per_seq``
+    wide); returns its bytes.  Every batch up to ``max_batch`` then fits
+    without growing.  The plan's split count falls as the batch grows, so
+    every batch size is checked."""
+    need = 0
+    for b in range(1, int(max_batch) + 1):
+        ns, _ = decode_plan(b, num_q_heads, num_kv_heads, max_blocks_per_seq, block_size, kv_dtype)
+        need = max(need, lib().nq_decode_workspace_bytes(b, num_q_heads, head_dim, ns))
+    if need > 0:
+        decode_workspace(device, need)
+    return need
 
 
 def prefill_workspace(device) -> torch.Tensor:
-    """Persistent work-queue counters of the prefill kernel for ``device``.
+    """Work-queue counters of the prefill kernel for the current stream of
+    ``device``.
 
     Zeroed once here; every completed prefill call leaves them zero again, so
-    the same tensor serves every later call (and graph replays).  Calls that
-    share it must not overlap (one stream).
+    the same tensor serves every later call on that stream (and graph
+    replays).  Each stream has its own, so launches on different streams
+    never share counters.  With ``NQ_DEBUG_PREFILL_QUEUE=1`` every prefill
+    synchronizes and checks that it left them zero.
     """
-    idx = torch.device(device).index or 0
-    ws = _prefill_queues.get(idx)
-    if ws is None:
-        nbytes = lib().nq_prefill_workspace_bytes()
-        ws = torch.zeros((nbytes + 3) // 4, dtype=torch.int32, device=device)
-        _prefill_queues[idx] = ws
-    return ws
+    return _grow(_prefill_queues, _key(device), lib().nq_prefill_workspace_bytes(), torch.int32, device,
+                 zero=True)
+
+
+def _check_queue_zero(ws):
+    torch.cuda.current_stream(ws.device).synchronize()
+    if int(ws.count_nonzero()) != 0:
+        raise RuntimeError("varlen_prefill: the work-queue counters are not zero after the launch "
+                           f"({ws[:16].tolist()}); a launch on this stream did not complete")
 
 
 def _gate3(gate, n, hq, d, what):
@@ -159,35 +209,32 @@ def output_gate(out, gate):
     return out
 
 
-_gather_ws: dict[int, torch.Tensor] = {}
-
-
-def kv_gather_dequant(k_cache, v_cache, block_table, cu_seqlens_k, max_seqlen_k, k_scale, v_scale, dtype):
-    """Paged fp8 K/V -> packed 16-bit K/V ``[N * max_seqlen_k, Hkv, D]`` (rows
+def kv_gather_dequant(k_cache, v_cache, block_table, cu_seqlens_k, max_seqlen_k, k_scale, v_scale, dtype,
+                      total_k=None):
+    """Paged fp8 K/V -> packed 16-bit K/V ``[rows, Hkv, D]`` (rows
     ``cu_seqlens_k[s] + j``), dequantized as ``rnd(code * scale)``; views of a
-    persistent, grow-only workspace of the device."""
+    persistent, grow-only workspace of the stream.  ``rows`` is ``total_k``
+    (= ``cu_seqlens_k[-1]``, known to the host that built the metadata) when
+    given, else the bound ``num_seqs * max_seqlen_k``."""
     nb, bs, hkv, d = k_cache.shape
     n = cu_seqlens_k.numel() - 1
-    rows = n * int(max_seqlen_k)
+    rows = int(total_k) if total_k is not None else n * int(max_seqlen_k)
     need = 2 * rows * hkv * d
-    idx = torch.device(k_cache.device).index or 0
-    ws = _gather_ws.get(idx)
-    if ws is None or ws.numel() < need:
-        ws = torch.empty(max(need, 1 << 20), dtype=dtype, device=k_cache.device)
-        _gather_ws[idx] = ws
-    ws = ws[:need].view(dtype) if ws.dtype != dtype else ws[:need]
+    item = torch.empty((), dtype=dtype).element_size()
+    ws = _grow(_gather_ws, _key(k_cache.device), need * item, dtype, k_cache.device)
+    ws = ws[:need]
     kb = ws[:rows * hkv * d].view(rows, hkv, d)
     vb = ws[rows * hkv * d:need].view(rows, hkv, d)
     rc = lib().nq_kv_gather_dequant(ptr(k_cache), ptr(v_cache), ptr(block_table), block_table.stride(0),
                                     block_table.shape[1], nb, ptr(cu_seqlens_k), n, int(max_seqlen_k), bs, hkv, d,
-                                    ptr(k_scale), ptr(v_scale), ptr(kb), ptr(vb), dtype_code(dtype),
+                                    ptr(k_scale), ptr(v_scale), ptr(kb), ptr(vb), rows, dtype_code(dtype),
                                     stream_of(k_cache))
     check(rc, "kv_gather_dequant")
     return kb, vb
 
 
 def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
-                   causal=True, block_table=None, k_scale=None, v_scale=None, out=None, gate=None):
+                   causal=True, block_table=None, k_scale=None, v_scale=None, out=None, gate=None, total_k=None):
     """Causal varlen attention; ``q [Tq, Hq, D]`` -> ``[Tq, Hq, D]``.
 
     Without ``block_table``: ``k, v [Tk, Hkv, D]`` packed by ``cu_seqlens_k``.
@@ -207,7 +254,8 @@ def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen
             and block_table.dtype == torch.int32 and block_table.stride(-1) == 1):
         # fp8 cache at head_dim 128: dequantize the sequences' K/V into packed
         # 16-bit rows and run the persistent 16-bit kernel on them.
-        k, v = kv_gather_dequant(k, v, block_table, cu_seqlens_k, max_seqlen_k, k_scale, v_scale, q.dtype)
+        k, v = kv_gather_dequant(k, v, block_table, cu_seqlens_k, max_seqlen_k, k_scale, v_scale, q.dtype,
+                                 total_k=total_k)
         block_table = k_scale = v_scale = None
     if block_table is None:
         tk, hkv, d2 = k.shape
@@ -241,6 +289,8 @@ def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen
         g3 = _gate3(gate, tq, hq, d, "varlen_prefill")
         rc = lib().nq_varlen_prefill_gated(*args, ptr(g3), g3.stride(0), g3.stride(1), tq, stream_of(q))
     check(rc, "varlen_prefill")
+    if _DEBUG_QUEUE:
+        _check_queue_zero(ws)
     return out
 
 

@@ -139,3 +139,76 @@ def conv1d_silu(x, weight, conv_state, state_indices, cu_seqlens=None, dtype="bf
         if has:
             conv_state[slot] = seq[:, -(K - 1):]
     return out
+
+
+def gdn_prefill_chunked(q, k, v, a, b, A_log, dt_bias, cu_seqlens, state, state_indices, from_slot=False,
+                        chunk=64):
+    """The same prefill through the chunked (WY) form of the gated delta rule
+    that the reference's prefill kernel computes (layers/fla/chunk.py:23-72:
+    chunk_local_cumsum, then chunk_fwd.py's fused k k^T + triangular solve +
+    w/u recompute, chunk_delta_h.py's state pass over chunks, chunk_o.py's
+    outputs), in float64 torch on the tensors' device, all heads at once.
+
+    Per chunk of length C with local log-decay cumsum G (G_i = sum_{j<=i} g_j),
+    unit keys k_i, beta_i and the state S0 entering the chunk ([V, K]):
+      A[i, j] = beta_i exp(G_i - G_j) (k_i . k_j)        for j < i, else 0
+      T = (I + A)^-1
+      W = T (beta exp(G) k),  U = T (beta v)             (rows = tokens)
+      D = U - W S0^T                                     (the delta-rule updates)
+      o_i = scale exp(G_i) S0 q_i + scale sum_{j<=i} exp(G_i - G_j) (k_j . q_i) D_j
+      S_C = exp(G_C) S0 + sum_j exp(G_C - G_j) D_j k_j^T
+    which unrolls gdn_step over the chunk exactly (in exact arithmetic), so
+    the two restatements pin each other.  Inputs and outputs as gdn_prefill
+    (numpy arrays or torch tensors; ``state`` updated in place)."""
+    import torch
+    as_t = lambda x: x if isinstance(x, torch.Tensor) else torch.from_numpy(np.asarray(x))
+    was_np = not isinstance(q, torch.Tensor)
+    dev = as_t(q).device
+    f = lambda x: as_t(x).to(device=dev, dtype=torch.float64)
+    q, k, v, a, b = f(q), f(k), f(v), f(a), f(b)
+    A_log, dt_bias = f(A_log), f(dt_bias)
+    st = as_t(state)
+    T, H, K = q.shape
+    HV, V = v.shape[1], v.shape[2]
+    rep = HV // H
+    l2 = lambda x: x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+    qn = l2(q).repeat_interleave(rep, dim=1) * K ** -0.5      # [T, HV, K]
+    kn = l2(k).repeat_interleave(rep, dim=1)
+    g = -torch.exp(A_log) * torch.nn.functional.softplus(a + dt_bias)   # [T, HV]
+    beta = torch.sigmoid(b)
+    out = torch.zeros(T, HV, V, dtype=torch.float64, device=dev)
+    cu = [int(x) for x in (cu_seqlens.tolist() if hasattr(cu_seqlens, "tolist") else cu_seqlens)]
+    idx = [int(x) for x in (state_indices.tolist() if hasattr(state_indices, "tolist") else state_indices)]
+    for n in range(len(cu) - 1):
+        t0, t1 = cu[n], cu[n + 1]
+        slot = idx[n]
+        has = 0 <= slot < st.shape[0]
+        S = (as_t(st[slot]).to(dev, torch.float64).clone() if (from_slot and has)
+             else torch.zeros(HV, V, K, dtype=torch.float64, device=dev))
+        for c0 in range(t0, t1, chunk):
+            c1 = min(c0 + chunk, t1)
+            kc = kn[c0:c1].transpose(0, 1)                      # [HV, C, K]
+            qc = qn[c0:c1].transpose(0, 1)
+            vc = v[c0:c1].transpose(0, 1)                       # [HV, C, V]
+            bc = beta[c0:c1].transpose(0, 1)                    # [HV, C]
+            G = torch.cumsum(g[c0:c1].transpose(0, 1), dim=1)   # [HV, C]
+            C = c1 - c0
+            decay = torch.exp(G[:, :, None] - G[:, None, :])    # [HV, C, C], exp(G_i - G_j)
+            strict = torch.tril(torch.ones(C, C, dtype=torch.bool, device=dev), -1)
+            A = torch.where(strict, bc[:, :, None] * decay * (kc @ kc.transpose(1, 2)), 0.0)
+            Tm = torch.linalg.inv(torch.eye(C, dtype=torch.float64, device=dev) + A)
+            W = Tm @ (bc[:, :, None] * torch.exp(G)[:, :, None] * kc)
+            U = Tm @ (bc[:, :, None] * vc)
+            Dl = U - W @ S.transpose(1, 2)                      # [HV, C, V]
+            causal = torch.tril(torch.ones(C, C, dtype=torch.bool, device=dev))
+            P = torch.where(causal, decay * (qc @ kc.transpose(1, 2)), 0.0)
+            o = torch.exp(G)[:, :, None] * (qc @ S.transpose(1, 2)) + P @ Dl
+            out[c0:c1] = o.transpose(0, 1)
+            GC = G[:, -1]
+            S = torch.exp(GC)[:, None, None] * S + (Dl * torch.exp(GC[:, None] - G)[:, :, None]).transpose(1, 2) @ kc
+        if has:
+            if isinstance(st, torch.Tensor) and not was_np:
+                st[slot] = S.to(st.dtype)
+            else:
+                state[slot] = S.cpu().numpy()
+    return out.cpu().numpy() if was_np else out

@@ -9,7 +9,9 @@ bottom-right causal mask, because ``is_causal=True`` is top-left aligned
 when ``Lk > Lq``.  fp8 caches are dequantized inside the timed region.
 
 Follows layers/attention.py:59-75 (store, then prefill or decode) and the
-semantics stated in ``oracle/paged.py``.
+semantics stated in ``oracle/paged.py``.  The functions run on whatever
+device their tensors are on: the GPU parity tests also use them, in float32
+on the device, as the checker of every output row of the full-size configs.
 """
 from __future__ import annotations
 
@@ -52,15 +54,15 @@ def paged_decode(q, k_cache, v_cache, block_tables, context_lens, scale,
     B, hq, d = q.shape
     hkv = k_cache.shape[2]
     g = hq // hkv
-    out = torch.zeros(B, hq, d, dtype=compute_dtype)
+    out = torch.zeros(B, hq, d, dtype=compute_dtype, device=q.device)
     ctx = context_lens.tolist()
     for b in range(B):
         if ctx[b] <= 0:
             continue
         k = _gather(k_cache, block_tables[b], ctx[b], k_scale).to(compute_dtype)
         v = _gather(v_cache, block_tables[b], ctx[b], v_scale).to(compute_dtype)
-        k = k.transpose(0, 1).repeat_interleave(g, dim=0)        # [Hq, ctx, D]
-        v = v.transpose(0, 1).repeat_interleave(g, dim=0)
+        k = k.transpose(0, 1).repeat_interleave(g, dim=0).contiguous()        # [Hq, ctx, D]
+        v = v.transpose(0, 1).repeat_interleave(g, dim=0).contiguous()
         qq = q[b].to(compute_dtype).unsqueeze(1)                  # [Hq, 1, D]
         out[b] = F.scaled_dot_product_attention(qq, k, v, scale=scale).squeeze(1)
     return out
@@ -74,7 +76,7 @@ def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, scale, block_tables=None
     g = hq // hkv
     cq = cu_seqlens_q.tolist()
     ck = cu_seqlens_k.tolist()
-    out = torch.zeros(tq, hq, d, dtype=compute_dtype)
+    out = torch.zeros(tq, hq, d, dtype=compute_dtype, device=q.device)
     for s in range(len(cq) - 1):
         lq, lk = cq[s + 1] - cq[s], ck[s + 1] - ck[s]
         if lq <= 0:
@@ -85,11 +87,11 @@ def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, scale, block_tables=None
         else:
             ks = _gather(k, block_tables[s], lk, k_scale)
             vs = _gather(v, block_tables[s], lk, v_scale)
-        ks = ks.to(compute_dtype).transpose(0, 1).repeat_interleave(g, dim=0)
-        vs = vs.to(compute_dtype).transpose(0, 1).repeat_interleave(g, dim=0)
-        qs = q[cq[s]:cq[s + 1]].to(compute_dtype).transpose(0, 1)          # [Hq, Lq, D]
+        ks = ks.to(compute_dtype).transpose(0, 1).repeat_interleave(g, dim=0).contiguous()
+        vs = vs.to(compute_dtype).transpose(0, 1).repeat_interleave(g, dim=0).contiguous()
+        qs = q[cq[s]:cq[s + 1]].to(compute_dtype).transpose(0, 1).contiguous()          # [Hq, Lq, D]
         p = lk - lq
-        mask = torch.arange(lk)[None, :] <= (torch.arange(lq)[:, None] + p)
+        mask = torch.arange(lk, device=q.device)[None, :] <= (torch.arange(lq, device=q.device)[:, None] + p)
         o = F.scaled_dot_product_attention(qs, ks, vs, attn_mask=mask, scale=scale)
         out[cq[s]:cq[s + 1]] = o.transpose(0, 1)
     return out

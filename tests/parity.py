@@ -149,3 +149,37 @@ def prefill_reference(case, seq_ids, rows_per_seq=None, seed=0):
         ref = paged.varlen_prefill(q, kc, vc, sub_cq, sub_ck, case["scale"], block_tables=table,
                                    rows=local_rows, k_scale=ks, v_scale=vs)
     return glob_rows[local_rows], ref[local_rows]
+
+
+def full_decode_check(case, out, tol):
+    """Every output row of a decode case against ``oracle/sdpa_path`` run in
+    float32 on the device over the cache after the (separately bit-checked)
+    store.  sdpa_path is pinned against the float64 oracle on the CPU."""
+    from oracle import sdpa_path
+    o = out.squeeze(1) if out.dim() == 4 else out
+    ref = sdpa_path.paged_decode(case["q"], case["k_cache"], case["v_cache"], case["block_tables"],
+                                 case["context_lens"].cpu(), case["scale"], case.get("k_scale"), case.get("v_scale"))
+    err = (o.float() - ref).abs()
+    mx, mn = float(err.max()), float(err.mean())
+    assert bool(torch.isfinite(o.float()).all()), f"{case['name']}: non-finite output"
+    assert mx <= tol["max_abs"] and mn <= tol["mean_abs"], \
+        f"{case['name']} all rows: max-abs {mx:.3e} (<= {tol['max_abs']}), mean-abs {mn:.3e} (<= {tol['mean_abs']})"
+    return mx, mn
+
+
+def full_prefill_check(case, out, tol):
+    """Every output row of a prefill case against ``oracle/sdpa_path`` in
+    float32 on the device (after the store, like full_decode_check)."""
+    from oracle import sdpa_path
+    if case["block_tables"] is None:
+        k, v, ks, vs = case["k_new"], case["v_new"], None, None
+    else:
+        k, v, ks, vs = case["k_cache"], case["v_cache"], case.get("k_scale"), case.get("v_scale")
+    ref = sdpa_path.varlen_prefill(case["q"], k, v, case["cu_seqlens_q"].cpu(), case["cu_seqlens_k"].cpu(),
+                                   case["scale"], block_tables=case["block_tables"], k_scale=ks, v_scale=vs)
+    err = (out.float() - ref).abs()
+    mx, mn = float(err.max()), float(err.mean())
+    assert bool(torch.isfinite(out.float()).all()), f"{case['name']}: non-finite output"
+    assert mx <= tol["max_abs"] and mn <= tol["mean_abs"], \
+        f"{case['name']} all rows: max-abs {mx:.3e} (<= {tol['max_abs']}), mean-abs {mn:.3e} (<= {tol['mean_abs']})"
+    return mx, mn

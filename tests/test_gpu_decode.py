@@ -10,7 +10,8 @@ import torch
 
 from nano_qwen_amd import kernels
 from oracle.inputs import make_decode_case
-from tests.parity import TOL_BF16, TOL_FP8, assert_close, decode_reference, f64, snapshot_decode
+from tests.parity import (TOL_BF16, TOL_FP8, assert_close, decode_reference, f64, full_decode_check,
+                          snapshot_decode)
 
 pytestmark = pytest.mark.gpu
 
@@ -25,14 +26,21 @@ def run_step(case):
     return out
 
 
-def check(case, seq_ids, tol):
+def check(case, seq_ids, tol, all_rows=False):
+    """The float64 oracle on ``seq_ids`` (end to end from the pre-store
+    cache); with ``all_rows`` also every row of the batch against the float32
+    device reference."""
     print(f"[decode] {case['name']} B={case['batch']} Hq={case['hq']} Hkv={case['hkv']} "
           f"kv={case['k_cache'].dtype} seqs={list(seq_ids)[:8]}", flush=True)
     snapshot_decode(case, seq_ids)
     out = run_step(case)
     assert out.shape == (case["batch"], 1, case["hq"], case["d"])
     ref = decode_reference(case, seq_ids)
-    return assert_close(f64(out[list(seq_ids), 0]), ref, **tol, what=case["name"])
+    res = assert_close(f64(out[list(seq_ids), 0]), ref, **tol, what=case["name"])
+    if all_rows:
+        mx, mn = full_decode_check(case, out, tol)
+        print(f"[decode] {case['name']} all {case['batch']} rows: max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
+    return res
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -169,20 +177,20 @@ def test_decode_hip_graph_replay(cuda):
 def test_decode_cfg2_full(cuda):
     case = make_decode_case("cfg2", seed=0, device=cuda)
     seqs = np.random.default_rng(0).choice(case["batch"], 12, replace=False).tolist()
-    check(case, seqs, TOL_BF16)
+    check(case, seqs, TOL_BF16, all_rows=True)
 
 
 @pytest.mark.slow
 def test_decode_cfg4_full_split_k(cuda):
     case = make_decode_case("cfg4", seed=0, device=cuda)
-    check(case, [0, 5], TOL_BF16)
+    check(case, [0, 5], TOL_BF16, all_rows=True)
 
 
 @pytest.mark.slow
 def test_decode_cfg5_full_fp8(cuda):
     case = make_decode_case("cfg5", seed=0, device=cuda)
     seqs = np.random.default_rng(1).choice(case["batch"], 10, replace=False).tolist()
-    check(case, seqs, TOL_FP8)
+    check(case, seqs, TOL_FP8, all_rows=True)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -224,3 +232,55 @@ def test_decode_head_dim_256_f16_groups(cuda):
     case = make_decode_case("cfg2", seed=9, device=cuda, batch=4, ctx=(300, 900), d=256, hq=8, hkv=8,
                             dtype=torch.float16)
     check(case, range(4), TOL_BF16)
+
+
+def test_decode_graph_survives_workspace_growth(cuda):
+    """A graph captured with a small split-K workspace keeps replaying
+    correctly after an eager decode on the same stream has grown that
+    stream's workspace with a bigger plan (the old buffer stays alive), and
+    its replays match the eager result bit for bit."""
+    mk = lambda seed: make_decode_case("cfg2", seed=seed, device=cuda, batch=4, ctx=(700, 2000), min_pool=80)
+    case = mk(12)
+    W = 8
+    static_bt = torch.full((4, W), -1, dtype=torch.int32, device=cuda)
+    static_bt[:, :case["block_tables"].shape[1]] = case["block_tables"]
+    static_ctx = case["context_lens"].clone()
+    out = torch.zeros(4, 1, case["hq"], 128, dtype=case["q"].dtype, device=cuda)
+    step = lambda: kernels.paged_decode(case["q"].unsqueeze(1), case["k_cache"], case["v_cache"], static_ctx,
+                                        static_bt, case["scale"], out=out)
+    assert kernels.decode_plan(4, case["hq"], case["hkv"], W, 256, case["k_cache"].dtype)[0] > 1
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()                                   # allocates this stream's workspace
+        side.synchronize()
+        key = kernels._key(cuda)
+        captured_ws = kernels._workspaces[key].data_ptr()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):   # the capture reuses that workspace
+            step()
+        assert kernels._workspaces[key].data_ptr() == captured_ws
+        eager = step().clone()
+        side.synchronize()
+        # an eager decode on the same stream with a plan that needs far more
+        # workspace: the shim replaces the buffer and keeps the old one alive
+        big = make_decode_case("cfg4", seed=13, device=cuda, batch=8, ctx=(30000, 32768))
+        kernels.paged_decode(big["q"].unsqueeze(1), big["k_cache"], big["v_cache"], big["context_lens"],
+                             big["block_tables"], big["scale"])
+        side.synchronize()
+        assert kernels._workspaces[key].data_ptr() != captured_ws, "the big plan must have grown the workspace"
+        assert any(t.data_ptr() == captured_ws for t in kernels._retired)
+        del big
+        torch.cuda.empty_cache()
+        junk = torch.full((1 << 26,), 7, dtype=torch.int32, device=cuda)   # reuse of freed memory would show
+        for rep in range(3):
+            out.zero_()
+            g.replay()
+            side.synchronize()
+            assert torch.equal(out, eager), f"replay {rep} after the workspace grew"
+        del junk
+    torch.cuda.synchronize()
+    snapshot_decode(case, list(range(4)))
+    ref = decode_reference(dict(case, slot_mapping=torch.full((4,), -1, dtype=torch.int32, device=cuda)),
+                           list(range(4)))
+    assert_close(f64(out[:, 0]), ref, **TOL_BF16, what="replay after growth vs oracle")

@@ -266,3 +266,75 @@ def test_gdn_core_layer_path(cuda):
     run(sum(lens), torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32))
     run(3, None)
     run(3, None)
+
+
+def test_gdn_decode_bench_shape(cuda):
+    """The bench's decode shape: B = 64 sequences, 16 key heads, 32 value
+    heads, every sequence on its own slot of a 64-slot pool."""
+    c = _case(B=64, H=16, HV=32, slots=64, seed=11)
+    c["idx"] = torch.randperm(64, generator=torch.Generator().manual_seed(12)).to(torch.int32)
+    state_dev = c["state"].clone().to(cuda)
+    out = _run(c, cuda, state_dev)
+    ref_state = c["state"].double().numpy()
+    ref = _ref(c, ref_state)
+    _check(c, out, ref, state_dev, ref_state, np.ones(64, bool))
+
+
+def _prefill_inputs(lens, H, HV, seed, slots):
+    g = torch.Generator().manual_seed(seed)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32)
+    T, bf = int(cu[-1]), torch.bfloat16
+    return dict(q=torch.randn(T, H, 128, generator=g).to(bf), k=torch.randn(T, H, 128, generator=g).to(bf),
+                v=torch.randn(T, HV, 128, generator=g).to(bf), a=torch.randn(T, HV, generator=g).to(bf),
+                b=torch.randn(T, HV, generator=g).to(bf), A_log=torch.randn(HV, generator=g) * 0.5,
+                dt=torch.randn(HV, generator=g) * 0.5, state=torch.randn(slots, HV, 128, 128, generator=g) * 0.05,
+                cu=cu)
+
+
+@pytest.mark.slow
+def test_gdn_prefill_cfg3_lengths(cuda):
+    """cfg3's 16 sequence lengths (19,041 tokens, 256 .. 2048 each) with the
+    bench's 16 key / 32 value heads, against the float64 chunked form run on
+    the device (pinned against the step recurrence on the CPU)."""
+    from oracle.inputs import make_prefill_case
+    lens = make_prefill_case("cfg3", seed=0, device="cpu", prefix_blocks=(0, 0), nseq=16, hq=8, hkv=8, d=128)["lq"]
+    H, HV = 16, 32
+    c = _prefill_inputs(lens, H, HV, seed=13, slots=20)
+    idx = torch.randperm(20, generator=torch.Generator().manual_seed(14))[:16].to(torch.int32)
+    print(f"[gdn] prefill cfg3 lengths: {sum(lens)} tokens, H={H} HV={HV}", flush=True)
+    d = {k: v.to(cuda) for k, v in c.items()}
+    state_dev = d["state"].clone()
+    out = kernels.gdn_prefill(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt"], d["cu"], state_dev,
+                              idx.to(cuda), initial_state_from_slot=True)
+    ref_state = d["state"].double().clone()
+    ref = gdn.gdn_prefill_chunked(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt"], c["cu"], ref_state,
+                                  idx, from_slot=True)
+    torch.cuda.synchronize()
+    err = (out.double() - ref).abs()
+    assert bool((err <= 2 ** -8 * ref.abs() + 1e-3 * ref.abs().max()).all()), float(err.max())
+    assert float((state_dev.double() - ref_state).abs().max()) <= 2e-5 * float(ref_state.abs().max())
+
+
+def test_gdn_prefill_empty_sequences(cuda):
+    """Zero-length sequences (in the middle and last, where cu_seqlens[n] is
+    one past the last row) write no output and store their initial state."""
+    lens = [0, 9, 0, 70, 0]
+    c = _prefill_inputs(lens, 2, 4, seed=15, slots=6)
+    idx = torch.tensor([5, 0, 1, 3, 4], dtype=torch.int32)
+    for from_slot in (False, True):
+        d = {k: v.to(cuda) for k, v in c.items()}
+        state_dev = d["state"].clone()
+        out = kernels.gdn_prefill(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt"], d["cu"],
+                                  state_dev, idx.to(cuda), initial_state_from_slot=from_slot)
+        torch.cuda.synchronize()
+        f = lambda t: t.double().numpy()
+        ref_state = c["state"].double().numpy()
+        ref = gdn.gdn_prefill(f(c["q"]), f(c["k"]), f(c["v"]), f(c["a"]), f(c["b"]), f(c["A_log"]), f(c["dt"]),
+                              c["cu"].numpy(), ref_state, idx.numpy(), from_slot=from_slot)
+        o = out.float().cpu().numpy()
+        assert np.all(np.abs(o - ref) <= 2 ** -8 * np.abs(ref) + 1e-3 * np.abs(ref).max())
+        s = state_dev.cpu().double().numpy()
+        assert np.abs(s - ref_state).max() <= 2e-5 * np.abs(ref_state).max()
+        for slot in (5, 1, 4):   # the empty sequences' slots
+            want = c["state"][slot] if from_slot else torch.zeros(4, 128, 128)
+            assert torch.equal(state_dev[slot].cpu(), want)

@@ -10,7 +10,8 @@ import torch
 
 from nano_qwen_amd import kernels
 from oracle.inputs import make_prefill_case
-from tests.parity import TOL_BF16, TOL_FP8, assert_close, f64, prefill_reference, snapshot_prefill
+from tests.parity import (TOL_BF16, TOL_FP8, assert_close, f64, full_prefill_check, prefill_reference,
+                          snapshot_prefill)
 
 pytestmark = pytest.mark.gpu
 
@@ -29,14 +30,21 @@ def run_step(case):
     return out
 
 
-def check(case, seq_ids, tol, rows_per_seq=None):
+def check(case, seq_ids, tol, rows_per_seq=None, all_rows=False):
+    """The float64 oracle on ``seq_ids`` (``rows_per_seq`` sampled rows each);
+    with ``all_rows`` also every output row against the float32 device
+    reference."""
     print(f"[prefill] {case['name']} n={case['nseq']} lq={case['lq'][:6]} prefix={case['prefix'][:6]} "
           f"kv={case['k_cache'].dtype} paged={case['block_tables'] is not None}", flush=True)
     snapshot_prefill(case, seq_ids)
     out = run_step(case)
     assert out.shape == case["q"].shape
     rows, ref = prefill_reference(case, seq_ids, rows_per_seq)
-    return assert_close(f64(out[torch.from_numpy(rows).to(out.device)]), ref, **tol, what=case["name"])
+    res = assert_close(f64(out[torch.from_numpy(rows).to(out.device)]), ref, **tol, what=case["name"])
+    if all_rows:
+        mx, mn = full_prefill_check(case, out, tol)
+        print(f"[prefill] {case['name']} all {out.shape[0]} rows: max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
+    return res
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -127,7 +135,15 @@ def test_decode_equals_last_prefill_row(cuda):
 @pytest.mark.slow
 def test_prefill_cfg3_full(cuda):
     case = make_prefill_case("cfg3", seed=0, device=cuda)
-    check(case, list(range(16)), TOL_BF16, rows_per_seq=24)
+    check(case, list(range(16)), TOL_BF16, rows_per_seq=24, all_rows=True)
+
+
+@pytest.mark.slow
+def test_prefill_cfg3_full_fp8(cuda):
+    """cfg3's sequences over an fp8 cache: every output row against the
+    float32 device reference over the dequantized cache."""
+    case = make_prefill_case("cfg3", seed=0, device=cuda, kv="fp8")
+    check(case, [0, 3, 8], TOL_FP8, rows_per_seq=24, all_rows=True)
 
 
 def test_prefill_queue_resets_between_calls(cuda):
@@ -220,3 +236,67 @@ def test_kv_gather_dequant_bit_exact(cuda):
             ref = round_to((F.decode_e4m3fn(row).astype(np.float32) * ks[:, None]).astype(np.float32), "bf16")
             got = kb[int(cu[s]) + j].float().cpu().numpy()
             assert np.array_equal(got, ref), (s, j)
+
+
+def test_prefill_two_streams_own_queues(cuda):
+    """Launches on two streams at once use their own work-queue counters:
+    both outputs equal the single-stream results, and both streams' counters
+    read zero afterwards."""
+    a = make_prefill_case("cfg3", seed=40, device=cuda, nseq=5, lq=(200, 900), prefix_blocks=(1, 2))
+    b = make_prefill_case("cfg3", seed=41, device=cuda, nseq=3, lq=(100, 700), prefix_blocks=(0, 0))
+    ra, rb = run_step(a).clone(), run_step(b).clone()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for s in (s1, s2):
+        s.wait_stream(torch.cuda.current_stream())
+    outs = {}
+    for rep in range(3):
+        with torch.cuda.stream(s1):
+            outs["a"] = run_step_async(a)
+            q1 = kernels.prefill_workspace(cuda)
+        with torch.cuda.stream(s2):
+            outs["b"] = run_step_async(b)
+            q2 = kernels.prefill_workspace(cuda)
+        assert q1.data_ptr() != q2.data_ptr()
+        torch.cuda.synchronize()
+        assert torch.equal(outs["a"], ra) and torch.equal(outs["b"], rb), f"rep {rep}"
+        assert int(q1.count_nonzero()) == 0 and int(q2.count_nonzero()) == 0
+
+
+def run_step_async(case):
+    """The attention call of run_step (K/V already stored), without a sync."""
+    if case["block_tables"] is None:
+        k, v, ks, vs = case["k_new"], case["v_new"], None, None
+    else:
+        k, v, ks, vs = case["k_cache"], case["v_cache"], case["k_scale"], case["v_scale"]
+    return kernels.varlen_prefill(case["q"], k, v, case["cu_seqlens_q"], case["cu_seqlens_k"],
+                                  case["max_seqlen_q"], case["max_seqlen_k"], case["scale"], causal=True,
+                                  block_table=case["block_tables"], k_scale=ks, v_scale=vs)
+
+
+def test_prefill_queue_debug_check(cuda, monkeypatch):
+    """NQ_DEBUG_PREFILL_QUEUE makes every prefill verify on the host that
+    the launch left its work-queue counters at zero."""
+    monkeypatch.setattr(kernels, "_DEBUG_QUEUE", True)
+    case = make_prefill_case("cfg3", seed=42, device=cuda, nseq=3, lq=(50, 400), prefix_blocks=(1, 1))
+    check(case, range(3), TOL_BF16)
+
+
+def test_fp8_gather_sized_by_total_keys(cuda):
+    """fp8 prefill with the host-known key count: the dequantized K/V take
+    total_k rows, not num_seqs * max_seqlen_k (one long sequence among many
+    short ones), and the result matches the bound-sized call bit for bit."""
+    case = make_prefill_case("cfg3", seed=43, device=cuda, nseq=12, lq=(5, 40), prefix_blocks=(1, 1), kv="fp8")
+    snapshot_prefill(case, [0, 1])
+    base = run_step(case).clone()
+    total_k = int(case["cu_seqlens_k"][-1])
+    assert total_k < case["nseq"] * case["max_seqlen_k"]
+    kernels._gather_ws.clear()
+    out = kernels.varlen_prefill(case["q"], case["k_cache"], case["v_cache"], case["cu_seqlens_q"],
+                                 case["cu_seqlens_k"], case["max_seqlen_q"], case["max_seqlen_k"], case["scale"],
+                                 block_table=case["block_tables"], k_scale=case["k_scale"], v_scale=case["v_scale"],
+                                 total_k=total_k)
+    torch.cuda.synchronize()
+    ws = kernels._gather_ws[kernels._key(cuda)]
+    hkv, d = case["k_cache"].shape[2:]
+    assert ws.numel() == max(2 * total_k * hkv * d, (1 << 20) // 2)
+    assert torch.equal(out, base)

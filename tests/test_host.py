@@ -48,6 +48,15 @@ def test_abi_rejects_bad_arguments_without_launching():
                                128, 256, 0.1, 1, 2, 1, None, None, None, 0, None)
     assert rc == -2  # bf16 q with f16 kv
     assert lib.nq_prefill_workspace_bytes() >= 36  # 8 per-XCD counters + 1 finish counter
+    # a split wider than 63 blocks: each split holds its block-table entries
+    # one per lane, so the ABI refuses it (nq_decode_plan never makes one)
+    fake = ctypes.c_void_p(1 << 20)
+    args = lambda st, ns: (fake, 1024, 128, fake, fake, fake, 64, 64, fake, fake, 1024, 128, 2, 8, 2, 128, 256,
+                           64, 0.1, ns, st, fake, 1 << 30, 2, 2, None, None, None)
+    rc = lib.nq_paged_decode(*args(63 * 256 // 128 * 128 + 128, 2))
+    assert rc == -1 and b"split_tokens" in lib.nq_last_error()
+    ns, st = kernels.decode_plan(1, 8, 2, 4096, 256, torch.bfloat16)
+    assert st <= 63 * 256
 
 
 def test_decode_plan_covers_table_and_respects_env(monkeypatch):
@@ -69,7 +78,7 @@ def test_context_roundtrip():
     assert ctx.is_prefill and ctx.max_seqlen_k == 5 and ctx.context_lens is None
     assert [f for f in C.Context.__slots__] == ["is_prefill", "cu_seqlens_q", "cu_seqlens_k", "max_seqlen_q",
                                                "max_seqlen_k", "slot_mapping", "context_lens", "block_tables",
-                                               "state_indices"]
+                                               "state_indices", "total_k"]
     C.reset_context()
     assert C.get_context().cu_seqlens_q is None
 
@@ -119,6 +128,7 @@ def test_runner_prepare_prefill_on_cpu_matches_oracle():
     assert ctx.slot_mapping.tolist() == md["slot_mapping"]
     assert ctx.cu_seqlens_q.tolist() == md["cu_seqlens_q"] and ctx.cu_seqlens_k.tolist() == md["cu_seqlens_k"]
     assert (ctx.max_seqlen_q, ctx.max_seqlen_k) == (md["max_seqlen_q"], md["max_seqlen_k"])
+    assert ctx.total_k == md["cu_seqlens_k"][-1]
     want = md["block_tables"]
     assert (ctx.block_tables is None) == (want is None)
     if want is not None:

@@ -89,3 +89,90 @@ def test_gated_rmsnorm_oracle():
     assert np.all(gdn.gated_rmsnorm(x, z, np.zeros_like(w), 1e-6, "bf16") == 0)
     y0 = gdn.gated_rmsnorm(x, z, w, 0.0, "bf16")
     assert np.array_equal(gdn.gated_rmsnorm(x * F32(8), z, w, 0.0, "bf16"), y0)
+
+
+def test_chunked_form_equals_recurrence():
+    """gdn_prefill (a loop over gdn_step) against gdn_prefill_chunked (the WY
+    form the reference's chunk kernel computes: triangular solve per chunk,
+    state carried across chunks) -- two independent restatements, equal to
+    float64 round-off for chunk sizes 1, 16 and 64, lengths that cross chunk
+    boundaries, zero or pooled initial states and a skipped slot."""
+    lens = [1, 5, 64, 65, 130, 3, 0]
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    T, H, HV = int(cu[-1]), 2, 4
+    q, k = rng.standard_normal((T, H, 128)), rng.standard_normal((T, H, 128))
+    v = rng.standard_normal((T, HV, 128))
+    a, b = rng.standard_normal((T, HV)), rng.standard_normal((T, HV)) * 2
+    A_log, dt = rng.standard_normal(HV) * 0.5, rng.standard_normal(HV) * 0.5
+    st0 = rng.standard_normal((9, HV, 128, 128)) * 0.05
+    idx = np.array([6, 0, -1, 3, 5, 7, 8])
+    for from_slot in (False, True):
+        s1 = st0.copy()
+        o1 = gdn.gdn_prefill(q, k, v, a, b, A_log, dt, cu, s1, idx, from_slot=from_slot)
+        for chunk in (1, 16, 64):
+            s2 = st0.copy()
+            o2 = gdn.gdn_prefill_chunked(q, k, v, a, b, A_log, dt, cu, s2, idx, from_slot=from_slot, chunk=chunk)
+            assert np.abs(o1 - o2).max() <= 1e-12 * np.abs(o1).max()
+            assert np.abs(s1 - s2).max() <= 1e-12 * np.abs(s1).max()
+        # the empty last sequence keeps its initial state
+        assert np.array_equal(s1[8], st0[8] if from_slot else np.zeros_like(st0[8]))
+    # a dropped decay factor in the chunked form's state pass would fail here
+    s3 = st0.copy()
+    o3 = gdn.gdn_prefill_chunked(q, k, v, a, b, A_log - 50.0, dt, cu, s3, idx)   # g -> 0: pure delta rule
+    s4 = st0.copy()
+    o4 = gdn.gdn_prefill(q, k, v, a, b, A_log - 50.0, dt, cu, s4, idx)
+    assert np.abs(o3 - o4).max() <= 1e-12 * np.abs(o4).max()
+    assert np.abs(o3 - o1).max() > 1e-3 * np.abs(o1).max()
+
+
+def _bits(x):
+    """Signed-magnitude order key of bf16 values given as float32."""
+    u = (np.asarray(x, np.float32).view(np.uint32) >> 16).astype(np.int64)
+    return np.where(u & 0x8000, 0x8000 - u, u)
+
+
+def test_conv1d_silu_matches_torch_conv1d():
+    """conv1d_silu against the reference's own torch ops on bf16 CPU tensors:
+    prefill = F.silu(conv1d(x, padding=K-1, groups=C)[..., :S]) from zeros
+    (layers/gated_delta_net.py:178-180), decode = F.silu(F.conv1d(cat(state,
+    x), padding=0, groups=C)) on the last position with the state shifted
+    (:218-227), and the prefill state = the last K-1 raw inputs (:207-213).
+    Within one bf16 ulp (torch's accumulation order and exp are free), and
+    bit-exact on integer-valued inputs, where every sum is exact."""
+    from oracle.qk_norm_rope import round_to
+    import torch.nn.functional as F
+    C, K, L = 96, 4, 23
+    x = round_to(rng.standard_normal((L, C)).astype(np.float32) * 2, "bf16")
+    w = round_to(rng.standard_normal((C, K)).astype(np.float32) * 0.5, "bf16")
+    st = np.zeros((3, C, K - 1), np.float32)
+    got = gdn.conv1d_silu(x, w, st, np.array([1]), np.array([0, L]))
+    xt = torch.from_numpy(x).bfloat16().T[None]                      # (1, C, S)
+    wt = torch.from_numpy(w).bfloat16()[:, None, :]                  # (C, 1, K)
+    ref = F.silu(F.conv1d(xt, wt, padding=K - 1, groups=C)[:, :, :L])[0].T.float().numpy()
+    d = np.abs(_bits(got) - _bits(ref))
+    assert d.max() <= 1 and (d > 0).mean() < 0.02
+    assert np.array_equal(st[1], x[-(K - 1):].T) and not st[0].any() and not st[2].any()
+    # decode: one token per sequence on the pooled state
+    xd = round_to(rng.standard_normal((1, C)).astype(np.float32) * 2, "bf16")
+    prev = st[1].copy()
+    gotd = gdn.conv1d_silu(xd, w, st, np.array([1]))
+    win = torch.cat([torch.from_numpy(prev).bfloat16()[None], torch.from_numpy(xd).bfloat16().T[None]], dim=-1)
+    refd = F.silu(F.conv1d(win, wt, padding=0, groups=C))[:, :, -1:][0].T.float().numpy()
+    d = np.abs(_bits(gotd) - _bits(refd))
+    assert d.max() <= 1 and (d > 0).mean() < 0.05
+    assert np.array_equal(st[1], win[0, :, -(K - 1):].float().numpy())
+    # integer-valued inputs: every product and sum is exact in float32 and
+    # the pre-activation fits bf16, so the conv itself agrees bit for bit
+    xi = rng.integers(-3, 4, (L, C)).astype(np.float32)
+    wi = rng.integers(-2, 3, (C, K)).astype(np.float32)
+    st = np.zeros((2, C, K - 1), np.float32)
+    yi = gdn.conv1d_silu(xi, wi, st, np.array([0]), np.array([0, L]))
+    pre = F.conv1d(torch.from_numpy(xi).double().T[None], torch.from_numpy(wi).double()[:, None, :],
+                   padding=K - 1, groups=C)[:, :, :L][0].T
+    exact = F.silu(pre.bfloat16().float()).bfloat16().float().numpy()
+    d = np.abs(_bits(yi) - _bits(exact))
+    assert d.max() <= 1 and (d > 0).mean() < 0.02
+    # a window off by one tap (a plausible indexing mistake) is far off
+    shifted = np.concatenate([np.zeros((1, C), np.float32), xi[:-1]])
+    ys = gdn.conv1d_silu(shifted, wi, np.zeros((2, C, K - 1), np.float32), np.array([0]), np.array([0, L]))
+    assert (np.abs(_bits(ys) - _bits(exact)) > 1).mean() > 0.5
