@@ -221,8 +221,8 @@ def kv_gather_dequant(k_cache, v_cache, block_table, cu_seqlens_k, max_seqlen_k,
     rows = int(total_k) if total_k is not None else n * int(max_seqlen_k)
     need = 2 * rows * hkv * d
     item = torch.empty((), dtype=dtype).element_size()
-    ws = _grow(_gather_ws, _key(k_cache.device), need * item, dtype, k_cache.device)
-    ws = ws[:need]
+    ws = _grow(_gather_ws, _key(k_cache.device), need * item, torch.uint8, k_cache.device)
+    ws = ws[:need * item].view(dtype)
     kb = ws[:rows * hkv * d].view(rows, hkv, d)
     vb = ws[rows * hkv * d:need].view(rows, hkv, d)
     rc = lib().nq_kv_gather_dequant(ptr(k_cache), ptr(v_cache), ptr(block_table), block_table.stride(0),
