@@ -142,6 +142,31 @@ int nq_paged_decode_gated(const void *q, int64_t q_batch_stride, int64_t q_head_
                           void *stream);
 
 /*
+ * nq_paged_decode without a caller workspace, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference: it is
+ * nq_paged_decode with the split-K partials in a static device array of
+ * NQ_DECODE_NOALLOC_SCRATCH_BYTES per device, which each device holds until
+ * the process ends.  It calls no allocating routine; the array's address is
+ * looked up (hipGetSymbolAddress) on the first call on each device.
+ * Every other argument is as for nq_paged_decode.  A plan whose
+ * nq_decode_workspace_bytes exceeds the array returns NQ_EINVAL.  All calls
+ * on one device share its array: calls that overlap on one device (several
+ * streams or host threads) race and must be ordered by the caller.
+ */
+#define NQ_DECODE_NOALLOC_SCRATCH_BYTES (64LL << 20)
+int nq_paged_decode_noalloc(const void *q, int64_t q_batch_stride, int64_t q_head_stride,
+                            const void *k_cache, const void *v_cache,
+                            const int32_t *block_tables, int64_t bt_stride,
+                            int max_blocks_per_seq, const int32_t *context_lens,
+                            void *out, int64_t out_batch_stride, int64_t out_head_stride,
+                            int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                            int block_size, int64_t num_blocks, float softmax_scale,
+                            int num_splits, int split_tokens,
+                            int q_dtype, int kv_dtype,
+                            const float *k_scale, const float *v_scale, void *stream);
+
+/*
  * Qwen3.5's attention output gate as one in-place pass:
  *   out[i, h, :] = rnd(out[i, h, :] * rnd(sigmoid(gate[i, h, :])))
  * Replaces attn_output * torch.sigmoid(gate) (models/qwen3_5.py:140-142)

@@ -40,6 +40,10 @@ _SIGS = {
                                       c_int, c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_int, c_int,
                                       c_int, c_int64, c_float, c_int, c_int, c_void_p, c_int64, c_int, c_int,
                                       c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
+    "nq_paged_decode_noalloc": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_int,
+                                        c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_int, c_int, c_int,
+                                        c_int64, c_float, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
+                                        c_void_p]),
     "nq_output_gate": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int, c_int,
                                c_int, c_void_p]),
     "nq_varlen_prefill": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p,

@@ -31,6 +31,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "nq_device.hpp"
 
@@ -606,4 +607,66 @@ extern "C" int nq_paged_decode_gated(const void *q, int64_t q_batch_stride, int6
                            num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, softmax_scale,
                            num_splits, split_tokens, workspace, workspace_bytes, q_dtype, kv_dtype, k_scale,
                            v_scale, gate, gate_batch_stride, gate_head_stride, stream);
+}
+
+// ---------------------------------------------------------------------------
+// nq_paged_decode_noalloc: the same kernels with the split-K partials in a
+// static device array, for callers that cannot allocate.  Every call on a
+// device shares that device's array; calls that overlap on one device (two
+// streams, or two host threads) race on it.  The partials need no clearing:
+// the merge reads only the splits the main kernel wrote in the same call.
+namespace {
+constexpr int64_t kScratchBytes = NQ_DECODE_NOALLOC_SCRATCH_BYTES;  // per device
+constexpr int kMaxDevices = 64;
+__device__ __attribute__((aligned(256))) uint8_t scratch[kScratchBytes];
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+// Device address of the current device's copy of `scratch`, looked up once
+// per device (each device holds its own copy at its own address).  The
+// array's name is only a host-side handle: kernels get this address.
+int scratch_address(void **out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(NQ_ELAUNCH, "paged_decode_noalloc: no current device (or device id %d >= %d)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(NQ_ELAUNCH, "paged_decode_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return NQ_OK;
+}
+}  // namespace
+
+extern "C" int nq_paged_decode_noalloc(const void *q, int64_t q_batch_stride, int64_t q_head_stride,
+                                       const void *k_cache, const void *v_cache, const int32_t *block_tables,
+                                       int64_t bt_stride, int max_blocks_per_seq, const int32_t *context_lens,
+                                       void *out, int64_t out_batch_stride, int64_t out_head_stride, int batch,
+                                       int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                                       int64_t num_blocks, float softmax_scale, int num_splits, int split_tokens,
+                                       int q_dtype, int kv_dtype, const float *k_scale, const float *v_scale,
+                                       void *stream) {
+  // The address is looked up on the first call on a device, whatever the
+  // plan, so a caller's first (eager) call does it before any graph capture.
+  void *ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != NQ_OK) return rc;
+  if (num_splits > 1) {
+    const int64_t need = nq_decode_workspace_bytes(batch, num_q_heads, head_dim, num_splits);
+    if (need > kScratchBytes)
+      return fail(NQ_EINVAL,
+                  "paged_decode_noalloc: the plan (batch %d x %d heads x %d splits) needs %lld bytes of split-K "
+                  "scratch, more than the static %lld",
+                  batch, num_q_heads, num_splits, (long long)need, (long long)kScratchBytes);
+  }
+  return paged_decode_impl(q, q_batch_stride, q_head_stride, k_cache, v_cache, block_tables, bt_stride,
+                           max_blocks_per_seq, context_lens, out, out_batch_stride, out_head_stride, batch,
+                           num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, softmax_scale,
+                           num_splits, split_tokens, ws, kScratchBytes, q_dtype, kv_dtype, k_scale, v_scale,
+                           nullptr, 0, 0, stream);
 }
