@@ -3,20 +3,24 @@
 Restates, for the paged attention path only, engine/model_runner.py:
 ``allocate_kv_cache`` (:186-204), ``allocate_decode_buffers`` (:206-218),
 ``prepare_block_tables`` (:236-240), ``prepare_prefill`` (:242-283) and
-``prepare_decode`` (:285-306).  The decode metadata kernel is the HIP
+``prepare_decode`` (:285-306), ``run_model`` (:319-336) and
+``capture_cudagraph`` (:421-456).  The decode metadata kernel is the HIP
 ``nq_prepare_decode`` instead of Triton.  Model construction, sampling,
-TP control plane and the engine loop are out of scope.
+TP control plane and the engine loop are out of scope: the caller hands
+``capture_cudagraph`` the model (anything called as
+``model(input_ids, positions)`` whose attention layers read ``get_context()``).
 
 fp8 extension: ``allocate_kv_cache(..., kv_cache_dtype=torch.float8_e4m3fn)``
 also creates ``kv_scales [2, L, Hkv]`` float32 (initialised to 1) and binds
-``module.k_scale = kv_scales[0, l]`` / ``module.v_scale = kv_scales[1, l]``.
+``module.k_scale = kv_scales[0, l]`` / ``module.v_scale = kv_scales[1, l]``;
+``calibrate_kv_scales`` sets them to absmax/448 per (layer, kv head).
 """
 from __future__ import annotations
 
 import torch
 
 from .. import kernels
-from ..utils.context import set_context
+from ..utils.context import get_context, reset_context, set_context
 
 
 class ModelRunner:
@@ -28,6 +32,12 @@ class ModelRunner:
         self._pin = self.device.type == "cuda"
         self.kv_cache = None
         self.kv_scales = None
+        self.model = None
+        self.enforce_eager = False
+        self.graphs = {}
+        self.graph_bs = []
+        self.graph_pool = None
+        self.graph_vars = None
         # MRV2-style persistent batch: batch_idx -> request slot, and the last
         # sampled token of every slot (engine/model_runner.py:100-106).
         self.sampled_token_ids_gpu = torch.zeros(max_num_seqs, dtype=torch.int64, device=self.device)
@@ -57,6 +67,36 @@ class ModelRunner:
                     module.v_scale = self.kv_scales[1, layer_id]
                 layer_id += 1
         return layer_id
+
+    def calibrate_kv_scales(self, kv_per_layer):
+        """fp8 pools: ``kv_scales[0, l, h] = absmax(K_l[..., h, :]) / 448``
+        and likewise for V, so the largest calibration value of each
+        (layer, kv head) maps to e4m3's largest finite value and nothing
+        saturates.  ``kv_per_layer[l] = (k, v)``, each a tensor ``[..., Hkv,
+        D]`` or a list of them (e.g. the new keys and values of a
+        calibration prefill, and the prefix already in the pool).  A head
+        whose values are all zero keeps scale 1.  The scales are updated in
+        place, so the layers' bound ``k_scale`` / ``v_scale`` views see them.
+
+        The reference allocates the pool here (engine/model_runner.py:186-204)
+        but has no fp8 cache; the rule is the one its fp8 KV configuration
+        states (per-(layer, kv_head) absmax/448)."""
+        if self.kv_scales is None:
+            raise RuntimeError("calibrate_kv_scales: the KV pool is not float8_e4m3fn")
+        _, n_layers, hkv = self.kv_scales.shape
+        if len(kv_per_layer) != n_layers:
+            raise ValueError(f"calibrate_kv_scales: {len(kv_per_layer)} layers given, the pool has {n_layers}")
+        for layer, pair in enumerate(kv_per_layer):
+            for which, xs in enumerate(pair):
+                amax = None
+                for x in (xs if isinstance(xs, (list, tuple)) else [xs]):
+                    if x.shape[-2] != hkv:
+                        raise ValueError(f"calibrate_kv_scales: {x.shape[-2]} kv heads, the pool has {hkv}")
+                    a = x.float().abs().reshape(-1, hkv, x.shape[-1]).amax(dim=(0, 2))
+                    amax = a if amax is None else torch.maximum(amax, a)
+                s = (amax / 448.0).to(self.kv_scales.device)
+                self.kv_scales[which, layer] = torch.where(s > 0, s, torch.ones_like(s))
+        return self.kv_scales
 
     def allocate_decode_buffers(self):
         size = self.max_num_seqs
@@ -142,3 +182,88 @@ class ModelRunner:
         block_tables = self.prepare_block_tables(seqs)
         set_context(False, slot_mapping=slot_mapping, context_lens=context_lens, block_tables=block_tables)
         return input_ids, positions
+
+    # ------------------------------------------------------- graph capture
+    @torch.inference_mode()
+    def run_model(self, input_ids: torch.Tensor, positions: torch.Tensor, is_prefill: bool):
+        """engine/model_runner.py:319-336: prefill, eager mode and batches
+        above 512 run the model directly; a decode batch replays the graph of
+        the smallest bucket that holds it, after copying its inputs into the
+        static ``graph_vars`` -- padding rows get ``slot_mapping = -1`` (the
+        store skips them) and ``context_lens = 0`` (decode writes zeros), and
+        block-table entries past a row's context are never read.  Returns the
+        model's ``compute_logits`` of the output when it has one, else the
+        output (``[bs, hidden]``)."""
+        model = self.model
+        if is_prefill or self.enforce_eager or input_ids.size(0) > 512 or not self.graphs:
+            return self._logits(model(input_ids, positions))
+        bs = input_ids.size(0)
+        context = get_context()
+        graph = self.graphs[next(x for x in self.graph_bs if x >= bs)]
+        gv = self.graph_vars
+        gv["input_ids"][:bs] = input_ids
+        gv["positions"][:bs] = positions
+        gv["slot_mapping"].fill_(-1)
+        gv["slot_mapping"][:bs] = context.slot_mapping
+        gv["context_lens"].zero_()
+        gv["context_lens"][:bs] = context.context_lens
+        gv["block_tables"][:bs, :context.block_tables.size(1)] = context.block_tables
+        graph.replay()
+        return self._logits(gv["outputs"][:bs])
+
+    def _logits(self, hidden):
+        f = getattr(self.model, "compute_logits", None)
+        return f(hidden) if f is not None else hidden
+
+    @torch.inference_mode()
+    def capture_cudagraph(self, model, hidden_size: int, max_model_len: int,
+                          dtype: torch.dtype | None = None):
+        """engine/model_runner.py:421-456: one HIP graph per decode batch
+        bucket ``[1, 2, 4, 8, 16, 32, ..]`` up to ``min(max_num_seqs, 512)``,
+        largest first, all in one memory pool, over static ``graph_vars``
+        sized for the largest bucket and ``max_model_len``'s block-table
+        width.
+
+        Differences from the reference, both so a capture cannot disturb the
+        cache or leave a batch size without a graph: the capture inputs have
+        ``slot_mapping = -1`` (the reference's zeros make the warmup and
+        capture store into slot 0), and when ``max_bs`` is not itself a
+        bucket it is added as the last one (the reference's bucket list skips
+        sizes between its last multiple of 16 and ``max_bs``, or names
+        buckets above ``max_bs`` that capture fewer rows).
+
+        Every kernel the decode step launches keeps its buffers across
+        replays: the split-K workspace belongs to the capture stream and is
+        never freed while a graph may hold it (a later, larger plan on that
+        stream allocates a new one and keeps the old alive), and nothing in
+        the step records a memset node.
+        """
+        self.model = model
+        dev = self.device
+        max_bs = min(self.max_num_seqs, 512)
+        max_num_blocks = (max_model_len + self.block_size - 1) // self.block_size
+        input_ids = torch.zeros(max_bs, dtype=torch.int64, device=dev)
+        positions = torch.zeros(max_bs, dtype=torch.int64, device=dev)
+        slot_mapping = torch.full((max_bs,), -1, dtype=torch.int32, device=dev)
+        context_lens = torch.zeros(max_bs, dtype=torch.int32, device=dev)
+        block_tables = torch.zeros(max_bs, max_num_blocks, dtype=torch.int32, device=dev)
+        outputs = torch.zeros(max_bs, hidden_size, dtype=dtype or torch.get_default_dtype(), device=dev)
+        self.graph_bs = [x for x in [1, 2, 4, 8] + list(range(16, max_bs + 1, 16)) if x <= max_bs]
+        if self.graph_bs[-1] != max_bs:
+            self.graph_bs.append(max_bs)
+        self.graphs = {}
+        self.graph_pool = None
+        for bs in reversed(self.graph_bs):
+            graph = torch.cuda.CUDAGraph()
+            set_context(False, slot_mapping=slot_mapping[:bs], context_lens=context_lens[:bs],
+                        block_tables=block_tables[:bs])
+            outputs[:bs] = model(input_ids[:bs], positions[:bs])    # warmup
+            with torch.cuda.graph(graph, self.graph_pool):
+                outputs[:bs] = model(input_ids[:bs], positions[:bs])    # capture
+            if self.graph_pool is None:
+                self.graph_pool = graph.pool()
+            self.graphs[bs] = graph
+            torch.cuda.synchronize()
+            reset_context()
+        self.graph_vars = dict(input_ids=input_ids, positions=positions, slot_mapping=slot_mapping,
+                               context_lens=context_lens, block_tables=block_tables, outputs=outputs)

@@ -32,8 +32,10 @@ def store_kvcache(key, value, k_cache, v_cache, slot_mapping, k_scale=None, v_sc
         hk = key.shape[1]
         kr = (kr.float().view(-1, hk, key.shape[2]) * (1.0 / k_scale).view(1, hk, 1)).clamp(-448, 448)
         vr = (vr.float().view(-1, hk, key.shape[2]) * (1.0 / v_scale).view(1, hk, 1)).clamp(-448, 448)
-        kr = kr.reshape(kr.shape[0], -1).to(torch.float8_e4m3fn)
-        vr = vr.reshape(vr.shape[0], -1).to(torch.float8_e4m3fn)
+        # byte views: torch has no fp8 index_copy_ on the device
+        kr = kr.reshape(kr.shape[0], -1).to(torch.float8_e4m3fn).view(torch.uint8)
+        vr = vr.reshape(vr.shape[0], -1).to(torch.float8_e4m3fn).view(torch.uint8)
+        kc, vc = kc.view(torch.uint8), vc.view(torch.uint8)
     kc.index_copy_(0, idx, kr)
     vc.index_copy_(0, idx, vr)
 

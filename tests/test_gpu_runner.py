@@ -8,6 +8,7 @@ from torch import nn
 
 from nano_qwen_amd.engine import ModelRunner, Sequence
 from nano_qwen_amd.layers import Attention
+from nano_qwen_amd.layers.attention import store_kvcache
 from nano_qwen_amd.utils.context import get_context, reset_context
 from oracle import metadata, paged
 from tests.parity import TOL_BF16, TOL_FP8, assert_close, f64
@@ -142,3 +143,33 @@ def test_runner_warmup_prefill_without_cache(cuda):
     ref = paged.varlen_prefill(f64(q), f64(k), f64(v), [0, 300, 377], [0, 300, 377], D ** -0.5)
     assert_close(f64(o), ref, **TOL_BF16, what="warmup prefill")
     reset_context()
+
+
+def test_calibrated_fp8_store_uses_full_range(cuda):
+    """After ``calibrate_kv_scales`` on a batch's new K/V, the HIP store of
+    that batch puts each (layer, kv head)'s absmax element at e4m3's largest
+    finite value, +-448, and nothing beyond: the scale spends the whole range
+    without saturating."""
+    model = TwoLayers()
+    runner = ModelRunner(block_size=BS, max_num_seqs=4, device=cuda)
+    runner.allocate_kv_cache(model, 2, 8, HKV, D, torch.bfloat16, kv_cache_dtype=torch.float8_e4m3fn)
+    runner.kv_cache.view(torch.uint8).zero_()
+    g = torch.Generator(device=cuda).manual_seed(2)
+    n = 300
+    kv = [(torch.randn(n, HKV, D, generator=g, device=cuda).to(torch.bfloat16) * (li + 1),
+           torch.randn(n, HKV, D, generator=g, device=cuda).to(torch.bfloat16) * 0.1) for li in range(2)]
+    runner.calibrate_kv_scales(kv)
+    slots = torch.arange(n, dtype=torch.int32, device=cuda) + 17
+    for li, layer in enumerate(model.attn):
+        k, v = kv[li]
+        store_kvcache(k, v, layer.k_cache, layer.v_cache, slots, layer.k_scale, layer.v_scale)
+    torch.cuda.synchronize()
+    for li in range(2):
+        for which in range(2):
+            codes = runner.kv_cache[which, li].reshape(-1, HKV, D)[17:17 + n].float()
+            amax = codes.abs().amax(dim=(0, 2))
+            assert torch.all(amax == 448.0), (li, which, amax)
+            deq = codes * runner.kv_scales[which, li].view(1, HKV, 1)
+            x = kv[li][which].float()
+            # e4m3 keeps 3 mantissa bits: relative error at most 2^-4, plus the subnormal step
+            assert torch.all((deq - x).abs() <= x.abs() * 2.0 ** -4 + runner.kv_scales[which, li].view(1, HKV, 1) * 2.0 ** -10)

@@ -149,3 +149,73 @@ def test_runner_allocate_kv_cache_binds_layers():
     assert r.kv_cache.shape == (2, 2, 3, 256, 2, 128)
     assert m.b.k_cache.data_ptr() == r.kv_cache[0, 1].data_ptr()
     assert m.a.k_scale.shape == (2,) and m.b.v_scale.data_ptr() == r.kv_scales[1, 1].data_ptr()
+
+
+def test_run_model_eager_paths():
+    """Prefill and batches above 512 never replay a graph
+    (engine/model_runner.py:320); the model's ``compute_logits`` is applied
+    when it has one."""
+    import torch
+    from nano_qwen_amd.engine import ModelRunner
+    runner = ModelRunner(block_size=256, max_num_seqs=8, device="cpu")
+    runner.graphs = {8: None}    # a replay would fail on this
+    runner.graph_bs = [8]
+    called = []
+    runner.model = lambda i, p: called.append(i.numel()) or torch.zeros(i.numel(), 4)
+    ids = torch.zeros(513, dtype=torch.int64)
+    assert runner.run_model(ids, ids, False).shape == (513, 4)
+    assert runner.run_model(ids[:3], ids[:3], True).shape == (3, 4)
+    assert called == [513, 3]
+
+    class WithLogits:
+        def __call__(self, i, p):
+            return torch.ones(i.numel(), 2)
+
+        def compute_logits(self, h):
+            return h * 3
+    runner.model = WithLogits()
+    runner.enforce_eager = True
+    assert torch.equal(runner.run_model(ids[:2], ids[:2], False), torch.full((2, 2), 3.0))
+
+
+def test_calibrate_kv_scales():
+    """absmax/448 per (layer, kv head), in place behind the layers' views;
+    all-zero heads keep 1; lists of tensors combine; non-fp8 pools refuse."""
+    import pytest
+    import torch
+    from torch import nn
+    from nano_qwen_amd.engine import ModelRunner
+    from nano_qwen_amd.layers import Attention
+    from oracle.inputs import fp8_scales
+
+    class M(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.a = nn.ModuleList([Attention(4, 16, 0.25, 2) for _ in range(3)])
+
+    model = M()
+    runner = ModelRunner(block_size=16, max_num_seqs=4, device="cpu")
+    runner.allocate_kv_cache(model, 3, 4, 2, 16, torch.bfloat16, kv_cache_dtype=torch.float8_e4m3fn)
+    g = torch.Generator().manual_seed(0)
+    kv = []
+    for layer in range(3):
+        k = torch.randn(37, 2, 16, generator=g).to(torch.bfloat16) * (layer + 1)
+        v1 = torch.randn(5, 2, 16, generator=g).to(torch.bfloat16)
+        v2 = torch.randn(2, 3, 2, 16, generator=g).to(torch.bfloat16) * 4
+        if layer == 2:
+            k[:, 1] = 0    # an all-zero head
+        kv.append((k, [v1, v2]))
+    runner.calibrate_kv_scales(kv)
+    for layer, (k, vs) in enumerate(kv):
+        assert torch.equal(runner.kv_scales[0, layer], fp8_scales(k))
+        assert torch.equal(runner.kv_scales[1, layer], fp8_scales(*vs))
+        assert model.a[layer].k_scale.data_ptr() == runner.kv_scales[0, layer].data_ptr()
+    assert runner.kv_scales[0, 2, 1].item() == 1.0
+    k0 = kv[0][0].float()
+    assert torch.allclose(runner.kv_scales[0, 0] * 448, k0.abs().amax(dim=(0, 2)))
+    with pytest.raises(ValueError):
+        runner.calibrate_kv_scales(kv[:2])
+    bf = ModelRunner(block_size=16, max_num_seqs=4, device="cpu")
+    bf.allocate_kv_cache(M(), 3, 4, 2, 16, torch.bfloat16)
+    with pytest.raises(RuntimeError):
+        bf.calibrate_kv_scales(kv)
