@@ -240,26 +240,6 @@ int nq_varlen_prefill_gated(const void *q, int64_t q_row_stride, int64_t q_head_
                             const void *gate, int64_t gate_row_stride, int64_t gate_head_stride,
                             int64_t total_q, void *stream);
 
-/*
- * Paged fp8 K/V -> packed, dequantized 16-bit K/V: for sequence s < num_seqs
- * and key j < Lk_s = cu_seqlens_k[s+1] - cu_seqlens_k[s], cache row
- * block_tables[s*bt_stride + j/block_size]*block_size + j%block_size of
- * k_cache/v_cache (e4m3fn [num_blocks, block_size, num_kv_heads, head_dim])
- * goes to row cu_seqlens_k[s] + j of k_out/v_out ([rows, num_kv_heads,
- * head_dim] of out_dtype, F16/BF16) as rnd(code * scale[h]) (fp32 product,
- * round to nearest even); missing blocks give zeros.  This is the K/V the fp8
- * attention contract is stated against, so nq_varlen_prefill on the packed
- * result (block_tables == NULL) computes fp8 prefill on the 16-bit kernel.
- * k_out/v_out hold out_rows rows (normally cu_seqlens_k[num_seqs]): rows at or
- * past out_rows, and keys past max_seqlen_k, are never written, whatever
- * cu_seqlens_k holds; head_dim % 16 == 0; 16-byte aligned.
- */
-int nq_kv_gather_dequant(const void *k_cache, const void *v_cache, const int32_t *block_tables,
-                         int64_t bt_stride, int max_blocks_per_seq, int64_t num_blocks,
-                         const int32_t *cu_seqlens_k, int num_seqs, int max_seqlen_k, int block_size,
-                         int num_kv_heads, int head_dim, const float *k_scale, const float *v_scale,
-                         void *k_out, void *v_out, int64_t out_rows, int out_dtype, void *stream);
-
 /* Bytes of device workspace nq_varlen_prefill needs (work-queue counters). */
 int64_t nq_prefill_workspace_bytes(void);
 

@@ -56,9 +56,6 @@ _SIGS = {
                                         c_int, c_int, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
                                         c_int64, c_int64, c_void_p]),
     "nq_prefill_workspace_bytes": (c_int64, []),
-    "nq_kv_gather_dequant": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int64, c_void_p, c_int, c_int,
-                                     c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int,
-                                     c_void_p]),
     "nq_prepare_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_int, c_int, c_void_p]),
     "nq_gdn_decode": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,

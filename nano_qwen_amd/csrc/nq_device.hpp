@@ -197,6 +197,9 @@ __device__ inline u32x4 lds_load_b128(uint32_t addr) {
   const auto *p = reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(static_cast<uintptr_t>(addr));
   return p[OFF / 16];
 }
+__device__ inline void lds_store_b128(uint32_t addr, const u32x4 &v) {
+  *reinterpret_cast<__attribute__((address_space(3))) u32x4 *>(static_cast<uintptr_t>(addr)) = v;
+}
 template <int OFF>
 __device__ inline u32x2 lds_load_tr16(uint32_t addr) {
   static_assert(OFF % 8 == 0 && OFF >= 0 && OFF < 65536, "ds offset");

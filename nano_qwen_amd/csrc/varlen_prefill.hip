@@ -638,14 +638,20 @@ __device__ __forceinline__ Item describe_by_cost(const PrefillArgs &a, const Cos
 // waits count only younger stream entries -- except that a new item's first
 // kAhead tiles may precede the Q loads and the previous item's output stores
 // (a fixed count per wave), which the waits then add.
-template <class T, int D, class S, bool GATED>
+template <class T, int D, class S, bool GATED, bool FP8>
 __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   using DT = DTile<T, D>;
   using PT = PTile<T, false, D>;
   constexpr int NW = S::NW, QS = S::QS, kSlots = S::SLOTS, kAhead = S::AHEAD;
   constexpr int RW = 16 * QS;        // query rows per wave
   constexpr int CR = kKeys / NW;     // tile rows each wave copies
-  constexpr int COPS = CR / 4;       // 1 KiB loads per K (or V) per wave and entry
+  constexpr int SRC_ROWB = FP8 ? D : 2 * D;  // bytes of one key of one kv head in the cache
+  constexpr int COPS = CR * SRC_ROWB / 1024;  // 1 KiB loads per K (or V) per wave and entry
+  // fp8: a wave's copies land in the upper half of its own rows of the slot
+  // (CR rows of 16-bit keys), which it widens in place before the barrier
+  // that publishes the tile.
+  static_assert(!FP8 || (CR == 8 && COPS == 1), "fp8 copies: 8 rows of 128 bytes per wave");
+  static_assert(!FP8 || kSlots == 4, "fp8: ring slot of a stream entry by mask");
   constexpr int QOPS = QS * PT::NKK;        // Q loads per wave and item
   constexpr int SOPS = QS * (PT::NJ / 2);   // output stores per wave and item
   // Stores that write nothing, after the Q loads: the compiler counts them
@@ -668,7 +674,9 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int m = lane & 15, g = lane >> 4;
-  const float sl2 = a.scale_log2;
+  // log2(e) x the softmax scale; with fp8 K also x the item's K scale (the
+  // products are formed from the unscaled codes)
+  float sl2 = a.scale_log2;
   const bool paged = a.block_tables != nullptr;
   const int row_in_item = RW * (wave / a.G4);  // this wave's first row within an item
   const int head_in_item = wave % a.G4;
@@ -751,19 +759,25 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   int bad_seen = 0, plain_end = 0;
   // This wave's rows of a tile and its 16-byte pieces (the kv head's offset
   // is in the source address).
+  // fp8: rows as they are (widened and swizzled later), 16 codes per lane.
   uint32_t src_k[COPS], src_v[COPS];
 #pragma unroll
   for (int c = 0; c < COPS; ++c) {
-    const int drow = CR * wave + 4 * c + (lane >> 4);
-    const uint32_t row_off = static_cast<uint32_t>(drow * kv_rs);
-    src_k[c] = row_off + (((lane & 15) ^ swz_k(drow)) << 4);
-    src_v[c] = row_off + (((lane & 15) ^ swz_v(drow)) << 4);
+    if constexpr (FP8) {
+      const int drow = CR * wave + (lane >> 3);
+      src_k[c] = src_v[c] = static_cast<uint32_t>(drow * kv_rs + ((lane & 7) << 4));
+    } else {
+      const int drow = CR * wave + 4 * c + (lane >> 4);
+      const uint32_t row_off = static_cast<uint32_t>(drow * kv_rs);
+      src_k[c] = row_off + (((lane & 15) ^ swz_k(drow)) << 4);
+      src_v[c] = row_off + (((lane & 15) ^ swz_v(drow)) << 4);
+    }
   }
   // Block-table entry bidx of a sequence's row (paged only).
   auto blk_entry = [&](const int32_t *bt, int bidx) { return bidx < max_blocks ? ld_const(bt + bidx) : -1; };
   auto queue_copy = [&](const Item &it) {
     nx_rem = (it.live && it.n_kt > 0) ? it.key_end : 0;
-    nx_head = it.kvh * DT::ROWB;
+    nx_head = it.kvh * SRC_ROWB;
     if (paged) {
       const int32_t *bt = a.block_tables + static_cast<int64_t>(it.s) * a.bt_stride;
       nx_base = static_cast<int64_t>(reinterpret_cast<uintptr_t>(bt));
@@ -820,7 +834,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   };
   auto issue = [&]() {
     if (run_left == 0) next_run();
-    const uint32_t dst = st_dst + wave * (CR * DT::ROWB);
+    const uint32_t dst = st_dst + wave * (CR * DT::ROWB) + (FP8 ? CR * DT::ROWB / 2 : 0);
     const u32x4 rk = rsrc_words(st_src, st_nrec);
     const u32x4 rv = rsrc_words(st_src + v_minus_k, st_nrec);
 #pragma unroll
@@ -832,6 +846,36 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
     st_dst = st_dst == lds_last ? lds0 : st_dst + DT::SLOT_B;
     --run_left;
     ++st_pos;
+  };
+  // fp8: widens this wave's rows of stream entries cv_pos .. upto (whose
+  // copies are complete) to 16 bits, in place.  Lane l holds codes of dims
+  // 16(l & 7) .. +15 of row CR * wave + (l >> 3): the wave reads all its
+  // codes (the upper half of its rows) before it writes any row, and no
+  // other wave touches these rows before the next barrier.  The widening
+  // is exact (every e4m3 value is a bf16 and an f16 value); the scales are
+  // applied to the scores and the output instead.
+  int cv_pos = 0;
+  auto widen = [&](int upto) {
+    if constexpr (FP8) {
+      asm volatile("" ::: "memory");  // after the wait for the copies
+      const int r = CR * wave + (lane >> 3), c0 = 2 * (lane & 7);
+      for (; cv_pos <= upto; ++cv_pos) {
+        const uint32_t slot = lds0 + (cv_pos & (kSlots - 1)) * DT::SLOT_B;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const uint32_t tile = slot + t * DT::TILE_B;
+          const u32x4 raw = lds_load_b128<0>(tile + wave * (CR * DT::ROWB) + CR * DT::ROWB / 2 + 16 * lane);
+          const u32x4 lo = u32x4{T::template fp8x2<false>(raw[0]), T::template fp8x2<true>(raw[0]),
+                                 T::template fp8x2<false>(raw[1]), T::template fp8x2<true>(raw[1])};
+          const u32x4 hi = u32x4{T::template fp8x2<false>(raw[2]), T::template fp8x2<true>(raw[2]),
+                                 T::template fp8x2<false>(raw[3]), T::template fp8x2<true>(raw[3])};
+          const int sw = t ? swz_v(r) : swz_k(r);
+          const uint32_t row = tile + r * DT::ROWB;
+          lds_store_b128(row + ((c0 ^ sw) << 4), lo);
+          lds_store_b128(row + (((c0 + 1) ^ sw) << 4), hi);
+        }
+      }
+    }
   };
 
   // ------------------------------------------------------- operand offsets
@@ -890,6 +934,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   // end (and a wave with no rows) are dropped by the range check, not skipped.
   auto store_out_plain = [&](const Item &it) {
     const bool odd = (g & 1) != 0;
+    const float vscale = FP8 ? ld_const(a.v_scale + it.kvh) : 1.f;  // fp8: V's scale (P V from the codes)
     const int wrow0 = it.row_begin + row_in_item;
     const int head = it.head0 + head_in_item;
     const uint8_t *obase = a.out + static_cast<int64_t>(it.q0) * a.o_rs + static_cast<int64_t>(head) * a.o_hs;
@@ -899,7 +944,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
     for (int qs = 0; qs < QS; ++qs) {
       const float l = sum32(sum16(lsum[qs]));  // the row sum of row m (lanes m, m + 16, m + 32, m + 48)
       const int row = wrow0 + 16 * qs + m;
-      const float inv = l > 0.f ? 1.0f / l : 0.f;
+      const float inv = (l > 0.f ? 1.0f / l : 0.f) * vscale;
       const uint32_t roff = row < it.Lq ? static_cast<uint32_t>(row * a.o_rs) : 0x7fffffffu;
 #pragma unroll
       for (int p = 0; p < PT::NJ / 2; ++p) {
@@ -924,6 +969,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
 
   auto store_out_gated = [&](const Item &it) {
     const bool odd = (g & 1) != 0;
+    const float vscale = FP8 ? ld_const(a.v_scale + it.kvh) : 1.f;  // fp8: V's scale (P V from the codes)
     const int wrow0 = it.row_begin + row_in_item;
     const int head = it.head0 + head_in_item;
     const uint8_t *obase = a.out + static_cast<int64_t>(it.q0) * a.o_rs + static_cast<int64_t>(head) * a.o_hs;
@@ -952,7 +998,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
           gv[p] = buffer_load16_nt(rg, static_cast<int>(goff));
         }
       }
-      const float inv = l > 0.f ? 1.0f / l : 0.f;
+      const float inv = (l > 0.f ? 1.0f / l : 0.f) * vscale;
       const uint32_t roff = row < it.Lq ? static_cast<uint32_t>(row * a.o_rs) : 0x7fffffffu;
 #pragma unroll
       for (int p = 0; p < PT::NJ / 2; ++p) {
@@ -1045,7 +1091,10 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         wait_vmcnt<2 * COPS * (kAhead - 1) + EOPS>();
       else
         wait_vmcnt<2 * COPS * (kAhead - 1)>();
+      widen(p0);
+      wait_lgkmcnt0();
       raw_barrier();
+      if constexpr (FP8) sl2 = a.scale_log2 * ld_const(a.k_scale + cur.kvh);
 
       const int Lq = cur.Lq, Lk = cur.Lk, P = cur.P, n_kt = cur.n_kt;
       const int wrow0 = cur.row_begin + row_in_item;
@@ -1103,6 +1152,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         kread(lds0 + (p0 % kSlots) * DT::SLOT_B, kf);
         qk(kf, sc);
       }
+      const int epi_tiles = epi_pos - p0 - 1;  // leading tiles whose wait adds the item's start operations
 
       // Scores of the tile whose P is being formed, and the subtrahend of its
       // exponents (the running maximum after the tile's rescale check).
@@ -1267,6 +1317,18 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs) pb[qs] = u32x4{pw[qs][0], pw[qs][1], pw[qs][2], pw[qs][3]};
         __builtin_amdgcn_sched_barrier(0);  // the two sections are scheduled apart
+        if constexpr (FP8) {
+          // Widen tile jt + 2 here, while the products run, rather than
+          // before the barrier that publishes it.  Its copies are complete
+          // once at most the entry issued above is younger (plus the item's
+          // start operations, if it preceded them).
+          if (jt + 1 < epi_tiles)
+            wait_vmcnt<2 * COPS + EOPS>();
+          else
+            wait_vmcnt<2 * COPS>();
+          widen(p0 + jt + 2);
+          __builtin_amdgcn_sched_barrier(0);
+        }
         f32x4 sn[QS][2];
         qk_v(kf, sn, slot, vf);
 #pragma unroll
@@ -1278,12 +1340,12 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
       // for this wave's copies of tile jt + 1 (younger: kAhead - 2 stream
       // entries, plus the Q loads and stores of the item's start if tile
       // jt + 1 preceded them).
-      const int epi_tiles = epi_pos - p0 - 1;  // leading tiles whose wait adds the item's start operations
       auto sync = [&](int jt) {
         if (jt < epi_tiles)
           wait_vmcnt<2 * COPS * (kAhead - 2) + EOPS>();
         else
           wait_vmcnt<2 * COPS * (kAhead - 2)>();
+        widen(p0 + jt + 1);
         wait_lgkmcnt0();  // and its reads of tiles jt - 1 and jt are done
         raw_barrier();    // tile jt + 1 complete; slot of tile jt - 1 free
       };
@@ -1372,10 +1434,10 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
 
 // The body lives in a device function: its inline assembly uses register
 // constraints that only the device compilation accepts.
-template <class T, int D, class S, bool GATED>
+template <class T, int D, class S, bool GATED, bool FP8>
 __global__ __launch_bounds__(64 * S::NW) __attribute__((amdgpu_waves_per_eu(S::WPE)))
 void varlen_prefill_dma_kernel(const PrefillArgs a) {
-  prefill_persistent<T, D, S, GATED>(a);
+  prefill_persistent<T, D, S, GATED, FP8>(a);
 }
 
 // Launch shape of the 16-bit kernel: C (two independent 4-wave workgroups
@@ -1389,7 +1451,7 @@ char prefill_shape() {
   return shape;
 }
 
-template <class T, int D, class S>
+template <class T, int D, class S, bool FP8>
 int launch_prefill_dma(PrefillArgs a, hipStream_t st) {
   const int rows_per_item = S::ITEM_ROWS / a.G4;
   a.n_qtiles = (a.max_seqlen_q + rows_per_item - 1) / rows_per_item;
@@ -1411,20 +1473,22 @@ int launch_prefill_dma(PrefillArgs a, hipStream_t st) {
   if (grid > total) grid = total;  // work_grid() is a multiple of 8 when pinned
   if constexpr (GATED_OK<S>) {
     if (a.gate) {
-      varlen_prefill_dma_kernel<T, D, S, true><<<static_cast<int>(grid), 64 * S::NW, S::LDS_BYTES, st>>>(a);
+      varlen_prefill_dma_kernel<T, D, S, true, FP8><<<static_cast<int>(grid), 64 * S::NW, S::LDS_BYTES, st>>>(a);
       return check_launch("varlen_prefill(gated)");
     }
   }
-  varlen_prefill_dma_kernel<T, D, S, false><<<static_cast<int>(grid), 64 * S::NW, S::LDS_BYTES, st>>>(a);
+  varlen_prefill_dma_kernel<T, D, S, false, FP8><<<static_cast<int>(grid), 64 * S::NW, S::LDS_BYTES, st>>>(a);
   return check_launch("varlen_prefill");
 }
 
 template <class T, bool FP8, int D>
 int launch_prefill(PrefillArgs a, hipStream_t s) {
-  if constexpr (!FP8 && D == 128) {
+  if constexpr (FP8 && D == 128) {
+    return launch_prefill_dma<T, D, ShapeC, true>(a, s);  // the copies assume 8 rows per wave
+  } else if constexpr (D == 128) {
     switch (prefill_shape()) {
-      case 'c': return launch_prefill_dma<T, D, ShapeC>(a, s);
-      default: return launch_prefill_dma<T, D, ShapeA>(a, s);
+      case 'c': return launch_prefill_dma<T, D, ShapeC, false>(a, s);
+      default: return launch_prefill_dma<T, D, ShapeA, false>(a, s);
     }
   } else {
     using PT = PTile<T, FP8, D>;
@@ -1514,7 +1578,7 @@ static int varlen_prefill_impl(const void *q, int64_t q_row_stride, int64_t q_he
   // The gate rides in the output store of the register-staged kernel (fp8
   // K/V, head_dim 256) and of the default persistent shape; the other
   // persistent shape gets the same arithmetic from one in-place pass.
-  const bool fused_gate = gate && (fp8 || head_dim == 256 || prefill_shape() == 'c');
+  const bool fused_gate = gate && (fp8 || head_dim == 256 || prefill_shape() == 'c');  // fp8 D=128: shape C
   if (gate) {
     if ((gate_row_stride * qsz) % 16 || (gate_head_stride * qsz) % 16 || !aligned(gate, 16))
       return fail(NQ_EINVAL, "varlen_prefill_gated: gate alignment");

@@ -151,14 +151,13 @@ class ModelRunner:
                 slot_mapping.extend(range(base + lo, base + hi))
         if cu_seqlens_k[-1] > cu_seqlens_q[-1]:    # prefix cache
             block_tables = self.prepare_block_tables(seqs)
-        total_k = cu_seqlens_k[-1]
         input_ids = self._to_device(input_ids, torch.int64)
         positions = self._to_device(positions, torch.int64)
         cu_seqlens_q = self._to_device(cu_seqlens_q, torch.int32)
         cu_seqlens_k = self._to_device(cu_seqlens_k, torch.int32)
         slot_mapping = self._to_device(slot_mapping, torch.int32)
         set_context(True, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, slot_mapping, None,
-                    block_tables, total_k=total_k)
+                    block_tables)
         return input_ids, positions
 
     def prepare_decode(self, seqs):

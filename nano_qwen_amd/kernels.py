@@ -28,7 +28,6 @@ from ._lib import check, dtype_code, lib, ptr, require_cuda, stream_of
 # hold its address, and replays must keep writing into valid memory.
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 _prefill_queues: dict[tuple[int, int], torch.Tensor] = {}
-_gather_ws: dict[tuple[int, int], torch.Tensor] = {}
 _retired: list[torch.Tensor] = []
 _DEBUG_QUEUE = os.environ.get("NQ_DEBUG_PREFILL_QUEUE", "0") not in ("", "0")
 
@@ -209,32 +208,8 @@ def output_gate(out, gate):
     return out
 
 
-def kv_gather_dequant(k_cache, v_cache, block_table, cu_seqlens_k, max_seqlen_k, k_scale, v_scale, dtype,
-                      total_k=None):
-    """Paged fp8 K/V -> packed 16-bit K/V ``[rows, Hkv, D]`` (rows
-    ``cu_seqlens_k[s] + j``), dequantized as ``rnd(code * scale)``; views of a
-    persistent, grow-only workspace of the stream.  ``rows`` is ``total_k``
-    (= ``cu_seqlens_k[-1]``, known to the host that built the metadata) when
-    given, else the bound ``num_seqs * max_seqlen_k``."""
-    nb, bs, hkv, d = k_cache.shape
-    n = cu_seqlens_k.numel() - 1
-    rows = int(total_k) if total_k is not None else n * int(max_seqlen_k)
-    need = 2 * rows * hkv * d
-    item = torch.empty((), dtype=dtype).element_size()
-    ws = _grow(_gather_ws, _key(k_cache.device), need * item, torch.uint8, k_cache.device)
-    ws = ws[:need * item].view(dtype)
-    kb = ws[:rows * hkv * d].view(rows, hkv, d)
-    vb = ws[rows * hkv * d:need].view(rows, hkv, d)
-    rc = lib().nq_kv_gather_dequant(ptr(k_cache), ptr(v_cache), ptr(block_table), block_table.stride(0),
-                                    block_table.shape[1], nb, ptr(cu_seqlens_k), n, int(max_seqlen_k), bs, hkv, d,
-                                    ptr(k_scale), ptr(v_scale), ptr(kb), ptr(vb), rows, dtype_code(dtype),
-                                    stream_of(k_cache))
-    check(rc, "kv_gather_dequant")
-    return kb, vb
-
-
 def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
-                   causal=True, block_table=None, k_scale=None, v_scale=None, out=None, gate=None, total_k=None):
+                   causal=True, block_table=None, k_scale=None, v_scale=None, out=None, gate=None):
     """Causal varlen attention; ``q [Tq, Hq, D]`` -> ``[Tq, Hq, D]``.
 
     Without ``block_table``: ``k, v [Tk, Hkv, D]`` packed by ``cu_seqlens_k``.
@@ -250,13 +225,6 @@ def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen
     if cu_seqlens_q.dtype != torch.int32 or cu_seqlens_k.dtype != torch.int32:
         raise RuntimeError("varlen_prefill: cu_seqlens must be int32")
     n = cu_seqlens_q.numel() - 1
-    if (k.dtype == torch.float8_e4m3fn and block_table is not None and q.shape[-1] == 128
-            and block_table.dtype == torch.int32 and block_table.stride(-1) == 1):
-        # fp8 cache at head_dim 128: dequantize the sequences' K/V into packed
-        # 16-bit rows and run the persistent 16-bit kernel on them.
-        k, v = kv_gather_dequant(k, v, block_table, cu_seqlens_k, max_seqlen_k, k_scale, v_scale, q.dtype,
-                                 total_k=total_k)
-        block_table = k_scale = v_scale = None
     if block_table is None:
         tk, hkv, d2 = k.shape
         if k.stride(-1) != 1 or k.stride(1) != d or k.stride(0) != v.stride(0) or v.stride(1) != d:

@@ -65,8 +65,7 @@ class Attention(nn.Module):
                                        context.max_seqlen_q, context.max_seqlen_k,
                                        softmax_scale=self.scale, causal=True,
                                        block_table=context.block_tables,
-                                       k_scale=k_scale, v_scale=v_scale, gate=gate,
-                                       total_k=context.total_k)
+                                       k_scale=k_scale, v_scale=v_scale, gate=gate)
         else:    # decode
             o = kernels.paged_decode(q.unsqueeze(1), k_cache, v_cache,
                                      cache_seqlens=context.context_lens,

@@ -3,10 +3,7 @@
 Field-for-field restatement of the reference's ``Context``
 (utils/context.py:5-28): the model runner fills it before each forward and
 ``Attention.forward`` reads it.  ``state_indices`` is carried for parity
-(the reference uses it only for its linear-attention layers).  One optional
-field is added at the end: ``total_k``, the host-known ``cu_seqlens_k[-1]``
-of a prefill (sizes the fp8 prefill's dequantized K/V without a device
-read); callers that do not set it get a bound instead.
+(the reference uses it only for its linear-attention layers).
 """
 from __future__ import annotations
 
@@ -26,7 +23,6 @@ class Context:
     context_lens: torch.Tensor | None = None
     block_tables: torch.Tensor | None = None
     state_indices: torch.Tensor | None = None
-    total_k: int | None = None
 
 
 _CONTEXT = Context()
@@ -37,10 +33,10 @@ def get_context() -> Context:
 
 
 def set_context(is_prefill, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=0, max_seqlen_k=0,
-                slot_mapping=None, context_lens=None, block_tables=None, state_indices=None, total_k=None):
+                slot_mapping=None, context_lens=None, block_tables=None, state_indices=None):
     global _CONTEXT
     _CONTEXT = Context(is_prefill, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
-                       slot_mapping, context_lens, block_tables, state_indices, total_k)
+                       slot_mapping, context_lens, block_tables, state_indices)
 
 
 def reset_context():

@@ -95,8 +95,8 @@ def test_output_gate_f16_and_errors(cuda):
 
 @pytest.mark.parametrize("kind", ["packed", "fp8"])
 def test_prefill_gated_other_paths(cuda, kind):
-    """Packed K/V (no block table) on the persistent kernel's fused store, and
-    fp8 K/V on the register-staged kernel's fused store: gated == gate(ungated)."""
+    """Packed K/V (no block table) and paged fp8 K/V on the persistent
+    kernel's fused store: gated == gate(ungated)."""
     from oracle.inputs import make_prefill_case
     if kind == "packed":
         c = make_prefill_case("cfg3", seed=8, device="cuda", prefix_blocks=(0, 0), lq=(100, 700))

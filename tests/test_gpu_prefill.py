@@ -119,6 +119,35 @@ def test_prefill_fp8_paged(cuda, dtype):
     check(case, range(4), TOL_FP8)
 
 
+def test_prefill_fp8_group_sizes(cuda):
+    """fp8 K/V on the persistent kernel at GQA groups 1, 2, 8 and 16: each
+    item takes the K and V scales of its own kv head."""
+    for G, hkv in ((1, 4), (2, 4), (8, 2), (16, 1)):
+        case = make_prefill_case("cfg3", seed=12, device=cuda, nseq=3, lq=(20, 300), prefix_blocks=(1, 1),
+                                 hq=G * hkv, hkv=hkv, kv="fp8")
+        check(case, range(3), TOL_FP8)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_fp8_packed(cuda, dtype):
+    """fp8 K/V packed by cu_seqlens_k (no block table), partial last tiles
+    included: against the float32 reference over the dequantized codes."""
+    from oracle import sdpa_path
+    from oracle.inputs import fp8_scales, quantize_fp8_torch
+    case = make_prefill_case("cfg3", seed=13, device=cuda, nseq=5, lq=(1, 500), prefix_blocks=(0, 0), dtype=dtype)
+    k, v = case["k_new"], case["v_new"]
+    ks, vs = fp8_scales(k) * 1.5, fp8_scales(v) * 0.75   # 0.75: the largest values saturate at 448
+    k8, v8 = quantize_fp8_torch(k, ks), quantize_fp8_torch(v, vs)
+    out = kernels.varlen_prefill(case["q"], k8, v8, case["cu_seqlens_q"], case["cu_seqlens_k"], case["max_seqlen_q"],
+                                 case["max_seqlen_k"], case["scale"], causal=True, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    kd = k8.float() * ks.view(1, -1, 1)
+    vd = v8.float() * vs.view(1, -1, 1)
+    ref = sdpa_path.varlen_prefill(case["q"].float(), kd, vd, case["cu_seqlens_q"], case["cu_seqlens_k"],
+                                   case["scale"])
+    assert_close(f64(out), f64(ref), **TOL_FP8, what="fp8 packed")
+
+
 def test_decode_equals_last_prefill_row(cuda):
     """Cross-kernel invariant: the decode output of a sequence equals the last
     row of the causal prefill over the same keys."""
@@ -215,29 +244,6 @@ def test_prefill_head_dim_256_gated(cuda):
     assert int(diff.max()) <= 1 and float((diff > 0).float().mean()) <= 1e-3
 
 
-def test_kv_gather_dequant_bit_exact(cuda):
-    """The fp8 -> packed 16-bit gather that feeds fp8 prefill: row cu_k[s] + j
-    is rnd(code * scale[h]) of cache row bt[s][j / bs] * bs + j % bs (fp32
-    product, nearest even), bit for bit."""
-    from oracle import fp8 as F
-    from oracle.qk_norm_rope import round_to
-    case = make_prefill_case("cfg3", seed=31, device=cuda, nseq=3, lq=(1, 300), prefix_blocks=(1, 2), kv="fp8")
-    kb, vb = kernels.kv_gather_dequant(case["k_cache"], case["v_cache"], case["block_tables"], case["cu_seqlens_k"],
-                                       case["max_seqlen_k"], case["k_scale"], case["v_scale"], torch.bfloat16)
-    torch.cuda.synchronize()
-    kc = case["k_cache"].view(torch.uint8).cpu().numpy()
-    ks = case["k_scale"].cpu().numpy()
-    bt = case["block_tables"].cpu().numpy()
-    cu = case["cu_seqlens_k"].cpu().numpy()
-    bs = kc.shape[1]
-    for s in range(3):
-        for j in range(0, int(cu[s + 1] - cu[s]), 37):
-            row = kc[bt[s, j // bs], j % bs]                      # [Hkv, D] codes
-            ref = round_to((F.decode_e4m3fn(row).astype(np.float32) * ks[:, None]).astype(np.float32), "bf16")
-            got = kb[int(cu[s]) + j].float().cpu().numpy()
-            assert np.array_equal(got, ref), (s, j)
-
-
 def test_prefill_two_streams_own_queues(cuda):
     """Launches on two streams at once use their own work-queue counters:
     both outputs equal the single-stream results, and both streams' counters
@@ -281,22 +287,3 @@ def test_prefill_queue_debug_check(cuda, monkeypatch):
     check(case, range(3), TOL_BF16)
 
 
-def test_fp8_gather_sized_by_total_keys(cuda):
-    """fp8 prefill with the host-known key count: the dequantized K/V take
-    total_k rows, not num_seqs * max_seqlen_k (one long sequence among many
-    short ones), and the result matches the bound-sized call bit for bit."""
-    case = make_prefill_case("cfg3", seed=43, device=cuda, nseq=12, lq=(5, 40), prefix_blocks=(1, 1), kv="fp8")
-    snapshot_prefill(case, [0, 1])
-    base = run_step(case).clone()
-    total_k = int(case["cu_seqlens_k"][-1])
-    assert total_k < case["nseq"] * case["max_seqlen_k"]
-    kernels._gather_ws.clear()
-    out = kernels.varlen_prefill(case["q"], case["k_cache"], case["v_cache"], case["cu_seqlens_q"],
-                                 case["cu_seqlens_k"], case["max_seqlen_q"], case["max_seqlen_k"], case["scale"],
-                                 block_table=case["block_tables"], k_scale=case["k_scale"], v_scale=case["v_scale"],
-                                 total_k=total_k)
-    torch.cuda.synchronize()
-    ws = kernels._gather_ws[kernels._key(cuda)]
-    hkv, d = case["k_cache"].shape[2:]
-    assert ws.numel() == max(2 * total_k * hkv * d * 2, 1 << 20)   # bytes
-    assert torch.equal(out, base)

@@ -78,7 +78,7 @@ def test_context_roundtrip():
     assert ctx.is_prefill and ctx.max_seqlen_k == 5 and ctx.context_lens is None
     assert [f for f in C.Context.__slots__] == ["is_prefill", "cu_seqlens_q", "cu_seqlens_k", "max_seqlen_q",
                                                "max_seqlen_k", "slot_mapping", "context_lens", "block_tables",
-                                               "state_indices", "total_k"]
+                                               "state_indices"]
     C.reset_context()
     assert C.get_context().cu_seqlens_q is None
 
@@ -128,7 +128,6 @@ def test_runner_prepare_prefill_on_cpu_matches_oracle():
     assert ctx.slot_mapping.tolist() == md["slot_mapping"]
     assert ctx.cu_seqlens_q.tolist() == md["cu_seqlens_q"] and ctx.cu_seqlens_k.tolist() == md["cu_seqlens_k"]
     assert (ctx.max_seqlen_q, ctx.max_seqlen_k) == (md["max_seqlen_q"], md["max_seqlen_k"])
-    assert ctx.total_k == md["cu_seqlens_k"][-1]
     want = md["block_tables"]
     assert (ctx.block_tables is None) == (want is None)
     if want is not None:
