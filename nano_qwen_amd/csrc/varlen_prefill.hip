@@ -9,16 +9,13 @@
 // block table (any prefix hit in the batch, engine/model_runner.py:275-276)
 // K/V are the whole paged cache (layers/attention.py:65-66).
 //
-// Two kernels share the tile layout and the softmax:
-//  * varlen_prefill_dma_kernel (16-bit K/V): persistent workgroups (G4 <= 4
-//    query heads of one kv head x row blocks), resident on every CU and
-//    pulling work items from per-XCD queues; K/V tiles of 32 keys are copied
-//    HBM -> LDS by the LDS DMA into a ring (no VGPRs), the QK products of
-//    tile j+1 overlap the softmax of tile j.
-//  * varlen_prefill_kernel (fp8 K/V): 4-wave workgroups, one per query tile,
-//    K/V staged through registers (global -> convert -> LDS) into a double
-//    buffer.
-// Common to both:
+// One kernel, varlen_prefill_dma_kernel, for 16-bit and fp8 K/V at head_dim
+// 128 and 256:
+//  * Persistent workgroups (G4 <= 4 query heads of one kv head x row
+//    blocks), resident on every CU and pulling work items from per-XCD
+//    queues; K/V tiles of 32 keys are copied HBM -> LDS by the LDS DMA into
+//    a ring (no VGPRs), the QK products of tile j+1 overlap the softmax of
+//    tile j.  fp8 codes are widened to 16 bits in the ring, in place.
 //  * GQA sharing in LDS: the waves of a workgroup are query heads of the SAME
 //    kv head, so every K/V tile staged in LDS serves all of them.
 //  * A tile never crosses a cache block (block_size % 32 == 0), so one buffer
@@ -39,10 +36,7 @@
 namespace nq {
 namespace {
 
-constexpr int kPWaves = 4;
-constexpr int kPThreads = 64 * kPWaves;
 constexpr int kKeys = 32;    // keys per LDS tile
-constexpr int kMaxBt = 4096;  // block-table entries staged in LDS (1M tokens at 256)
 constexpr float kRescale = 8.0f;  // log2 growth of a row max that forces a rescale
 constexpr int kMaxLevels = 1024;  // work-queue cost levels (key tiles per item, coarsened past it)
 constexpr int kMaxSeqs = 1024;    // sequences whose bounds the persistent kernel keeps in LDS
@@ -76,8 +70,6 @@ struct PrefillArgs {
   int64_t g_rs, g_hs;   // bytes
 };
 
-__device__ inline int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1) | (row & 8); }
-
 // Chunk swizzles of the 16-bit DMA kernel's LDS tiles (16-byte chunk c of
 // key row r is stored at chunk c ^ swz(r)), one per tile because the two
 // operand reads want different ones.  Measured with SQ_LDS_BANK_CONFLICT on
@@ -89,309 +81,15 @@ __device__ inline int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1) 
 __device__ inline int swz_k(int row) { return row & 15; }
 __device__ inline int swz_v(int row) { return ((row & 7) << 1) | ((row >> 3) & 1); }
 
-// Work item of a workgroup: query tile qt of kv-head slot y (kv head x quad)
-// of sequence s.
-struct Work {
-  int qt, y, s;
-};
-
-// Groups u = s * n_y + y -- the workgroups that read the same K/V -- are
-// pinned to XCD u % 8 (the hardware places workgroup L on XCD L % 8), so they
-// share that XCD's L2; y varies fastest in u, so every XCD gets a share of
-// every sequence and the XCDs stay balanced however the lengths vary.  Within
-// an XCD the workgroups run in query-tile order from the last tile (the most
-// keys) down, across all of the XCD's groups, so the longest work starts
-// first and the short tiles fill the tail.  Fewer than 8 groups: no pinning.
-__device__ inline bool map_work(int L, int n_x, int n_y, int num_seqs, Work &w) {
-  const int U = n_y * num_seqs;
-  int u;
-  if (U >= 8) {
-    const int x = L & 7, i = L >> 3;
-    const int cx = (U - x + 7) >> 3;
-    if (i >= cx * n_x) return false;
-    w.qt = n_x - 1 - i / cx;
-    u = x + 8 * (i % cx);
-  } else {
-    if (L >= U * n_x) return false;
-    w.qt = n_x - 1 - L / U;
-    u = L % U;
-  }
-  w.y = u % n_y;
-  w.s = u / n_y;
-  return true;
-}
-
-// Grid size for map_work.
+// Groups u = s * n_y + y (kv-head slot y of sequence s) -- the work items
+// that read the same K/V -- are pinned to XCD u % 8 (the hardware places
+// workgroup L on XCD L % 8), so they share that XCD's L2; y varies fastest in
+// u, so every XCD gets a share of every sequence and the XCDs stay balanced
+// however the lengths vary.  Fewer than 8 groups: no pinning.
+// Work items of the queues: n_x query tiles of each group, 8 equal queues
+// when pinned.
 inline int64_t work_grid(int64_t n_x, int64_t U) { return U >= 8 ? 8 * ((U + 7) / 8) * n_x : U * n_x; }
 
-template <class T, bool FP8, int D>
-struct PTile {
-  // swz() permutes chunks within aligned groups of 16 and rows are a multiple
-  // of 256 bytes apart, so the reads stay conflict-free at D = 256 too.
-  static_assert(D == 128 || D == 256, "head_dim 128 or 256");
-  static constexpr int ROWB = D * 2;            // LDS row: one key, 16-bit elements
-  static constexpr int TILE_B = kKeys * ROWB;   // one K (or V) tile
-  static constexpr int SRC_ROWB = FP8 ? D : D * 2;
-  static constexpr int SRC_CHUNKS = SRC_ROWB / 16;
-  static constexpr int LOADS = kKeys * SRC_CHUNKS / kPThreads;  // 16-byte loads per thread per tile
-  static constexpr int NKK = D / 32;
-  static constexpr int NJ = D / 16;
-  static constexpr int LDS_BYTES = 4 * TILE_B + kMaxBt * 4;  // K,V x 2 buffers + block table
-
-  // Issue the loads of key tile [kbase, kbase + 32) of kv head kvh; keys at or
-  // past key_end (or in a missing block) read as zeros.
-  __device__ static inline void load(const PrefillArgs &a, const int32_t *lds_bt, int k0, int kvh, int kbase,
-                                     int key_end, u32x4 (&kr)[LOADS], u32x4 (&vr)[LOADS]) {
-    int64_t row0;
-    if (a.block_tables == nullptr) {
-      row0 = static_cast<int64_t>(k0) + kbase;
-    } else {
-      const int blk = __builtin_amdgcn_readfirstlane(lds_bt[kbase / a.block_size]);
-      row0 = (blk >= 0 && blk < a.num_blocks) ? static_cast<int64_t>(blk) * a.block_size + kbase % a.block_size : -1;
-    }
-    const int nvalid = row0 >= 0 ? max(0, min(kKeys, key_end - kbase)) : 0;
-    const int64_t base_off = (row0 >= 0 ? row0 : 0) * a.kv_rs + static_cast<int64_t>(kvh) * SRC_ROWB;
-    const uint32_t nbytes = nvalid > 0 ? static_cast<uint32_t>((nvalid - 1) * a.kv_rs + SRC_ROWB) : 0u;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k + base_off, nbytes);
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v + base_off, nbytes);
-#pragma unroll
-    for (int c = 0; c < LOADS; ++c) {
-      const int idx = threadIdx.x + c * kPThreads;
-      const int row = idx / SRC_CHUNKS, ch = idx % SRC_CHUNKS;
-      const int off = static_cast<int>(row * a.kv_rs) + ch * 16;
-      kr[c] = buffer_load16_nt(rk, off);
-      vr[c] = buffer_load16_nt(rv, off);
-    }
-  }
-
-  // Write a loaded tile into LDS (row = key, 16-bit elements, swizzled chunks).
-  __device__ static inline void stage(uint8_t *kt, uint8_t *vt, const u32x4 (&kr)[LOADS],
-                                      const u32x4 (&vr)[LOADS]) {
-#pragma unroll
-    for (int c = 0; c < LOADS; ++c) {
-      const int idx = threadIdx.x + c * kPThreads;
-      const int row = idx / SRC_CHUNKS, ch = idx % SRC_CHUNKS;
-      uint8_t *kp = kt + row * ROWB, *vp = vt + row * ROWB;
-      if constexpr (!FP8) {
-        *reinterpret_cast<u32x4 *>(kp + ((ch ^ swz(row)) << 4)) = kr[c];
-        *reinterpret_cast<u32x4 *>(vp + ((ch ^ swz(row)) << 4)) = vr[c];
-      } else {
-        const u32x4 &k = kr[c], &v = vr[c];
-        *reinterpret_cast<u32x4 *>(kp + (((2 * ch) ^ swz(row)) << 4)) =
-            u32x4{T::template fp8x2<false>(k[0]), T::template fp8x2<true>(k[0]), T::template fp8x2<false>(k[1]),
-                  T::template fp8x2<true>(k[1])};
-        *reinterpret_cast<u32x4 *>(kp + (((2 * ch + 1) ^ swz(row)) << 4)) =
-            u32x4{T::template fp8x2<false>(k[2]), T::template fp8x2<true>(k[2]), T::template fp8x2<false>(k[3]),
-                  T::template fp8x2<true>(k[3])};
-        *reinterpret_cast<u32x4 *>(vp + (((2 * ch) ^ swz(row)) << 4)) =
-            u32x4{T::template fp8x2<false>(v[0]), T::template fp8x2<true>(v[0]), T::template fp8x2<false>(v[1]),
-                  T::template fp8x2<true>(v[1])};
-        *reinterpret_cast<u32x4 *>(vp + (((2 * ch + 1) ^ swz(row)) << 4)) =
-            u32x4{T::template fp8x2<false>(v[2]), T::template fp8x2<true>(v[2]), T::template fp8x2<false>(v[3]),
-                  T::template fp8x2<true>(v[3])};
-      }
-    }
-  }
-
-  // K operand: lane (m, g) = key row 16*ks + m, dims 8(g + 4kk) .. +8.
-  __device__ static inline u32x4 kfrag(const uint8_t *kt, int ks, int kk, int m, int g) {
-    const int row = 16 * ks + m;
-    return *reinterpret_cast<const u32x4 *>(kt + row * ROWB + (((g + 4 * kk) ^ swz(row)) << 4));
-  }
-
-  // V^T operand of output block j over the tile's 32 keys: lane (m, g) takes
-  // V[psi(g, i)][16j + m], psi(g, i) = 4g + i (i < 4) or 16 + 4g + i - 4.
-  __device__ static inline u32x4 vfrag(const uint8_t *vt, int j, int lane) {
-    const int g = lane >> 4, k = (lane >> 2) & 3, q = lane & 3;
-    const int r0 = 4 * g + k, r1 = r0 + 16;
-    const int lc = 2 * j + (q >> 1), sub = (q & 1) * 8;
-    const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t *>(vt + r0 * ROWB + ((lc ^ swz(r0)) << 4) + sub));
-    const u32x2 hi = lds_read_tr16(reinterpret_cast<const uint16_t *>(vt + r1 * ROWB + ((lc ^ swz(r1)) << 4) + sub));
-    return u32x4{lo[0], lo[1], hi[0], hi[1]};
-  }
-};
-
-// Query rows per wave of the register-staged kernel: 32 at D = 128; 16 at
-// D = 256, where the accumulators and Q operands of each row double, so that
-// two waves per SIMD still fit.
-template <int D>
-constexpr int kRegQS = D == 256 ? 1 : 2;
-
-template <class T, bool FP8, int D>
-__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2)))
-void varlen_prefill_kernel(const PrefillArgs a) {
-  constexpr int QS = kRegQS<D>;       // 16-row sub-tiles per wave
-  constexpr int RW = 16 * QS;         // query rows per wave
-  using PT = PTile<T, FP8, D>;
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  int32_t *lds_bt = reinterpret_cast<int32_t *>(smem + 4 * PT::TILE_B);
-
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int m = lane & 15, g = lane >> 4;
-
-  Work w;
-  if (!map_work(blockIdx.x, a.n_qtiles, a.Hkv * a.quads, a.num_seqs, w)) return;
-  const int qt = w.qt, y = w.y, s = w.s;
-  const int kvh = y / a.quads, quad = y % a.quads;
-  const int rb = 4 / a.G4;  // row blocks of 32 per workgroup
-  const int head = kvh * a.G + quad * 4 + (wave % a.G4);
-  const int q0 = a.cu_q[s], Lq = a.cu_q[s + 1] - q0;
-  const int row_begin = qt * RW * rb;
-  if (row_begin >= Lq) return;
-  const int k0 = a.cu_k[s], Lk = a.cu_k[s + 1] - k0;
-  const int P = Lk - Lq;
-  const int row_last = min(row_begin + RW * rb, Lq) - 1;
-  const int key_end = a.causal ? max(0, min(Lk, row_last + P + 1)) : Lk;
-  const int n_kt = (key_end + kKeys - 1) / kKeys;
-
-  const float kscale = FP8 ? a.k_scale[kvh] : 1.0f;
-  const float vscale = FP8 ? a.v_scale[kvh] : 1.0f;
-  const float sl2 = a.scale_log2 * kscale;
-
-  // stage the sequence's block-table entries once
-  if (a.block_tables != nullptr) {
-    const int n_bt = min(min((key_end + a.block_size - 1) / a.block_size, a.max_blocks), kMaxBt);
-    for (int i = threadIdx.x; i < n_bt; i += kPThreads) lds_bt[i] = a.block_tables[s * a.bt_stride + i];
-  }
-
-  // This wave's rows: wrow0 .. wrow0 + RW - 1 (QS 16-row sub-tiles).
-  const int wrow0 = row_begin + RW * (wave / a.G4);
-  const bool wave_live = wrow0 < Lq;
-  const int wrow_last = min(wrow0 + RW - 1, Lq - 1);
-  const int wave_key_end = a.causal ? min(Lk, wrow_last + P + 1) : Lk;
-
-  u32x4 qf[QS][PT::NKK];
-#pragma unroll
-  for (int qs = 0; qs < QS; ++qs) {
-    const int r = wrow0 + 16 * qs + m;
-    const bool ok = r < Lq;
-    const uint8_t *qp = a.q + static_cast<int64_t>(q0 + (ok ? r : 0)) * a.q_rs + static_cast<int64_t>(head) * a.q_hs;
-#pragma unroll
-    for (int kk = 0; kk < PT::NKK; ++kk) qf[qs][kk] = ok ? load16(qp + (8 * g + 32 * kk) * 2) : u32x4{0, 0, 0, 0};
-  }
-
-  float m_use[QS], l_run[QS];
-  f32x4 o[QS][PT::NJ];
-#pragma unroll
-  for (int qs = 0; qs < QS; ++qs) {
-    m_use[qs] = kNegInf;
-    l_run[qs] = 0.f;
-  }
-#pragma unroll
-  for (int qs = 0; qs < QS; ++qs)
-#pragma unroll
-    for (int j = 0; j < PT::NJ; ++j) o[qs][j] = f32x4{0, 0, 0, 0};
-
-  __syncthreads();  // block table visible
-  u32x4 kr[PT::LOADS], vr[PT::LOADS];
-  if (n_kt > 0) {
-    PT::load(a, lds_bt, k0, kvh, 0, key_end, kr, vr);
-    PT::stage(smem, smem + PT::TILE_B, kr, vr);
-  }
-  __syncthreads();
-
-  for (int jt = 0; jt < n_kt; ++jt) {
-    const int kbase = jt * kKeys;
-    const uint8_t *kt = smem + (jt & 1) * 2 * PT::TILE_B;
-    const uint8_t *vt = kt + PT::TILE_B;
-    const bool more = jt + 1 < n_kt;
-    if (more) PT::load(a, lds_bt, k0, kvh, kbase + kKeys, key_end, kr, vr);
-    if (wave_live && kbase < wave_key_end) {
-      f32x4 sc[QS][2];
-#pragma unroll
-      for (int qs = 0; qs < QS; ++qs)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = f32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int kk = 0; kk < PT::NKK; ++kk) {
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const u32x4 kf = PT::kfrag(kt, ks, kk, m, g);
-#pragma unroll
-          for (int qs = 0; qs < QS; ++qs) sc[qs][ks] = T::mfma16x16x32(kf, qf[qs][kk], sc[qs][ks]);
-        }
-      }
-      // mask only where the tile crosses the causal diagonal or the key end
-      const bool need_mask = kbase + kKeys - 1 > wrow0 + P || kbase + kKeys > Lk;
-      u32x4 pb[QS];
-#pragma unroll
-      for (int qs = 0; qs < QS; ++qs) {
-        const int row = wrow0 + 16 * qs + m;
-        const int lim = a.causal ? min(Lk - 1, row + P) : Lk - 1;  // last visible key
-        float x[8];
-        float mloc = kNegInf;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const int j = kbase + 16 * ks + 4 * g + rr;
-            float v = sc[qs][ks][rr] * sl2;
-            if (need_mask && j > lim) v = kNegInf;
-            x[4 * ks + rr] = v;
-            mloc = fmaxf(mloc, v);
-          }
-        mloc = max32(max16(mloc));
-        // lazy rescale: only when some row of the wave grew by > 2^kRescale
-        if (__builtin_amdgcn_ballot_w64(mloc > m_use[qs] + kRescale) != 0) {
-          const float m_new = fmaxf(m_use[qs], mloc);
-          const float alpha = (m_use[qs] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(m_use[qs] - m_new);
-          l_run[qs] *= alpha;
-#pragma unroll
-          for (int j = 0; j < PT::NJ; ++j) o[qs][j] *= alpha;
-          m_use[qs] = m_new;
-        }
-        const float mref = (m_use[qs] == kNegInf) ? 0.f : m_use[qs];
-        float psum = 0.f;
-        uint32_t pw[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float p0 = __builtin_amdgcn_exp2f(x[2 * t] - mref);
-          const float p1 = __builtin_amdgcn_exp2f(x[2 * t + 1] - mref);
-          psum += p0 + p1;
-          pw[t] = T::pack2(p0, p1);
-        }
-        l_run[qs] += psum;
-        pb[qs] = u32x4{pw[0], pw[1], pw[2], pw[3]};
-      }
-#pragma unroll
-      for (int j = 0; j < PT::NJ; ++j) {
-        const u32x4 vf = PT::vfrag(vt, j, lane);
-#pragma unroll
-        for (int qs = 0; qs < QS; ++qs) o[qs][j] = T::mfma16x16x32(vf, pb[qs], o[qs][j]);
-      }
-    }
-    if (more) {
-      uint8_t *nk = smem + ((jt + 1) & 1) * 2 * PT::TILE_B;
-      PT::stage(nk, nk + PT::TILE_B, kr, vr);
-    }
-    __syncthreads();
-  }
-
-  if (!wave_live) return;
-#pragma unroll
-  for (int qs = 0; qs < QS; ++qs) {
-    const float l = sum32(sum16(l_run[qs]));
-    const int row = wrow0 + 16 * qs + m;
-    if (row >= Lq) continue;
-    const float inv = l > 0.f ? vscale / l : 0.f;
-    uint8_t *op = a.out + static_cast<int64_t>(q0 + row) * a.o_rs + static_cast<int64_t>(head) * a.o_hs;
-    if (a.gate) {  // Qwen3.5's output gate (models/qwen3_5.py:140-142) in the store
-      const uint8_t *gp = a.gate + static_cast<int64_t>(q0 + row) * a.g_rs + static_cast<int64_t>(head) * a.g_hs;
-#pragma unroll
-      for (int j = 0; j < PT::NJ; ++j)
-        *reinterpret_cast<u32x2 *>(op + (16 * j + 4 * g) * 2) =
-            gate4<T>(o[qs][j] * inv, *reinterpret_cast<const u32x2 *>(gp + (16 * j + 4 * g) * 2));
-    } else {
-#pragma unroll
-      for (int j = 0; j < PT::NJ; ++j) {
-        const f32x4 v = o[qs][j] * inv;
-        *reinterpret_cast<u32x2 *>(op + (16 * j + 4 * g) * 2) = u32x2{T::pack2(v[0], v[1]), T::pack2(v[2], v[3])};
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
 // 16-bit K/V: persistent workgroups fed by an LDS DMA ring.
 //
 // K/V tiles of 32 keys go HBM/L2 -> LDS directly (buffer loads to LDS, no
@@ -410,9 +108,11 @@ void varlen_prefill_kernel(const PrefillArgs a) {
 // so one's stalls overlap the other's work.
 template <class T, int D>
 struct DTile {
-  static_assert(D == 128, "tile layout assumes head_dim 128");
+  static_assert(D == 128 || D == 256, "head_dim 128 or 256");
+  static constexpr int NKK = D / 32;  // 32-dim slices of a QK product
+  static constexpr int NJ = D / 16;   // 16-dim blocks of O
   static constexpr int ROWB = D * 2;
-  static constexpr int TILE_B = kKeys * ROWB;   // 8 KiB per K (or V) tile
+  static constexpr int TILE_B = kKeys * ROWB;   // 8 (16) KiB per K (or V) tile at head_dim 128 (256)
   static constexpr int SLOT_B = 2 * TILE_B;     // K + V
 };
 
@@ -420,12 +120,12 @@ struct DTile {
 // query rows of one head; WPE waves per SIMD (so WPE * 4 / NW resident
 // workgroups per CU); a ring of SLOTS K/V tiles, copies SLOTS - 1 ahead.
 // Two waves per SIMD: a wave owns at most 256 VGPRs.
-template <int NW_, int QS_, int WPE_, int SLOTS_>
+template <int NW_, int QS_, int WPE_, int SLOTS_, int D_ = 128>
 struct PShape {
-  static constexpr int NW = NW_, QS = QS_, WPE = WPE_, SLOTS = SLOTS_, AHEAD = SLOTS_ - 1;
+  static constexpr int NW = NW_, QS = QS_, WPE = WPE_, SLOTS = SLOTS_, AHEAD = SLOTS_ - 1, D = D_;
   static constexpr int WG_PER_CU = WPE * 4 / NW;
   static constexpr int ITEM_ROWS = 16 * QS * NW;  // query rows x heads of one work item
-  static constexpr int RING_BYTES = SLOTS * 2 * kKeys * 256;
+  static constexpr int RING_BYTES = SLOTS * 2 * kKeys * 2 * D;
   // ring, queue item slots (4 words), queue size (4 words), cost-level
   // starts, sequence bounds (cu_q, cu_k)
   static constexpr int LDS_BYTES = RING_BYTES + 32 + 4 * kMaxLevels + 8 * (kMaxSeqs + 1);
@@ -434,9 +134,12 @@ struct PShape {
 };
 using ShapeA = PShape<8, 2, 2, 5>;  // one workgroup per CU, two 32-row waves per SIMD
 using ShapeC = PShape<4, 2, 2, 4>;  // two independent workgroups per CU, 32-row waves
-// Launch shapes built with the output gate in their store (the default one).
+// head_dim 256: one workgroup per CU, two 16-row waves per SIMD (a 32 KiB
+// ring slot; the 16-row wave keeps O, Q and a tile's operands in 256 VGPRs)
+using ShapeD = PShape<8, 1, 2, 4, 256>;
+// Launch shapes built with the output gate in their store (the default ones).
 template <class S>
-constexpr bool GATED_OK = std::is_same<S, ShapeC>::value;
+constexpr bool GATED_OK = std::is_same<S, ShapeC>::value || std::is_same<S, ShapeD>::value;
 
 // A work item of the persistent kernel: query tile qt (S::ITEM_ROWS/G4 rows
 // of G4 heads) of kv-head slot y of sequence s, described by wave-uniform
@@ -609,7 +312,7 @@ __device__ __forceinline__ Item describe_by_cost(const PrefillArgs &a, const Cos
 // busy when one-per-CU workgroups of very different lengths are launched as
 // a plain grid; a queue keeps every CU fed until the work runs out.
 //
-// Queue: items are grouped as in map_work -- XCD x (workgroups L with
+// Queue: items are grouped as described above work_grid -- XCD x (workgroups L with
 // L % 8 == x) owns the groups u = x, x + 8, ... and serves them from its own
 // counter queue[x], in query-tile order from the last tile down (longest
 // first).  Thread 0 fetches two items ahead; indices reach the other waves
@@ -641,19 +344,21 @@ __device__ __forceinline__ Item describe_by_cost(const PrefillArgs &a, const Cos
 template <class T, int D, class S, bool GATED, bool FP8>
 __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   using DT = DTile<T, D>;
-  using PT = PTile<T, false, D>;
   constexpr int NW = S::NW, QS = S::QS, kSlots = S::SLOTS, kAhead = S::AHEAD;
   constexpr int RW = 16 * QS;        // query rows per wave
   constexpr int CR = kKeys / NW;     // tile rows each wave copies
   constexpr int SRC_ROWB = FP8 ? D : 2 * D;  // bytes of one key of one kv head in the cache
   constexpr int COPS = CR * SRC_ROWB / 1024;  // 1 KiB loads per K (or V) per wave and entry
+  constexpr int LPR = SRC_ROWB / 16;          // lanes per row in a copy (16 bytes each)
   // fp8: a wave's copies land in the upper half of its own rows of the slot
   // (CR rows of 16-bit keys), which it widens in place before the barrier
   // that publishes the tile.
-  static_assert(!FP8 || (CR == 8 && COPS == 1), "fp8 copies: 8 rows of 128 bytes per wave");
+  static_assert(S::D == D, "launch shape built for this head_dim");
+  static_assert(COPS >= 1 && CR * SRC_ROWB == 1024 * COPS, "a wave copies whole 1 KiB pieces");
+  static_assert(!FP8 || COPS == 1, "fp8: one 1 KiB copy of codes per K (or V) per wave");
   static_assert(!FP8 || kSlots == 4, "fp8: ring slot of a stream entry by mask");
-  constexpr int QOPS = QS * PT::NKK;        // Q loads per wave and item
-  constexpr int SOPS = QS * (PT::NJ / 2);   // output stores per wave and item
+  constexpr int QOPS = QS * DT::NKK;        // Q loads per wave and item
+  constexpr int SOPS = QS * (DT::NJ / 2);   // output stores per wave and item
   // Stores that write nothing, after the Q loads: the compiler counts them
   // (it does not see the K/V copies), so one wait for at most kPad
   // operations shows it -- as it holds on the hardware, where at least these
@@ -764,13 +469,13 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
 #pragma unroll
   for (int c = 0; c < COPS; ++c) {
     if constexpr (FP8) {
-      const int drow = CR * wave + (lane >> 3);
-      src_k[c] = src_v[c] = static_cast<uint32_t>(drow * kv_rs + ((lane & 7) << 4));
+      const int drow = CR * wave + lane / LPR;
+      src_k[c] = src_v[c] = static_cast<uint32_t>(drow * kv_rs + ((lane % LPR) << 4));
     } else {
-      const int drow = CR * wave + 4 * c + (lane >> 4);
+      const int drow = CR * wave + (64 / LPR) * c + lane / LPR;
       const uint32_t row_off = static_cast<uint32_t>(drow * kv_rs);
-      src_k[c] = row_off + (((lane & 15) ^ swz_k(drow)) << 4);
-      src_v[c] = row_off + (((lane & 15) ^ swz_v(drow)) << 4);
+      src_k[c] = row_off + (((lane % LPR) ^ swz_k(drow)) << 4);
+      src_v[c] = row_off + (((lane % LPR) ^ swz_v(drow)) << 4);
     }
   }
   // Block-table entry bidx of a sequence's row (paged only).
@@ -849,7 +554,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   };
   // fp8: widens this wave's rows of stream entries cv_pos .. upto (whose
   // copies are complete) to 16 bits, in place.  Lane l holds codes of dims
-  // 16(l & 7) .. +15 of row CR * wave + (l >> 3): the wave reads all its
+  // 16(l % LPR) .. +15 of row CR * wave + l / LPR: the wave reads all its
   // codes (the upper half of its rows) before it writes any row, and no
   // other wave touches these rows before the next barrier.  The widening
   // is exact (every e4m3 value is a bf16 and an f16 value); the scales are
@@ -858,7 +563,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   auto widen = [&](int upto) {
     if constexpr (FP8) {
       asm volatile("" ::: "memory");  // after the wait for the copies
-      const int r = CR * wave + (lane >> 3), c0 = 2 * (lane & 7);
+      const int r = CR * wave + lane / LPR, c0 = 2 * (lane % LPR);
       for (; cv_pos <= upto; ++cv_pos) {
         const uint32_t slot = lds0 + (cv_pos & (kSlots - 1)) * DT::SLOT_B;
 #pragma unroll
@@ -904,7 +609,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   // queue) loads an existing row instead; its scores and output are computed
   // but never stored, and nothing selects on the loaded values, which would
   // make the compiler wait for them -- and for every K/V copy in flight.
-  u32x4 qf[QS][PT::NKK];
+  u32x4 qf[QS][DT::NKK];
   auto load_q = [&](const Item &it) {
     const int head = it.live ? it.head0 + head_in_item : 0;
 #pragma unroll
@@ -913,17 +618,17 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
       const int row = (it.live && r < it.Lq) ? it.q0 + r : it.q0;
       const uint8_t *qp = a.q + static_cast<int64_t>(row) * a.q_rs + static_cast<int64_t>(head) * a.q_hs;
 #pragma unroll
-      for (int kk = 0; kk < PT::NKK; ++kk) qf[qs][kk] = load16(qp + (8 * g + 32 * kk) * 2);
+      for (int kk = 0; kk < DT::NKK; ++kk) qf[qs][kk] = load16(qp + (8 * g + 32 * kk) * 2);
     }
   };
 
-  f32x4 o[QS][PT::NJ];  // O^T accumulators of the item computed last
+  f32x4 o[QS][DT::NJ];  // O^T accumulators of the item computed last
   float lsum[QS];       // its row sums of P: this lane's keys (the four lanes of a row add up at the store)
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) {
     lsum[qs] = 0.f;
 #pragma unroll
-    for (int j = 0; j < PT::NJ; ++j) o[qs][j] = f32x4{0, 0, 0, 0};
+    for (int j = 0; j < DT::NJ; ++j) o[qs][j] = f32x4{0, 0, 0, 0};
   }
   // Output of an item: SOPS stores per wave.  Lane (g, m) holds dims
   // 16j + 4g .. +3 of row m for every j.  The lanes of lane groups g and g^1
@@ -947,7 +652,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
       const float inv = (l > 0.f ? 1.0f / l : 0.f) * vscale;
       const uint32_t roff = row < it.Lq ? static_cast<uint32_t>(row * a.o_rs) : 0x7fffffffu;
 #pragma unroll
-      for (int p = 0; p < PT::NJ / 2; ++p) {
+      for (int p = 0; p < DT::NJ / 2; ++p) {
         const f32x4 v0 = o[qs][2 * p] * inv, v1 = o[qs][2 * p + 1] * inv;
         const uint32_t c00 = T::pack2(v0[0], v0[1]), c01 = T::pack2(v0[2], v0[3]);
         const uint32_t c10 = T::pack2(v1[0], v1[1]), c11 = T::pack2(v1[2], v1[3]);
@@ -989,11 +694,11 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
     for (int qs = 0; qs < QS; ++qs) {
       const float l = sum32(sum16(lsum[qs]));  // the row sum of row m (lanes m, m + 16, m + 32, m + 48)
       const int row = wrow0 + 16 * qs + m;
-      u32x4 gv[PT::NJ / 2];
+      u32x4 gv[DT::NJ / 2];
       if constexpr (GATED) {
         const auto rg = make_rsrc(gbase, grange);
 #pragma unroll
-        for (int p = 0; p < PT::NJ / 2; ++p) {
+        for (int p = 0; p < DT::NJ / 2; ++p) {
           const uint32_t goff = row < it.Lq ? static_cast<uint32_t>(row * a.g_rs + dim0_of(p) * 2) : 0x7fffffffu;
           gv[p] = buffer_load16_nt(rg, static_cast<int>(goff));
         }
@@ -1001,7 +706,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
       const float inv = (l > 0.f ? 1.0f / l : 0.f) * vscale;
       const uint32_t roff = row < it.Lq ? static_cast<uint32_t>(row * a.o_rs) : 0x7fffffffu;
 #pragma unroll
-      for (int p = 0; p < PT::NJ / 2; ++p) {
+      for (int p = 0; p < DT::NJ / 2; ++p) {
         const f32x4 v0 = o[qs][2 * p] * inv, v1 = o[qs][2 * p + 1] * inv;
         const uint32_t c00 = T::pack2(v0[0], v0[1]), c01 = T::pack2(v0[2], v0[3]);
         const uint32_t c10 = T::pack2(v1[0], v1[1]), c11 = T::pack2(v1[2], v1[3]);
@@ -1109,21 +814,21 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
       const int32_t *bt_row = paged ? a.block_tables + static_cast<int64_t>(cur.s) * a.bt_stride : nullptr;
 
       // K^T operands of the tile in ring slot `kt` (its LDS address).
-      auto kread = [&](uint32_t kt, u32x4 (&kf)[PT::NKK][2]) {
+      auto kread = [&](uint32_t kt, u32x4 (&kf)[DT::NKK][2]) {
 #pragma unroll
-        for (int kk = 0; kk < PT::NKK; ++kk) {
+        for (int kk = 0; kk < DT::NKK; ++kk) {
           const uint32_t ka = ((kk << 6) ^ kx_l) + (kt + kbase_l);
           kf[kk][0] = lds_load_b128<0>(ka);
           kf[kk][1] = lds_load_b128<16 * DT::ROWB>(ka);
         }
       };
-      auto qk = [&](const u32x4 (&kf)[PT::NKK][2], f32x4 (&sc)[QS][2]) {
+      auto qk = [&](const u32x4 (&kf)[DT::NKK][2], f32x4 (&sc)[QS][2]) {
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) sc[qs][ks] = f32x4{0, 0, 0, 0};
 #pragma unroll
-        for (int kk = 0; kk < PT::NKK; ++kk)
+        for (int kk = 0; kk < DT::NKK; ++kk)
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -1136,7 +841,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         m_use[qs] = kNegInf;
         lsum[qs] = 0.f;
 #pragma unroll
-        for (int j = 0; j < PT::NJ; ++j) o[qs][j] = f32x4{0, 0, 0, 0};
+        for (int j = 0; j < DT::NJ; ++j) o[qs][j] = f32x4{0, 0, 0, 0};
       }
       // Q is complete from here on: at most kPad operations are younger than
       // the Q loads' padding, which follows them.
@@ -1144,10 +849,10 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
 #pragma unroll
       for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
-        for (int kk = 0; kk < PT::NKK; ++kk) asm volatile("" : "+v"(qf[qs][kk]));
+        for (int kk = 0; kk < DT::NKK; ++kk) asm volatile("" : "+v"(qf[qs][kk]));
       f32x4 sc[QS][2];  // scores of the tile whose P is formed next
       if (wave_nkt > 0) {
-        u32x4 kf[PT::NKK][2];
+        u32x4 kf[DT::NKK][2];
         unhoist();
         kread(lds0 + (p0 % kSlots) * DT::SLOT_B, kf);
         qk(kf, sc);
@@ -1224,7 +929,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
-          for (int j = 0; j < PT::NJ; ++j) o[qs][j] *= alpha[qs];
+          for (int j = 0; j < DT::NJ; ++j) o[qs][j] *= alpha[qs];
       };
       // V^T operand j of the tile in ring slot `slot`: rows r0 and r0 + 16.
       auto vread = [&](uint32_t slot, int j) {
@@ -1237,46 +942,56 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
       // unit, two exponentials and a pack, per two products -- so that the
       // exponentials run while the matrix core works.  The K reads of tile
       // jt + 1 (ring slot slot_next) are issued halfway.
-      auto pv_p = [&](const u32x4 (&vf)[PT::NJ], const u32x4 (&pb)[QS], uint32_t (&pw)[QS][4], uint32_t slot_next,
-                      u32x4 (&kf)[PT::NKK][2]) {
-        static_assert(PT::NJ * QS == 16, "two products per unit of P");
+      auto pv_p = [&](const u32x4 (&vf)[DT::NJ], const u32x4 (&pb)[QS], uint32_t (&pw)[QS][4], uint32_t slot_next,
+                      u32x4 (&kf)[DT::NKK][2]) {
+        // 16 products either way: 8 query rows x 2 ... -- PPU products per unit
+        // of P (2 with two 16-row blocks at head_dim 128, 4 with one at 256)
+        constexpr int NP = DT::NJ * QS, U = 4 * QS, PPU = NP / U;
+        static_assert(NP == 16 && (PPU == 2 || PPU == 4), "16 products, 2 or 4 per unit of P");
         kread(slot_next, kf);
 #pragma unroll
-        for (int i = 0; i < PT::NJ * QS; ++i) {
+        for (int i = 0; i < NP; ++i) {
           const int j = i / QS, qs = i % QS;
           o[qs][j] = T::mfma16x16x32(vf[j], pb[qs], o[qs][j]);
-          if (i % 2 == 1) {
-            const int u = i / 2;
+          if (i % PPU == PPU - 1) {
+            const int u = i / PPU;
             pw[u / 4][u % 4] = p_unit(u / 4, u % 4);
           }
         }
 #pragma unroll
-        for (int u = 0; u < 4 * QS; ++u) {
+        for (int u = 0; u < U; ++u) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
           __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
           __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);  // transcendental
+          if (PPU == 4) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
           __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
-          if (u == 2 * QS - 1) __builtin_amdgcn_sched_group_barrier(0x100, 2 * PT::NKK, 0);  // DS read (K)
+          if (PPU == 4) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          if (u == U / 2 - 1) __builtin_amdgcn_sched_group_barrier(0x100, 2 * DT::NKK, 0);  // DS read (K)
         }
       };
       auto p_only = [&](uint32_t (&pw)[QS][4]) {
 #pragma unroll
         for (int u = 0; u < 4 * QS; ++u) pw[u / 4][u % 4] = p_unit(u / 4, u % 4);
       };
-      auto pv_only = [&](const u32x4 (&vf)[PT::NJ], const u32x4 (&pb)[QS]) {
+      auto pv_only = [&](const u32x4 (&vf)[DT::NJ], const u32x4 (&pb)[QS]) {
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
-          for (int j = 0; j < PT::NJ; ++j) o[qs][j] = T::mfma16x16x32(vf[j], pb[qs], o[qs][j]);
+          for (int j = 0; j < DT::NJ; ++j) o[qs][j] = T::mfma16x16x32(vf[j], pb[qs], o[qs][j]);
       };
       // QK products of tile jt + 1 (kf) into sn, with the V^T operands of
       // tile jt (ring slot `slot`) read into vf in between: one transposing
       // read per product.  Products that share an accumulator are 2 QS
       // apart.
-      auto qk_v = [&](const u32x4 (&kf)[PT::NKK][2], f32x4 (&sn)[QS][2], uint32_t slot, u32x4 (&vf)[PT::NJ]) {
-        constexpr int NP = PT::NKK * 2 * QS;  // products
-        static_assert(NP == 2 * PT::NJ, "one V operand per two products");
+      auto qk_v = [&](const u32x4 (&kf)[DT::NKK][2], f32x4 (&sn)[QS][2], uint32_t slot, u32x4 (&vf)[DT::NJ]) {
+        // V^T operands per product: 1/2 at head_dim 128 (two 16-row
+        // blocks), 1 at 256 (one); each operand is two transposing reads.
+        // K operands die as V operands fill, so the two never hold all
+        // their registers at once.
+        constexpr int NP = DT::NKK * 2 * QS;  // products
+        static_assert(NP == 2 * DT::NJ || NP == DT::NJ, "one V operand per one or two products");
+        constexpr int PPV = NP / DT::NJ;      // products per V operand
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
@@ -1285,12 +1000,12 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         for (int i = 0; i < NP; ++i) {
           const int kk = i / (2 * QS), ks = (i / QS) % 2, qs = i % QS;
           sn[qs][ks] = T::mfma16x16x32(kf[kk][ks], qf[qs][kk], sn[qs][ks]);
-          if (i % 2 == 0) vf[i / 2] = vread(slot, i / 2);
+          if (i % PPV == 0) vf[i / PPV] = vread(slot, i / PPV);
         }
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 2 / PPV, 0);  // DS read
         }
       };
       // One key tile jt (ring slot `slot`; tile jt + 1 in slot_next), after
@@ -1301,13 +1016,13 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
       // On return vf and pb hold tile jt's operands and sc tile jt + 1's
       // scores.
       auto tile = [&](auto pv_tag, auto mask_tag, int jt, uint32_t slot, uint32_t slot_next, bool blk_ok,
-                      u32x4 (&vf)[PT::NJ], u32x4 (&pb)[QS]) {
+                      u32x4 (&vf)[DT::NJ], u32x4 (&pb)[QS]) {
         unhoist();
         if (pend) rescale(alpha);  // tile jt - 1's maxima, before its products join o
         pend = check(mask_tag, jt, blk_ok, alpha);
         issue();
         uint32_t pw[QS][4];
-        u32x4 kf[PT::NKK][2];  // tile jt + 1 (discarded past the last)
+        u32x4 kf[DT::NKK][2];  // tile jt + 1 (discarded past the last)
         if constexpr (decltype(pv_tag)::value) {
           pv_p(vf, pb, pw, slot_next, kf);
         } else {
@@ -1363,7 +1078,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         slot = slot_next;
         slot_next = slot_next == lds_last ? lds0 : slot_next + DT::SLOT_B;
       };
-      u32x4 vf[PT::NJ], pb[QS];  // V^T operands and P of the tile whose products are pending
+      u32x4 vf[DT::NJ], pb[QS];  // V^T operands and P of the tile whose products are pending
       int jt = 0;
       plain_end = bad_seen ? 0 : n_plain;
       if (n_kt > 0) {  // tile 0: no earlier tile's products
@@ -1483,21 +1198,16 @@ int launch_prefill_dma(PrefillArgs a, hipStream_t st) {
 
 template <class T, bool FP8, int D>
 int launch_prefill(PrefillArgs a, hipStream_t s) {
-  if constexpr (FP8 && D == 128) {
-    return launch_prefill_dma<T, D, ShapeC, true>(a, s);  // the copies assume 8 rows per wave
-  } else if constexpr (D == 128) {
+  if constexpr (D == 256) {
+    return launch_prefill_dma<T, D, ShapeD, FP8>(a, s);
+  } else if constexpr (FP8) {
+    return launch_prefill_dma<T, D, ShapeC, true>(a, s);  // fp8 copies: one 1 KiB piece per wave
+  } else {
     switch (prefill_shape()) {
       case 'c': return launch_prefill_dma<T, D, ShapeC, false>(a, s);
       default: return launch_prefill_dma<T, D, ShapeA, false>(a, s);
     }
-  } else {
-    using PT = PTile<T, FP8, D>;
-    const int64_t total = work_grid(a.n_qtiles, static_cast<int64_t>(a.Hkv) * a.quads * a.num_seqs);
-    if (total > 0x7fffffff) return fail(NQ_EINVAL, "varlen_prefill: grid too large");
-    const int grid = static_cast<int>(total);
-    varlen_prefill_kernel<T, FP8, D><<<grid, kPThreads, PT::LDS_BYTES, s>>>(a);
   }
-  return check_launch("varlen_prefill");
 }
 
 }  // namespace
@@ -1542,9 +1252,6 @@ static int varlen_prefill_impl(const void *q, int64_t q_row_stride, int64_t q_he
       return fail(NQ_EINVAL, "varlen_prefill: block table width");
     if (static_cast<int64_t>(max_blocks_per_seq) * block_size < max_seqlen_k)
       return fail(NQ_EINVAL, "varlen_prefill: block table narrower than max_seqlen_k");
-    if ((max_seqlen_k + block_size - 1) / block_size > kMaxBt)
-      return fail(NQ_EUNSUPPORTED, "varlen_prefill: max_seqlen_k %d needs more than %d table entries", max_seqlen_k,
-                  kMaxBt);
   }
   const int qsz = 2, ksz = fp8 ? 1 : 2;
   if ((q_row_stride * qsz) % 16 || (q_head_stride * qsz) % 16 || !aligned(q, 16) || (kv_row_stride * ksz) % 16 ||
@@ -1575,10 +1282,10 @@ static int varlen_prefill_impl(const void *q, int64_t q_row_stride, int64_t q_he
   a.out = static_cast<uint8_t *>(out);
   a.o_rs = out_row_stride * qsz;
   a.o_hs = out_head_stride * qsz;
-  // The gate rides in the output store of the register-staged kernel (fp8
-  // K/V, head_dim 256) and of the default persistent shape; the other
-  // persistent shape gets the same arithmetic from one in-place pass.
-  const bool fused_gate = gate && (fp8 || head_dim == 256 || prefill_shape() == 'c');  // fp8 D=128: shape C
+  // The gate rides in the output store of the default launch shapes (C at
+  // head_dim 128, and fp8; D at 256); shape A gets the same arithmetic from
+  // one in-place pass.
+  const bool fused_gate = gate && (fp8 || head_dim == 256 || prefill_shape() == 'c');
   if (gate) {
     if ((gate_row_stride * qsz) % 16 || (gate_head_stride * qsz) % 16 || !aligned(gate, 16))
       return fail(NQ_EINVAL, "varlen_prefill_gated: gate alignment");
@@ -1600,10 +1307,6 @@ static int varlen_prefill_impl(const void *q, int64_t q_row_stride, int64_t q_he
   a.num_seqs = num_seqs;
   a.max_seqlen_q = max_seqlen_q;
   a.max_seqlen_k = max_seqlen_k;
-  // Query rows per workgroup of the register-staged kernel (the persistent
-  // kernel sets its own tiling at launch).
-  const int rows_per_wg = 16 * (head_dim == 256 ? kRegQS<256> : kRegQS<128>) * (4 / a.G4);
-  a.n_qtiles = (max_seqlen_q + rows_per_wg - 1) / rows_per_wg;
   a.causal = causal;
   a.scale_log2 = softmax_scale * kLog2e;
   a.k_scale = k_scale;
