@@ -17,7 +17,7 @@ gate (``cfg2_gate``: gated vs plain decode; ``cfg3_gate``: gated vs plain
 prefill, and the stand-alone in-place gate pass for comparison), head_dim 256
 (``cfg2_d256``, ``cfg5_d256``, ``cfg3_d256``) and the Gated DeltaNet decode
 step (``gdn_decode``: HBM GB/s over the state pool) and prefill
-(``gdn_prefill``: recurrent form over cfg3's sequence lengths), and the gated
+(``gdn_prefill``: chunked form over cfg3's sequence lengths), and the gated
 RMS norm of its output (``gdn_norm``) and the causal conv1d before it
 (``gdn_conv``), HBM GB/s; and cfg3 with an fp8 KV cache (``cfg3_fp8``).
 ``roofline`` covers the dominant kernel of the headline workload (paged
@@ -229,11 +229,13 @@ def bench_gdn(steps, warmup, seed=0, B=64, H=16, HV=32):
 
 
 def bench_gdn_prefill(steps, warmup, seed=0, H=16, HV=32):
-    """Gated DeltaNet prefill (recurrent form) over cfg3's sequence lengths
-    (16 sequences, Lq ~ U[256, 2048]): each (sequence, value head, 16-row
-    slice) is one wave that carries its state through the tokens in
-    registers.  Reported: tokens/s and the fp32 VALU rate of the recurrence
-    (8 V K flops per token and value head)."""
+    """Gated DeltaNet prefill (chunked WY form on MFMA) over cfg3's sequence
+    lengths (16 sequences, Lq ~ U[256, 2048]): one 4-wave workgroup per
+    (sequence, value head) walks its 64-token chunks.  Reported: tokens/s and
+    the MFMA rate of the chunk products -- per chunk and value head K K^T,
+    Q K^T, P D (64x64x128 each), K S^T, Q S^T (64x128x128), Tu V + Tw Y
+    (2 x 64x128x64) and the state update (128x128x64): 11 x 64x64x128
+    multiply-adds, counted over padded chunks."""
     import torch
     from nano_qwen_amd import kernels
     from oracle.inputs import make_prefill_case
@@ -252,9 +254,11 @@ def bench_gdn_prefill(steps, warmup, seed=0, H=16, HV=32):
     out = torch.empty(T, HV, 128, dtype=torch.bfloat16, device="cuda")
     ms = _events_time(lambda i: kernels.gdn_prefill(q, k, v, a, b, A_log, dt, cu, state, idx, out=out),
                       steps, max(warmup, 3))
-    fl = 8 * 128 * 128 * HV * T
-    return dict(ms_per_step=ms, tokens=T, tokens_per_s=T / (ms * 1e-3), valu_tflops=fl / (ms * 1e-3) / 1e12,
-                valu_frac=fl / (ms * 1e-3) / 1e12 / 157.3, k_heads=H, v_heads=HV), None
+    chunks = sum((int(x) + 63) // 64 for x in lq)
+    fl = 2.0 * 11 * 64 * 64 * 128 * chunks * HV
+    return dict(ms_per_step=ms, tokens=T, tokens_per_s=T / (ms * 1e-3), chunks=chunks,
+                mfma_tflops=fl / (ms * 1e-3) / 1e12, mfma_frac=fl / (ms * 1e-3) / 1e12 / 2500.0, k_heads=H,
+                v_heads=HV), None
 
 
 def bench_gated_norm(steps, warmup, seed=0, HV=32):

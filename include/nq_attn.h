@@ -338,20 +338,23 @@ int nq_gdn_decode(const void *q, int64_t q_row_stride, const void *k, int64_t k_
                   int head_k_dim, int head_v_dim, int dtype, void *stream);
 
 /*
- * Gated DeltaNet prefill (recurrent form) for a batch of sequences.
+ * Gated DeltaNet prefill for a batch of sequences, in the chunked (WY) form
+ * over 64-token chunks on MFMA.
  * Replaces chunk_gated_delta_rule (layers/gated_delta_net.py:44-82, the
- * Triton chunk kernel of layers/fla/ with use_qk_l2norm_in_kernel=True and
+ * Triton chunk kernels of layers/fla/ with use_qk_l2norm_in_kernel=True and
  * initial_state=None), the gating computed before it (:197-198) and the
  * final-state write to the pool after it (:210-214), called per sequence by
  * models/qwen3_5.py:215-224.
  * Sequence n < num_seqs owns token rows [cu_seqlens[n], cu_seqlens[n+1]) of
  * q, k [T, num_k_heads, 128], v, out [T, num_v_heads, 128] and a, b
  * [T, num_v_heads].  Its state starts at zero (initial_state_from_slot == 0,
- * as in the reference) or at state[state_indices[n]], runs the step of
+ * as in the reference) or at state[state_indices[n]], follows the step of
  * nq_gdn_decode over the tokens in order, writing out for every token, and
  * is stored to state[state_indices[n]] (a slot outside [0, num_slots) keeps
- * nothing and starts from zero).  Types, layouts and alignment as for
- * nq_gdn_decode; cu_seqlens int32 [num_seqs + 1].
+ * nothing and starts from zero).  Products take 16-bit operands with
+ * float32 accumulation, as the reference's kernels do; the state stays
+ * float32 between chunks.  Types as for nq_gdn_decode; q, k, v, out and
+ * their row strides 16-byte aligned; cu_seqlens int32 [num_seqs + 1].
  */
 int nq_gdn_prefill(const void *q, int64_t q_row_stride, const void *k, int64_t k_row_stride,
                    const void *v, int64_t v_row_stride, const void *a, int64_t a_row_stride,

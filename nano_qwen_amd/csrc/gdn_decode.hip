@@ -16,8 +16,10 @@
 //   o      = S (q * K^-1/2)
 // Here one launch covers the whole batch and updates the pool in place.
 //
+// Prefill (nq_gdn_prefill) runs the chunked form in gdn_chunk.hip.
+//
 // One one-wave workgroup per (sequence, value head, slice of 2 NL state
-// rows; NL = 4 in decode, 8 in prefill), K = V = 128: no workgroup barrier,
+// rows; NL = 4), K = V = 128: no workgroup barrier,
 // many small workgroups, few registers.  The wave owning rows
 // 2NL w .. 2NL w + 2NL - 1 reads with load i of lane l the 16 bytes at row
 // 2NL w + 2i + l/32, columns 4(l%32) .. +3: every load instruction covers
@@ -30,6 +32,12 @@
 #include "nq_device.hpp"
 
 namespace nq {
+// gdn_chunk.hip: the chunked (WY) prefill on MFMA.
+int launch_gdn_chunk_prefill(const void *q, int64_t q_rs, const void *k, int64_t k_rs, const void *v, int64_t v_rs,
+                             const void *a, int64_t a_rs, const void *b, int64_t b_rs, const float *A_log,
+                             const float *dt_bias, const int32_t *cu, int num_seqs, float *state,
+                             const int32_t *idx, int64_t num_slots, int from_slot, void *out, int64_t o_rs, int H,
+                             int HV, int dtype, hipStream_t s);
 namespace {
 
 constexpr int kThreads = 64;
@@ -85,12 +93,9 @@ __device__ inline float reduce_rows(float (&p)[N], int lane) {
   return r;
 }
 
-// A wave owns 2 * NL state rows (NL loads per lane).  Decode uses NL = 4:
-// more, smaller waves hide the HBM latency better.  Prefill uses NL = 8: its
-// waves are latency-bound chains whose fixed per-token work (norms, gates,
-// reductions) does not shrink with fewer rows.
+// A wave owns 2 * NL state rows (NL loads per lane); NL = 4: more, smaller
+// waves hide the HBM latency better.
 constexpr int kDecodeLoads = 4;
-constexpr int kPrefillLoads = 8;
 // Lane bits below the row index after reduce_rows<NL>.
 template <int NL>
 constexpr int kShOf = NL == 16 ? 1 : (NL == 8 ? 2 : 3);
@@ -186,67 +191,6 @@ __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(const GdnArgs a) {
   for (int i = 0; i < NL; ++i) __builtin_nontemporal_store(s[i], reinterpret_cast<f32x4 *>(sp + 2 * i * kDim));
 }
 
-// Prefill: sequence n owns token rows [cu[n], cu[n+1]); the state starts from
-// zero (or the slot's contents) and stays in registers across the tokens;
-// each token's inputs are loaded kAheadTok tokens before it is processed.
-constexpr int kAheadTok = 4;
-
-template <class T>
-__global__ __launch_bounds__(kThreads) void gdn_prefill_kernel(const GdnArgs a, const int32_t *cu, int from_slot) {
-  constexpr int NL = kPrefillLoads, kRowsW = 2 * NL, kSh = kShOf<NL>;
-  const int hv = blockIdx.x, n = blockIdx.y, w = blockIdx.z;
-  const int lane = threadIdx.x;
-  const int32_t slot = a.idx[n];
-  const bool has_slot = slot >= 0 && slot < a.num_slots;
-  const int h = hv / (a.HV / a.H);
-  const int r0 = kRowsW * w + (lane >> 5);
-  const int c0 = 4 * (lane & 31);
-  const int my_row = 2 * ((lane >> kSh) & (NL - 1)) + (lane >> 5);
-  const bool writer = (lane & ((1 << kSh) - 1)) == 0;
-  const int64_t t0 = cu[n], t1 = cu[n + 1];
-
-  float *sp = a.state + ((static_cast<int64_t>(has_slot ? slot : 0) * a.HV + hv) * kDim + r0) * kDim + c0;
-  f32x4 s[NL];
-#pragma unroll
-  for (int i = 0; i < NL; ++i)
-    s[i] = (from_slot && has_slot) ? __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(sp + 2 * i * kDim))
-                                   : f32x4{0, 0, 0, 0};
-  const float neg_a = -expf(a.A_log[hv]), dtb = a.dt_bias[hv];
-  __shared__ float urow[kRowsW];
-  const int vrow = kRowsW * w + my_row;
-  // Prefetch ring: token indices past the end are clamped to the last token
-  // (loaded, never used), so the steady-state loop has no branches and the
-  // compiler's waits count exactly the loads each token needs.
-  // An empty sequence loads no token (its t0 may be one past the last row):
-  // its final state is the initial one.
-  if (t1 > t0) {
-    const int64_t last = t1 - 1;
-    TokIn ring[kAheadTok];
-#pragma unroll
-    for (int j = 0; j < kAheadTok; ++j) ring[j] = load_tok<T>(a, min(t0 + j, last), h, hv, vrow, c0);
-    int64_t t = t0;
-    for (; t + kAheadTok <= t1; t += kAheadTok) {
-#pragma unroll
-      for (int j = 0; j < kAheadTok; ++j) {
-        const TokIn in = ring[j];
-        ring[j] = load_tok<T>(a, min(t + j + kAheadTok, last), h, hv, vrow, c0);
-        uint16_t *orow = reinterpret_cast<uint16_t *>(a.out + (t + j) * a.o_rs + hv * kDim * 2) + kRowsW * w;
-        gdn_token<T, NL>(s, in, neg_a, dtb, a.eps, a.scale, lane, urow, my_row, writer, orow);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < kAheadTok - 1; ++j) {  // the tail: fewer than kAheadTok tokens
-      if (t + j >= t1) break;
-      uint16_t *orow = reinterpret_cast<uint16_t *>(a.out + (t + j) * a.o_rs + hv * kDim * 2) + kRowsW * w;
-      gdn_token<T, NL>(s, ring[j], neg_a, dtb, a.eps, a.scale, lane, urow, my_row, writer, orow);
-    }
-  }
-  if (has_slot) {
-#pragma unroll
-    for (int i = 0; i < NL; ++i) __builtin_nontemporal_store(s[i], reinterpret_cast<f32x4 *>(sp + 2 * i * kDim));
-  }
-}
-
 }  // namespace
 }  // namespace nq
 
@@ -318,34 +262,12 @@ extern "C" int nq_gdn_prefill(const void *q, int64_t q_row_stride, const void *k
   if (num_seqs == 0) return NQ_OK;
   if (!q || !k || !v || !a || !b || !A_log || !dt_bias || !cu_seqlens || !state || !state_indices || !out)
     return fail(NQ_EINVAL, "gdn_prefill: null pointer");
-  if (!aligned(state, 16) || !aligned(q, 8) || !aligned(k, 8) || (q_row_stride * 2) % 8 || (k_row_stride * 2) % 8)
-    return fail(NQ_EINVAL, "gdn_prefill: state 16-byte, q/k rows 8-byte alignment");
+  if (!aligned(state, 16) || !aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16) ||
+      (q_row_stride * 2) % 16 || (k_row_stride * 2) % 16 || (v_row_stride * 2) % 16 || (out_row_stride * 2) % 16)
+    return fail(NQ_EINVAL, "gdn_prefill: state, q/k/v/out rows 16-byte alignment");
   if (num_seqs > 65535 || num_v_heads > 65535) return fail(NQ_EINVAL, "gdn_prefill: grid too large");
-  GdnArgs g{};
-  g.q = static_cast<const uint8_t *>(q);
-  g.k = static_cast<const uint8_t *>(k);
-  g.v = static_cast<const uint8_t *>(v);
-  g.q_rs = q_row_stride * 2;
-  g.k_rs = k_row_stride * 2;
-  g.v_rs = v_row_stride * 2;
-  g.a = static_cast<const uint8_t *>(a);
-  g.b = static_cast<const uint8_t *>(b);
-  g.a_rs = a_row_stride * 2;
-  g.b_rs = b_row_stride * 2;
-  g.A_log = A_log;
-  g.dt_bias = dt_bias;
-  g.state = state;
-  g.idx = state_indices;
-  g.num_slots = num_slots;
-  g.out = static_cast<uint8_t *>(out);
-  g.o_rs = out_row_stride * 2;
-  g.H = num_k_heads;
-  g.HV = num_v_heads;
-  g.eps = 1e-6f;
-  g.scale = 1.0f / sqrtf(static_cast<float>(head_k_dim));
-  dim3 grid(num_v_heads, num_seqs, kDim / (2 * kPrefillLoads));
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == NQ_BF16) gdn_prefill_kernel<BF16><<<grid, kThreads, 0, s>>>(g, cu_seqlens, initial_state_from_slot);
-  else gdn_prefill_kernel<F16><<<grid, kThreads, 0, s>>>(g, cu_seqlens, initial_state_from_slot);
-  return check_launch("gdn_prefill");
+  return launch_gdn_chunk_prefill(q, q_row_stride * 2, k, k_row_stride * 2, v, v_row_stride * 2, a, a_row_stride * 2,
+                                  b, b_row_stride * 2, A_log, dt_bias, cu_seqlens, num_seqs, state, state_indices,
+                                  num_slots, initial_state_from_slot, out, out_row_stride * 2, num_k_heads, num_v_heads,
+                                  dtype, static_cast<hipStream_t>(stream));
 }

@@ -53,6 +53,25 @@ def _check(c, out, ref, state_dev, ref_state, live):
     assert np.abs(s - ref_state).max() <= 2e-5 * np.abs(ref_state).max()
 
 
+def _prefill_close(out, ref, state, ref_state):
+    """Chunked prefill against the exact recurrence: the kernel's products
+    take 16-bit operands (rounded unit keys and queries, the state, the
+    inverse, the updates) with float32 accumulation, as the reference's
+    Triton chunk kernels do, so errors are a few 16-bit ulps of the largest
+    values, not of each element: max within 2% and mean within 0.1% of the
+    largest reference magnitude, for the outputs and for the final states."""
+    o = np.asarray(out, dtype=np.float64)
+    r = np.asarray(ref, dtype=np.float64)
+    s = np.asarray(state, dtype=np.float64)
+    rs = np.asarray(ref_state, dtype=np.float64)
+    assert np.all(np.isfinite(o)) and np.all(np.isfinite(s))
+    om, sm = np.abs(r).max(), np.abs(rs).max()
+    eo, es = np.abs(o - r), np.abs(s - rs)
+    assert eo.max() <= 2e-2 * om and eo.mean() <= 1e-3 * om, (float(eo.max()), float(eo.mean()), float(om))
+    assert es.max() <= 2e-2 * sm and es.mean() <= 1e-3 * sm, (float(es.max()), float(es.mean()), float(sm))
+    return float(eo.max() / om), float(es.max() / sm)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_gdn_decode_matches_oracle(cuda, dtype):
     c = _case(dtype=dtype, seed=1)
@@ -129,15 +148,35 @@ def test_gdn_prefill_matches_oracle(cuda, from_slot):
     ref_state = state.double().numpy()
     ref = gdn.gdn_prefill(f(q), f(k), f(v), f(a), f(b), f(A_log), f(dt), cu.numpy(), ref_state, idx.numpy(),
                           from_slot=from_slot)
-    o = out.float().cpu().numpy()
-    assert np.all(np.abs(o - ref) <= 2 ** -8 * np.abs(ref) + 1e-3 * np.abs(ref).max()), float(np.abs(o - ref).max())
-    s = state_dev.cpu().double().numpy()
-    assert np.abs(s - ref_state).max() <= 2e-5 * np.abs(ref_state).max()
+    live = [i for i in range(8) if i in idx.tolist()]
+    _prefill_close(out.float().cpu().numpy(), ref, state_dev.cpu().numpy()[live], ref_state[live])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gdn_prefill_chunk_edges(cuda, dtype):
+    """Lengths on both sides of the 64-token chunk (one short of, equal to,
+    one past, two chunks and the same +-1), state carried from the slots."""
+    lens = [63, 64, 65, 127, 128, 129, 1]
+    c = _prefill_inputs(lens, 2, 4, seed=16, slots=8, dtype=dtype)
+    idx = torch.tensor([7, 0, 1, 2, 3, 4, 6], dtype=torch.int32)
+    d = {k: v.to(cuda) for k, v in c.items()}
+    state_dev = d["state"].clone()
+    out = kernels.gdn_prefill(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt"], d["cu"], state_dev,
+                              idx.to(cuda), initial_state_from_slot=True)
+    torch.cuda.synchronize()
+    f = lambda t: t.double().numpy()
+    ref_state = c["state"].double().numpy()
+    ref = gdn.gdn_prefill(f(c["q"]), f(c["k"]), f(c["v"]), f(c["a"]), f(c["b"]), f(c["A_log"]), f(c["dt"]),
+                          c["cu"].numpy(), ref_state, idx.numpy(), from_slot=True)
+    eo, es = _prefill_close(out.float().cpu().numpy(), ref, state_dev.cpu().numpy(), ref_state)
+    if dtype == torch.float16:  # 11-bit operands: an order of magnitude closer
+        assert eo <= 2e-3 and es <= 2e-3, (eo, es)
+    assert torch.equal(state_dev[5].cpu(), c["state"][5])   # slot no sequence names
 
 
 def test_gdn_prefill_then_decode_equals_longer_prefill(cuda):
     """Prefill of L tokens then one decode step == prefill of L + 1 tokens
-    (same final state, same last output)."""
+    (same final state and last output, to the chunked form's precision)."""
     g = torch.Generator().manual_seed(7)
     L, H, HV, bf = 50, 1, 2, torch.bfloat16
     q, k = torch.randn(L + 1, H, 128, generator=g).to(bf), torch.randn(L + 1, H, 128, generator=g).to(bf)
@@ -154,8 +193,10 @@ def test_gdn_prefill_then_decode_equals_longer_prefill(cuda):
     o_all = kernels.gdn_prefill(q, k, v, a, b, A_log, dt,
                                 torch.tensor([0, L + 1], dtype=torch.int32, device=cuda), st2, idx)
     torch.cuda.synchronize()
-    assert torch.equal(st1, st2)
-    assert torch.equal(o_dec[0].view(torch.int16), o_all[L].view(torch.int16))
+    sm = float(st2.abs().max())
+    assert float((st1 - st2).abs().max()) <= 2e-2 * sm
+    om = float(o_all.float().abs().max())
+    assert float((o_dec[0].float() - o_all[L].float()).abs().max()) <= 2e-2 * om
 
 
 @pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float16, 128), (torch.bfloat16, 256),
@@ -260,7 +301,8 @@ def test_gdn_core_layer_path(cuda):
         ref = gdn.gated_rmsnorm(yb, z.float().numpy().reshape(-1, D), nw, 1e-6, "bf16").reshape(T, HV * D)
         o = out.float().cpu().numpy()
         assert np.all(np.abs(o - ref) <= 2 ** -6 * np.abs(ref) + 2e-2 * np.abs(ref).max()), float(np.abs(o - ref).max())
-        assert np.abs(layer.recurrent_states.cpu().double().numpy() - ref_rec).max() <= 1e-4 * max(1.0, np.abs(ref_rec).max())
+        # the chunked prefill's 16-bit operands (see _prefill_close); decode steps are float32
+        assert np.abs(layer.recurrent_states.cpu().double().numpy() - ref_rec).max() <= 2e-2 * max(1.0, np.abs(ref_rec).max())
         assert torch.equal(layer.conv_states.cpu().float(), torch.from_numpy(ref_conv))
 
     run(sum(lens), torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32))
@@ -280,10 +322,10 @@ def test_gdn_decode_bench_shape(cuda):
     _check(c, out, ref, state_dev, ref_state, np.ones(64, bool))
 
 
-def _prefill_inputs(lens, H, HV, seed, slots):
+def _prefill_inputs(lens, H, HV, seed, slots, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
     cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32)
-    T, bf = int(cu[-1]), torch.bfloat16
+    T, bf = int(cu[-1]), dtype
     return dict(q=torch.randn(T, H, 128, generator=g).to(bf), k=torch.randn(T, H, 128, generator=g).to(bf),
                 v=torch.randn(T, HV, 128, generator=g).to(bf), a=torch.randn(T, HV, generator=g).to(bf),
                 b=torch.randn(T, HV, generator=g).to(bf), A_log=torch.randn(HV, generator=g) * 0.5,
@@ -310,9 +352,10 @@ def test_gdn_prefill_cfg3_lengths(cuda):
     ref = gdn.gdn_prefill_chunked(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt"], c["cu"], ref_state,
                                   idx, from_slot=True)
     torch.cuda.synchronize()
-    err = (out.double() - ref).abs()
-    assert bool((err <= 2 ** -8 * ref.abs() + 1e-3 * ref.abs().max()).all()), float(err.max())
-    assert float((state_dev.double() - ref_state).abs().max()) <= 2e-5 * float(ref_state.abs().max())
+    live = idx.tolist()
+    eo, es = _prefill_close(out.double().cpu().numpy(), ref.cpu().numpy(), state_dev.double().cpu().numpy()[live],
+                            ref_state.cpu().numpy()[live])
+    print(f"[gdn] cfg3 lengths: max error {eo:.2e} (outputs), {es:.2e} (states) of the largest magnitude", flush=True)
 
 
 def test_gdn_prefill_empty_sequences(cuda):
@@ -331,10 +374,8 @@ def test_gdn_prefill_empty_sequences(cuda):
         ref_state = c["state"].double().numpy()
         ref = gdn.gdn_prefill(f(c["q"]), f(c["k"]), f(c["v"]), f(c["a"]), f(c["b"]), f(c["A_log"]), f(c["dt"]),
                               c["cu"].numpy(), ref_state, idx.numpy(), from_slot=from_slot)
-        o = out.float().cpu().numpy()
-        assert np.all(np.abs(o - ref) <= 2 ** -8 * np.abs(ref) + 1e-3 * np.abs(ref).max())
-        s = state_dev.cpu().double().numpy()
-        assert np.abs(s - ref_state).max() <= 2e-5 * np.abs(ref_state).max()
+        live = [i for i in range(6) if i in idx.tolist()]
+        _prefill_close(out.float().cpu().numpy(), ref, state_dev.cpu().numpy()[live], ref_state[live])
         for slot in (5, 1, 4):   # the empty sequences' slots
             want = c["state"][slot] if from_slot else torch.zeros(4, 128, 128)
             assert torch.equal(state_dev[slot].cpu(), want)
