@@ -7,7 +7,12 @@ A "step" is one pass of the path over one batch of synthetic input:
   prefill (cfg3):           store_kvcache of the new tokens + causal varlen prefill
 Inputs are resident in HBM before timing starts.  Decode steps alternate
 between two independent KV pools (each larger than the 256 MB MALL), so no
-step re-reads KV the previous step left in the Infinity Cache.
+step re-reads KV the previous step left in the Infinity Cache; the same step
+replayed as a HIP graph (the runner's path) is reported as ``graph_ms``.
+Every measurement warms up for at least 20 ms
+and times each step between two events: ``ms_per_step`` is the mean over
+the timed steps (the whole-step rates, and the headline, use it) and
+``ms_median`` their median (the per-kernel rates under ``extra`` use it).
 
 The headline (``value``) is cfg2's algorithmic HBM bandwidth in GB/s; cfg3's
 TFLOP/s and the other decode configurations are reported under ``extra``, as
@@ -40,18 +45,37 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 
 
+_LAST = {}  # the mean ms per step of the last _events_time call (timed region / steps)
+MIN_WARM_MS = 20.0
+
+
 def _events_time(fn, steps, warmup):
+    """Warm up for at least `warmup` steps and MIN_WARM_MS of them (so the
+    clocks have ramped), then time `steps` steps, each between two events on
+    the current stream.  Returns the median ms per step; _LAST["mean"] holds
+    the mean (the whole timed region / steps).  fn(i) gets a running step
+    index (pools alternate on it)."""
     import torch
+    i = 0
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps):
-        fn(warmup + i)
-    end.record()
+    i = warmup
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < MIN_WARM_MS:
+        for _ in range(4):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record()
+    for k in range(steps):
+        fn(i + k)
+        ev[k + 1].record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps  # ms per step
+    per = [ev[k].elapsed_time(ev[k + 1]) for k in range(steps)]
+    _LAST["mean"] = ev[0].elapsed_time(ev[steps]) / steps
+    return statistics.median(per)
 
 
 def _second_pool(case):
@@ -87,6 +111,21 @@ def bench_decode(name, steps, warmup, seed=0, **override):
                              case["k_scale"], case["v_scale"], out=out)
 
     ms = _events_time(step, steps, warmup)
+    ms_mean = _LAST["mean"]
+    # The step as a graph replay of store + decode (engine run_model's path),
+    # one graph per pool, for comparison.
+    side = torch.cuda.Stream()
+    graphs = []
+    for p in range(2):
+        with torch.cuda.stream(side):
+            step(p)  # the capture stream's workspace exists before the capture
+        side.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            step(p)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    ms_graph = _events_time(lambda i: graphs[i % 2].replay(), steps, warmup)
     ms_attn = _events_time(attn_only, steps, warmup)
     nbytes = decode_bytes(case)
     store_bytes = 2 * case["batch"] * case["hkv"] * case["d"] * (case["q"].element_size() +
@@ -96,8 +135,10 @@ def bench_decode(name, steps, warmup, seed=0, **override):
     ns, st = kernels.decode_plan(case["batch"], case["hq"], case["hkv"], W, case["block_size"],
                                  case["k_cache"].dtype)
     res = dict(
-        ms_per_step=ms, gbs=nbytes / (ms * 1e-3) / 1e9, tokens_per_s=case["batch"] / (ms * 1e-3),
-        hbm_frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, bytes_per_step=nbytes,
+        ms_per_step=ms_mean, ms_median=ms, graph_ms=ms_graph, gbs=nbytes / (ms_mean * 1e-3) / 1e9,
+        tokens_per_s=case["batch"] / (ms_mean * 1e-3), median_gbs=nbytes / (ms * 1e-3) / 1e9,
+        hbm_frac=nbytes / (ms_mean * 1e-3) / 1e9 / HBM_PEAK_GBS, bytes_per_step=nbytes,
+        graph_hbm_frac=nbytes / (ms_graph * 1e-3) / 1e9 / HBM_PEAK_GBS,
         tflops=decode_flops(case) / (ms * 1e-3) / 1e12,
         attn_ms=ms_attn, attn_gbs=attn_bytes / (ms_attn * 1e-3) / 1e9, attn_bytes=attn_bytes,
         splits=ns, split_tokens=st, batch=case["batch"], hq=case["hq"], hkv=case["hkv"],
@@ -127,12 +168,13 @@ def bench_prefill(name, steps, warmup, seed=0, **override):
         attn(i)
 
     ms = _events_time(step, steps, warmup)
+    ms_mean = _LAST["mean"]
     ms_attn = _events_time(attn, steps, warmup)
     fl = prefill_flops(case)
-    return dict(ms_per_step=ms, tflops=fl / (ms * 1e-3) / 1e12, attn_ms=ms_attn,
+    return dict(ms_per_step=ms_mean, ms_median=ms, tflops=fl / (ms_mean * 1e-3) / 1e12, attn_ms=ms_attn,
                 attn_tflops=fl / (ms_attn * 1e-3) / 1e12, mfma_frac=fl / (ms_attn * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
-                flops=fl, tokens_per_s=sum(case["lq"]) / (ms * 1e-3), total_q=sum(case["lq"]),
-                gbs=prefill_bytes(case) / (ms * 1e-3) / 1e9), case
+                flops=fl, tokens_per_s=sum(case["lq"]) / (ms_mean * 1e-3), total_q=sum(case["lq"]),
+                gbs=prefill_bytes(case) / (ms_mean * 1e-3) / 1e9), case
 
 
 def bench_norm_rope(name, steps, warmup, seed=0):
@@ -346,7 +388,19 @@ def cpu_baseline_decode(case, n_seqs=8, reps=5):
     return dict(value=nbytes / t / 1e9, unit="GB/s", cores=cores, kind="port",
                 sample=f"{case['name']} first {n_seqs} of {case['batch']} sequences (sum ctx "
                        f"{int(ctx.sum())}), store + decode, torch {torch.__version__} CPU, median of {reps}",
-                seconds=t, cpu=platform.processor() or platform.machine())
+                seconds=t, cpu=cpu_model())
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), else the platform's."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def cpu_baseline_prefill(case, n_seqs=2, reps=3):
@@ -385,23 +439,27 @@ def cpu_baseline_prefill(case, n_seqs=2, reps=3):
     fl = prefill_flops(dict(case, lq=lq, lk=lk))
     return dict(value=fl / t / 1e12, unit="TFLOP/s", cores=cores, kind="port",
                 sample=f"{case['name']} first {n_seqs} of {case['nseq']} sequences (Lq {lq}, Lk {lk}), "
-                       f"attention only, median of {reps}", seconds=t)
+                       f"attention only, median of {reps}", seconds=t, cpu=cpu_model())
 
 
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "paged_decode_cfg2_traffic.md")
 
 
 def measured_traffic(path=TRAFFIC_FILE):
-    """HBM bytes per launch of the headline kernels, from the committed
-    rocprofv3 counter summary (a line `traffic_bytes_per_launch: N`), or None."""
+    """HBM bytes per launch of the headline kernels and the commit they were
+    measured at, from the committed rocprofv3 counter summary (lines
+    `traffic_bytes_per_launch: N` and `measured_at_commit: H`), or (None, None)."""
+    n = commit = None
     try:
         with open(path) as f:
             for line in f:
                 if line.strip().startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1].strip())
+                    n = int(line.split(":", 1)[1].strip())
+                elif line.strip().startswith("measured_at_commit:"):
+                    commit = line.split(":", 1)[1].strip()
     except OSError:
-        return None
-    return None
+        pass
+    return n, commit
 
 
 def copy_calibration(nbytes, reps=3):
@@ -517,7 +575,8 @@ def main():
         line["roofline"] = {
             "bound": "hbm", "kernel": "paged_decode (main + split-K merge)",
             "achieved": round(head["attn_gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(head["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+            "frac": round(head["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic()[0],
+            "traffic_measured_at_commit": measured_traffic()[1],
             "attn_ms": round(head["attn_ms"], 5), "algorithmic_bytes": head["attn_bytes"],
         }
     if "cfg3" in extra:
