@@ -10,9 +10,10 @@ between two independent KV pools (each larger than the 256 MB MALL), so no
 step re-reads KV the previous step left in the Infinity Cache; the same step
 replayed as a HIP graph (the runner's path) is reported as ``graph_ms``.
 Every measurement warms up for at least 20 ms
-and times each step between two events: ``ms_per_step`` is the mean over
-the timed steps (the whole-step rates, and the headline, use it) and
-``ms_median`` their median (the per-kernel rates under ``extra`` use it).
+and times its steps back to back in five groups between events:
+``ms_per_step`` is the mean over all timed steps (the whole-step rates, and
+the headline, use it) and ``ms_median`` the median of the groups' means (the
+per-kernel rates under ``extra`` use it).
 
 The headline (``value``) is cfg2's algorithmic HBM bandwidth in GB/s; cfg3's
 TFLOP/s and the other decode configurations are reported under ``extra``, as
@@ -49,14 +50,15 @@ _LAST = {}  # the mean ms per step of the last _events_time call (timed region /
 MIN_WARM_MS = 20.0
 
 
-def _events_time(fn, steps, warmup):
+def _events_time(fn, steps, warmup, groups=5):
     """Warm up for at least `warmup` steps and MIN_WARM_MS of them (so the
-    clocks have ramped), then time `steps` steps, each between two events on
-    the current stream.  Returns the median ms per step; _LAST["mean"] holds
-    the mean (the whole timed region / steps).  fn(i) gets a running step
-    index (pools alternate on it)."""
+    clocks have ramped), then time `steps` steps back to back in `groups`
+    consecutive groups, with an event on the current stream between groups
+    (an event between every step would add its own gap to each step).
+    Returns the median over the groups of their ms per step; _LAST["mean"]
+    holds the mean (the whole timed region / steps).  fn(i) gets a running
+    step index (pools alternate on it)."""
     import torch
-    i = 0
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -67,14 +69,17 @@ def _events_time(fn, steps, warmup):
             fn(i)
             i += 1
         torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    groups = max(1, min(groups, steps))
+    bounds = [round(steps * g / groups) for g in range(groups + 1)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(groups + 1)]
     ev[0].record()
-    for k in range(steps):
-        fn(i + k)
-        ev[k + 1].record()
+    for g in range(groups):
+        for k in range(bounds[g], bounds[g + 1]):
+            fn(i + k)
+        ev[g + 1].record()
     torch.cuda.synchronize()
-    per = [ev[k].elapsed_time(ev[k + 1]) for k in range(steps)]
-    _LAST["mean"] = ev[0].elapsed_time(ev[steps]) / steps
+    per = [ev[g].elapsed_time(ev[g + 1]) / (bounds[g + 1] - bounds[g]) for g in range(groups)]
+    _LAST["mean"] = ev[0].elapsed_time(ev[groups]) / steps
     return statistics.median(per)
 
 
