@@ -22,14 +22,15 @@
 // arithmetic.  (W = T diag(beta exp(G)) K of the reference is never formed:
 // W S^T = (T diag(..)) (K S^T).)
 //
-// One 4-wave workgroup per (sequence, value head) walks the sequence's
-// chunks.  The state lives in MFMA accumulators (wave w owns value rows
-// 32w .. 32w + 31), in float32 across the whole sequence, with a 16-bit copy
-// in LDS for the products that read it; every product runs on
-// v_mfma_f32_32x32x16 with 16-bit operands and float32 accumulation, as the
-// reference's kernels do (their tl.dot operands are the input dtype).  The
-// 64x64 triangular inverse runs in float32 on the VALU, blocked in 16x16
-// diagonal blocks.
+// One 8-wave workgroup (two waves per SIMD) per (sequence, value head) walks
+// the sequence's chunks.  The state lives in MFMA accumulators (wave w owns
+// value rows 32 (w / 2) .. +31 against key columns 64 (w % 2) .. +63), in
+// float32 across the whole sequence, with a 16-bit copy in LDS for the
+// products that read it; every product runs on v_mfma_f32_32x32x16 with
+// 16-bit operands and float32 accumulation, as the reference's kernels do
+// (their tl.dot operands are the input dtype).  The 64x64 triangular inverse
+// runs in float32 on the VALU of waves 0-3, blocked in 16x16 diagonal
+// blocks, while waves 4-7 form K S^T and Q S^T, which do not depend on it.
 //
 // LDS tiles are row-major with 16-byte chunks XOR-swizzled per row: tiles
 // read only as row operands (ds_read_b128) use swz_r, tiles also read down
@@ -41,7 +42,7 @@ namespace {
 
 constexpr int kC = 64;       // tokens per chunk
 constexpr int kD = 128;      // K = V
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;  // 8 waves, two per SIMD
 
 struct ChunkArgs {
   const uint8_t *q, *k, *v;  // [T, H, K], [T, H, K], [T, HV, V] (dtype T)
@@ -66,14 +67,14 @@ constexpr int kOffQ = kOffK + kTile;         // Q (scaled unit queries), swz_r; 
 constexpr int kOffV = kOffQ + kTile;         // V, swz_c; then D
 constexpr int kOffS = kOffV + kTile;         // S, 16-bit [V][K], swz_r
 constexpr int kTfStride = 68;                // floats per row of the fp32 64x64 matrix
-constexpr int kOffT = kOffS + kD * kD * 2;   // A, then T (fp32 64 x 68); then Y (64 x 128, swz_c)
+constexpr int kOffT = kOffS + kD * kD * 2;   // A, then T (fp32 64 x 68)
 constexpr int kOffTw = kOffT + kC * kTfStride * 4;
 constexpr int kOffTu = kOffTw + kC * kC * 2;  // 64 x 64 16-bit, swz_6
 constexpr int kOffP = kOffTu + kC * kC * 2;
 constexpr int kOffG = kOffP + kC * kC * 2;    // G[64], beta[64] (fp32)
 constexpr int kOffM = kOffG + 2 * kC * 4;     // 3 x 16 x 16 fp32: off-diagonal products of the inverse
-constexpr int kLds = kOffM + 3 * 256 * 4;
-static_assert(kOffT + kTile <= kOffTw, "Y fits where T was");
+constexpr int kOffY = kOffM + 3 * 256 * 4;    // Y = K S^T, 64 x 128 16-bit, swz_c
+constexpr int kLds = kOffY + kTile;
 static_assert(kLds <= 160 * 1024, "LDS");
 
 // Chunk swizzles of the 128-column tiles (16 chunks a row) and of the
@@ -137,16 +138,16 @@ __device__ inline f32x4 unpack2x2(uint32_t w0, uint32_t w1) {
   return f32x4{T::to_float(w0 & 0xffffu), T::to_float(w0 >> 16), T::to_float(w1 & 0xffffu), T::to_float(w1 >> 16)};
 }
 
-// 16-bit copy of the state (float32 accumulators, wave w's value rows) into
-// the S tile.
+// 16-bit copy of a wave's state blocks (value rows 32 vb .. +31, key
+// columns 32 kb0 .. +63) into the S tile.
 template <class T>
-__device__ inline void write_state(uint32_t s_base, const f32x16 (&S)[4], int wave, int lane) {
+__device__ inline void write_state(uint32_t s_base, const f32x16 (&S)[2], int vb, int kb0, int lane) {
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int v = 32 * wave + acc_row(r, lane), kc = 32 * nb + (lane & 31);
-      st16(a128(s_base, v, kc >> 3, false) + 2 * (kc & 7), T::from_float(S[nb][r]));
+      const int v = 32 * vb + acc_row(r, lane), kc = 32 * (kb0 + j) + (lane & 31);
+      st16(a128(s_base, v, kc >> 3, false) + 2 * (kc & 7), T::from_float(S[j][r]));
     }
 }
 
@@ -155,7 +156,8 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t L = lds_addr(smem);
   const uint32_t LK = L + kOffK, LQ = L + kOffQ, LV = L + kOffV, LS = L + kOffS, LT = L + kOffT, LTw = L + kOffTw,
-                 LTu = L + kOffTu, LP = L + kOffP, LG = L + kOffG, LB = L + kOffG + kC * 4, LM = L + kOffM;
+                 LTu = L + kOffTu, LP = L + kOffP, LG = L + kOffG, LB = L + kOffG + kC * 4, LM = L + kOffM,
+                 LY = L + kOffY;
   const int tid0 = threadIdx.x, wave = tid0 >> 6;
   const int hv = blockIdx.x, n = blockIdx.y;
   const int h = hv / (a.HV / a.H);
@@ -165,26 +167,28 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
   float *st = has ? a.state + (static_cast<int64_t>(slot) * a.HV + hv) * kD * kD : nullptr;
   const float neg_a = -expf(a.A_log[hv]), dtb = a.dt_bias[hv];
 
-  // The state: wave w's value rows 32w .. +31 against key columns 32nb .. +31.
-  f32x16 S[4];
+  // This wave's state blocks: value rows 32 vb .. +31, key columns 32 (kb0 + j) .. +31.
+  const int vb = wave >> 1, kb0 = 2 * (wave & 1);
+  f32x16 S[2];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r)
-      S[nb][r] = (has && a.from_slot) ? st[(32 * wave + acc_row(r, tid0 & 63)) * kD + 32 * nb + (tid0 & 31)] : 0.f;
+      S[j][r] = (has && a.from_slot) ? st[(32 * vb + acc_row(r, tid0 & 63)) * kD + 32 * (kb0 + j) + (tid0 & 31)]
+                                     : 0.f;
 
-  if (t1 > t0) write_state<T>(LS, S, wave, tid0 & 63);
-  // Inputs of a chunk, fetched one chunk ahead: row tid / 4 (columns
-  // 32 (tid % 4) .. +31) of q, k, v, and (wave 0) lane's gate inputs.
-  u32x4 qv[4], kv[4], vv[4];
+  if (t1 > t0) write_state<T>(LS, S, vb, kb0, tid0 & 63);
+  // Inputs of a chunk, fetched one chunk ahead: row tid / 8 (columns
+  // 16 (tid % 8) .. +15) of q, k, v, and (wave 0) lane's gate inputs.
+  u32x4 qv[2], kv[2], vv[2];
   uint32_t gab = 0;  // a (low half) and b (high half) of token lane
   auto fetch = [&](int c0, int tid) {
-    const int r = tid >> 2, qd = tid & 3;
+    const int r = tid >> 3, e = tid & 7;
     const bool ok = r < t1 - c0;
     const int64_t t = c0 + r;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = 32 * qd + 8 * j;
+    for (int j = 0; j < 2; ++j) {
+      const int col = 16 * e + 8 * j;
       qv[j] = ok ? *reinterpret_cast<const u32x4 *>(a.q + t * a.q_rs + (h * kD + col) * 2) : u32x4{0, 0, 0, 0};
       kv[j] = ok ? *reinterpret_cast<const u32x4 *>(a.k + t * a.k_rs + (h * kD + col) * 2) : u32x4{0, 0, 0, 0};
       vv[j] = ok ? *reinterpret_cast<const u32x4 *>(a.v + t * a.v_rs + (hv * kD + col) * 2) : u32x4{0, 0, 0, 0};
@@ -208,40 +212,41 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
     // ---- unit keys, scaled unit queries (float32 norms, rounded to 16
     // bits) and values into LDS; gates and their inclusive sum G.
     {
-      const int r = tid >> 2, qd = tid & 3;
-      float fq[32], fk[32];
+      const int r = tid >> 3, e = tid & 7;
+      float fq[16], fk[16];
       float sq = 0.f, sk = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 2; ++j) {
         const f32x4 q0 = unpack2x2<T>(qv[j][0], qv[j][1]), q1 = unpack2x2<T>(qv[j][2], qv[j][3]);
         const f32x4 k0 = unpack2x2<T>(kv[j][0], kv[j][1]), k1 = unpack2x2<T>(kv[j][2], kv[j][3]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          fq[8 * j + e] = q0[e];
-          fq[8 * j + 4 + e] = q1[e];
-          fk[8 * j + e] = k0[e];
-          fk[8 * j + 4 + e] = k1[e];
+        for (int x = 0; x < 4; ++x) {
+          fq[8 * j + x] = q0[x];
+          fq[8 * j + 4 + x] = q1[x];
+          fk[8 * j + x] = k0[x];
+          fk[8 * j + 4 + x] = k1[x];
         }
       }
 #pragma unroll
-      for (int e = 0; e < 32; ++e) {
-        sq += fq[e] * fq[e];
-        sk += fk[e] * fk[e];
+      for (int x = 0; x < 16; ++x) {
+        sq += fq[x] * fq[x];
+        sk += fk[x] * fk[x];
       }
-      sq += __shfl_xor(sq, 1, 64);
-      sk += __shfl_xor(sk, 1, 64);
-      sq += __shfl_xor(sq, 2, 64);
-      sk += __shfl_xor(sk, 2, 64);
+#pragma unroll
+      for (int off = 1; off < 8; off <<= 1) {
+        sq += __shfl_xor(sq, off, 64);
+        sk += __shfl_xor(sk, off, 64);
+      }
       const float rq = a.scale / sqrtf(sq + a.eps), rk = 1.0f / sqrtf(sk + a.eps);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 2; ++j) {
         u32x4 wq, wk;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          wq[e] = T::pack2(fq[8 * j + 2 * e] * rq, fq[8 * j + 2 * e + 1] * rq);
-          wk[e] = T::pack2(fk[8 * j + 2 * e] * rk, fk[8 * j + 2 * e + 1] * rk);
+        for (int x = 0; x < 4; ++x) {
+          wq[x] = T::pack2(fq[8 * j + 2 * x] * rq, fq[8 * j + 2 * x + 1] * rq);
+          wk[x] = T::pack2(fk[8 * j + 2 * x] * rk, fk[8 * j + 2 * x + 1] * rk);
         }
-        const int chunk = 4 * qd + j;
+        const int chunk = 2 * e + j;
         lds_store_b128(a128(LQ, r, chunk, false), wq);
         lds_store_b128(a128(LK, r, chunk, true), wk);
         lds_store_b128(a128(LV, r, chunk, true), vv[j]);
@@ -266,52 +271,84 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
     if (c0 + kC < t1) fetch(c0 + kC, tid);  // in flight while this chunk computes
     __syncthreads();
 
-    // ---- K K^T -> A (fp32) and Q K^T -> P (16-bit): block (w / 2, w % 2).
+    // ---- waves 0-3: K K^T -> A (fp32); waves 4-7: Q K^T -> P (16-bit);
+    // block (bm, bn) = ((w / 2) % 2, w % 2).
     {
-      const int bm = wave >> 1, bn = wave & 1;
-      f32x16 kk = f32x16{}, qk = f32x16{};
+      const int bm = (wave >> 1) & 1, bn = wave & 1;
+      const bool qk = wave >= 4;
+      f32x16 acc = f32x16{};
 #pragma unroll
       for (int s = 0; s < kD / 16; ++s) {
         const u32x4 kb = row_op(LK, 32 * bn, s, lane, true);
-        kk = T::mfma32x32x16(row_op(LK, 32 * bm, s, lane, true), kb, kk);
-        qk = T::mfma32x32x16(row_op(LQ, 32 * bm, s, lane, false), kb, qk);
+        const u32x4 ab = qk ? row_op(LQ, 32 * bm, s, lane, false) : row_op(LK, 32 * bm, s, lane, true);
+        acc = T::mfma32x32x16(ab, kb, acc);
       }
       const int j = 32 * bn + (lane & 31);
       const float Gj = ldf(LG + 4 * j);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int i = 32 * bm + acc_row(r, lane);
-        const float Gi = ldf(LG + 4 * i), bi = ldf(LB + 4 * i);
+        const float Gi = ldf(LG + 4 * i);
         const float dec = __expf(j <= i ? Gi - Gj : 0.f);
-        stf(LT + 4 * (i * kTfStride + j), j < i ? bi * dec * kk[r] : 0.f);
-        st16(a64(LP, i, j >> 3) + 2 * (j & 7), T::from_float(j <= i ? dec * qk[r] : 0.f));
+        if (qk)
+          st16(a64(LP, i, j >> 3) + 2 * (j & 7), T::from_float(j <= i ? dec * acc[r] : 0.f));
+        else
+          stf(LT + 4 * (i * kTfStride + j), j < i ? ldf(LB + 4 * i) * dec * acc[r] : 0.f);
       }
     }
     __syncthreads();
 
-    // ---- T = (I + A)^-1 in place: the four 16x16 diagonal blocks by forward
-    // substitution (wave b, lane = column), then the block rows 1..3.
-    if (lane < 16) {
-      const int b0 = 16 * wave, c = lane;
-      float x[16];
+    // ---- waves 0-3: the four 16x16 diagonal blocks of T = (I + A)^-1 by
+    // forward substitution (lane = column); waves 4-7: Y = K S^T (to LDS)
+    // and O = diag(exp(G)) Q S^T for value columns 32 (w - 4) .. +31.
+    f32x16 O[2];
+    if (wave < 4) {
+      if (lane < 16) {
+        const int b0 = 16 * wave, c = lane;
+        float x[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float acc = i == c ? 1.f : 0.f;
+        for (int i = 0; i < 16; ++i) {
+          float acc = i == c ? 1.f : 0.f;
 #pragma unroll
-        for (int j4 = 0; j4 < i; j4 += 4) {
-          const f32x4 av = ldf4(LT + 4 * ((b0 + i) * kTfStride + b0 + j4));
+          for (int j4 = 0; j4 < i; j4 += 4) {
+            const f32x4 av = ldf4(LT + 4 * ((b0 + i) * kTfStride + b0 + j4));
 #pragma unroll
-          for (int j = j4; j < j4 + 4 && j < i; ++j) acc -= av[j - j4] * x[j];
+            for (int j = j4; j < j4 + 4 && j < i; ++j) acc -= av[j - j4] * x[j];
+          }
+          x[i] = i < c ? 0.f : acc;
         }
-        x[i] = i < c ? 0.f : acc;
-      }
 #pragma unroll
-      for (int i = 0; i < 16; ++i) stf(LT + 4 * ((b0 + i) * kTfStride + b0 + c), x[i]);
+        for (int i = 0; i < 16; ++i) stf(LT + 4 * ((b0 + i) * kTfStride + b0 + c), x[i]);
+      }
+    } else {
+      const int bn = wave - 4;
+      f32x16 Y[2] = {f32x16{}, f32x16{}};
+      O[0] = f32x16{};
+      O[1] = f32x16{};
+#pragma unroll
+      for (int s = 0; s < kD / 16; ++s) {
+        const u32x4 sb = row_op(LS, 32 * bn, s, lane, false);  // S^T operand: row v, columns K
+#pragma unroll
+        for (int bm = 0; bm < 2; ++bm) {
+          Y[bm] = T::mfma32x32x16(row_op(LK, 32 * bm, s, lane, true), sb, Y[bm]);
+          O[bm] = T::mfma32x32x16(row_op(LQ, 32 * bm, s, lane, false), sb, O[bm]);
+        }
+      }
+      const int v = 32 * bn + (lane & 31);
+#pragma unroll
+      for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int t = 32 * bm + acc_row(r, lane);
+          st16(a128(LY, t, v >> 3, true) + 2 * (v & 7), T::from_float(Y[bm][r]));
+          O[bm][r] *= __expf(ldf(LG + 4 * t));
+        }
     }
     __syncthreads();
-    // Block row bi: M_bj = sum_{kb = bj}^{bi - 1} A_{bi,kb} T_{kb,bj}, then
-    // T_{bi,bj} = -T_{bi,bi} M_bj (every M first: A_{bi,bj} is an operand of
-    // the M of smaller bj).  Thread: block bj = tid / 64, row ii, 4 columns.
+    // Block row bi of T: M_bj = sum_{kb = bj}^{bi - 1} A_{bi,kb} T_{kb,bj},
+    // then T_{bi,bj} = -T_{bi,bi} M_bj (every M first: A_{bi,bj} is an
+    // operand of the M of smaller bj).  Threads 0-255: block bj = tid / 64,
+    // row ii, 4 columns.
     {
       const int bj = tid >> 6, ii = (tid >> 2) & 15, j4 = 4 * (tid & 3);
 #pragma unroll
@@ -344,92 +381,58 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
         __syncthreads();
       }
     }
-    // Tw = -T diag(beta exp(G)), Tu = T diag(beta): row tid / 4, columns 16 (tid % 4) .. +15.
+    // Tw = -T diag(beta exp(G)), Tu = T diag(beta): row tid / 8, columns 8 (tid % 8) .. +7.
     {
-      const int i = tid >> 2, j0 = 16 * (tid & 3);
+      const int i = tid >> 3, j0 = 8 * (tid & 7);
+      u32x4 ww, wu;
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        u32x4 ww, wu;
+      for (int x = 0; x < 4; ++x) {
+        float tw[2], tu[2];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float tw[2], tu[2];
-#pragma unroll
-          for (int z = 0; z < 2; ++z) {
-            const int j = j0 + 8 * half + 2 * e + z;
-            const float tij = j <= i ? ldf(LT + 4 * (i * kTfStride + j)) : 0.f;
-            const float bj = ldf(LB + 4 * j);
-            tu[z] = tij * bj;
-            tw[z] = -tij * bj * __expf(ldf(LG + 4 * j));
-          }
-          ww[e] = T::pack2(tw[0], tw[1]);
-          wu[e] = T::pack2(tu[0], tu[1]);
+        for (int z = 0; z < 2; ++z) {
+          const int j = j0 + 2 * x + z;
+          const float tij = j <= i ? ldf(LT + 4 * (i * kTfStride + j)) : 0.f;
+          const float bj = ldf(LB + 4 * j);
+          tu[z] = tij * bj;
+          tw[z] = -tij * bj * __expf(ldf(LG + 4 * j));
         }
-        lds_store_b128(a64(LTw, i, (j0 >> 3) + half), ww);
-        lds_store_b128(a64(LTu, i, (j0 >> 3) + half), wu);
+        ww[x] = T::pack2(tw[0], tw[1]);
+        wu[x] = T::pack2(tu[0], tu[1]);
+      }
+      lds_store_b128(a64(LTw, i, j0 >> 3), ww);
+      lds_store_b128(a64(LTu, i, j0 >> 3), wu);
+    }
+    __syncthreads();
+
+    // ---- D = Tu V + Tw Y: block (bm, bn) = (w / 4, w % 4); D takes V's place.
+    {
+      const int bm = wave >> 2, bn = wave & 3;
+      f32x16 Dv = f32x16{};
+#pragma unroll
+      for (int s = 0; s < kC / 16; ++s) {
+        Dv = T::mfma32x32x16(row_op64(LTu, 32 * bm, s, lane), col_op(LV, 32 * bn, s, lane), Dv);
+        Dv = T::mfma32x32x16(row_op64(LTw, 32 * bm, s, lane), col_op(LY, 32 * bn, s, lane), Dv);
+      }
+      __syncthreads();  // V read by every wave
+      const int v = 32 * bn + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = 32 * bm + acc_row(r, lane);
+        st16(a128(LV, t, v >> 3, true) + 2 * (v & 7), T::from_float(Dv[r]));
       }
     }
     __syncthreads();
 
-    // ---- Y = K S^T and O = Q S^T for value columns 32w .. +31 (both row blocks).
-    f32x16 O[2];
-    {
-      f32x16 Y[2] = {f32x16{}, f32x16{}};
-      O[0] = f32x16{};
-      O[1] = f32x16{};
+    // ---- waves 4-7: O += P D, 16-bit output tile where Q was.
+    if (wave >= 4) {
+      const int bn = wave - 4;
 #pragma unroll
-      for (int s = 0; s < kD / 16; ++s) {
-        const u32x4 sb = row_op(LS, 32 * wave, s, lane, false);  // S^T operand: row v, columns K
+      for (int s = 0; s < kC / 16; ++s) {
+        const u32x4 db = col_op(LV, 32 * bn, s, lane);
 #pragma unroll
-        for (int bm = 0; bm < 2; ++bm) {
-          Y[bm] = T::mfma32x32x16(row_op(LK, 32 * bm, s, lane, true), sb, Y[bm]);
-          O[bm] = T::mfma32x32x16(row_op(LQ, 32 * bm, s, lane, false), sb, O[bm]);
-        }
+        for (int bm = 0; bm < 2; ++bm) O[bm] = T::mfma32x32x16(row_op64(LP, 32 * bm, s, lane), db, O[bm]);
       }
-      const int v = 32 * wave + (lane & 31);
-#pragma unroll
-      for (int bm = 0; bm < 2; ++bm)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int t = 32 * bm + acc_row(r, lane);
-          st16(a128(LT, t, v >> 3, true) + 2 * (v & 7), T::from_float(Y[bm][r]));
-          O[bm][r] *= __expf(ldf(LG + 4 * t));
-        }
-    }
-    __syncthreads();
-
-    // ---- D = Tu V + Tw Y for value columns 32w .. +31.
-    f32x16 Dv[2] = {f32x16{}, f32x16{}};
-#pragma unroll
-    for (int s = 0; s < kC / 16; ++s) {
-      const u32x4 vb = col_op(LV, 32 * wave, s, lane), yb = col_op(LT, 32 * wave, s, lane);
-#pragma unroll
-      for (int bm = 0; bm < 2; ++bm) {
-        Dv[bm] = T::mfma32x32x16(row_op64(LTu, 32 * bm, s, lane), vb, Dv[bm]);
-        Dv[bm] = T::mfma32x32x16(row_op64(LTw, 32 * bm, s, lane), yb, Dv[bm]);
-      }
-    }
-    __syncthreads();  // V and Y read by every wave: D takes V's place
-    {
-      const int v = 32 * wave + (lane & 31);
-#pragma unroll
-      for (int bm = 0; bm < 2; ++bm)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int t = 32 * bm + acc_row(r, lane);
-          st16(a128(LV, t, v >> 3, true) + 2 * (v & 7), T::from_float(Dv[bm][r]));
-        }
-    }
-    __syncthreads();
-
-    // ---- O += P D; 16-bit output tile where Q was, then coalesced stores.
-#pragma unroll
-    for (int s = 0; s < kC / 16; ++s) {
-      const u32x4 db = col_op(LV, 32 * wave, s, lane);
-#pragma unroll
-      for (int bm = 0; bm < 2; ++bm) O[bm] = T::mfma32x32x16(row_op64(LP, 32 * bm, s, lane), db, O[bm]);
-    }
-    {
-      const int v = 32 * wave + (lane & 31);
+      const int v = 32 * bn + (lane & 31);
 #pragma unroll
       for (int bm = 0; bm < 2; ++bm)
 #pragma unroll
@@ -438,46 +441,46 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
           st16(a128(LQ, t, v >> 3, false) + 2 * (v & 7), T::from_float(O[bm][r]));
         }
     }
-    // ---- S <- exp(G_C) S + (diag(exp(G_C - G)) D)^T K.
+    // ---- S <- exp(G_C) S + (diag(exp(G_C - G)) D)^T K, this wave's blocks.
     {
       const float GC = ldf(LG + 4 * (kC - 1));
       const float eC = __expf(GC);
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) S[nb] *= eC;
+      for (int j = 0; j < 2; ++j) S[j] *= eC;
 #pragma unroll
       for (int s = 0; s < kC / 16; ++s) {
-        // A operand: value row v = 32w + l % 32, tokens 16 s + 8 (l / 32) .. +7, scaled.
-        const u32x4 d = col_op(LV, 32 * wave, s, lane);
+        // A operand: value row 32 vb + l % 32, tokens 16 s + 8 (l / 32) .. +7, scaled.
+        const u32x4 d = col_op(LV, 32 * vb, s, lane);
         const int tb = 16 * s + 8 * (lane >> 5);
         u32x4 da;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float f0 = __expf(GC - ldf(LG + 4 * (tb + 2 * e))), f1 = __expf(GC - ldf(LG + 4 * (tb + 2 * e + 1)));
-          da[e] = T::pack2(T::to_float(d[e] & 0xffffu) * f0, T::to_float(d[e] >> 16) * f1);
+        for (int x = 0; x < 4; ++x) {
+          const float f0 = __expf(GC - ldf(LG + 4 * (tb + 2 * x))), f1 = __expf(GC - ldf(LG + 4 * (tb + 2 * x + 1)));
+          da[x] = T::pack2(T::to_float(d[x] & 0xffffu) * f0, T::to_float(d[x] >> 16) * f1);
         }
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) S[nb] = T::mfma32x32x16(da, col_op(LK, 32 * nb, s, lane), S[nb]);
+        for (int j = 0; j < 2; ++j) S[j] = T::mfma32x32x16(da, col_op(LK, 32 * (kb0 + j), s, lane), S[j]);
       }
     }
     __syncthreads();  // every read of S, K and D of this chunk is done; the output tile is complete
     {
-      const int r = tid >> 2, qd = tid & 3;
+      const int r = tid >> 3, e = tid & 7;
       if (r < ck) {
         uint8_t *o = a.out + static_cast<int64_t>(c0 + r) * a.o_rs + hv * kD * 2;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          *reinterpret_cast<u32x4 *>(o + (32 * qd + 8 * j) * 2) = lds_load_b128<0>(a128(LQ, r, 4 * qd + j, false));
+        for (int j = 0; j < 2; ++j)
+          *reinterpret_cast<u32x4 *>(o + (16 * e + 8 * j) * 2) = lds_load_b128<0>(a128(LQ, r, 2 * e + j, false));
       }
     }
-    write_state<T>(LS, S, wave, lane);
+    write_state<T>(LS, S, vb, kb0, lane);
     __syncthreads();  // the next chunk overwrites K, Q, V
   }
   if (has) {
     const int lane = tid0 & 63;
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) st[(32 * wave + acc_row(r, lane)) * kD + 32 * nb + (lane & 31)] = S[nb][r];
+      for (int r = 0; r < 16; ++r) st[(32 * vb + acc_row(r, lane)) * kD + 32 * (kb0 + j) + (lane & 31)] = S[j][r];
   }
 }
 
