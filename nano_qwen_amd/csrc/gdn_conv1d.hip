@@ -11,11 +11,17 @@
 //   y = rnd(sum_j w[c][j] * x[t - K + 1 + j])    (fp32, j = 0 .. K-1 in order)
 //   out = rnd(y / (1 + exp(-y)))
 // with rnd = round to the 16-bit type, as torch computes the bf16 conv and the
-// silu on its bf16 result.  One lane per pair of channels and run of kRun
-// consecutive tokens: the last K - 1 inputs stay in registers (a sliding
-// window), so each token costs one coalesced 4-byte load and one store per
-// lane; the runs of a sequence are independent, so prefill is parallel over
-// tokens too.
+// silu on its bf16 result.
+//
+// Prefill (conv_prefill8, channel counts that are multiples of 8 with
+// 16-byte aligned rows): one lane per 8 channels and run of kRun8 tokens;
+// the lane issues the 16-byte loads of all kRun8 + K - 1 input rows of its
+// run before computing any output, so a wave keeps that many loads in
+// flight, and stores each output row as one 16-byte store.  The runs of a
+// sequence are independent, so prefill is parallel over tokens too.
+// Decode and other channel counts (conv_kernel): one lane per pair of
+// channels and run of kRun tokens, the last K - 1 inputs kept in registers
+// as a sliding window.
 #include "nq_device.hpp"
 
 namespace nq {
@@ -152,6 +158,96 @@ __global__ __launch_bounds__(kThreads) void conv_kernel(const ConvArgs a) {
     }
 }
 
+constexpr int kRun8 = 16;  // tokens per lane and run (prefill, 8 channels per lane)
+
+// Prefill from a zero state, 8 channels per lane (C % 8 == 0, rows 16-byte
+// aligned).  grid.x covers channel groups, grid.y = sequence, grid.z walks
+// the sequence's runs (run z, z + gridDim.z, ...).
+template <class T, int K>
+__global__ __launch_bounds__(kThreads) void conv_prefill8(const ConvArgs a) {
+  const int c = 8 * (blockIdx.x * kThreads + threadIdx.x);
+  if (c >= a.C) return;
+  const int n = blockIdx.y;
+  const int64_t t0 = a.cu[n], t1 = a.cu[n + 1];
+  float w[8][K];
+#pragma unroll
+  for (int ch = 0; ch < 8; ++ch)
+#pragma unroll
+    for (int j = 0; j < K; ++j) w[ch][j] = ld16<T>(a.w, static_cast<int64_t>(c + ch) * K + j);
+  // Eight channels of input position p (zero before the sequence: prefill
+  // starts from a zero state).
+  auto in8 = [&](int64_t p) -> u32x4 {
+    return (p >= t0 && p < t1) ? *reinterpret_cast<const u32x4 *>(a.x + p * a.x_rs + 2 * c) : u32x4{0, 0, 0, 0};
+  };
+  auto unpack = [](const u32x4 &v, int ch) -> float {
+    const uint32_t word = v[ch >> 1];
+    return T::to_float(static_cast<uint16_t>((ch & 1) ? (word >> 16) : (word & 0xffffu)));
+  };
+  const int64_t nrun = (t1 - t0 + kRun8 - 1) / kRun8;
+  for (int64_t run = blockIdx.z; run < nrun; run += gridDim.z) {
+    const int64_t ts = t0 + run * kRun8;
+    u32x4 xin[kRun8 + K - 1];  // input rows ts - K + 1 .. ts + kRun8 - 1
+#pragma unroll
+    for (int i = 0; i < kRun8 + K - 1; ++i) xin[i] = in8(ts - (K - 1) + i);
+#pragma unroll
+    for (int i = 0; i < kRun8; ++i) {
+      const int64_t t = ts + i;
+      float r[8];
+#pragma unroll
+      for (int ch = 0; ch < 8; ++ch) {
+        // The product of two 16-bit values is exact in float32, so the
+        // fused multiply-add rounds exactly as the add after the multiply.
+        float y = 0.f;
+#pragma unroll
+        for (int j = 0; j < K; ++j) y = __builtin_fmaf(w[ch][j], unpack(xin[i + j], ch), y);
+        y = rnd16<T>(y);
+        // silu with the hardware exp2 and reciprocal (about 1 ulp each);
+        // the result is rounded to 16 bits.
+        r[ch] = y * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(y * -1.4426950408889634f));
+      }
+      u32x4 o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float r0 = r[2 * q], r1 = r[2 * q + 1];
+        asm("" : "+v"(r0), "+v"(r1));
+        o[q] = T::pack2(r0, r1);
+      }
+      if (t < t1) __builtin_nontemporal_store(o, reinterpret_cast<u32x4 *>(a.out + t * a.o_rs + 2 * c));
+    }
+  }
+  // The state after the sequence: its last K - 1 inputs (zero before it).
+  const int32_t slot = a.idx[n];
+  if (slot < 0 || slot >= a.num_slots || blockIdx.z != 0) return;
+  uint16_t *sp = reinterpret_cast<uint16_t *>(a.state) + static_cast<int64_t>(slot) * a.C * (K - 1);
+#pragma unroll
+  for (int j = 0; j < K - 1; ++j) {
+    const u32x4 v = in8(t1 - (K - 1) + j);
+#pragma unroll
+    for (int ch = 0; ch < 8; ++ch)
+      sp[static_cast<int64_t>(c + ch) * (K - 1) + j] = static_cast<uint16_t>((ch & 1) ? (v[ch >> 1] >> 16) : (v[ch >> 1] & 0xffffu));
+  }
+}
+
+template <class T, int K>
+int launch_prefill8(const ConvArgs &g, hipStream_t s) {
+  const int groups = g.C / 8;
+  dim3 grid((groups + kThreads - 1) / kThreads, g.N, 64);  // 64 runs at a time
+  conv_prefill8<T, K><<<grid, kThreads, 0, s>>>(g);
+  return check_launch("gdn_conv1d");
+}
+template <class T>
+int launch_prefill8_k(const ConvArgs &g, hipStream_t s) {
+  switch (g.K) {
+    case 2: return launch_prefill8<T, 2>(g, s);
+    case 3: return launch_prefill8<T, 3>(g, s);
+    case 4: return launch_prefill8<T, 4>(g, s);
+    case 5: return launch_prefill8<T, 5>(g, s);
+    case 6: return launch_prefill8<T, 6>(g, s);
+    case 7: return launch_prefill8<T, 7>(g, s);
+    default: return launch_prefill8<T, 8>(g, s);
+  }
+}
+
 }  // namespace
 }  // namespace nq
 
@@ -186,10 +282,13 @@ extern "C" int nq_gdn_conv1d(const void *x, int64_t x_row_stride, const void *we
   g.C = channels;
   g.K = kernel_size;
   g.N = num_seqs;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (cu_seqlens && channels % 8 == 0 && aligned(x, 16) && aligned(out, 16) && (x_row_stride * 2) % 16 == 0 &&
+      (out_row_stride * 2) % 16 == 0)
+    return dtype == NQ_BF16 ? launch_prefill8_k<BF16>(g, s) : launch_prefill8_k<F16>(g, s);
   // Channel pairs over grid.x; the tokens of a prefill sequence over grid.z.
   const int pairs = (channels + 1) / 2;
   dim3 grid((pairs + kThreads - 1) / kThreads, num_seqs, cu_seqlens ? 64 : 1);  // 64 runs at a time
-  hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == NQ_BF16) conv_kernel<BF16><<<grid, kThreads, 0, s>>>(g);
   else conv_kernel<F16><<<grid, kThreads, 0, s>>>(g);
   return check_launch("gdn_conv1d");

@@ -221,34 +221,39 @@ def test_gated_rmsnorm_matches_oracle(cuda, dtype, d):
     assert int(ulps.max()) <= 1 and float((ulps > 0).float().mean()) <= 5e-3
 
 
-def test_conv1d_decode_and_prefill(cuda):
+@pytest.mark.parametrize("C,K,bf", [(1000, 4, torch.bfloat16), (1004, 4, torch.bfloat16), (2048, 3, torch.float16),
+                                    (4096, 2, torch.bfloat16), (512, 8, torch.bfloat16)])
+def test_conv1d_decode_and_prefill(cuda, C, K, bf):
     """Prefill of packed sequences from zero state, then decode steps on the
     pooled state: outputs within one ulp of the oracle on <= 0.5% of elements
     (exp's last bit is free), states bit-exact; prefill(L) then decode equals
-    prefill(L + 1)'s last output."""
+    prefill(L + 1)'s last output.  Channel counts that are multiples of 8
+    take the 8-channels-per-lane prefill kernel (runs of 16 tokens: the
+    lengths cover a run's edges), 1004 the channel-pair one."""
     g = torch.Generator().manual_seed(9)
-    C, K, bf = 1000, 4, torch.bfloat16
-    lens = [1, 2, 7, 130]
+    lens = [1, 2, 7, 130, 16, 17, 33]
     cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32)
     T = int(cu[-1])
     x = (torch.randn(T, C, generator=g) * 2).to(bf)
     w = (torch.randn(C, 1, K, generator=g) * 0.5).to(bf)
-    state = torch.zeros(6, C, K - 1, dtype=bf)
-    idx = torch.tensor([4, 0, -1, 2], dtype=torch.int32)
+    state = torch.zeros(9, C, K - 1, dtype=bf)
+    idx = torch.tensor([4, 0, -1, 2, 7, 8, 5], dtype=torch.int32)
     st_dev = state.clone().to(cuda)
     out = kernels.gdn_conv1d(x.to(cuda), w.to(cuda), st_dev, idx.to(cuda), cu_seqlens=cu.to(cuda))
     torch.cuda.synchronize()
     ref_state = state.float().numpy()
-    ref = gdn.conv1d_silu(x.float().numpy(), w.reshape(C, K).float().numpy(), ref_state, idx.numpy(), cu.numpy())
+    dt = "bf16" if bf == torch.bfloat16 else "f16"
+    ref = gdn.conv1d_silu(x.float().numpy(), w.reshape(C, K).float().numpy(), ref_state, idx.numpy(), cu.numpy(),
+                          dtype=dt)
     key = lambda t: (lambda b: torch.where(b < 0, -(b + 32768), b))(t.contiguous().view(torch.int16).int())
     ulps = (key(out.cpu()) - key(torch.from_numpy(ref).to(bf))).abs()
     assert int(ulps.max()) <= 1 and float((ulps > 0).float().mean()) <= 5e-3
     assert torch.equal(st_dev.cpu().float(), torch.from_numpy(ref_state))
-    # decode: one new token for each of the 4 sequences
-    xd = (torch.randn(4, C, generator=g) * 2).to(bf)
+    # decode: one new token for each sequence
+    xd = (torch.randn(len(lens), C, generator=g) * 2).to(bf)
     od = kernels.gdn_conv1d(xd.to(cuda), w.to(cuda), st_dev, idx.to(cuda))
     torch.cuda.synchronize()
-    refd = gdn.conv1d_silu(xd.float().numpy(), w.reshape(C, K).float().numpy(), ref_state, idx.numpy())
+    refd = gdn.conv1d_silu(xd.float().numpy(), w.reshape(C, K).float().numpy(), ref_state, idx.numpy(), dtype=dt)
     live = idx >= 0
     ulps = (key(od.cpu()[live]) - key(torch.from_numpy(refd).to(bf)[live])).abs()
     assert int(ulps.max()) <= 1 and float((ulps > 0).float().mean()) <= 5e-3
