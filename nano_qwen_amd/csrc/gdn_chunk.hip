@@ -29,8 +29,9 @@
 // products that read it; every product runs on v_mfma_f32_32x32x16 with
 // 16-bit operands and float32 accumulation, as the reference's kernels do
 // (their tl.dot operands are the input dtype).  The 64x64 triangular inverse
-// runs in float32 on the VALU of waves 0-3, blocked in 16x16 diagonal
-// blocks, while waves 4-7 form K S^T and Q S^T, which do not depend on it.
+// runs in float32: its four 16x16 diagonal blocks on the VALU of waves 0-3
+// while waves 4-7 form K S^T and Q S^T, which do not depend on it, then the
+// off-diagonal blocks as float32 products (v_mfma_f32_16x16x4f32).
 //
 // LDS tiles are row-major with 16-byte chunks XOR-swizzled per row: tiles
 // read only as row operands (ds_read_b128) use swz_r, tiles also read down
@@ -72,7 +73,7 @@ constexpr int kOffTw = kOffT + kC * kTfStride * 4;
 constexpr int kOffTu = kOffTw + kC * kC * 2;  // 64 x 64 16-bit, swz_6
 constexpr int kOffP = kOffTu + kC * kC * 2;
 constexpr int kOffG = kOffP + kC * kC * 2;    // G[64], beta[64] (fp32)
-constexpr int kOffM = kOffG + 2 * kC * 4;     // 3 x 16 x 16 fp32: off-diagonal products of the inverse
+constexpr int kOffM = kOffG + 2 * kC * 4;     // 3 x 16 x 16 fp32: one product M per block column of the inverse
 constexpr int kOffY = kOffM + 3 * 256 * 4;    // Y = K S^T, 64 x 128 16-bit, swz_c
 constexpr int kLds = kOffY + kTile;
 static_assert(kLds <= 160 * 1024, "LDS");
@@ -151,6 +152,14 @@ __device__ inline void write_state(uint32_t s_base, const f32x16 (&S)[2], int vb
     }
 }
 
+// Workgroup barrier after this wave's LDS writes complete, without the
+// fence of __syncthreads(), which would also wait for the next chunk's
+// global loads in flight and the output stores.
+__device__ inline void lds_sync() {
+  wait_lgkmcnt0();
+  raw_barrier();
+}
+
 template <class T>
 __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -209,6 +218,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
     int tid = tid0;
     asm volatile("" : "+v"(tid));
     const int lane = tid & 63;
+    const int wv = tid >> 6;  // the wave index for addresses (branches use the uniform `wave`)
     // ---- unit keys, scaled unit queries (float32 norms, rounded to 16
     // bits) and values into LDS; gates and their inclusive sum G.
     {
@@ -269,7 +279,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
       stf(LB + 4 * lane, beta);
     }
     if (c0 + kC < t1) fetch(c0 + kC, tid);  // in flight while this chunk computes
-    __syncthreads();
+    lds_sync();
 
     // ---- waves 0-3: K K^T -> A (fp32); waves 4-7: Q K^T -> P (16-bit);
     // block (bm, bn) = ((w / 2) % 2, w % 2).
@@ -296,7 +306,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
           stf(LT + 4 * (i * kTfStride + j), j < i ? ldf(LB + 4 * i) * dec * acc[r] : 0.f);
       }
     }
-    __syncthreads();
+    lds_sync();
 
     // ---- waves 0-3: the four 16x16 diagonal blocks of T = (I + A)^-1 by
     // forward substitution (lane = column); waves 4-7: Y = K S^T (to LDS)
@@ -304,7 +314,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
     f32x16 O[2];
     if (wave < 4) {
       if (lane < 16) {
-        const int b0 = 16 * wave, c = lane;
+        const int b0 = 16 * wv, c = lane;
         float x[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -344,43 +354,47 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
           O[bm][r] *= __expf(ldf(LG + 4 * t));
         }
     }
-    __syncthreads();
-    // Block row bi of T: M_bj = sum_{kb = bj}^{bi - 1} A_{bi,kb} T_{kb,bj},
-    // then T_{bi,bj} = -T_{bi,bi} M_bj (every M first: A_{bi,bj} is an
-    // operand of the M of smaller bj).  Threads 0-255: block bj = tid / 64,
-    // row ii, 4 columns.
-    {
-      const int bj = tid >> 6, ii = (tid >> 2) & 15, j4 = 4 * (tid & 3);
+    lds_sync();
+    // Off-diagonal blocks of T, one block column per wave (waves 0-2):
+    // wave bj forms T_{bi,bj} = -T_{bi,bi} sum_{kb = bj}^{bi - 1} A_{bi,kb} T_{kb,bj}
+    // for bi = bj + 1 .. 3 as float32 products (v_mfma_f32_16x16x4f32).
+    // Every operand is a diagonal block, a block of A or an earlier block of
+    // the wave's own column, so the block rows need no barrier.  T_{bi,bj} is
+    // stored at block position (bj, bi) of the array (its unused upper
+    // triangle): A's lower blocks, operands of the other columns, stay intact.
+    if (wave < 3) {
+      const int bj = wv;
+      auto blk = [&](int r, int c) { return LT + 4 * (16 * r * kTfStride + 16 * c); };
+      // acc + X Y for 16x16 float32 blocks X, Y (row strides xs, ys floats):
+      // k-slice q takes X[l % 16][4q + l / 16] and Y[4q + l / 16][l % 16].
+      auto prod = [&](uint32_t x, int xs, uint32_t y, int ys, f32x4 acc) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float av = ldf(x + 4 * ((lane & 15) * xs + 4 * q + (lane >> 4)));
+          const float bv = ldf(y + 4 * ((4 * q + (lane >> 4)) * ys + (lane & 15)));
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+        }
+        return acc;
+      };
+      const uint32_t lm = LM + 4 * 256 * bj;
 #pragma unroll
       for (int bi = 1; bi < 4; ++bi) {
-        if (bj < bi) {
-          f32x4 m = f32x4{0, 0, 0, 0};
+        if (bi <= bj) continue;
+        f32x4 m = f32x4{0, 0, 0, 0};
 #pragma unroll
-          for (int kb = 0; kb < bi; ++kb) {
-            if (kb < bj) continue;
+        for (int kb = 0; kb < bi; ++kb)
+          if (kb >= bj) m = prod(blk(bi, kb), kTfStride, kb == bj ? blk(bj, bj) : blk(bj, kb), kTfStride, m);
+        // M (accumulator element r of lane l: row 4 (l / 16) + r, column
+        // l % 16) through LDS into operand layout; the wave's own write and
+        // read, in order.
 #pragma unroll
-            for (int x4 = 0; x4 < 16; x4 += 4) {
-              const f32x4 av = ldf4(LT + 4 * ((16 * bi + ii) * kTfStride + 16 * kb + x4));
+        for (int r = 0; r < 4; ++r) stf(lm + 4 * ((4 * (lane >> 4) + r) * 16 + (lane & 15)), m[r]);
+        const f32x4 t = prod(blk(bi, bi), kTfStride, lm, 16, f32x4{0, 0, 0, 0});
 #pragma unroll
-              for (int x = 0; x < 4; ++x) m += av[x] * ldf4(LT + 4 * ((16 * kb + x4 + x) * kTfStride + 16 * bj + j4));
-            }
-          }
-          stf4(LM + 4 * (256 * bj + 16 * ii + j4), m);
-        }
-        __syncthreads();
-        if (bj < bi) {
-          f32x4 t = f32x4{0, 0, 0, 0};
-#pragma unroll
-          for (int x4 = 0; x4 < 16; x4 += 4) {
-            const f32x4 tv = ldf4(LT + 4 * ((16 * bi + ii) * kTfStride + 16 * bi + x4));
-#pragma unroll
-            for (int x = 0; x < 4; ++x) t -= tv[x] * ldf4(LM + 4 * (256 * bj + 16 * (x4 + x) + j4));
-          }
-          stf4(LT + 4 * ((16 * bi + ii) * kTfStride + 16 * bj + j4), t);
-        }
-        __syncthreads();
+        for (int r = 0; r < 4; ++r) stf(blk(bj, bi) + 4 * ((4 * (lane >> 4) + r) * kTfStride + (lane & 15)), -t[r]);
       }
     }
+    lds_sync();
     // Tw = -T diag(beta exp(G)), Tu = T diag(beta): row tid / 8, columns 8 (tid % 8) .. +7.
     {
       const int i = tid >> 3, j0 = 8 * (tid & 7);
@@ -391,7 +405,12 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
 #pragma unroll
         for (int z = 0; z < 2; ++z) {
           const int j = j0 + 2 * x + z;
-          const float tij = j <= i ? ldf(LT + 4 * (i * kTfStride + j)) : 0.f;
+          // T[i][j]: a diagonal block in place, an off-diagonal one at the
+          // transposed block position
+          const int bi_ = i >> 4, bj_ = j >> 4;
+          const float tij = j > i ? 0.f
+                                  : ldf(bj_ == bi_ ? LT + 4 * (i * kTfStride + j)
+                                                   : LT + 4 * ((16 * bj_ + (i & 15)) * kTfStride + 16 * bi_ + (j & 15)));
           const float bj = ldf(LB + 4 * j);
           tu[z] = tij * bj;
           tw[z] = -tij * bj * __expf(ldf(LG + 4 * j));
@@ -402,7 +421,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
       lds_store_b128(a64(LTw, i, j0 >> 3), ww);
       lds_store_b128(a64(LTu, i, j0 >> 3), wu);
     }
-    __syncthreads();
+    lds_sync();
 
     // ---- D = Tu V + Tw Y: block (bm, bn) = (w / 4, w % 4); D takes V's place.
     {
@@ -413,7 +432,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
         Dv = T::mfma32x32x16(row_op64(LTu, 32 * bm, s, lane), col_op(LV, 32 * bn, s, lane), Dv);
         Dv = T::mfma32x32x16(row_op64(LTw, 32 * bm, s, lane), col_op(LY, 32 * bn, s, lane), Dv);
       }
-      __syncthreads();  // V read by every wave
+      lds_sync();  // V read by every wave
       const int v = 32 * bn + (lane & 31);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -421,7 +440,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
         st16(a128(LV, t, v >> 3, true) + 2 * (v & 7), T::from_float(Dv[r]));
       }
     }
-    __syncthreads();
+    lds_sync();
 
     // ---- waves 4-7: O += P D, 16-bit output tile where Q was.
     if (wave >= 4) {
@@ -462,7 +481,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
         for (int j = 0; j < 2; ++j) S[j] = T::mfma32x32x16(da, col_op(LK, 32 * (kb0 + j), s, lane), S[j]);
       }
     }
-    __syncthreads();  // every read of S, K and D of this chunk is done; the output tile is complete
+    lds_sync();  // every read of S, K and D of this chunk is done; the output tile is complete
     {
       const int r = tid >> 3, e = tid & 7;
       if (r < ck) {
@@ -473,7 +492,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
       }
     }
     write_state<T>(LS, S, vb, kb0, lane);
-    __syncthreads();  // the next chunk overwrites K, Q, V
+    lds_sync();  // the next chunk overwrites K, Q, V
   }
   if (has) {
     const int lane = tid0 & 63;
