@@ -72,9 +72,9 @@ constexpr int kOffT = kOffS + kD * kD * 2;   // A, then T (fp32 64 x 68)
 constexpr int kOffTw = kOffT + kC * kTfStride * 4;
 constexpr int kOffTu = kOffTw + kC * kC * 2;  // 64 x 64 16-bit, swz_6
 constexpr int kOffP = kOffTu + kC * kC * 2;
-constexpr int kOffG = kOffP + kC * kC * 2;    // G[64], beta[64] (fp32)
-constexpr int kOffM = kOffG + 2 * kC * 4;     // 3 x 16 x 16 fp32: one product M per block column of the inverse
-constexpr int kOffY = kOffM + 3 * 256 * 4;    // Y = K S^T, 64 x 128 16-bit, swz_c
+constexpr int kOffG = kOffP + kC * kC * 2;    // G, beta, exp(G), exp(G_C - G): 64 fp32 each
+constexpr int kOffM = kOffG + 4 * kC * 4;     // 4 x 16 x 16 fp32: block products of the inverse
+constexpr int kOffY = kOffM + 4 * 256 * 4;    // Y = K S^T, 64 x 128 16-bit, swz_c
 constexpr int kLds = kOffY + kTile;
 static_assert(kLds <= 160 * 1024, "LDS");
 
@@ -134,9 +134,53 @@ __device__ inline int acc_row(int r, int lane) { return (r & 3) + 4 * (lane >> 5
 
 __device__ inline float softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
 
+template <int CTRL, int ROW_MASK>
+__device__ inline float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, false));
+}
+// Sum over the 8 lanes of an aligned group (xor 1, xor 2 within quads, then
+// the mirrored quad); every lane of the group gets the same bits.
+__device__ inline float sum8(float v) {
+  v += dpp_f<0xb1, 0xf>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_f<0x4e, 0xf>(v);   // quad_perm [2, 3, 0, 1]
+  return v + dpp_f<0x141, 0xf>(v);  // row_half_mirror
+}
+// Inclusive prefix sum over the wave: shifts by 1, 2, 4, 8 within each
+// 16-lane row, then each row's running total into the rows after it
+// (row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3); lanes
+// whose source is out of range add 0.
+__device__ inline float wave_scan(float v) {
+  v += dpp_f<0x111, 0xf>(v);  // row_shr:1
+  v += dpp_f<0x112, 0xf>(v);  // row_shr:2
+  v += dpp_f<0x114, 0xf>(v);  // row_shr:4
+  v += dpp_f<0x118, 0xf>(v);  // row_shr:8
+  v += dpp_f<0x142, 0xa>(v);  // row_bcast:15
+  return v + dpp_f<0x143, 0xc>(v);  // row_bcast:31
+}
+
 template <class T>
 __device__ inline f32x4 unpack2x2(uint32_t w0, uint32_t w1) {
   return f32x4{T::to_float(w0 & 0xffffu), T::to_float(w0 >> 16), T::to_float(w1 & 0xffffu), T::to_float(w1 >> 16)};
+}
+
+// acc + X Y for 16x16 float32 blocks in LDS (row strides xs, ys floats) on
+// v_mfma_f32_16x16x4f32: k-slice q takes X[l % 16][4q + l / 16] and
+// Y[4q + l / 16][l % 16]; element r of lane l of the result is row
+// 4 (l / 16) + r, column l % 16.
+__device__ inline f32x4 prod16(uint32_t x, int xs, uint32_t y, int ys, f32x4 acc, int lane) {
+  float av[4], bv[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    av[q] = ldf(x + 4 * ((lane & 15) * xs + 4 * q + (lane >> 4)));
+    bv[q] = ldf(y + 4 * ((4 * q + (lane >> 4)) * ys + (lane & 15)));
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[q], bv[q], acc, 0, 0, 0);
+  return acc;
+}
+__device__ inline void store16x16(uint32_t base, int stride, const f32x4 &v, float sign, int lane) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) stf(base + 4 * ((4 * (lane >> 4) + r) * stride + (lane & 15)), sign * v[r]);
 }
 
 // 16-bit copy of a wave's state blocks (value rows 32 vb .. +31, key
@@ -165,9 +209,10 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t L = lds_addr(smem);
   const uint32_t LK = L + kOffK, LQ = L + kOffQ, LV = L + kOffV, LS = L + kOffS, LT = L + kOffT, LTw = L + kOffTw,
-                 LTu = L + kOffTu, LP = L + kOffP, LG = L + kOffG, LB = L + kOffG + kC * 4, LM = L + kOffM,
-                 LY = L + kOffY;
-  const int tid0 = threadIdx.x, wave = tid0 >> 6;
+                 LTu = L + kOffTu, LP = L + kOffP, LG = L + kOffG, LB = LG + kC * 4, LEG = LB + kC * 4,
+                 LEC = LEG + kC * 4, LM = L + kOffM, LY = L + kOffY;
+  const int tid0 = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid0 >> 6);  // uniform: branches on it are scalar
   const int hv = blockIdx.x, n = blockIdx.y;
   const int h = hv / (a.HV / a.H);
   const int t0 = a.cu[n], t1 = a.cu[n + 1];
@@ -191,16 +236,23 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
   // 16 (tid % 8) .. +15) of q, k, v, and (wave 0) lane's gate inputs.
   u32x4 qv[2], kv[2], vv[2];
   uint32_t gab = 0;  // a (low half) and b (high half) of token lane
+  // Through buffer descriptors over the chunk's rows of this head: rows past
+  // the sequence are out of range and read as zeros.
   auto fetch = [&](int c0, int tid) {
     const int r = tid >> 3, e = tid & 7;
-    const bool ok = r < t1 - c0;
-    const int64_t t = c0 + r;
+    const int rows = min(kC, t1 - c0);
+    const auto rq = make_rsrc(a.q + static_cast<int64_t>(c0) * a.q_rs + h * kD * 2,
+                              static_cast<uint32_t>((rows - 1) * a.q_rs + kD * 2));
+    const auto rk = make_rsrc(a.k + static_cast<int64_t>(c0) * a.k_rs + h * kD * 2,
+                              static_cast<uint32_t>((rows - 1) * a.k_rs + kD * 2));
+    const auto rv = make_rsrc(a.v + static_cast<int64_t>(c0) * a.v_rs + hv * kD * 2,
+                              static_cast<uint32_t>((rows - 1) * a.v_rs + kD * 2));
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int col = 16 * e + 8 * j;
-      qv[j] = ok ? *reinterpret_cast<const u32x4 *>(a.q + t * a.q_rs + (h * kD + col) * 2) : u32x4{0, 0, 0, 0};
-      kv[j] = ok ? *reinterpret_cast<const u32x4 *>(a.k + t * a.k_rs + (h * kD + col) * 2) : u32x4{0, 0, 0, 0};
-      vv[j] = ok ? *reinterpret_cast<const u32x4 *>(a.v + t * a.v_rs + (hv * kD + col) * 2) : u32x4{0, 0, 0, 0};
+      const int col2 = (16 * e + 8 * j) * 2;
+      qv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, r * static_cast<int>(a.q_rs) + col2, 0, 0));
+      kv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, r * static_cast<int>(a.k_rs) + col2, 0, 0));
+      vv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, r * static_cast<int>(a.v_rs) + col2, 0, 0));
     }
     if (tid < 64) {
       const int64_t tg = c0 + tid;
@@ -242,12 +294,9 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
         sq += fq[x] * fq[x];
         sk += fk[x] * fk[x];
       }
-#pragma unroll
-      for (int off = 1; off < 8; off <<= 1) {
-        sq += __shfl_xor(sq, off, 64);
-        sk += __shfl_xor(sk, off, 64);
-      }
-      const float rq = a.scale / sqrtf(sq + a.eps), rk = 1.0f / sqrtf(sk + a.eps);
+      sq = sum8(sq);
+      sk = sum8(sk);
+      const float rq = a.scale * __builtin_amdgcn_rsqf(sq + a.eps), rk = __builtin_amdgcn_rsqf(sk + a.eps);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         u32x4 wq, wk;
@@ -270,51 +319,76 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
         g = neg_a * softplus(ga + dtb);
         beta = 1.0f / (1.0f + expf(-gb));
       }
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float y = __shfl_up(g, off, 64);
-        if (lane >= off) g += y;
-      }
+      g = wave_scan(g);
+      // G_C = G of the chunk's last token (tokens past the sequence add 0)
+      const float gc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, g), 63));
       stf(LG + 4 * lane, g);
       stf(LB + 4 * lane, beta);
+      stf(LEG + 4 * lane, __expf(g));
+      stf(LEC + 4 * lane, __expf(gc - g));
     }
     if (c0 + kC < t1) fetch(c0 + kC, tid);  // in flight while this chunk computes
     lds_sync();
 
     // ---- waves 0-3: K K^T -> A (fp32); waves 4-7: Q K^T -> P (16-bit);
-    // block (bm, bn) = ((w / 2) % 2, w % 2).
+    // block (bm, bn) = ((w / 2) % 2, w % 2).  Each wave's LDS reads are
+    // issued together ahead of their uses, so their latencies overlap.
     {
-      const int bm = (wave >> 1) & 1, bn = wave & 1;
-      const bool qk = wave >= 4;
+      const int bm = (wv >> 1) & 1, bn = wv & 1;
       f32x16 acc = f32x16{};
 #pragma unroll
-      for (int s = 0; s < kD / 16; ++s) {
-        const u32x4 kb = row_op(LK, 32 * bn, s, lane, true);
-        const u32x4 ab = qk ? row_op(LQ, 32 * bm, s, lane, false) : row_op(LK, 32 * bm, s, lane, true);
-        acc = T::mfma32x32x16(ab, kb, acc);
-      }
-      const int j = 32 * bn + (lane & 31);
-      const float Gj = ldf(LG + 4 * j);
+      for (int h2 = 0; h2 < 2; ++h2) {  // two halves of the 8 k-steps
+        u32x4 kb[4], ab[4];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int i = 32 * bm + acc_row(r, lane);
-        const float Gi = ldf(LG + 4 * i);
-        const float dec = __expf(j <= i ? Gi - Gj : 0.f);
-        if (qk)
+        for (int s4 = 0; s4 < 4; ++s4) {
+          kb[s4] = row_op(LK, 32 * bn, 4 * h2 + s4, lane, true);
+          ab[s4] = wave < 4 ? row_op(LK, 32 * bm, 4 * h2 + s4, lane, true) : row_op(LQ, 32 * bm, 4 * h2 + s4, lane, false);
+        }
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) acc = T::mfma32x32x16(ab[s4], kb[s4], acc);
+      }
+      // rows i = 32 bm + acc_row(r): four runs of 4 consecutive rows
+      const int j = 32 * bn + (lane & 31);
+      const int i0 = 32 * bm + 4 * (lane >> 5);
+      const float Gj = ldf(LG + 4 * j);
+      f32x4 Gi[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) Gi[q] = ldf4(LG + 4 * (i0 + 8 * q));
+      if (wave < 4) {
+        f32x4 Bi[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) Bi[q] = ldf4(LB + 4 * (i0 + 8 * q));
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int i = i0 + (r & 3) + 8 * (r >> 2);
+          const float dec = __expf(j <= i ? Gi[r >> 2][r & 3] - Gj : 0.f);
+          stf(LT + 4 * (i * kTfStride + j), j < i ? Bi[r >> 2][r & 3] * dec * acc[r] : 0.f);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int i = i0 + (r & 3) + 8 * (r >> 2);
+          const float dec = __expf(j <= i ? Gi[r >> 2][r & 3] - Gj : 0.f);
           st16(a64(LP, i, j >> 3) + 2 * (j & 7), T::from_float(j <= i ? dec * acc[r] : 0.f));
-        else
-          stf(LT + 4 * (i * kTfStride + j), j < i ? ldf(LB + 4 * i) * dec * acc[r] : 0.f);
+        }
       }
     }
     lds_sync();
 
-    // ---- waves 0-3: the four 16x16 diagonal blocks of T = (I + A)^-1 by
-    // forward substitution (lane = column); waves 4-7: Y = K S^T (to LDS)
-    // and O = diag(exp(G)) Q S^T for value columns 32 (w - 4) .. +31.
+    // ---- T = (I + A)^-1 in float32, by halves: T_A and T_B, the inverses of
+    // the two diagonal 32x32 halves, and the lower-left half
+    // X = -T_B A_BA T_A.  Waves 0 and 1 invert the diagonal 16x16 blocks
+    // 2w and 2w + 1 by forward substitution (lane = block and column), then
+    // the block between them, T_{2w+1,2w} = -T_{2w+1,2w+1} A_{2w+1,2w} T_{2w,2w};
+    // waves 4-7 meanwhile form Y = K S^T (to LDS) and O = diag(exp(G)) Q S^T
+    // for value columns 32 (w - 4) .. +31.  An off-diagonal block T_{i,j} is
+    // stored at block position (j, i), the unused upper triangle, so A's
+    // lower blocks stay intact.
     f32x16 O[2];
-    if (wave < 4) {
-      if (lane < 16) {
-        const int b0 = 16 * wv, c = lane;
+    auto blk = [&](int r, int c) { return LT + 4 * (16 * r * kTfStride + 16 * c); };
+    if (wave < 2) {
+      if (lane < 32) {
+        const int b0 = 16 * (2 * wv + (lane >> 4)), c = lane & 15;
         float x[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -330,19 +404,37 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
 #pragma unroll
         for (int i = 0; i < 16; ++i) stf(LT + 4 * ((b0 + i) * kTfStride + b0 + c), x[i]);
       }
-    } else {
-      const int bn = wave - 4;
+      // the wave's own LDS writes and reads, in order
+      const int d = 2 * wv;
+      const uint32_t lm = LM + 4 * 256 * wv;
+      store16x16(lm, 16, prod16(blk(d + 1, d), kTfStride, blk(d, d), kTfStride, f32x4{0, 0, 0, 0}, lane), 1.f, lane);
+      store16x16(blk(d, d + 1), kTfStride, prod16(blk(d + 1, d + 1), kTfStride, lm, 16, f32x4{0, 0, 0, 0}, lane), -1.f,
+                 lane);
+    } else if (wave >= 4) {
+      const int bn = wv - 4;
       f32x16 Y[2] = {f32x16{}, f32x16{}};
       O[0] = f32x16{};
       O[1] = f32x16{};
+      // operands of two k-steps at a time, read ahead of their products
 #pragma unroll
-      for (int s = 0; s < kD / 16; ++s) {
-        const u32x4 sb = row_op(LS, 32 * bn, s, lane, false);  // S^T operand: row v, columns K
+      for (int s = 0; s < kD / 16; s += 2) {
+        u32x4 sb[2], kr[2][2], qr[2][2];
 #pragma unroll
-        for (int bm = 0; bm < 2; ++bm) {
-          Y[bm] = T::mfma32x32x16(row_op(LK, 32 * bm, s, lane, true), sb, Y[bm]);
-          O[bm] = T::mfma32x32x16(row_op(LQ, 32 * bm, s, lane, false), sb, O[bm]);
+        for (int u = 0; u < 2; ++u) {
+          sb[u] = row_op(LS, 32 * bn, s + u, lane, false);  // S^T operand: row v, columns K
+#pragma unroll
+          for (int bm = 0; bm < 2; ++bm) {
+            kr[u][bm] = row_op(LK, 32 * bm, s + u, lane, true);
+            qr[u][bm] = row_op(LQ, 32 * bm, s + u, lane, false);
+          }
         }
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int bm = 0; bm < 2; ++bm) {
+            Y[bm] = T::mfma32x32x16(kr[u][bm], sb[u], Y[bm]);
+            O[bm] = T::mfma32x32x16(qr[u][bm], sb[u], O[bm]);
+          }
       }
       const int v = 32 * bn + (lane & 31);
 #pragma unroll
@@ -351,48 +443,26 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
         for (int r = 0; r < 16; ++r) {
           const int t = 32 * bm + acc_row(r, lane);
           st16(a128(LY, t, v >> 3, true) + 2 * (v & 7), T::from_float(Y[bm][r]));
-          O[bm][r] *= __expf(ldf(LG + 4 * t));
+          O[bm][r] *= ldf(LEG + 4 * t);
         }
     }
     lds_sync();
-    // Off-diagonal blocks of T, one block column per wave (waves 0-2):
-    // wave bj forms T_{bi,bj} = -T_{bi,bi} sum_{kb = bj}^{bi - 1} A_{bi,kb} T_{kb,bj}
-    // for bi = bj + 1 .. 3 as float32 products (v_mfma_f32_16x16x4f32).
-    // Every operand is a diagonal block, a block of A or an earlier block of
-    // the wave's own column, so the block rows need no barrier.  T_{bi,bj} is
-    // stored at block position (bj, bi) of the array (its unused upper
-    // triangle): A's lower blocks, operands of the other columns, stay intact.
-    if (wave < 3) {
-      const int bj = wv;
-      auto blk = [&](int r, int c) { return LT + 4 * (16 * r * kTfStride + 16 * c); };
-      // acc + X Y for 16x16 float32 blocks X, Y (row strides xs, ys floats):
-      // k-slice q takes X[l % 16][4q + l / 16] and Y[4q + l / 16][l % 16].
-      auto prod = [&](uint32_t x, int xs, uint32_t y, int ys, f32x4 acc) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float av = ldf(x + 4 * ((lane & 15) * xs + 4 * q + (lane >> 4)));
-          const float bv = ldf(y + 4 * ((4 * q + (lane >> 4)) * ys + (lane & 15)));
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
-        }
-        return acc;
-      };
-      const uint32_t lm = LM + 4 * 256 * bj;
-#pragma unroll
-      for (int bi = 1; bi < 4; ++bi) {
-        if (bi <= bj) continue;
-        f32x4 m = f32x4{0, 0, 0, 0};
-#pragma unroll
-        for (int kb = 0; kb < bi; ++kb)
-          if (kb >= bj) m = prod(blk(bi, kb), kTfStride, kb == bj ? blk(bj, bj) : blk(bj, kb), kTfStride, m);
-        // M (accumulator element r of lane l: row 4 (l / 16) + r, column
-        // l % 16) through LDS into operand layout; the wave's own write and
-        // read, in order.
-#pragma unroll
-        for (int r = 0; r < 4; ++r) stf(lm + 4 * ((4 * (lane >> 4) + r) * 16 + (lane & 15)), m[r]);
-        const f32x4 t = prod(blk(bi, bi), kTfStride, lm, 16, f32x4{0, 0, 0, 0});
-#pragma unroll
-        for (int r = 0; r < 4; ++r) stf(blk(bj, bi) + 4 * ((4 * (lane >> 4) + r) * kTfStride + (lane & 15)), -t[r]);
-      }
+    // Lower-left half: waves 0-3 each own block (p, q) = (2 + w / 2, w % 2),
+    // Y_pq = sum_r A_{p,r} T_{r,q} (r = q, 1), then X_pq = -sum_r T_{p,r} Y_{r,q}
+    // (r = 2 .. p).
+    if (wave < 4) {
+      const int p = 2 + (wv >> 1), q = wv & 1;
+      f32x4 y = prod16(blk(p, 1), kTfStride, q == 1 ? blk(1, 1) : blk(0, 1), kTfStride, f32x4{0, 0, 0, 0}, lane);
+      if (q == 0) y = prod16(blk(p, 0), kTfStride, blk(0, 0), kTfStride, y, lane);
+      store16x16(LM + 4 * 256 * wv, 16, y, 1.f, lane);
+    }
+    lds_sync();
+    if (wave < 4) {
+      const int p = 2 + (wv >> 1), q = wv & 1;
+      // Y_{2,q} is block q of LM, Y_{3,q} block 2 + q
+      f32x4 x = prod16(p == 2 ? blk(2, 2) : blk(2, 3), kTfStride, LM + 4 * 256 * q, 16, f32x4{0, 0, 0, 0}, lane);
+      if (p == 3) x = prod16(blk(3, 3), kTfStride, LM + 4 * 256 * (2 + q), 16, x, lane);
+      store16x16(blk(q, p), kTfStride, x, -1.f, lane);
     }
     lds_sync();
     // Tw = -T diag(beta exp(G)), Tu = T diag(beta): row tid / 8, columns 8 (tid % 8) .. +7.
@@ -413,7 +483,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
                                                    : LT + 4 * ((16 * bj_ + (i & 15)) * kTfStride + 16 * bi_ + (j & 15)));
           const float bj = ldf(LB + 4 * j);
           tu[z] = tij * bj;
-          tw[z] = -tij * bj * __expf(ldf(LG + 4 * j));
+          tw[z] = -tij * bj * ldf(LEG + 4 * j);
         }
         ww[x] = T::pack2(tw[0], tw[1]);
         wu[x] = T::pack2(tu[0], tu[1]);
@@ -425,12 +495,20 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
 
     // ---- D = Tu V + Tw Y: block (bm, bn) = (w / 4, w % 4); D takes V's place.
     {
-      const int bm = wave >> 2, bn = wave & 3;
+      const int bm = wv >> 2, bn = wv & 3;
       f32x16 Dv = f32x16{};
+      u32x4 tu[4], tw[4], vc[4], yc[4];
 #pragma unroll
       for (int s = 0; s < kC / 16; ++s) {
-        Dv = T::mfma32x32x16(row_op64(LTu, 32 * bm, s, lane), col_op(LV, 32 * bn, s, lane), Dv);
-        Dv = T::mfma32x32x16(row_op64(LTw, 32 * bm, s, lane), col_op(LY, 32 * bn, s, lane), Dv);
+        tu[s] = row_op64(LTu, 32 * bm, s, lane);
+        vc[s] = col_op(LV, 32 * bn, s, lane);
+        tw[s] = row_op64(LTw, 32 * bm, s, lane);
+        yc[s] = col_op(LY, 32 * bn, s, lane);
+      }
+#pragma unroll
+      for (int s = 0; s < kC / 16; ++s) {
+        Dv = T::mfma32x32x16(tu[s], vc[s], Dv);
+        Dv = T::mfma32x32x16(tw[s], yc[s], Dv);
       }
       lds_sync();  // V read by every wave
       const int v = 32 * bn + (lane & 31);
@@ -444,13 +522,18 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
 
     // ---- waves 4-7: O += P D, 16-bit output tile where Q was.
     if (wave >= 4) {
-      const int bn = wave - 4;
+      const int bn = wv - 4;
+      u32x4 db[4], pr[4][2];
 #pragma unroll
       for (int s = 0; s < kC / 16; ++s) {
-        const u32x4 db = col_op(LV, 32 * bn, s, lane);
+        db[s] = col_op(LV, 32 * bn, s, lane);
 #pragma unroll
-        for (int bm = 0; bm < 2; ++bm) O[bm] = T::mfma32x32x16(row_op64(LP, 32 * bm, s, lane), db, O[bm]);
+        for (int bm = 0; bm < 2; ++bm) pr[s][bm] = row_op64(LP, 32 * bm, s, lane);
       }
+#pragma unroll
+      for (int s = 0; s < kC / 16; ++s)
+#pragma unroll
+        for (int bm = 0; bm < 2; ++bm) O[bm] = T::mfma32x32x16(pr[s][bm], db[s], O[bm]);
       const int v = 32 * bn + (lane & 31);
 #pragma unroll
       for (int bm = 0; bm < 2; ++bm)
@@ -462,23 +545,34 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
     }
     // ---- S <- exp(G_C) S + (diag(exp(G_C - G)) D)^T K, this wave's blocks.
     {
-      const float GC = ldf(LG + 4 * (kC - 1));
-      const float eC = __expf(GC);
+      const float eC = ldf(LEG + 4 * (kC - 1));
 #pragma unroll
       for (int j = 0; j < 2; ++j) S[j] *= eC;
+      // two k-steps at a time: operands and factors read ahead of the products
 #pragma unroll
-      for (int s = 0; s < kC / 16; ++s) {
-        // A operand: value row 32 vb + l % 32, tokens 16 s + 8 (l / 32) .. +7, scaled.
-        const u32x4 d = col_op(LV, 32 * vb, s, lane);
-        const int tb = 16 * s + 8 * (lane >> 5);
-        u32x4 da;
+      for (int s = 0; s < kC / 16; s += 2) {
+        u32x4 d[2], kc[2][2];
+        f32x4 f[2][2];
 #pragma unroll
-        for (int x = 0; x < 4; ++x) {
-          const float f0 = __expf(GC - ldf(LG + 4 * (tb + 2 * x))), f1 = __expf(GC - ldf(LG + 4 * (tb + 2 * x + 1)));
-          da[x] = T::pack2(T::to_float(d[x] & 0xffffu) * f0, T::to_float(d[x] >> 16) * f1);
+        for (int u = 0; u < 2; ++u) {
+          // A operand: value row 32 vb + l % 32, tokens 16 (s + u) + 8 (l / 32) .. +7, scaled.
+          d[u] = col_op(LV, 32 * vb, s + u, lane);
+          const int tb = 16 * (s + u) + 8 * (lane >> 5);
+          f[u][0] = ldf4(LEC + 4 * tb);
+          f[u][1] = ldf4(LEC + 4 * (tb + 4));
+#pragma unroll
+          for (int j = 0; j < 2; ++j) kc[u][j] = col_op(LK, 32 * (kb0 + j), s + u, lane);
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j) S[j] = T::mfma32x32x16(da, col_op(LK, 32 * (kb0 + j), s, lane), S[j]);
+        for (int u = 0; u < 2; ++u) {
+          u32x4 da;
+#pragma unroll
+          for (int x = 0; x < 4; ++x)
+            da[x] = T::pack2(T::to_float(d[u][x] & 0xffffu) * f[u][x >> 1][2 * (x & 1)],
+                             T::to_float(d[u][x] >> 16) * f[u][x >> 1][2 * (x & 1) + 1]);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) S[j] = T::mfma32x32x16(da, kc[u][j], S[j]);
+        }
       }
     }
     lds_sync();  // every read of S, K and D of this chunk is done; the output tile is complete
