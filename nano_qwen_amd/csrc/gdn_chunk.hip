@@ -390,16 +390,28 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
       if (lane < 32) {
         const int b0 = 16 * (2 * wv + (lane >> 4)), c = lane & 15;
         float x[16];
+        // four rows at a time: their A values are read together, then
+        // consumed; two partial sums per row shorten the dependent chain
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float acc = i == c ? 1.f : 0.f;
+        for (int g = 0; g < 4; ++g) {
+          f32x4 av[4][4];
 #pragma unroll
-          for (int j4 = 0; j4 < i; j4 += 4) {
-            const f32x4 av = ldf4(LT + 4 * ((b0 + i) * kTfStride + b0 + j4));
+          for (int ii = 0; ii < 4; ++ii)
 #pragma unroll
-            for (int j = j4; j < j4 + 4 && j < i; ++j) acc -= av[j - j4] * x[j];
+            for (int jc = 0; jc <= g; ++jc) av[ii][jc] = ldf4(LT + 4 * ((b0 + 4 * g + ii) * kTfStride + b0 + 4 * jc));
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            const int i = 4 * g + ii;
+            float acc0 = i == c ? 1.f : 0.f, acc1 = 0.f;
+#pragma unroll
+            for (int j = 0; j < i; ++j) {
+              if (j & 1)
+                acc1 -= av[ii][j >> 2][j & 3] * x[j];
+              else
+                acc0 -= av[ii][j >> 2][j & 3] * x[j];
+            }
+            x[i] = i < c ? 0.f : acc0 + acc1;
           }
-          x[i] = i < c ? 0.f : acc;
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) stf(LT + 4 * ((b0 + i) * kTfStride + b0 + c), x[i]);
@@ -437,13 +449,19 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
           }
       }
       const int v = 32 * bn + (lane & 31);
+      // exp(G) of the rows: runs of 4 consecutive tokens at 8q + 4 (l / 32)
+      f32x4 eg[2][4];
+#pragma unroll
+      for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) eg[bm][q] = ldf4(LEG + 4 * (32 * bm + 8 * q + 4 * (lane >> 5)));
 #pragma unroll
       for (int bm = 0; bm < 2; ++bm)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int t = 32 * bm + acc_row(r, lane);
           st16(a128(LY, t, v >> 3, true) + 2 * (v & 7), T::from_float(Y[bm][r]));
-          O[bm][r] *= ldf(LEG + 4 * t);
+          O[bm][r] *= eg[bm][r >> 2][r & 3];
         }
     }
     lds_sync();
