@@ -57,9 +57,11 @@ struct ChunkArgs {
   uint8_t *out;  // [T, HV, V]
   int64_t o_rs;
   const int32_t *cu;
-  int H, HV, from_slot;
+  int H, HV, from_slot, num_seqs;
   float eps, scale;
 };
+
+constexpr int kSortSeqs = 64;  // batches up to this size run their longest sequences first
 
 // LDS layout (bytes).
 constexpr int kTile = kC * kD * 2;           // 64 x 128 16-bit values
@@ -213,7 +215,29 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
                  LEC = LEG + kC * 4, LM = L + kOffM, LY = L + kOffY;
   const int tid0 = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid0 >> 6);  // uniform: branches on it are scalar
-  const int hv = blockIdx.x, n = blockIdx.y;
+  const int hv = blockIdx.x;
+  // Workgroups start in grid order and a sequence's chunks run one after
+  // another, so the longest sequences go first (row y of the grid takes the
+  // sequence of rank y by length, ties by index); wave 0 ranks them.
+  int n = blockIdx.y;
+  if (a.num_seqs <= kSortSeqs) {
+    if (wave == 0) {
+      const int lane = tid0 & 63;
+      const int len = lane < a.num_seqs ? a.cu[lane + 1] - a.cu[lane] : -1;
+      int rank = 0;
+      for (int s2 = 0; s2 < a.num_seqs; ++s2) {
+        const int l2 = __builtin_amdgcn_readlane(len, s2);
+        rank += (l2 > len || (l2 == len && s2 < lane)) ? 1 : 0;
+      }
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < a.num_seqs && rank == static_cast<int>(blockIdx.y));
+      if (lane == 0) *reinterpret_cast<__attribute__((address_space(3))) int *>(static_cast<uintptr_t>(L + kOffM)) =
+          static_cast<int>(__builtin_ctzll(hit));
+    }
+    lds_sync();
+    n = __builtin_amdgcn_readfirstlane(
+        *reinterpret_cast<const __attribute__((address_space(3))) int *>(static_cast<uintptr_t>(L + kOffM)));
+    lds_sync();  // read by every wave before the region is reused
+  }
   const int h = hv / (a.HV / a.H);
   const int t0 = a.cu[n], t1 = a.cu[n + 1];
   const int slot = a.idx[n];
@@ -645,6 +669,7 @@ int launch_gdn_chunk_prefill(const void *q, int64_t q_rs, const void *k, int64_t
   c.cu = cu;
   c.H = H;
   c.HV = HV;
+  c.num_seqs = num_seqs;
   c.from_slot = from_slot;
   c.eps = 1e-6f;
   c.scale = 1.0f / sqrtf(static_cast<float>(kD));

@@ -384,3 +384,29 @@ def test_gdn_prefill_empty_sequences(cuda):
         for slot in (5, 1, 4):   # the empty sequences' slots
             want = c["state"][slot] if from_slot else torch.zeros(4, 128, 128)
             assert torch.equal(state_dev[slot].cpu(), want)
+
+
+@pytest.mark.parametrize("nseq", [63, 64, 65, 90])
+def test_gdn_prefill_batch_orders(cuda, nseq):
+    """Batches of up to 64 sequences run longest first (the kernel ranks them
+    by length, ties by index), larger ones in index order: both sides of that
+    bound, with equal lengths among the sequences, against the float64
+    chunked form on the device."""
+    rng = np.random.default_rng(nseq)
+    lens = [int(x) for x in rng.integers(1, 140, nseq)]
+    lens[3] = lens[7] = lens[11] = 129  # ties
+    H, HV = 2, 4
+    c = _prefill_inputs(lens, H, HV, seed=nseq, slots=nseq + 3)
+    idx = torch.randperm(nseq + 3, generator=torch.Generator().manual_seed(nseq))[:nseq].to(torch.int32)
+    print(f"[gdn] prefill {nseq} sequences, {sum(lens)} tokens", flush=True)
+    d = {k: v.to(cuda) for k, v in c.items()}
+    state_dev = d["state"].clone()
+    out = kernels.gdn_prefill(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt"], d["cu"], state_dev,
+                              idx.to(cuda), initial_state_from_slot=True)
+    ref_state = d["state"].double().clone()
+    ref = gdn.gdn_prefill_chunked(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt"], c["cu"], ref_state,
+                                  idx, from_slot=True)
+    torch.cuda.synchronize()
+    live = idx.tolist()
+    _prefill_close(out.double().cpu().numpy(), ref.cpu().numpy(), state_dev.double().cpu().numpy()[live],
+                   ref_state.cpu().numpy()[live])
