@@ -67,16 +67,17 @@ constexpr int kSortSeqs = 64;  // batches up to this size run their longest sequ
 constexpr int kTile = kC * kD * 2;           // 64 x 128 16-bit values
 constexpr int kOffK = 0;                     // K (unit keys), swz_c
 constexpr int kOffQ = kOffK + kTile;         // Q (scaled unit queries), swz_r; then the output tile
-constexpr int kOffV = kOffQ + kTile;         // V, swz_c; then D
-constexpr int kOffS = kOffV + kTile;         // S, 16-bit [V][K], swz_r
+constexpr int kOffV = kOffQ + kTile;         // V, swz_c; then D^T ([V][T], 128 x 64, swz_6)
+constexpr int kOffS = kOffV + kTile;         // S^T, 16-bit [K][V], swz_c
 constexpr int kTfStride = 68;                // floats per row of the fp32 64x64 matrix
 constexpr int kOffT = kOffS + kD * kD * 2;   // A, then T (fp32 64 x 68)
 constexpr int kOffTw = kOffT + kC * kTfStride * 4;
 constexpr int kOffTu = kOffTw + kC * kC * 2;  // 64 x 64 16-bit, swz_6
 constexpr int kOffP = kOffTu + kC * kC * 2;
-constexpr int kOffG = kOffP + kC * kC * 2;    // G, beta, exp(G), exp(G_C - G): 64 fp32 each
-constexpr int kOffM = kOffG + 4 * kC * 4;     // 4 x 16 x 16 fp32: block products of the inverse
-constexpr int kOffY = kOffM + 4 * 256 * 4;    // Y = K S^T, 64 x 128 16-bit, swz_c
+constexpr int kGates = 4 * kC * 4;            // G, beta, exp(G), exp(G_C - G): 64 fp32 each
+constexpr int kOffG = kOffP + kC * kC * 2;    // two gate sets: this chunk's and the next one's
+constexpr int kOffM = kOffG + 2 * kGates;     // 4 x 16 x 16 fp32: block products of the inverse
+constexpr int kOffY = kOffM + 4 * 256 * 4;    // Y^T = S K^T, [V][T] 128 x 64 16-bit, swz_6
 constexpr int kLds = kOffY + kTile;
 static_assert(kLds <= 160 * 1024, "LDS");
 
@@ -185,17 +186,30 @@ __device__ inline void store16x16(uint32_t base, int stride, const f32x4 &v, flo
   for (int r = 0; r < 4; ++r) stf(base + 4 * ((4 * (lane >> 4) + r) * stride + (lane & 15)), sign * v[r]);
 }
 
+__device__ inline void lds_store_b64(uint32_t addr, const u32x2 &v) {
+  *reinterpret_cast<__attribute__((address_space(3))) u32x2 *>(static_cast<uintptr_t>(addr)) = v;
+}
+// 16-bit copy of a 32x32 accumulator block, transposed: element
+// (m0 + acc_row(r, l), n0 + l % 32) goes to tile row n0 + l % 32, column
+// m0 + acc_row(r, l).  Each lane's runs of 4 consecutive M rows become
+// 8-byte writes.  The tile has 128 columns (swz_c) or 64 (swz_6).
+template <class T>
+__device__ inline void st_acc_t(uint32_t tile, bool c128, int m0, int n0, const f32x16 &acc, int lane) {
+  const int row = n0 + (lane & 31);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int col = m0 + 8 * q + 4 * (lane >> 5);
+    const u32x2 w = u32x2{T::pack2(acc[4 * q], acc[4 * q + 1]), T::pack2(acc[4 * q + 2], acc[4 * q + 3])};
+    const uint32_t ca = c128 ? a128(tile, row, col >> 3, true) : a64(tile, row, col >> 3);
+    lds_store_b64(ca + 2 * (col & 7), w);
+  }
+}
 // 16-bit copy of a wave's state blocks (value rows 32 vb .. +31, key
-// columns 32 kb0 .. +63) into the S tile.
+// columns 32 kb0 .. +63) into the S^T tile ([K][V], swz_c).
 template <class T>
 __device__ inline void write_state(uint32_t s_base, const f32x16 (&S)[2], int vb, int kb0, int lane) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int v = 32 * vb + acc_row(r, lane), kc = 32 * (kb0 + j) + (lane & 31);
-      st16(a128(s_base, v, kc >> 3, false) + 2 * (kc & 7), T::from_float(S[j][r]));
-    }
+  for (int j = 0; j < 2; ++j) st_acc_t<T>(s_base, true, 32 * vb, 32 * (kb0 + j), S[j], lane);
 }
 
 // Workgroup barrier after this wave's LDS writes complete, without the
@@ -211,8 +225,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t L = lds_addr(smem);
   const uint32_t LK = L + kOffK, LQ = L + kOffQ, LV = L + kOffV, LS = L + kOffS, LT = L + kOffT, LTw = L + kOffTw,
-                 LTu = L + kOffTu, LP = L + kOffP, LG = L + kOffG, LB = LG + kC * 4, LEG = LB + kC * 4,
-                 LEC = LEG + kC * 4, LM = L + kOffM, LY = L + kOffY;
+                 LTu = L + kOffTu, LP = L + kOffP, LM = L + kOffM, LY = L + kOffY;
   const int tid0 = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid0 >> 6);  // uniform: branches on it are scalar
   const int hv = blockIdx.x;
@@ -285,8 +298,35 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
                           : 0u;
     }
   };
-  if (t1 > t0) fetch(t0, tid0);
+  // Gates of the chunk whose inputs gab holds (wave 0; lane = token): G, the
+  // in-chunk inclusive sum of the log decays, beta, exp(G) and exp(G_C - G)
+  // into gate set `set`.
+  auto gates = [&](int ck, int set) {
+    const int lane = tid0 & 63;
+    const uint32_t g0 = L + kOffG + set * kGates;
+    float g = 0.f, beta = 0.f;
+    if (lane < ck) {
+      const float ga = T::to_float(static_cast<uint16_t>(gab & 0xffffu));
+      const float gb = T::to_float(static_cast<uint16_t>(gab >> 16));
+      g = neg_a * softplus(ga + dtb);
+      beta = 1.0f / (1.0f + expf(-gb));
+    }
+    g = wave_scan(g);
+    // G_C = G of the chunk's last token (tokens past the sequence add 0)
+    const float gc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, g), 63));
+    stf(g0 + 4 * lane, g);
+    stf(g0 + 4 * (kC + lane), beta);
+    stf(g0 + 4 * (2 * kC + lane), __expf(g));
+    stf(g0 + 4 * (3 * kC + lane), __expf(gc - g));
+  };
+  if (t1 > t0) {
+    fetch(t0, tid0);
+    if (wave == 0) gates(min(kC, t1 - t0), 0);
+  }
   for (int c0 = t0; c0 < t1; c0 += kC) {
+    // this chunk's gate set (the next chunk's is written during this one)
+    const int gset = ((c0 - t0) / kC) & 1;
+    const uint32_t LG = L + kOffG + gset * kGates, LB = LG + kC * 4, LEG = LB + kC * 4, LEC = LEG + kC * 4;
     const int ck = min(kC, t1 - c0);
     // The thread index from an instruction the compiler cannot hoist: the
     // hundreds of LDS addresses derived from it are recomputed per chunk
@@ -334,22 +374,6 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
         lds_store_b128(a128(LK, r, chunk, true), wk);
         lds_store_b128(a128(LV, r, chunk, true), vv[j]);
       }
-    }
-    if (wave == 0) {
-      float g = 0.f, beta = 0.f;
-      if (lane < ck) {
-        const float ga = T::to_float(static_cast<uint16_t>(gab & 0xffffu));
-        const float gb = T::to_float(static_cast<uint16_t>(gab >> 16));
-        g = neg_a * softplus(ga + dtb);
-        beta = 1.0f / (1.0f + expf(-gb));
-      }
-      g = wave_scan(g);
-      // G_C = G of the chunk's last token (tokens past the sequence add 0)
-      const float gc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, g), 63));
-      stf(LG + 4 * lane, g);
-      stf(LB + 4 * lane, beta);
-      stf(LEG + 4 * lane, __expf(g));
-      stf(LEC + 4 * lane, __expf(gc - g));
     }
     if (c0 + kC < t1) fetch(c0 + kC, tid);  // in flight while this chunk computes
     lds_sync();
@@ -457,7 +481,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
         u32x4 sb[2], kr[2][2], qr[2][2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          sb[u] = row_op(LS, 32 * bn, s + u, lane, false);  // S^T operand: row v, columns K
+          sb[u] = col_op(LS, 32 * bn, s + u, lane);  // S^T operand: keys of column v of the [K][V] tile
 #pragma unroll
           for (int bm = 0; bm < 2; ++bm) {
             kr[u][bm] = row_op(LK, 32 * bm, s + u, lane, true);
@@ -472,7 +496,6 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
             O[bm] = T::mfma32x32x16(qr[u][bm], sb[u], O[bm]);
           }
       }
-      const int v = 32 * bn + (lane & 31);
       // exp(G) of the rows: runs of 4 consecutive tokens at 8q + 4 (l / 32)
       f32x4 eg[2][4];
 #pragma unroll
@@ -480,13 +503,11 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
 #pragma unroll
         for (int q = 0; q < 4; ++q) eg[bm][q] = ldf4(LEG + 4 * (32 * bm + 8 * q + 4 * (lane >> 5)));
 #pragma unroll
-      for (int bm = 0; bm < 2; ++bm)
+      for (int bm = 0; bm < 2; ++bm) {
+        st_acc_t<T>(LY, false, 32 * bm, 32 * bn, Y[bm], lane);  // Y^T: [V][T]
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int t = 32 * bm + acc_row(r, lane);
-          st16(a128(LY, t, v >> 3, true) + 2 * (v & 7), T::from_float(Y[bm][r]));
-          O[bm][r] *= eg[bm][r >> 2][r & 3];
-        }
+        for (int r = 0; r < 16; ++r) O[bm][r] *= eg[bm][r >> 2][r & 3];
+      }
     }
     lds_sync();
     // Lower-left half: waves 0-3 each own block (p, q) = (2 + w / 2, w % 2),
@@ -507,25 +528,29 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
       store16x16(blk(q, p), kTfStride, x, -1.f, lane);
     }
     lds_sync();
-    // Tw = -T diag(beta exp(G)), Tu = T diag(beta): row tid / 8, columns 8 (tid % 8) .. +7.
+    // Tw = -T diag(beta exp(G)), Tu = T diag(beta): row tid / 8, columns 8 (tid % 8) .. +7,
+    // which lie in one block of T: a diagonal block in place (zero above its
+    // diagonal), a lower one at the transposed block position, an upper one
+    // zero.
     {
       const int i = tid >> 3, j0 = 8 * (tid & 7);
+      const int bi_ = i >> 4, bj_ = j0 >> 4;
+      const uint32_t src = bj_ == bi_ ? LT + 4 * (i * kTfStride + j0)
+                                      : LT + 4 * ((16 * bj_ + (i & 15)) * kTfStride + 16 * bi_ + (j0 & 15));
+      f32x4 t4[2] = {ldf4(src), ldf4(src + 16)};
+      if (bj_ > bi_) t4[0] = t4[1] = f32x4{0, 0, 0, 0};
+      const f32x4 b4[2] = {ldf4(LB + 4 * j0), ldf4(LB + 4 * j0 + 16)};
+      const f32x4 e4[2] = {ldf4(LEG + 4 * j0), ldf4(LEG + 4 * j0 + 16)};
       u32x4 ww, wu;
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
         float tw[2], tu[2];
 #pragma unroll
         for (int z = 0; z < 2; ++z) {
-          const int j = j0 + 2 * x + z;
-          // T[i][j]: a diagonal block in place, an off-diagonal one at the
-          // transposed block position
-          const int bi_ = i >> 4, bj_ = j >> 4;
-          const float tij = j > i ? 0.f
-                                  : ldf(bj_ == bi_ ? LT + 4 * (i * kTfStride + j)
-                                                   : LT + 4 * ((16 * bj_ + (i & 15)) * kTfStride + 16 * bi_ + (j & 15)));
-          const float bj = ldf(LB + 4 * j);
-          tu[z] = tij * bj;
-          tw[z] = -tij * bj * ldf(LEG + 4 * j);
+          const int e = 2 * x + z;
+          const float tb = t4[e >> 2][e & 3] * b4[e >> 2][e & 3];
+          tu[z] = tb;
+          tw[z] = -tb * e4[e >> 2][e & 3];
         }
         ww[x] = T::pack2(tw[0], tw[1]);
         wu[x] = T::pack2(tu[0], tu[1]);
@@ -545,7 +570,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
         tu[s] = row_op64(LTu, 32 * bm, s, lane);
         vc[s] = col_op(LV, 32 * bn, s, lane);
         tw[s] = row_op64(LTw, 32 * bm, s, lane);
-        yc[s] = col_op(LY, 32 * bn, s, lane);
+        yc[s] = row_op64(LY, 32 * bn, s, lane);
       }
 #pragma unroll
       for (int s = 0; s < kC / 16; ++s) {
@@ -553,12 +578,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
         Dv = T::mfma32x32x16(tw[s], yc[s], Dv);
       }
       lds_sync();  // V read by every wave
-      const int v = 32 * bn + (lane & 31);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int t = 32 * bm + acc_row(r, lane);
-        st16(a128(LV, t, v >> 3, true) + 2 * (v & 7), T::from_float(Dv[r]));
-      }
+      st_acc_t<T>(LV, false, 32 * bm, 32 * bn, Dv, lane);  // D^T: [V][T]
     }
     lds_sync();
 
@@ -568,7 +588,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
       u32x4 db[4], pr[4][2];
 #pragma unroll
       for (int s = 0; s < kC / 16; ++s) {
-        db[s] = col_op(LV, 32 * bn, s, lane);
+        db[s] = row_op64(LV, 32 * bn, s, lane);
 #pragma unroll
         for (int bm = 0; bm < 2; ++bm) pr[s][bm] = row_op64(LP, 32 * bm, s, lane);
       }
@@ -598,7 +618,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           // A operand: value row 32 vb + l % 32, tokens 16 (s + u) + 8 (l / 32) .. +7, scaled.
-          d[u] = col_op(LV, 32 * vb, s + u, lane);
+          d[u] = row_op64(LV, 32 * vb, s + u, lane);
           const int tb = 16 * (s + u) + 8 * (lane >> 5);
           f[u][0] = ldf4(LEC + 4 * tb);
           f[u][1] = ldf4(LEC + 4 * (tb + 4));
@@ -617,6 +637,9 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
         }
       }
     }
+    // wave 0: the next chunk's gates (its inputs arrived with the prefetch),
+    // into the other gate set, while waves 4-7 finish the output
+    if (wave == 0 && c0 + kC < t1) gates(min(kC, t1 - c0 - kC), gset ^ 1);
     lds_sync();  // every read of S, K and D of this chunk is done; the output tile is complete
     {
       const int r = tid >> 3, e = tid & 7;
