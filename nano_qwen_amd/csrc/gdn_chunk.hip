@@ -582,7 +582,8 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
     }
     lds_sync();
 
-    // ---- waves 4-7: O += P D, 16-bit output tile where Q was.
+    // ---- waves 4-7: O += P D, stored as 16-bit values straight from the
+    // accumulators (rows past the sequence fall outside the descriptor).
     if (wave >= 4) {
       const int bn = wv - 4;
       u32x4 db[4], pr[4][2];
@@ -596,14 +597,18 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
       for (int s = 0; s < kC / 16; ++s)
 #pragma unroll
         for (int bm = 0; bm < 2; ++bm) O[bm] = T::mfma32x32x16(pr[s][bm], db[s], O[bm]);
-      const int v = 32 * bn + (lane & 31);
+      const auto ro = make_rsrc(a.out + static_cast<int64_t>(c0) * a.o_rs + hv * kD * 2,
+                                static_cast<uint32_t>((ck - 1) * a.o_rs + kD * 2));
+      // row t = 32 bm + (r & 3) + 8 (r >> 2) + 4 (l / 32): the lane's part in the
+      // vector offset, the rest (uniform) in the scalar one
+      const int ors = static_cast<int>(a.o_rs);
+      const int voff = 4 * (lane >> 5) * ors + 2 * (32 * bn + (lane & 31));
 #pragma unroll
       for (int bm = 0; bm < 2; ++bm)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int t = 32 * bm + acc_row(r, lane);
-          st16(a128(LQ, t, v >> 3, false) + 2 * (v & 7), T::from_float(O[bm][r]));
-        }
+        for (int r = 0; r < 16; ++r)
+          __builtin_amdgcn_raw_buffer_store_b16(T::from_float(O[bm][r]), ro, voff,
+                                                (32 * bm + (r & 3) + 8 * (r >> 2)) * ors, 0);
     }
     // ---- S <- exp(G_C) S + (diag(exp(G_C - G)) D)^T K, this wave's blocks.
     {
@@ -640,18 +645,9 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
     // wave 0: the next chunk's gates (its inputs arrived with the prefetch),
     // into the other gate set, while waves 4-7 finish the output
     if (wave == 0 && c0 + kC < t1) gates(min(kC, t1 - c0 - kC), gset ^ 1);
-    lds_sync();  // every read of S, K and D of this chunk is done; the output tile is complete
-    {
-      const int r = tid >> 3, e = tid & 7;
-      if (r < ck) {
-        uint8_t *o = a.out + static_cast<int64_t>(c0 + r) * a.o_rs + hv * kD * 2;
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          *reinterpret_cast<u32x4 *>(o + (16 * e + 8 * j) * 2) = lds_load_b128<0>(a128(LQ, r, 2 * e + j, false));
-      }
-    }
+    // The S^T tile was last read by the Y and Q S^T products, barriers ago.
     write_state<T>(LS, S, vb, kb0, lane);
-    lds_sync();  // the next chunk overwrites K, Q, V
+    lds_sync();  // the next chunk overwrites K, Q, V; every read of K and D of this chunk is done
   }
   if (has) {
     const int lane = tid0 & 63;
