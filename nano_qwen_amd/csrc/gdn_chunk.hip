@@ -73,7 +73,7 @@ constexpr int kTfStride = 68;                // floats per row of the fp32 64x64
 constexpr int kOffT = kOffS + kD * kD * 2;   // A, then T (fp32 64 x 68)
 constexpr int kOffTw = kOffT + kC * kTfStride * 4;
 constexpr int kOffTu = kOffTw + kC * kC * 2;  // 64 x 64 16-bit, swz_6
-constexpr int kOffP = kOffTu + kC * kC * 2;
+constexpr int kOffP = kOffTu + kC * kC * 2;  // P^T [j][i], swz_6
 constexpr int kGates = 4 * kC * 4;            // G, beta, exp(G), exp(G_C - G): 64 fp32 each
 constexpr int kOffG = kOffP + kC * kC * 2;    // two gate sets: this chunk's and the next one's
 constexpr int kOffM = kOffG + 2 * kGates;     // 4 x 16 x 16 fp32: block products of the inverse
@@ -128,6 +128,17 @@ __device__ inline u32x4 col_op(uint32_t base, int c0, int s, int lane) {
   const int chunk = (c0 >> 3) + 2 * (grp & 1) + ((i & 3) >> 1);
   const uint32_t lo_a = a128(base, row, chunk, true) + 8 * (i & 1);
   const uint32_t hi_a = a128(base, row + 4, chunk, true) + 8 * (i & 1);
+  const u32x2 lo = lds_load_tr16<0>(lo_a), hi = lds_load_tr16<0>(hi_a);
+  return u32x4{lo[0], lo[1], hi[0], hi[1]};
+}
+
+// The same from a 64-column tile (swz_6).
+__device__ inline u32x4 col_op64(uint32_t base, int c0, int s, int lane) {
+  const int i = lane & 15, grp = lane >> 4;
+  const int row = 16 * s + 8 * (lane >> 5) + (i >> 2);
+  const int chunk = (c0 >> 3) + 2 * (grp & 1) + ((i & 3) >> 1);
+  const uint32_t lo_a = a64(base, row, chunk) + 8 * (i & 1);
+  const uint32_t hi_a = a64(base, row + 4, chunk) + 8 * (i & 1);
   const u32x2 lo = lds_load_tr16<0>(lo_a), hi = lds_load_tr16<0>(hi_a);
   return u32x4{lo[0], lo[1], hi[0], hi[1]};
 }
@@ -413,12 +424,15 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
           stf(LT + 4 * (i * kTfStride + j), j < i ? Bi[r >> 2][r & 3] * dec * acc[r] : 0.f);
         }
       } else {
+        // P^T ([j][i], 8-byte writes), read back by columns as P D's row operand
+        f32x16 pv;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int i = i0 + (r & 3) + 8 * (r >> 2);
           const float dec = __expf(j <= i ? Gi[r >> 2][r & 3] - Gj : 0.f);
-          st16(a64(LP, i, j >> 3) + 2 * (j & 7), T::from_float(j <= i ? dec * acc[r] : 0.f));
+          pv[r] = j <= i ? dec * acc[r] : 0.f;
         }
+        st_acc_t<T>(LP, false, 32 * bm, 32 * bn, pv, lane);
       }
     }
     lds_sync();
@@ -591,7 +605,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
       for (int s = 0; s < kC / 16; ++s) {
         db[s] = row_op64(LV, 32 * bn, s, lane);
 #pragma unroll
-        for (int bm = 0; bm < 2; ++bm) pr[s][bm] = row_op64(LP, 32 * bm, s, lane);
+        for (int bm = 0; bm < 2; ++bm) pr[s][bm] = col_op64(LP, 32 * bm, s, lane);
       }
 #pragma unroll
       for (int s = 0; s < kC / 16; ++s)
