@@ -102,13 +102,20 @@ __device__ inline uint32_t fp8x4(float a, float b, float c, float d) {
 // ---------------------------------------------------------------- output gate
 // Qwen3.5's attention output gate (models/qwen3_5.py:141-142) as eager torch
 // computes it on 16-bit tensors: out = rnd(rnd(o) * rnd(sigmoid(g))), with
-// sigmoid(g) = 1 / (1 + exp(-g)) in fp32 and rnd = round to T.  The empty
-// asm statements keep each rounding separate (the compiler would otherwise
-// fold a product and its narrowing into one mixed-precision instruction).
+// sigmoid(g) = 1 / (1 + exp(-g)) in fp32 and rnd = round to T.  The sigmoid
+// uses the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32, about one
+// fp32 ulp each; 1 / (1 + 2^(-g log2 e)), exact at g = +-inf): it differs
+// from the correctly rounded fp32 sigmoid by a few fp32 ulps, which moves
+// rnd(sigmoid) by one 16-bit ulp only for values within those few ulps of a
+// rounding boundary -- about 1e-4 of the elements -- at a quarter of the
+// instructions of expf and an IEEE division (the gate is evaluated for every
+// output element of a fused store).  The empty asm statements keep each
+// rounding separate (the compiler would otherwise fold a product and its
+// narrowing into one mixed-precision instruction).
 template <class T>
 __device__ inline float gate_one(float o, uint32_t g16) {
   const float gf = T::to_float(static_cast<uint16_t>(g16));
-  float sg = 1.0f / (1.0f + expf(-gf));
+  float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gf * -1.4426950408889634f));
   asm("" : "+v"(sg));
   asm("" : "+v"(o));
   const float sr = T::to_float(T::from_float(sg));
