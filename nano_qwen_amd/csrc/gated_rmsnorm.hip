@@ -58,7 +58,11 @@ __global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint8_t *
   for (int i = 0; i < 8; ++i) {
     const float n = rnd16<T>(xv[i] * r);
     const float nw = rnd16<T>(n * T::to_float(T::from_float(wv[i])));
-    const float silu = zv[i] / (1.0f + expf(-zv[i]));
+    // silu(z) = z / (1 + e^-z) with the hardware exp2 and reciprocal (about
+    // one fp32 ulp each): the output's single rounding moves by one 16-bit
+    // ulp only for values within those few ulps of a rounding boundary, and
+    // the pass stays memory-bound instead of paying for expf and a division
+    const float silu = zv[i] * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zv[i] * -1.4426950408889634f));
     y[i] = nw * silu;
   }
   u32x4 o;
