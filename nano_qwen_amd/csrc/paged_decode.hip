@@ -141,13 +141,22 @@ struct DecodeWave {
       if constexpr (!FP8) {
         *reinterpret_cast<u32x4 *>(rp + ((ch ^ swz(row)) << 4)) = r[c];
       } else {
-        const u32x4 &w = r[c];
-        const u32x4 lo{T::template fp8x2<false>(w[0]), T::template fp8x2<true>(w[0]),
-                       T::template fp8x2<false>(w[1]), T::template fp8x2<true>(w[1])};
-        const u32x4 hi{T::template fp8x2<false>(w[2]), T::template fp8x2<true>(w[2]),
-                       T::template fp8x2<false>(w[3]), T::template fp8x2<true>(w[3])};
-        *reinterpret_cast<u32x4 *>(rp + (((2 * ch) ^ swz(row)) << 4)) = lo;
-        *reinterpret_cast<u32x4 *>(rp + (((2 * ch + 1) ^ swz(row)) << 4)) = hi;
+        // A lane's 16 codes widen to logical chunks 2ch (dims 16ch..+7) and
+        // 2ch + 1.  The first store takes chunk 2ch + f and the second the
+        // other, with f chosen so that every 16 lanes of a store hit 16
+        // distinct bank quads: at head_dim 128 those lanes are rows 2i, 2i + 1
+        // (8 lanes each), whose swizzles agree in bits 0 and 3, so the two
+        // rows take complementary chunk sets {c : c0 ^ c3 = f-parity}; at 256
+        // they are one row, whose two 256-byte halves share banks.  (All
+        // lanes storing 2ch first would put both rows on the same 8 quads.)
+        const int f = D == 128 ? (((lane >> 3) ^ (lane >> 2)) & 1) : ((lane >> 3) & 1);
+        const u32x4 w = f ? u32x4{r[c][2], r[c][3], r[c][0], r[c][1]} : r[c];
+        const u32x4 first{T::template fp8x2<false>(w[0]), T::template fp8x2<true>(w[0]),
+                          T::template fp8x2<false>(w[1]), T::template fp8x2<true>(w[1])};
+        const u32x4 second{T::template fp8x2<false>(w[2]), T::template fp8x2<true>(w[2]),
+                           T::template fp8x2<false>(w[3]), T::template fp8x2<true>(w[3])};
+        *reinterpret_cast<u32x4 *>(rp + (((2 * ch + f) ^ swz(row)) << 4)) = first;
+        *reinterpret_cast<u32x4 *>(rp + (((2 * ch + 1 - f) ^ swz(row)) << 4)) = second;
       }
     }
   }
