@@ -72,9 +72,14 @@ int nq_store_kvcache(const void *key, int64_t key_row_stride,
                      void *stream);
 
 /*
- * Split-K plan for nq_paged_decode, chosen from host-known shapes only (so
- * it is fixed under graph capture): fills *num_splits and *split_tokens
- * (a multiple of 128; split s covers tokens [s*split_tokens, (s+1)*split_tokens)).
+ * Split plan for nq_paged_decode, chosen from host-known shapes only (so it
+ * is fixed under graph capture): fills *num_splits and *split_tokens (a
+ * multiple of 128; split s covers tokens [s*split_tokens, (s+1)*split_tokens)).
+ * A multi-split plan for a kernel with one resident workgroup per CU (fp8
+ * caches with >= 8 kv heads) may carry more splits than the table needs:
+ * the workspace sized from them then also holds the stream-K partials, and
+ * nq_paged_decode splits the batch's tokens into equal per-CU ranges instead
+ * (NQ_DECODE_STREAMK=0 keeps split-K).
  */
 int nq_decode_plan(int batch, int num_q_heads, int num_kv_heads,
                    int max_blocks_per_seq, int block_size, int kv_dtype,
@@ -101,7 +106,9 @@ int64_t nq_decode_workspace_bytes(int batch, int num_q_heads, int head_dim,
  * num_kv_heads).  Entries past ceil(context_len / block_size) are never
  * read; rows with context_len <= 0 produce zeros.
  * num_splits/split_tokens come from nq_decode_plan; workspace (>=
- * nq_decode_workspace_bytes, 256-byte aligned) is caller-owned.
+ * nq_decode_workspace_bytes, 256-byte aligned) is caller-owned.  Results do
+ * not depend on which of the two multi-split schedules runs beyond float32
+ * rounding of the merge.
  */
 int nq_paged_decode(const void *q, int64_t q_batch_stride, int64_t q_head_stride,
                     const void *k_cache, const void *v_cache,

@@ -298,6 +298,22 @@ __device__ inline float max32_raw(float v) {
   return vmax_raw(u2f(a), u2f(b));
 }
 
+// Wave-wide inclusive prefix sum of an int through DPP: shifts by 1, 2, 4, 8
+// within each 16-lane row, then each row's running total broadcast into the
+// rows after it (row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2
+// and 3).  Lanes whose source is out of range add 0 (the `old` operand).
+__device__ __forceinline__ int wave_iscan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return v;
+}
+// Sum of an int over the 64 lanes, in every lane.
+__device__ __forceinline__ int wave_sum_i32(int v) { return __builtin_amdgcn_readlane(wave_iscan(v), 63); }
+
 // Transposing LDS read (ds_read_b64_tr_b16).  Within each 16-lane group,
 // lanes 4k..4k+3 address the four 8-byte pieces of "row" k (16 consecutive
 // 16-bit elements); lane i receives element i of rows 0..3, packed in order.

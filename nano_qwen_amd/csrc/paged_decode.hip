@@ -53,8 +53,11 @@ struct DecodeArgs {
   int64_t o_bs, o_hs;  // bytes
   const uint8_t *gate;  // null, or the output gate [B, Hq, D] (same type as out)
   int64_t g_bs, g_hs;   // bytes
-  float *ws_o;         // [B, Hq, S, D]
-  float *ws_lse;       // [B, Hq, S]
+  float *ws_o;         // split-K [B, Hq, S, D]; stream-K [W, 2, Hq, D]
+  float *ws_lse;       // split-K [B, Hq, S]; stream-K [W, 2, Hq]
+  int2 *sk_bnd;        // stream-K: [W] range starts (sequence, token)
+  uint8_t *ws_raw;     // the caller's workspace and its size
+  int64_t ws_bytes;
   int Hq, Hkv, G, block_size;
   int64_t num_blocks;
   int split_tokens, num_splits;
@@ -184,42 +187,19 @@ struct DecodeWave {
   }
 };
 
-// One workgroup = HPW waves = HPW consecutive kv heads of one (sequence,
-// split); wave w owns kv head blockIdx.y * HPW + w.  The waves of a workgroup
-// step through the same tokens together, so the workgroup streams whole
-// contiguous cache rows, and no cross-wave merge is needed: each wave owns
-// its heads' softmax state.
-template <class T, bool FP8, int D, int HPW, int DEPTH, int WPE>
-__global__ __launch_bounds__(64 * HPW) __attribute__((amdgpu_waves_per_eu(WPE)))
-void paged_decode_kernel(const DecodeArgs a) {
-  static_assert(DEPTH == 1 || DEPTH == 2, "prefetch depth");
+// The work of one wave on one piece of a sequence: kv head kvh of sequence
+// b over tokens [t_begin, t_end) (t_begin % 32 == 0, at most 63 blocks).  A
+// piece that is the whole context (single) writes `out`; any other writes
+// its heads' normalised partial O and log2-sum-exp to workspace row
+// ws_row + head * ws_head_stride, for a merge pass.
+template <class T, bool FP8, int D, int DEPTH>
+__device__ __forceinline__ void decode_piece(const DecodeArgs &a, uint8_t *tile, int b, int kvh, int t_begin,
+                                             int t_end, bool single, int64_t ws_row, int64_t ws_head_stride) {
   using W = DecodeWave<T, FP8, D>;
   using Gm = Geo<D, FP8>;
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const int m = lane & 15, g = lane >> 4;  // m: token row / head column, g: lane group
-  const int split = blockIdx.x, b = blockIdx.z;
-  const int kvh = blockIdx.y * HPW + wave;
-  if (kvh >= a.Hkv) return;  // whole wave; the kernel has no workgroup barrier
   const int G = a.G;
-  const int ctx = min(a.context_lens[b], a.max_tokens);
-  const int t_begin = split * a.split_tokens;
-
-  if (ctx <= 0) {  // padded graph row: defined zeros, no KV reads
-    if (split == 0) {
-      for (int it = lane; it < G * D / 4; it += 64) {
-        const int h = it / (D / 4), d4 = it % (D / 4);
-        uint8_t *o = a.out + b * a.o_bs + (kvh * G + h) * a.o_hs + d4 * 8;
-        *reinterpret_cast<u32x2 *>(o) = u32x2{0, 0};
-      }
-    }
-    return;
-  }
-  if (t_begin >= ctx) return;
-  const int t_end = min(t_begin + a.split_tokens, ctx);
-  const bool single = ctx <= a.split_tokens;
-
   const float kscale = FP8 ? a.k_scale[kvh] : 1.0f;
   const float vscale = FP8 ? a.v_scale[kvh] : 1.0f;
   const float sl2 = a.scale_log2 * kscale;
@@ -254,8 +234,6 @@ void paged_decode_kernel(const DecodeArgs a) {
     W::load(a.k_cache, a, rows[d], td, t_end, voff0, kraw[d]);
     W::load(a.v_cache, a, rows[d], td, t_end, voff0, vraw[d]);
   }
-
-  uint8_t *tile = smem + wave * W::LDS_PER_WAVE_B;
 
   float m_run = kNegInf, l_run = 0.f;
   f32x4 o[Gm::NJ];
@@ -348,11 +326,127 @@ void paged_decode_kernel(const DecodeArgs a) {
       }
     }
   } else {
-    const int64_t idx = (static_cast<int64_t>(b) * a.Hq + head) * a.num_splits + split;
+    const int64_t idx = ws_row + static_cast<int64_t>(head) * ws_head_stride;
     float *wp = a.ws_o + idx * D;
 #pragma unroll
     for (int j = 0; j < Gm::NJ; ++j) *reinterpret_cast<f32x4 *>(wp + 16 * j + 4 * g) = o[j] * inv;
     if (g == 0) a.ws_lse[idx] = (L > 0.f) ? m_run + __log2f(L) : kNegInf;
+  }
+}
+
+
+// Zeros for the heads of kv head kvh of a padded graph row (ctx 0).
+template <int D>
+__device__ __forceinline__ void decode_zero_row(const DecodeArgs &a, int b, int kvh, int lane) {
+  for (int it = lane; it < a.G * D / 4; it += 64) {
+    const int h = it / (D / 4), d4 = it % (D / 4);
+    uint8_t *o = a.out + b * a.o_bs + (kvh * a.G + h) * a.o_hs + d4 * 8;
+    *reinterpret_cast<u32x2 *>(o) = u32x2{0, 0};
+  }
+}
+
+// Split-K: one workgroup = HPW waves = HPW consecutive kv heads of one
+// (sequence, split); wave w owns kv head blockIdx.y * HPW + w.  The waves of
+// a workgroup step through the same tokens together, so the workgroup
+// streams whole contiguous cache rows, and no cross-wave merge is needed:
+// each wave owns its heads' softmax state.  The split index is the fastest
+// grid dimension: dispatching a sequence's splits together measured 6%
+// faster on cfg5 than all first splits first.
+template <class T, bool FP8, int D, int HPW, int DEPTH, int WPE>
+__global__ __launch_bounds__(64 * HPW) __attribute__((amdgpu_waves_per_eu(WPE)))
+void paged_decode_kernel(const DecodeArgs a) {
+  static_assert(DEPTH == 1 || DEPTH == 2, "prefetch depth");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int split = blockIdx.x, b = blockIdx.z;
+  const int kvh = blockIdx.y * HPW + wave;
+  if (kvh >= a.Hkv) return;  // whole wave; the kernel has no workgroup barrier
+  const int ctx = min(a.context_lens[b], a.max_tokens);
+  const int t_begin = split * a.split_tokens;
+  if (ctx <= 0) {  // padded graph row: defined zeros, no KV reads
+    if (split == 0) decode_zero_row<D>(a, b, kvh, lane);
+    return;
+  }
+  if (t_begin >= ctx) return;
+  const int t_end = min(t_begin + a.split_tokens, ctx);
+  decode_piece<T, FP8, D, DEPTH>(a, smem + wave * DecodeWave<T, FP8, D>::LDS_PER_WAVE_B, b, kvh, t_begin, t_end,
+                                 ctx <= a.split_tokens,
+                                 static_cast<int64_t>(b) * a.Hq * a.num_splits + split, a.num_splits);
+}
+
+// ---------------------------------------------------------------- stream-K
+// The contexts of the batch (clamped to [0, max_tokens]) laid end to end form
+// T tokens; workgroup w of W takes tokens [B(w), B(w + 1)) with B(w) the
+// token floor(w * T / W) rounded down to a multiple of 32 within its
+// sequence, so every workgroup carries the same work whatever the lengths
+// (a split-K grid of uneven splits leaves CUs idle while the longest splits
+// finish).  A sequence that lies within one workgroup's range is written
+// whole; a workgroup writes at most two partial pieces: slot 0 for a
+// sequence that began in an earlier range, slot 1 for one that continues
+// into a later range.  Workgroup w records B(w), and decode_merge_sk_kernel
+// finds a sequence's pieces from those boundaries.  T < 2^31 (host check).
+// A launch uses W = min(grid, max(one range per CU and group, T / 2048, the
+// ranges that keep each within 61 blocks)) of its workgroups: every range
+// then carries at least 2048 tokens where the batch has them (a range's
+// fixed costs -- Q load, first-step latency, partial write -- stay small),
+// and the rest record an empty range at the end (batch, 0) and exit.
+constexpr int kSkMinPiece = 2048;
+__device__ __forceinline__ int clamped_ctx(const DecodeArgs &a, int b) {
+  return max(0, min(a.context_lens[b], a.max_tokens));
+}
+__device__ __forceinline__ int sk_total(const DecodeArgs &a, int batch, int lane) {
+  int t = 0;
+  for (int b0 = 0; b0 < batch; b0 += 64) t += b0 + lane < batch ? clamped_ctx(a, b0 + lane) : 0;
+  return wave_sum_i32(t);
+}
+// Boundary B(w) as (sequence, token); B(W) = (batch, 0).  Whole waves.
+__device__ __forceinline__ int2 sk_boundary(const DecodeArgs &a, int batch, int total, int w, int W, int lane) {
+  if (w >= W) return int2{batch, 0};
+  const int gpos = static_cast<int>(static_cast<int64_t>(w) * total / W);  // < total
+  int base = 0;
+  for (int b0 = 0; b0 < batch; b0 += 64) {
+    const int c = b0 + lane < batch ? clamped_ctx(a, b0 + lane) : 0;
+    const int incl = base + wave_iscan(c);
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(incl > gpos);
+    if (hit != 0) {
+      const int l = static_cast<int>(__builtin_ctzll(hit));
+      const int start = __builtin_amdgcn_readlane(incl - c, l);
+      return int2{b0 + l, (gpos - start) & ~31};
+    }
+    base = __builtin_amdgcn_readlane(incl, 63);
+  }
+  return int2{batch, 0};  // not reached: gpos < T
+}
+
+// At most two waves per SIMD: the piece loop's state does not fit the
+// register share of three (168 VGPRs) without spills.
+template <class T, bool FP8, int D, int HPW, int DEPTH, int WPE>
+__global__ __launch_bounds__(64 * HPW) __attribute__((amdgpu_waves_per_eu(WPE)))
+void paged_decode_sk_kernel(const DecodeArgs a, int batch, int grid_w, int w_min) {
+  static_assert(DEPTH == 1 || DEPTH == 2, "prefetch depth");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int w = blockIdx.x;
+  const int kvh = blockIdx.y * HPW + wave;
+  if (kvh >= a.Hkv) return;  // whole wave; the kernel has no workgroup barrier
+  const int total = sk_total(a, batch, lane);
+  const int W = min(grid_w, max(w_min, max(total / kSkMinPiece, (total + 61 * a.block_size - 1) / (61 * a.block_size))));
+  if (w >= W) {
+    if (blockIdx.y == 0 && wave == 0 && lane == 0) a.sk_bnd[w] = int2{batch, 0};
+    return;
+  }
+  const int2 lo = sk_boundary(a, batch, total, w, W, lane);
+  const int2 hi = sk_boundary(a, batch, total, w + 1, W, lane);
+  if (blockIdx.y == 0 && wave == 0 && lane == 0) a.sk_bnd[w] = lo;
+  uint8_t *tile = smem + wave * DecodeWave<T, FP8, D>::LDS_PER_WAVE_B;
+  for (int b = lo.x; b < batch && (b < hi.x || (b == hi.x && hi.y > 0)); ++b) {
+    const int ctx = clamped_ctx(a, b);
+    const int t0 = b == lo.x ? lo.y : 0;
+    const int t1 = b == hi.x ? hi.y : ctx;
+    if (t1 <= t0) continue;
+    const int slot = t0 > 0 ? 0 : 1;
+    decode_piece<T, FP8, D, DEPTH>(a, tile, b, kvh, t0, t1, t0 == 0 && t1 == ctx,
+                                   (static_cast<int64_t>(w) * 2 + slot) * a.Hq, 1);
   }
 }
 
@@ -396,6 +490,69 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeArgs a, 
     *reinterpret_cast<u32x2 *>(op) = u32x2{T::pack2(acc[0], acc[1]), T::pack2(acc[2], acc[3])};
 }
 
+// Stream-K merge: every (sequence, head) whose tokens span several workgroup
+// ranges gets the lse-weighted sum of its partials; padded rows (ctx 0) get
+// zeros.  The pieces of sequence b are those of workgroups ws..we, where ws
+// is the last range starting at or before (b, 0) (its piece is in slot 1)
+// and we the last starting at or before (b, ctx - 1) (ws < w <= we: slot
+// 0); a range with no tokens (equal consecutive starts) holds nothing.
+template <class T, int D>
+__global__ __launch_bounds__(256) void decode_merge_sk_kernel(const DecodeArgs a, int batch, int W) {
+  constexpr int kPer = D / 4;  // threads per (b, head)
+  const int pair = blockIdx.x * (256 / kPer) + threadIdx.x / kPer;
+  const int d4 = threadIdx.x % kPer;
+  if (pair >= batch * a.Hq) return;
+  const int b = pair / a.Hq, head = pair % a.Hq;
+  const int ctx = max(0, min(a.context_lens[b], a.max_tokens));
+  uint8_t *op = a.out + b * a.o_bs + head * a.o_hs + d4 * 8;
+  if (ctx == 0) {
+    *reinterpret_cast<u32x2 *>(op) = u32x2{0, 0};
+    return;
+  }
+  // Last range starting at or before (b, t); range 0 starts at or before
+  // (b, 0) because sequence b has tokens.
+  auto last_le = [&](int t) {
+    int lo = 0, hi = W - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      const int2 s = a.sk_bnd[mid];
+      if (s.x < b || (s.x == b && s.y <= t)) lo = mid;
+      else hi = mid - 1;
+    }
+    return lo;
+  };
+  const int ws = last_le(0), we = last_le(ctx - 1);
+  if (ws == we) return;  // written whole by the workgroup of range ws
+  auto empty = [&](int w) {
+    if (w + 1 >= W) return false;
+    const int2 s0 = a.sk_bnd[w], s1 = a.sk_bnd[w + 1];
+    return s0.x == s1.x && s0.y == s1.y;
+  };
+  auto row = [&](int w) { return (static_cast<int64_t>(w) * 2 + (w == ws ? 1 : 0)) * a.Hq + head; };
+  float M = kNegInf;
+  for (int w = ws; w <= we; ++w)
+    if (!empty(w)) M = fmaxf(M, a.ws_lse[row(w)]);
+  float Wsum = 0.f;
+  f32x4 acc{0, 0, 0, 0};
+  if (M != kNegInf) {
+    for (int w = ws; w <= we; ++w) {
+      if (empty(w)) continue;
+      const int64_t r = row(w);
+      const float l = a.ws_lse[r];
+      const float wt = (l == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(l - M);
+      Wsum += wt;
+      acc += *reinterpret_cast<const f32x4 *>(a.ws_o + r * D + 4 * d4) * wt;
+    }
+  }
+  const float inv = Wsum > 0.f ? 1.0f / Wsum : 0.f;
+  acc *= inv;
+  if (a.gate)
+    *reinterpret_cast<u32x2 *>(op) =
+        gate4<T>(acc, *reinterpret_cast<const u32x2 *>(a.gate + b * a.g_bs + head * a.g_hs + d4 * 8));
+  else
+    *reinterpret_cast<u32x2 *>(op) = u32x2{T::pack2(acc[0], acc[1]), T::pack2(acc[2], acc[3])};
+}
+
 // kv heads (= waves) per workgroup: 4 for 16-bit caches, 8 for fp8
 // (measured best on MI355X); NQ_DECODE_HPW=4|8 overrides for tuning.
 int decode_heads_per_wg(int hkv, bool fp8) {
@@ -404,42 +561,142 @@ int decode_heads_per_wg(int hkv, bool fp8) {
   return (fp8 && hkv >= 8) ? 8 : 4;
 }
 
-template <class T, bool FP8, int D>
-int launch_decode(const DecodeArgs &a, int batch, hipStream_t s) {
-  using W = DecodeWave<T, FP8, D>;
-  int hpw = decode_heads_per_wg(a.Hkv, FP8);
-  if constexpr (D == 256 && !FP8) hpw = 4;  // eight waves of ~360 registers do not fit a CU
-  dim3 grid(a.num_splits, (a.Hkv + hpw - 1) / hpw, batch);
-  const size_t lds = static_cast<size_t>(hpw) * W::LDS_PER_WAVE_B;
-  // Register budget per wave = in-flight K/V (DEPTH steps) + state: two
-  // steps deep (bf16: 2 waves/SIMD, fp8: 3); NQ_DECODE_DEPTH=1 trades depth
-  // for occupancy.
+// Calls f.template run<HPW, DEPTH, WPE>() for the decode kernels' launch
+// shape: HPW kv heads (waves) per workgroup, DEPTH steps of raw K/V in
+// flight, WPE waves per SIMD.  Register budget per wave = in-flight K/V +
+// state: two steps deep (bf16: 2 waves/SIMD, fp8: 3); NQ_DECODE_DEPTH=1
+// trades depth for occupancy.  head_dim 256: twice the raw K/V per step, one
+// step in flight, one wave per SIMD.
+template <bool FP8, int D, class F>
+int with_decode_shape(int hpw, F &&f) {
   const int depth_env = env_int("NQ_DECODE_DEPTH", 0);
   const int depth = depth_env == 1 || depth_env == 2 ? depth_env : 2;
-#define NQ_DECODE_LAUNCH(H, DP, WP) paged_decode_kernel<T, FP8, D, H, DP, WP><<<grid, 64 * H, lds, s>>>(a)
   if constexpr (D == 256) {
-    // Twice the raw K/V per step: one step in flight, one wave per SIMD.
     if constexpr (FP8) {
-      if (hpw == 8) NQ_DECODE_LAUNCH(8, 1, 1);
-      else NQ_DECODE_LAUNCH(4, 1, 1);
+      if (hpw == 8) return f.template run<8, 1, 1>();
+      return f.template run<4, 1, 1>();
     } else {
-      NQ_DECODE_LAUNCH(4, 1, 1);
+      return f.template run<4, 1, 1>();
     }
   } else if (hpw == 8) {
-    if (depth == 2) NQ_DECODE_LAUNCH(8, 2, FP8 ? 3 : 2);
-    else NQ_DECODE_LAUNCH(8, 1, FP8 ? 4 : 3);
+    if (depth == 2) return f.template run<8, 2, FP8 ? 3 : 2>();
+    return f.template run<8, 1, FP8 ? 4 : 3>();
   } else {
-    if (depth == 2) NQ_DECODE_LAUNCH(4, 2, FP8 ? 3 : 2);
-    else NQ_DECODE_LAUNCH(4, 1, FP8 ? 4 : 3);
+    if (depth == 2) return f.template run<4, 2, FP8 ? 3 : 2>();
+    return f.template run<4, 1, FP8 ? 4 : 3>();
   }
-#undef NQ_DECODE_LAUNCH
-  int rc = check_launch("paged_decode");
-  if (rc != NQ_OK || a.num_splits <= 1) return rc;
-  constexpr int per_block = 256 / (D / 4);
-  dim3 rgrid((batch * a.Hq + per_block - 1) / per_block);
-  decode_reduce_kernel<T, D><<<rgrid, 256, 0, s>>>(a, batch);
-  return check_launch("paged_decode(reduce)");
 }
+template <bool FP8, int D>
+int decode_hpw(int hkv) {
+  const int hpw = decode_heads_per_wg(hkv, FP8);
+  return (D == 256 && !FP8) ? 4 : hpw;  // eight waves of ~360 registers do not fit a CU
+}
+
+// Resident workgroups per CU of a kernel (cached per kernel and device).
+int kernel_occupancy(const void *kernel, int threads, size_t lds) {
+  struct Entry {
+    const void *k;
+    int dev, threads;
+    size_t lds;
+    int occ;
+  };
+  static std::mutex mu;
+  static Entry cache[64];
+  static int n = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < n; ++i)
+    if (cache[i].k == kernel && cache[i].dev == dev && cache[i].threads == threads && cache[i].lds == lds)
+      return cache[i].occ;
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, lds) != hipSuccess || occ < 1) {
+    (void)hipGetLastError();
+    occ = 1;
+  }
+  if (n < 64) cache[n++] = Entry{kernel, dev, threads, lds, occ};
+  return occ;
+}
+
+// Stream-K applies to multi-split plans of at most 4096 sequences whose
+// tokens (batch x table width) stay below 2^31, for kernels with one
+// resident workgroup per CU (the fp8 and head_dim-256 shapes): its grid is
+// then one range per CU and group, all busy.  Measured on MI355X: cfg5 (fp8,
+// random contexts) 5.25 -> 6.0 TB/s against its split-K plan; the bf16
+// shapes, two workgroups per CU with already balanced split-K plans, lost
+// 10-18%.  NQ_DECODE_STREAMK=0 keeps split-K.
+bool sk_eligible(int batch, int64_t max_tokens) {
+  return env_int("NQ_DECODE_STREAMK", 1) != 0 && batch <= 4096 && batch * max_tokens < (int64_t{1} << 31);
+}
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+int64_t sk_workspace_bytes(int64_t W, int Hq, int D) {
+  return align256(W * 2 * Hq * D * 4) + align256(W * 2 * Hq * 4) + align256(W * 8);
+}
+// Workgroups per kv-head group: every resident slot of the device, and
+// enough that no range exceeds 61 blocks (a range spans at most 63 block-
+// table entries, one per lane, once its ends are rounded to 32 tokens).
+int sk_workgroups(int occ, int groups, int batch, int64_t max_tokens, int block_size) {
+  int64_t W = std::max<int64_t>(1, static_cast<int64_t>(device_cus()) * occ / groups);
+  W = std::max<int64_t>(W, (batch * max_tokens + 61LL * block_size - 1) / (61LL * block_size));
+  return static_cast<int>(std::min<int64_t>(W, 65535));
+}
+
+template <class T, bool FP8, int D>
+struct DecodeLaunch {
+  const DecodeArgs &a;
+  int batch;
+  hipStream_t s;
+  template <int H, int DP, int WP>
+  int run() const {
+    const int groups = (a.Hkv + H - 1) / H;
+    const size_t lds = static_cast<size_t>(H) * DecodeWave<T, FP8, D>::LDS_PER_WAVE_B;
+    constexpr int per_block = 256 / (D / 4);
+    const dim3 rgrid((batch * a.Hq + per_block - 1) / per_block);
+    auto *kern = paged_decode_sk_kernel<T, FP8, D, H, DP, (WP > 2 ? 2 : WP)>;
+    if (a.num_splits > 1 && sk_eligible(batch, a.max_tokens) &&
+        kernel_occupancy(reinterpret_cast<const void *>(kern), 64 * H, lds) == 1) {
+      const int W = sk_workgroups(1, groups, batch, a.max_tokens, a.block_size);
+      if (a.ws_raw && sk_workspace_bytes(W, a.Hq, D) <= a.ws_bytes) {
+        DecodeArgs k = a;
+        k.ws_o = reinterpret_cast<float *>(a.ws_raw);
+        k.ws_lse = reinterpret_cast<float *>(a.ws_raw + align256(static_cast<int64_t>(W) * 2 * a.Hq * D * 4));
+        k.sk_bnd = reinterpret_cast<int2 *>(a.ws_raw + align256(static_cast<int64_t>(W) * 2 * a.Hq * D * 4) +
+                                            align256(static_cast<int64_t>(W) * 2 * a.Hq * 4));
+        kern<<<dim3(W, groups), 64 * H, lds, s>>>(k, batch, W, std::max(1, device_cus() / groups));
+        const int rc = check_launch("paged_decode(stream-K)");
+        if (rc != NQ_OK) return rc;
+        decode_merge_sk_kernel<T, D><<<rgrid, 256, 0, s>>>(k, batch, W);
+        return check_launch("paged_decode(stream-K merge)");
+      }
+    }
+    paged_decode_kernel<T, FP8, D, H, DP, WP><<<dim3(a.num_splits, groups, batch), 64 * H, lds, s>>>(a);
+    const int rc = check_launch("paged_decode");
+    if (rc != NQ_OK || a.num_splits <= 1) return rc;
+    decode_reduce_kernel<T, D><<<rgrid, 256, 0, s>>>(a, batch);
+    return check_launch("paged_decode(reduce)");
+  }
+};
+
+template <class T, bool FP8, int D>
+int launch_decode(const DecodeArgs &a, int batch, hipStream_t s) {
+  return with_decode_shape<FP8, D>(decode_hpw<FP8, D>(a.Hkv), DecodeLaunch<T, FP8, D>{a, batch, s});
+}
+
+// Stream-K workgroups per group the head_dim-128 kernel would launch for
+// these shapes, or 0 if it runs split-K (a head_dim-256 stream-K launch has
+// as many workgroups; without workspace for it, it runs split-K).
+template <bool FP8>
+struct SkPlanWorkgroups {
+  int hkv, batch, block_size;
+  int64_t max_tokens;
+  template <int H, int DP, int WP>
+  int run() const {
+    const size_t lds = static_cast<size_t>(H) * DecodeWave<BF16, FP8, 128>::LDS_PER_WAVE_B;
+    const int occ = kernel_occupancy(
+        reinterpret_cast<const void *>(paged_decode_sk_kernel<BF16, FP8, 128, H, DP, (WP > 2 ? 2 : WP)>), 64 * H, lds);
+    return occ == 1 ? sk_workgroups(1, (hkv + H - 1) / H, batch, max_tokens, block_size) : 0;
+  }
+};
 
 }  // namespace
 }  // namespace nq
@@ -461,7 +718,7 @@ extern "C" int nq_decode_plan(int batch, int num_q_heads, int num_kv_heads, int 
   if (!num_splits || !split_tokens || batch <= 0 || num_kv_heads <= 0 || max_blocks_per_seq <= 0 ||
       block_size <= 0)
     return fail(NQ_EINVAL, "decode_plan: bad arguments");
-  (void)num_q_heads;
+  if (num_q_heads <= 0) return fail(NQ_EINVAL, "decode_plan: bad arguments");
   const int64_t max_tokens = static_cast<int64_t>(max_blocks_per_seq) * block_size;
   const int hpw = decode_heads_per_wg(num_kv_heads, kv_dtype == NQ_FP8_E4M3);
   const int64_t groups = (num_kv_heads + hpw - 1) / hpw;
@@ -481,7 +738,24 @@ extern "C" int nq_decode_plan(int batch, int num_q_heads, int num_kv_heads, int 
     *split_tokens = static_cast<int>((max_tokens + 127) / 128 * 128);
     return NQ_OK;
   }
-  *num_splits = static_cast<int>((max_tokens + split - 1) / split);
+  int64_t ns = (max_tokens + split - 1) / split;
+  // The workspace is sized from num_splits (nq_decode_workspace_bytes); a
+  // multi-split decode runs as stream-K when that workspace also holds the
+  // stream-K partials, so num_splits grows until it does (at head_dim 128
+  // and 256).
+  if (sk_eligible(batch, max_tokens)) {
+    const bool fp8 = kv_dtype == NQ_FP8_E4M3;
+    const int W = fp8 ? with_decode_shape<true, 128>(decode_hpw<true, 128>(num_kv_heads),
+                                                     SkPlanWorkgroups<true>{num_kv_heads, batch, block_size, max_tokens})
+                      : with_decode_shape<false, 128>(decode_hpw<false, 128>(num_kv_heads),
+                                                      SkPlanWorkgroups<false>{num_kv_heads, batch, block_size, max_tokens});
+    while (W > 0 && ns < 65535 && (nq_decode_workspace_bytes(batch, num_q_heads, 128, static_cast<int>(ns)) <
+                              sk_workspace_bytes(W, num_q_heads, 128) ||
+                          nq_decode_workspace_bytes(batch, num_q_heads, 256, static_cast<int>(ns)) <
+                              sk_workspace_bytes(W, num_q_heads, 256)))
+      ++ns;
+  }
+  *num_splits = static_cast<int>(ns);
   *split_tokens = static_cast<int>(split);
   return NQ_OK;
 }
@@ -525,7 +799,7 @@ static int paged_decode_impl(const void *q, int64_t q_batch_stride, int64_t q_he
     return fail(NQ_EINVAL, "paged_decode: null pointer");
   if (max_blocks_per_seq <= 0 || bt_stride < max_blocks_per_seq)
     return fail(NQ_EINVAL, "paged_decode: block table width");
-  if (num_splits <= 0 || split_tokens <= 0 || split_tokens % 128 != 0)
+  if (num_splits <= 0 || num_splits > 65535 || split_tokens <= 0 || split_tokens % 128 != 0)
     return fail(NQ_EINVAL, "paged_decode: bad split plan (%d x %d)", num_splits, split_tokens);
   // A split's block-table entries are held one per lane of a wave: a split
   // may span at most 63 blocks (the cap nq_decode_plan applies).
@@ -572,6 +846,8 @@ static int paged_decode_impl(const void *q, int64_t q_batch_stride, int64_t q_he
       return fail(NQ_EINVAL, "paged_decode: workspace %lld bytes < %lld needed (or unaligned)",
                   (long long)workspace_bytes, (long long)need);
     const int64_t n = static_cast<int64_t>(batch) * num_q_heads * num_splits;
+    a.ws_raw = static_cast<uint8_t *>(workspace);
+    a.ws_bytes = workspace_bytes;
     a.ws_o = static_cast<float *>(workspace);
     a.ws_lse = reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + (n * head_dim * 4 + 255) / 256 * 256);
   }

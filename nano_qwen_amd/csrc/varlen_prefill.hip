@@ -236,19 +236,6 @@ __device__ __forceinline__ int cost_level(const PrefillArgs &a, const CostQueue 
   const int key_end = a.causal ? max(0, min(Lk, row_last + Lk - Lq + 1)) : Lk;
   return min(((key_end + kKeys - 1) / kKeys) >> a.level_shift, a.n_levels - 1);
 }
-// Wave-wide inclusive prefix sum through DPP: shifts by 1, 2, 4, 8 within
-// each 16-lane row, then each row's running total broadcast into the rows
-// after it (row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3).
-// Lanes whose source is out of range add 0 (the `old` operand).
-__device__ __forceinline__ int wave_scan(int v, int) {
-  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
-  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
-  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
-  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
-  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
-  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
-  return v;
-}
 // Item at queue index idx.  Called by whole waves (all 64 lanes).
 __device__ __forceinline__ Item describe_by_cost(const PrefillArgs &a, const CostQueue &cq, int idx, int n_items) {
   Item it{};
@@ -288,7 +275,7 @@ __device__ __forceinline__ Item describe_by_cost(const PrefillArgs &a, const Cos
       nqt = max(0, qhi - qlo);
       cnt = nqt * n_slots(cq, first_slot(cq, s));
     }
-    const int incl = wave_scan(cnt, lane);
+    const int incl = wave_iscan(cnt);
     const int total = __builtin_amdgcn_readlane(incl, 63);
     if (r < total) {
       const int ls = __builtin_amdgcn_readfirstlane(
@@ -416,7 +403,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
       for (int top = a.n_levels - 1; top >= 0; top -= 64) {
         const int L = top - lane;
         const int c = L >= 0 ? lds_lev[L] : 0;
-        const int incl = wave_scan(c, lane);
+        const int incl = wave_iscan(c);
         if (L >= 0) lds_lev[L] = carry + incl - c;
         carry += __builtin_amdgcn_readlane(incl, 63);
       }

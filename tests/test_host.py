@@ -60,12 +60,23 @@ def test_abi_rejects_bad_arguments_without_launching():
 
 
 def test_decode_plan_covers_table_and_respects_env(monkeypatch):
-    for W, B in ((1, 1), (16, 64), (128, 8), (32, 128), (3, 5)):
-        ns, st = kernels.decode_plan(B, 32, 8, W, 256, torch.bfloat16)
-        assert st % 128 == 0 and ns * st >= W * 256 and (ns - 1) * st < W * 256
+    # A multi-split plan may carry more splits than the table needs: the
+    # workspace nq_decode_workspace_bytes sizes from them then also holds the
+    # stream-K partials.  With stream-K off the splits cover the table exactly.
+    for streamk in ("1", "0"):
+        monkeypatch.setenv("NQ_DECODE_STREAMK", streamk)
+        for W, B in ((1, 1), (16, 64), (128, 8), (32, 128), (3, 5)):
+            ns, st = kernels.decode_plan(B, 32, 8, W, 256, torch.bfloat16)
+            cover = -(-W * 256 // st)
+            assert st % 128 == 0 and ns * st >= W * 256 and ns >= cover
+            assert ns == cover if (streamk == "0" or cover == 1) else True
+    monkeypatch.setenv("NQ_DECODE_STREAMK", "0")
     monkeypatch.setenv("NQ_DECODE_SPLIT_TOKENS", "1024")
     ns, st = kernels.decode_plan(8, 64, 8, 128, 256, torch.bfloat16)
     assert (ns, st) == (32, 1024)
+    monkeypatch.setenv("NQ_DECODE_STREAMK", "1")
+    ns, st = kernels.decode_plan(8, 64, 8, 128, 256, torch.bfloat16)
+    assert ns >= 32 and st == 1024
     assert _lib.lib().nq_decode_workspace_bytes(8, 64, 128, 1) == 0
     assert _lib.lib().nq_decode_workspace_bytes(8, 64, 128, 32) >= 8 * 64 * 32 * (128 + 1) * 4
 
