@@ -496,9 +496,20 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeArgs a, 
 // is the last range starting at or before (b, 0) (its piece is in slot 1)
 // and we the last starting at or before (b, ctx - 1) (ws < w <= we: slot
 // 0); a range with no tokens (equal consecutive starts) holds nothing.
+// The range starts are staged in LDS (one load per thread) when they fit
+// kSkLdsRanges entries, so the searches do not chain global-memory round
+// trips.
+constexpr int kSkLdsRanges = 4096;
 template <class T, int D>
 __global__ __launch_bounds__(256) void decode_merge_sk_kernel(const DecodeArgs a, int batch, int W) {
   constexpr int kPer = D / 4;  // threads per (b, head)
+  __shared__ int2 lds_bnd[kSkLdsRanges];
+  const bool staged = W <= kSkLdsRanges;
+  if (staged) {
+    for (int i = threadIdx.x; i < W; i += 256) lds_bnd[i] = a.sk_bnd[i];
+    __syncthreads();
+  }
+  const int2 *bnd = staged ? lds_bnd : a.sk_bnd;
   const int pair = blockIdx.x * (256 / kPer) + threadIdx.x / kPer;
   const int d4 = threadIdx.x % kPer;
   if (pair >= batch * a.Hq) return;
@@ -515,7 +526,7 @@ __global__ __launch_bounds__(256) void decode_merge_sk_kernel(const DecodeArgs a
     int lo = 0, hi = W - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      const int2 s = a.sk_bnd[mid];
+      const int2 s = bnd[mid];
       if (s.x < b || (s.x == b && s.y <= t)) lo = mid;
       else hi = mid - 1;
     }
@@ -525,7 +536,7 @@ __global__ __launch_bounds__(256) void decode_merge_sk_kernel(const DecodeArgs a
   if (ws == we) return;  // written whole by the workgroup of range ws
   auto empty = [&](int w) {
     if (w + 1 >= W) return false;
-    const int2 s0 = a.sk_bnd[w], s1 = a.sk_bnd[w + 1];
+    const int2 s0 = bnd[w], s1 = bnd[w + 1];
     return s0.x == s1.x && s0.y == s1.y;
   };
   auto row = [&](int w) { return (static_cast<int64_t>(w) * 2 + (w == ws ? 1 : 0)) * a.Hq + head; };

@@ -557,26 +557,19 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         for (int t = 0; t < 2; ++t) {
           const uint32_t tile = slot + t * DT::TILE_B;
           const u32x4 raw = lds_load_b128<0>(tile + wave * (CR * DT::ROWB) + CR * DT::ROWB / 2 + 16 * lane);
-          // The lane's codes widen to logical chunks c0 and c0 + 1; the first
-          // store takes chunk c0 + f, the second the other, with f chosen so
-          // that the 16 lanes of each store hit 16 distinct bank quads.  At
-          // head_dim 128 they are rows 2i, 2i + 1 (8 lanes each): swz_k
-          // differs in bit 0 between the two (f = 0 is conflict-free), swz_v
-          // agrees in bits 0 and 3, so the rows take the complementary sets
-          // {c : c0 ^ c3 = f-parity}.  At 256 they are one row, whose two
-          // 256-byte halves share banks.
-          int f = 0;
-          if constexpr (D == 256) f = (lane >> 3) & 1;
-          else if (t == 1) f = ((lane >> 3) ^ (lane >> 2)) & 1;
-          const u32x4 w = f ? u32x4{raw[2], raw[3], raw[0], raw[1]} : raw;
-          const u32x4 first = u32x4{T::template fp8x2<false>(w[0]), T::template fp8x2<true>(w[0]),
-                                    T::template fp8x2<false>(w[1]), T::template fp8x2<true>(w[1])};
-          const u32x4 second = u32x4{T::template fp8x2<false>(w[2]), T::template fp8x2<true>(w[2]),
-                                     T::template fp8x2<false>(w[3]), T::template fp8x2<true>(w[3])};
+          // Every 16-lane store of the K rows covers 16 bank quads (rows 2i
+          // and 2i + 1 take opposite chunk parities under swz_k); the V rows'
+          // (swz_v agrees in bit 0 between them) conflict 2-way.  Choosing the
+          // first chunk per lane removes those conflicts but costs four
+          // selects per lane and tile, measured 1.7% slower on cfg3 over fp8.
+          const u32x4 lo = u32x4{T::template fp8x2<false>(raw[0]), T::template fp8x2<true>(raw[0]),
+                                 T::template fp8x2<false>(raw[1]), T::template fp8x2<true>(raw[1])};
+          const u32x4 hi = u32x4{T::template fp8x2<false>(raw[2]), T::template fp8x2<true>(raw[2]),
+                                 T::template fp8x2<false>(raw[3]), T::template fp8x2<true>(raw[3])};
           const int sw = t ? swz_v(r) : swz_k(r);
           const uint32_t row = tile + r * DT::ROWB;
-          lds_store_b128(row + (((c0 + f) ^ sw) << 4), first);
-          lds_store_b128(row + (((c0 + 1 - f) ^ sw) << 4), second);
+          lds_store_b128(row + ((c0 ^ sw) << 4), lo);
+          lds_store_b128(row + (((c0 + 1) ^ sw) << 4), hi);
         }
       }
     }
