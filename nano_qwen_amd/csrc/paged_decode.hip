@@ -680,7 +680,11 @@ struct DecodeLaunch {
         return check_launch("paged_decode(stream-K merge)");
       }
     }
-    paged_decode_kernel<T, FP8, D, H, DP, WP><<<dim3(a.num_splits, groups, batch), 64 * H, lds, s>>>(a);
+    // Splits past the table's tokens only size the workspace (for the
+    // stream-K partials of another head_dim): no workgroups for them.
+    const int64_t cover = (static_cast<int64_t>(a.max_tokens) + a.split_tokens - 1) / a.split_tokens;
+    const int nsplit = static_cast<int>(std::min<int64_t>(a.num_splits, cover));
+    paged_decode_kernel<T, FP8, D, H, DP, WP><<<dim3(nsplit, groups, batch), 64 * H, lds, s>>>(a);
     const int rc = check_launch("paged_decode");
     if (rc != NQ_OK || a.num_splits <= 1) return rc;
     decode_reduce_kernel<T, D><<<rgrid, 256, 0, s>>>(a, batch);
@@ -693,21 +697,24 @@ int launch_decode(const DecodeArgs &a, int batch, hipStream_t s) {
   return with_decode_shape<FP8, D>(decode_hpw<FP8, D>(a.Hkv), DecodeLaunch<T, FP8, D>{a, batch, s});
 }
 
-// Stream-K workgroups per group the head_dim-128 kernel would launch for
-// these shapes, or 0 if it runs split-K (a head_dim-256 stream-K launch has
-// as many workgroups; without workspace for it, it runs split-K).
-template <bool FP8>
+// Stream-K workgroups per group the head_dim-D kernel would launch for
+// these shapes, or 0 if it runs split-K.
+template <bool FP8, int D>
 struct SkPlanWorkgroups {
   int hkv, batch, block_size;
   int64_t max_tokens;
   template <int H, int DP, int WP>
   int run() const {
-    const size_t lds = static_cast<size_t>(H) * DecodeWave<BF16, FP8, 128>::LDS_PER_WAVE_B;
+    const size_t lds = static_cast<size_t>(H) * DecodeWave<BF16, FP8, D>::LDS_PER_WAVE_B;
     const int occ = kernel_occupancy(
-        reinterpret_cast<const void *>(paged_decode_sk_kernel<BF16, FP8, 128, H, DP, (WP > 2 ? 2 : WP)>), 64 * H, lds);
+        reinterpret_cast<const void *>(paged_decode_sk_kernel<BF16, FP8, D, H, DP, (WP > 2 ? 2 : WP)>), 64 * H, lds);
     return occ == 1 ? sk_workgroups(1, (hkv + H - 1) / H, batch, max_tokens, block_size) : 0;
   }
 };
+template <bool FP8, int D>
+int sk_plan_workgroups(int hkv, int batch, int64_t max_tokens, int block_size) {
+  return with_decode_shape<FP8, D>(decode_hpw<FP8, D>(hkv), SkPlanWorkgroups<FP8, D>{hkv, batch, block_size, max_tokens});
+}
 
 }  // namespace
 }  // namespace nq
@@ -752,19 +759,19 @@ extern "C" int nq_decode_plan(int batch, int num_q_heads, int num_kv_heads, int 
   int64_t ns = (max_tokens + split - 1) / split;
   // The workspace is sized from num_splits (nq_decode_workspace_bytes); a
   // multi-split decode runs as stream-K when that workspace also holds the
-  // stream-K partials, so num_splits grows until it does (at head_dim 128
-  // and 256).
+  // stream-K partials, so num_splits grows until it does, for whichever
+  // head_dim (128 or 256; the plan does not know which) runs stream-K.
   if (sk_eligible(batch, max_tokens)) {
     const bool fp8 = kv_dtype == NQ_FP8_E4M3;
-    const int W = fp8 ? with_decode_shape<true, 128>(decode_hpw<true, 128>(num_kv_heads),
-                                                     SkPlanWorkgroups<true>{num_kv_heads, batch, block_size, max_tokens})
-                      : with_decode_shape<false, 128>(decode_hpw<false, 128>(num_kv_heads),
-                                                      SkPlanWorkgroups<false>{num_kv_heads, batch, block_size, max_tokens});
-    while (W > 0 && ns < 65535 && (nq_decode_workspace_bytes(batch, num_q_heads, 128, static_cast<int>(ns)) <
-                              sk_workspace_bytes(W, num_q_heads, 128) ||
-                          nq_decode_workspace_bytes(batch, num_q_heads, 256, static_cast<int>(ns)) <
-                              sk_workspace_bytes(W, num_q_heads, 256)))
-      ++ns;
+    const int w128 = fp8 ? sk_plan_workgroups<true, 128>(num_kv_heads, batch, max_tokens, block_size)
+                         : sk_plan_workgroups<false, 128>(num_kv_heads, batch, max_tokens, block_size);
+    const int w256 = fp8 ? sk_plan_workgroups<true, 256>(num_kv_heads, batch, max_tokens, block_size)
+                         : sk_plan_workgroups<false, 256>(num_kv_heads, batch, max_tokens, block_size);
+    auto fits = [&](int D, int W) {
+      return W == 0 || nq_decode_workspace_bytes(batch, num_q_heads, D, static_cast<int>(ns)) >=
+                           sk_workspace_bytes(W, num_q_heads, D);
+    };
+    while (ns < 65535 && !(fits(128, w128) && fits(256, w256))) ++ns;
   }
   *num_splits = static_cast<int>(ns);
   *split_tokens = static_cast<int>(split);
