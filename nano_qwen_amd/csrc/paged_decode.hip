@@ -960,7 +960,17 @@ extern "C" int nq_paged_decode_noalloc(const void *q, int64_t q_batch_stride, in
   const int rc = scratch_address(&ws);
   if (rc != NQ_OK) return rc;
   if (num_splits > 1) {
-    const int64_t need = nq_decode_workspace_bytes(batch, num_q_heads, head_dim, num_splits);
+    int64_t need = nq_decode_workspace_bytes(batch, num_q_heads, head_dim, num_splits);
+    if (need > kScratchBytes && split_tokens > 0 && max_blocks_per_seq > 0) {
+      // Splits past the table's tokens only size a caller's workspace for
+      // stream-K partials; here the launch itself checks the array against
+      // those, so the plan needs only the splits that cover the table.
+      const int64_t cover = (static_cast<int64_t>(max_blocks_per_seq) * block_size + split_tokens - 1) / split_tokens;
+      if (cover < num_splits) {
+        num_splits = static_cast<int>(cover);
+        need = nq_decode_workspace_bytes(batch, num_q_heads, head_dim, num_splits);
+      }
+    }
     if (need > kScratchBytes)
       return fail(NQ_EINVAL,
                   "paged_decode_noalloc: the plan (batch %d x %d heads x %d splits) needs %lld bytes of split-K "

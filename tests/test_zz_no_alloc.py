@@ -78,3 +78,14 @@ def test_noalloc_rejects_plans_beyond_the_scratch(cuda):
         dtype_code(q.dtype), dtype_code(kc.dtype), None, None, stream_of(q))
     assert rc == -1
     assert b"scratch" in lib().nq_last_error()
+
+
+def test_noalloc_plan_grown_past_the_scratch(cuda):
+    # fp8 with many query heads: the plan's split count, grown so a caller's
+    # workspace would also hold stream-K partials at head_dim 256, sizes more
+    # than the static array; the entry point runs with the splits that cover
+    # the table and the launch fits its partials in the array.
+    case = make_decode_case("cfg5", seed=9, device=cuda, batch=1, ctx=(6000, 8000), hq=128, hkv=8)
+    ns, st = _plan(case)
+    assert lib().nq_decode_workspace_bytes(1, 128, 256, ns) > SCRATCH_BYTES
+    _compare(case)
