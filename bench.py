@@ -25,7 +25,9 @@ prefill, and the stand-alone in-place gate pass for comparison), head_dim 256
 step (``gdn_decode``: HBM GB/s over the state pool) and prefill
 (``gdn_prefill``: chunked form over cfg3's sequence lengths), and the gated
 RMS norm of its output (``gdn_norm``) and the causal conv1d before it
-(``gdn_conv``), HBM GB/s; and cfg3 with an fp8 KV cache (``cfg3_fp8``).
+(``gdn_conv``), HBM GB/s; cfg3 with an fp8 KV cache (``cfg3_fp8``); and the
+prefill kernel on long sequences (``cfg3_long``: 4 x 8192 new tokens, half
+with a prefix, causal), where item transitions are few.
 ``roofline`` covers the dominant kernel of the headline workload (paged
 decode: main kernel + split-K merge), timed with HIP events on the stream
 the kernels run on.  ``cpu_baseline`` times the CPU restatement of the path
@@ -487,7 +489,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None,
                     help="run one config (cfg2|cfg3|cfg4|cfg5|cfg3_norm_rope|cfg2_norm_rope|cfg2_gate|cfg3_gate|"
-                         "cfg2_d256|cfg5_d256|cfg3_d256|gdn_decode|gdn_prefill|gdn_norm|gdn_conv|cfg3_fp8)")
+                         "cfg2_d256|cfg5_d256|cfg3_d256|gdn_decode|gdn_prefill|gdn_norm|gdn_conv|cfg3_fp8|cfg3_long)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration)")
     args = ap.parse_args()
@@ -510,7 +512,7 @@ def main():
     todo = [args.only] if args.only else ["cfg2", "cfg3", "cfg4", "cfg5", "cfg3_norm_rope", "cfg2_norm_rope",
                                                    "cfg2_gate", "cfg3_gate", "cfg2_d256", "cfg5_d256",
                                                    "cfg3_d256", "gdn_decode", "gdn_prefill", "gdn_norm",
-                                                   "gdn_conv", "cfg3_fp8"]
+                                                   "gdn_conv", "cfg3_fp8", "cfg3_long"]
     cpu = None
     for name in todo:
         print(f"[bench] {name} ...", file=sys.stderr, flush=True)
@@ -530,6 +532,10 @@ def main():
             r, case = bench_prefill("cfg3", args.steps, args.warmup, kv="fp8")
         elif name == "cfg3_d256":
             r, case = bench_prefill("cfg3", args.steps, args.warmup, d=256, hq=16, hkv=4)
+        elif name == "cfg3_long":
+            # the same kernel and paged path on long sequences (4 x 8192 new
+            # tokens, half with a prefix): few item transitions per product
+            r, case = bench_prefill("cfg3", args.steps, args.warmup, nseq=4, lq=(8192, 8192))
         elif name.endswith("_d256"):
             # head_dim 256 (Qwen3.5's full-attention layers) with cfg2's / cfg5's
             # KV bytes per token: Hkv * D = 4 * 256
