@@ -179,40 +179,67 @@ __global__ __launch_bounds__(kThreads) void conv_prefill8(const ConvArgs a) {
   auto in8 = [&](int64_t p) -> u32x4 {
     return (p >= t0 && p < t1) ? *reinterpret_cast<const u32x4 *>(a.x + p * a.x_rs + 2 * c) : u32x4{0, 0, 0, 0};
   };
-  auto unpack = [](const u32x4 &v, int ch) -> float {
-    const uint32_t word = v[ch >> 1];
-    return T::to_float(static_cast<uint16_t>((ch & 1) ? (word >> 16) : (word & 0xffffu)));
+  // The eight channels of a row as floats, converted once per input row;
+  // the empty asm keeps the compiler from converting again at every tap.
+  auto unpack8 = [](const u32x4 &v, float (&f)[8]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f[2 * q] = T::to_float(static_cast<uint16_t>(v[q] & 0xffffu));
+      f[2 * q + 1] = T::to_float(static_cast<uint16_t>(v[q] >> 16));
+      asm("" : "+v"(f[2 * q]), "+v"(f[2 * q + 1]));
+    }
   };
   const int64_t nrun = (t1 - t0 + kRun8 - 1) / kRun8;
   for (int64_t run = blockIdx.z; run < nrun; run += gridDim.z) {
     const int64_t ts = t0 + run * kRun8;
-    u32x4 xin[kRun8 + K - 1];  // input rows ts - K + 1 .. ts + kRun8 - 1
+    // Input rows ts - K + 1 .. ts + kRun8 - 1 through a descriptor over the
+    // rows of the sequence among them: a row before or after the sequence
+    // lies outside it (its offset, negative or past the end, is out of
+    // range as an unsigned number) and reads as zeros.
+    const int64_t lo = ts - (K - 1) > t0 ? ts - (K - 1) : t0;
+    const int64_t hi = ts + kRun8 < t1 ? ts + kRun8 : t1;
+    const auto rs = make_rsrc(a.x + lo * a.x_rs, static_cast<uint32_t>((hi - lo) * a.x_rs));
+    const int off0 = static_cast<int>((ts - (K - 1) - lo) * a.x_rs) + 2 * c;
+    u32x4 xin[kRun8 + K - 1];
 #pragma unroll
-    for (int i = 0; i < kRun8 + K - 1; ++i) xin[i] = in8(ts - (K - 1) + i);
+    for (int i = 0; i < kRun8 + K - 1; ++i)
+      xin[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off0 + i * static_cast<int>(a.x_rs), 0, 0));
+    const auto ors = make_rsrc(a.out + ts * a.o_rs, static_cast<uint32_t>((hi - ts) * a.o_rs));
+    float win[K][8];  // input rows i .. i + K - 1 of output i
+#pragma unroll
+    for (int j = 0; j < K - 1; ++j) unpack8(xin[j], win[j + 1]);
 #pragma unroll
     for (int i = 0; i < kRun8; ++i) {
-      const int64_t t = ts + i;
-      float r[8];
+#pragma unroll
+      for (int j = 0; j < K - 1; ++j)
+#pragma unroll
+        for (int ch = 0; ch < 8; ++ch) win[j][ch] = win[j + 1][ch];
+      unpack8(xin[i + K - 1], win[K - 1]);
+      float y[8];
 #pragma unroll
       for (int ch = 0; ch < 8; ++ch) {
         // The product of two 16-bit values is exact in float32, so the
         // fused multiply-add rounds exactly as the add after the multiply.
-        float y = 0.f;
+        y[ch] = 0.f;
 #pragma unroll
-        for (int j = 0; j < K; ++j) y = __builtin_fmaf(w[ch][j], unpack(xin[i + j], ch), y);
-        y = rnd16<T>(y);
-        // silu with the hardware exp2 and reciprocal (about 1 ulp each);
-        // the result is rounded to 16 bits.
-        r[ch] = y * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(y * -1.4426950408889634f));
+        for (int j = 0; j < K; ++j) y[ch] = __builtin_fmaf(w[ch][j], win[j][ch], y[ch]);
       }
       u32x4 o;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        float r0 = r[2 * q], r1 = r[2 * q + 1];
-        asm("" : "+v"(r0), "+v"(r1));
-        o[q] = T::pack2(r0, r1);
+        // Both sums rounded to 16 bits by one pack, then silu with the
+        // hardware exp2 and reciprocal (about 1 ulp each), rounded again.
+        const uint32_t yp = T::pack2(y[2 * q], y[2 * q + 1]);
+        float r[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float v = T::to_float(static_cast<uint16_t>(h ? yp >> 16 : yp & 0xffffu));
+          r[h] = v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v * -1.4426950408889634f));
+        }
+        o[q] = T::pack2(r[0], r[1]);
       }
-      if (t < t1) __builtin_nontemporal_store(o, reinterpret_cast<u32x4 *>(a.out + t * a.o_rs + 2 * c));
+      // Rows past the sequence fall outside the descriptor and are dropped.
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), ors, i * static_cast<int>(a.o_rs) + 2 * c, 0, 2);
     }
   }
   // The state after the sequence: its last K - 1 inputs (zero before it).
@@ -283,8 +310,11 @@ extern "C" int nq_gdn_conv1d(const void *x, int64_t x_row_stride, const void *we
   g.K = kernel_size;
   g.N = num_seqs;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // The 8-channel prefill kernel addresses a run's input rows by 32-bit
+  // offsets from the run's first row, negative ones included.
   if (cu_seqlens && channels % 8 == 0 && aligned(x, 16) && aligned(out, 16) && (x_row_stride * 2) % 16 == 0 &&
-      (out_row_stride * 2) % 16 == 0)
+      (out_row_stride * 2) % 16 == 0 && x_row_stride >= channels && g.x_rs * (kRun8 + kMaxK) < (int64_t{1} << 31) &&
+      g.o_rs * kRun8 < (int64_t{1} << 31))
     return dtype == NQ_BF16 ? launch_prefill8_k<BF16>(g, s) : launch_prefill8_k<F16>(g, s);
   // Channel pairs over grid.x; the tokens of a prefill sequence over grid.z.
   const int pairs = (channels + 1) / 2;
