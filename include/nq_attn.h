@@ -392,7 +392,8 @@ int nq_gated_rmsnorm(const void *x, int64_t x_row_stride, const void *gate, int6
  * silu(conv1d(qkv)[:, :, :S]) and the state kept for decode (prefill,
  * :178-180, 207-213) and x = cat(conv_state, qkv); silu(conv1d(x)); the new
  * state x[:, 1:] (decode, :218-227).
- * x, out [rows, channels] (16-bit dtype), weight [channels, kernel_size]
+ * x, out [rows, channels] (16-bit dtype; row strides, in elements, at least
+ * channels: NQ_EINVAL otherwise), weight [channels, kernel_size]
  * (dtype; the reference's conv1d.weight [C, 1, K]), conv_state
  * [num_slots, channels, kernel_size - 1] (dtype, oldest input first).
  * cu_seqlens == NULL (decode): sequence b is row b, its window is the slot's

@@ -292,6 +292,9 @@ extern "C" int nq_gdn_conv1d(const void *x, int64_t x_row_stride, const void *we
     return fail(NQ_EUNSUPPORTED, "gdn_conv1d: prefill starts from a zero state (as the reference's does)");
   if (num_seqs == 0) return NQ_OK;
   if (!x || !weight || !conv_state || !state_indices || !out) return fail(NQ_EINVAL, "gdn_conv1d: null pointer");
+  if (x_row_stride < channels || out_row_stride < channels)
+    return fail(NQ_EINVAL, "gdn_conv1d: row strides %lld/%lld below the %d channels", static_cast<long long>(x_row_stride),
+                static_cast<long long>(out_row_stride), channels);
   if (!aligned(out, 4) || (out_row_stride * 2) % 4 || !aligned(x, 4) || (x_row_stride * 2) % 4)
     return fail(NQ_EINVAL, "gdn_conv1d: x and out rows 4-byte aligned");
   if (num_seqs > 65535) return fail(NQ_EINVAL, "gdn_conv1d: too many sequences for one launch");
@@ -313,7 +316,7 @@ extern "C" int nq_gdn_conv1d(const void *x, int64_t x_row_stride, const void *we
   // The 8-channel prefill kernel addresses a run's input rows by 32-bit
   // offsets from the run's first row, negative ones included.
   if (cu_seqlens && channels % 8 == 0 && aligned(x, 16) && aligned(out, 16) && (x_row_stride * 2) % 16 == 0 &&
-      (out_row_stride * 2) % 16 == 0 && x_row_stride >= channels && g.x_rs * (kRun8 + kMaxK) < (int64_t{1} << 31) &&
+      (out_row_stride * 2) % 16 == 0 && g.x_rs * (kRun8 + kMaxK) < (int64_t{1} << 31) &&
       g.o_rs * kRun8 < (int64_t{1} << 31))
     return dtype == NQ_BF16 ? launch_prefill8_k<BF16>(g, s) : launch_prefill8_k<F16>(g, s);
   // Channel pairs over grid.x; the tokens of a prefill sequence over grid.z.

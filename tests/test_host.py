@@ -57,6 +57,9 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert rc == -1 and b"split_tokens" in lib.nq_last_error()
     ns, st = kernels.decode_plan(1, 8, 2, 4096, 256, torch.bfloat16)
     assert st <= 63 * 256
+    # conv1d rows narrower than the channel count overlap: refused
+    rc = lib.nq_gdn_conv1d(fake, 512, fake, 4, fake, 2, fake, fake, 4, 0, fake, 1024, 1024, 2, None)
+    assert rc == -1 and b"row strides" in lib.nq_last_error()
 
 
 def test_decode_plan_covers_table_and_respects_env(monkeypatch):
