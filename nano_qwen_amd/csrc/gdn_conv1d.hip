@@ -161,13 +161,13 @@ __global__ __launch_bounds__(kThreads) void conv_kernel(const ConvArgs a) {
 constexpr int kRun8 = 16;  // tokens per lane and run (prefill, 8 channels per lane)
 
 // Prefill from a zero state, 8 channels per lane (C % 8 == 0, rows 16-byte
-// aligned).  grid.x covers channel groups, grid.y = sequence, grid.z walks
-// the sequence's runs (run z, z + gridDim.z, ...).
+// aligned).  grid.x covers channel groups, grid.z = sequence, grid.y walks
+// the sequence's runs (run y, y + gridDim.y, ...).
 template <class T, int K>
 __global__ __launch_bounds__(kThreads) void conv_prefill8(const ConvArgs a) {
   const int c = 8 * (blockIdx.x * kThreads + threadIdx.x);
   if (c >= a.C) return;
-  const int n = blockIdx.y;
+  const int n = blockIdx.z;
   const int64_t t0 = a.cu[n], t1 = a.cu[n + 1];
   float w[8][K];
 #pragma unroll
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(kThreads) void conv_prefill8(const ConvArgs a) {
     }
   };
   const int64_t nrun = (t1 - t0 + kRun8 - 1) / kRun8;
-  for (int64_t run = blockIdx.z; run < nrun; run += gridDim.z) {
+  for (int64_t run = blockIdx.y; run < nrun; run += gridDim.y) {
     const int64_t ts = t0 + run * kRun8;
     // Input rows ts - K + 1 .. ts + kRun8 - 1 through a descriptor over the
     // rows of the sequence among them: a row before or after the sequence
@@ -244,7 +244,7 @@ __global__ __launch_bounds__(kThreads) void conv_prefill8(const ConvArgs a) {
   }
   // The state after the sequence: its last K - 1 inputs (zero before it).
   const int32_t slot = a.idx[n];
-  if (slot < 0 || slot >= a.num_slots || blockIdx.z != 0) return;
+  if (slot < 0 || slot >= a.num_slots || blockIdx.y != 0) return;
   uint16_t *sp = reinterpret_cast<uint16_t *>(a.state) + static_cast<int64_t>(slot) * a.C * (K - 1);
 #pragma unroll
   for (int j = 0; j < K - 1; ++j) {
@@ -258,7 +258,9 @@ __global__ __launch_bounds__(kThreads) void conv_prefill8(const ConvArgs a) {
 template <class T, int K>
 int launch_prefill8(const ConvArgs &g, hipStream_t s) {
   const int groups = g.C / 8;
-  dim3 grid((groups + kThreads - 1) / kThreads, g.N, 64);  // 64 runs at a time
+  // A sequence's runs are neighbours in dispatch order: its rows are read
+  // and written as one region.
+  dim3 grid((groups + kThreads - 1) / kThreads, 64, g.N);  // 64 runs at a time
   conv_prefill8<T, K><<<grid, kThreads, 0, s>>>(g);
   return check_launch("gdn_conv1d");
 }
