@@ -79,7 +79,7 @@ int nq_store_kvcache(const void *key, int64_t key_row_stride,
  * caches with >= 8 kv heads) may carry more splits than the table needs:
  * the workspace sized from them then also holds the stream-K partials, and
  * nq_paged_decode splits the batch's tokens into equal per-CU ranges instead
- * (NQ_DECODE_STREAMK=0 keeps split-K).
+ * (NQ_DECODE_STREAMK=0 keeps split-K; nq_decode_schedule tells which).
  */
 int nq_decode_plan(int batch, int num_q_heads, int num_kv_heads,
                    int max_blocks_per_seq, int block_size, int kv_dtype,
@@ -88,6 +88,21 @@ int nq_decode_plan(int batch, int num_q_heads, int num_kv_heads,
 /* Bytes of device workspace nq_paged_decode needs for a plan (0 if one split). */
 int64_t nq_decode_workspace_bytes(int batch, int num_q_heads, int head_dim,
                                   int num_splits);
+
+/*
+ * Which multi-split schedule nq_paged_decode takes for these shapes, plan
+ * and workspace size: 1 = stream-K (equal per-CU token ranges and a
+ * boundary-searched merge), 0 = split-K (or a single split); negative on
+ * bad arguments.  No counterpart in the reference (flash_attn picks its
+ * split internally); it exists so tests and tuning can tell which path a
+ * launch ran.  Stream-K needs a multi-split plan, a kernel with one resident
+ * workgroup per CU, a workspace that holds its partials, at most 4096
+ * sequences, and batch x table tokens below 2^31 that fit 65535 ranges of
+ * 61 blocks; NQ_DECODE_STREAMK=0 forces split-K.  Needs a current device.
+ */
+int nq_decode_schedule(int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                       int max_blocks_per_seq, int block_size, int kv_dtype,
+                       int num_splits, int64_t workspace_bytes);
 
 /*
  * Paged decode attention (one query token per sequence).
@@ -156,10 +171,15 @@ int nq_paged_decode_gated(const void *q, int64_t q_batch_stride, int64_t q_head_
  * NQ_DECODE_NOALLOC_SCRATCH_BYTES per device, which each device holds until
  * the process ends.  It calls no allocating routine; the array's address is
  * looked up (hipGetSymbolAddress) on the first call on each device.
- * Every other argument is as for nq_paged_decode.  A plan whose
- * nq_decode_workspace_bytes exceeds the array returns NQ_EINVAL.  All calls
- * on one device share its array: calls that overlap on one device (several
- * streams or host threads) race and must be ordered by the caller.
+ * Every other argument is as for nq_paged_decode.  A plan whose splits
+ * were grown past the table (nq_decode_plan sizes a stream-K workspace that
+ * way) runs with the splits that cover the table when the grown plan's
+ * nq_decode_workspace_bytes exceeds the array; only a plan whose covering
+ * splits still need more than the array returns NQ_EINVAL.  All calls on one
+ * device share its array, which keeps the last call's partials: calls that
+ * overlap on one device (several streams or host threads) race and must be
+ * ordered by the caller.  Loading the library reserves the array on every
+ * device it runs on (64 MiB of HBM each) until the process ends.
  */
 #define NQ_DECODE_NOALLOC_SCRATCH_BYTES (64LL << 20)
 int nq_paged_decode_noalloc(const void *q, int64_t q_batch_stride, int64_t q_head_stride,

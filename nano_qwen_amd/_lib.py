@@ -32,6 +32,7 @@ _SIGS = {
                                  c_void_p]),
     "nq_decode_plan": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, POINTER(c_int), POINTER(c_int)]),
     "nq_decode_workspace_bytes": (c_int64, [c_int, c_int, c_int, c_int]),
+    "nq_decode_schedule": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int64]),
     "nq_paged_decode": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_int,
                                 c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_int, c_int, c_int,
                                 c_int64, c_float, c_int, c_int, c_void_p, c_int64, c_int, c_int, c_void_p,

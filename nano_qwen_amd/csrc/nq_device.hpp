@@ -157,11 +157,6 @@ __device__ inline T own_sgpr(T x) {
 __device__ inline u32x4 load16(const void *p) { return *reinterpret_cast<const u32x4 *>(p); }
 __device__ inline void store16(void *p, const u32x4 &v) { *reinterpret_cast<u32x4 *>(p) = v; }
 
-// Streaming (read-once) 16-byte load: slc/nt hint keeps KV out of L2 reuse sets.
-__device__ inline u32x4 load16_stream(const void *p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
-}
-
 // Buffer resource over [base, base + num_bytes): raw buffer loads outside the
 // range return 0 without touching memory.  Dword 3 is the gfx9-family raw
 // (untyped, 32-bit data format) descriptor word.

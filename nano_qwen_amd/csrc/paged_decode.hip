@@ -564,24 +564,19 @@ __global__ __launch_bounds__(256) void decode_merge_sk_kernel(const DecodeArgs a
     *reinterpret_cast<u32x2 *>(op) = u32x2{T::pack2(acc[0], acc[1]), T::pack2(acc[2], acc[3])};
 }
 
-// kv heads (= waves) per workgroup: 4 for 16-bit caches, 8 for fp8
-// (measured best on MI355X); NQ_DECODE_HPW=4|8 overrides for tuning.
-int decode_heads_per_wg(int hkv, bool fp8) {
-  const int env = env_int("NQ_DECODE_HPW", 0);
-  if (env == 4 || env == 8) return env;
-  return (fp8 && hkv >= 8) ? 8 : 4;
-}
+// kv heads (= waves) per workgroup: 4 for 16-bit caches, 8 for fp8 with
+// at least 8 kv heads (measured best on MI355X; eight 16-bit waves per
+// workgroup and one prefetch step with more waves per SIMD both measured
+// slower on the bench shapes).
+int decode_heads_per_wg(int hkv, bool fp8) { return (fp8 && hkv >= 8) ? 8 : 4; }
 
 // Calls f.template run<HPW, DEPTH, WPE>() for the decode kernels' launch
 // shape: HPW kv heads (waves) per workgroup, DEPTH steps of raw K/V in
 // flight, WPE waves per SIMD.  Register budget per wave = in-flight K/V +
-// state: two steps deep (bf16: 2 waves/SIMD, fp8: 3); NQ_DECODE_DEPTH=1
-// trades depth for occupancy.  head_dim 256: twice the raw K/V per step, one
-// step in flight, one wave per SIMD.
+// state: two steps deep (bf16: 2 waves/SIMD, fp8: 3).  head_dim 256: twice
+// the raw K/V per step, one step in flight, one wave per SIMD.
 template <bool FP8, int D, class F>
 int with_decode_shape(int hpw, F &&f) {
-  const int depth_env = env_int("NQ_DECODE_DEPTH", 0);
-  const int depth = depth_env == 1 || depth_env == 2 ? depth_env : 2;
   if constexpr (D == 256) {
     if constexpr (FP8) {
       if (hpw == 8) return f.template run<8, 1, 1>();
@@ -589,12 +584,9 @@ int with_decode_shape(int hpw, F &&f) {
     } else {
       return f.template run<4, 1, 1>();
     }
-  } else if (hpw == 8) {
-    if (depth == 2) return f.template run<8, 2, FP8 ? 3 : 2>();
-    return f.template run<8, 1, FP8 ? 4 : 3>();
   } else {
-    if (depth == 2) return f.template run<4, 2, FP8 ? 3 : 2>();
-    return f.template run<4, 1, FP8 ? 4 : 3>();
+    if (hpw == 8) return f.template run<8, 2, FP8 ? 3 : 2>();
+    return f.template run<4, 2, FP8 ? 3 : 2>();
   }
 }
 template <bool FP8, int D>
@@ -630,14 +622,19 @@ int kernel_occupancy(const void *kernel, int threads, size_t lds) {
 }
 
 // Stream-K applies to multi-split plans of at most 4096 sequences whose
-// tokens (batch x table width) stay below 2^31, for kernels with one
-// resident workgroup per CU (the fp8 and head_dim-256 shapes): its grid is
-// then one range per CU and group, all busy.  Measured on MI355X: cfg5 (fp8,
-// random contexts) 5.25 -> 6.0 TB/s against its split-K plan; the bf16
-// shapes, two workgroups per CU with already balanced split-K plans, lost
-// 10-18%.  NQ_DECODE_STREAMK=0 keeps split-K.
-bool sk_eligible(int batch, int64_t max_tokens) {
-  return env_int("NQ_DECODE_STREAMK", 1) != 0 && batch <= 4096 && batch * max_tokens < (int64_t{1} << 31);
+// tokens (batch x table width) stay below 2^31 and fit 65535 ranges of at
+// most 61 blocks each (a range's block-table entries are held one per lane,
+// so a longer range would read wrong blocks past lane 63), for kernels with
+// one resident workgroup per CU (the fp8 and head_dim-256 shapes): its grid
+// is then one range per CU and group, all busy.  Measured on MI355X: cfg5
+// (fp8, random contexts) 5.25 -> 6.0 TB/s against its split-K plan; the
+// bf16 shapes, two workgroups per CU with already balanced split-K plans,
+// lost 10-18%.  NQ_DECODE_STREAMK=0 keeps split-K.
+constexpr int64_t kSkMaxRanges = 65535;  // grid.x of the stream-K kernel
+bool sk_eligible(int batch, int64_t max_tokens, int block_size) {
+  const int64_t total = batch * max_tokens;
+  return env_int("NQ_DECODE_STREAMK", 1) != 0 && batch <= 4096 && total < (int64_t{1} << 31) &&
+         (total + 61LL * block_size - 1) / (61LL * block_size) <= kSkMaxRanges;
 }
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 int64_t sk_workspace_bytes(int64_t W, int Hq, int D) {
@@ -649,7 +646,21 @@ int64_t sk_workspace_bytes(int64_t W, int Hq, int D) {
 int sk_workgroups(int occ, int groups, int batch, int64_t max_tokens, int block_size) {
   int64_t W = std::max<int64_t>(1, static_cast<int64_t>(device_cus()) * occ / groups);
   W = std::max<int64_t>(W, (batch * max_tokens + 61LL * block_size - 1) / (61LL * block_size));
-  return static_cast<int>(std::min<int64_t>(W, 65535));
+  return static_cast<int>(std::min<int64_t>(W, kSkMaxRanges));  // sk_eligible keeps the 61-block bound within it
+}
+
+// Stream-K workgroups per group of a launch with these shapes on the
+// kernel <T, FP8, D, H, DP, WP>, or 0 when it runs split-K: multi-split
+// plans that sk_eligible accepts, on a kernel with one resident workgroup per
+// CU, whose workspace holds the stream-K partials.
+template <class T, bool FP8, int D, int H, int DP, int WP>
+int sk_ranges(int batch, int hq, int hkv, int64_t max_tokens, int block_size, int num_splits, int64_t ws_bytes) {
+  if (num_splits <= 1 || !sk_eligible(batch, max_tokens, block_size)) return 0;
+  const size_t lds = static_cast<size_t>(H) * DecodeWave<T, FP8, D>::LDS_PER_WAVE_B;
+  auto *kern = paged_decode_sk_kernel<T, FP8, D, H, DP, (WP > 2 ? 2 : WP)>;
+  if (kernel_occupancy(reinterpret_cast<const void *>(kern), 64 * H, lds) != 1) return 0;
+  const int W = sk_workgroups(1, (hkv + H - 1) / H, batch, max_tokens, block_size);
+  return sk_workspace_bytes(W, hq, D) <= ws_bytes ? W : 0;
 }
 
 template <class T, bool FP8, int D>
@@ -664,10 +675,10 @@ struct DecodeLaunch {
     constexpr int per_block = 256 / (D / 4);
     const dim3 rgrid((batch * a.Hq + per_block - 1) / per_block);
     auto *kern = paged_decode_sk_kernel<T, FP8, D, H, DP, (WP > 2 ? 2 : WP)>;
-    if (a.num_splits > 1 && sk_eligible(batch, a.max_tokens) &&
-        kernel_occupancy(reinterpret_cast<const void *>(kern), 64 * H, lds) == 1) {
-      const int W = sk_workgroups(1, groups, batch, a.max_tokens, a.block_size);
-      if (a.ws_raw && sk_workspace_bytes(W, a.Hq, D) <= a.ws_bytes) {
+    {
+      const int W = sk_ranges<T, FP8, D, H, DP, WP>(batch, a.Hq, a.Hkv, a.max_tokens, a.block_size, a.num_splits,
+                                                    a.ws_raw ? a.ws_bytes : 0);
+      if (W > 0) {
         DecodeArgs k = a;
         k.ws_o = reinterpret_cast<float *>(a.ws_raw);
         k.ws_lse = reinterpret_cast<float *>(a.ws_raw + align256(static_cast<int64_t>(W) * 2 * a.Hq * D * 4));
@@ -689,6 +700,17 @@ struct DecodeLaunch {
     if (rc != NQ_OK || a.num_splits <= 1) return rc;
     decode_reduce_kernel<T, D><<<rgrid, 256, 0, s>>>(a, batch);
     return check_launch("paged_decode(reduce)");
+  }
+};
+
+// Schedule of a launch (1 stream-K, 0 split-K) for nq_decode_schedule.
+template <bool FP8, int D>
+struct DecodeSchedule {
+  int batch, hq, hkv, block_size, num_splits;
+  int64_t max_tokens, ws_bytes;
+  template <int H, int DP, int WP>
+  int run() const {
+    return sk_ranges<BF16, FP8, D, H, DP, WP>(batch, hq, hkv, max_tokens, block_size, num_splits, ws_bytes) > 0;
   }
 };
 
@@ -761,7 +783,7 @@ extern "C" int nq_decode_plan(int batch, int num_q_heads, int num_kv_heads, int 
   // multi-split decode runs as stream-K when that workspace also holds the
   // stream-K partials, so num_splits grows until it does, for whichever
   // head_dim (128 or 256; the plan does not know which) runs stream-K.
-  if (sk_eligible(batch, max_tokens)) {
+  if (sk_eligible(batch, max_tokens, block_size)) {
     const bool fp8 = kv_dtype == NQ_FP8_E4M3;
     const int w128 = fp8 ? sk_plan_workgroups<true, 128>(num_kv_heads, batch, max_tokens, block_size)
                          : sk_plan_workgroups<false, 128>(num_kv_heads, batch, max_tokens, block_size);
@@ -776,6 +798,32 @@ extern "C" int nq_decode_plan(int batch, int num_q_heads, int num_kv_heads, int 
   *num_splits = static_cast<int>(ns);
   *split_tokens = static_cast<int>(split);
   return NQ_OK;
+}
+
+extern "C" int nq_decode_schedule(int batch, int num_q_heads, int num_kv_heads, int head_dim, int max_blocks_per_seq,
+                                  int block_size, int kv_dtype, int num_splits, int64_t workspace_bytes) {
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_blocks_per_seq <= 0 || block_size <= 0 ||
+      num_splits <= 0 || workspace_bytes < 0)
+    return fail(NQ_EINVAL, "decode_schedule: bad arguments");
+  if (head_dim != 128 && head_dim != 256)
+    return fail(NQ_EUNSUPPORTED, "decode_schedule: head_dim %d (built: 128, 256)", head_dim);
+  const int64_t max_tokens = std::min<int64_t>(static_cast<int64_t>(max_blocks_per_seq) * block_size, 0x7fffffff);
+  const bool fp8 = kv_dtype == NQ_FP8_E4M3;
+  if (head_dim == 256) {
+    return fp8 ? with_decode_shape<true, 256>(decode_hpw<true, 256>(num_kv_heads),
+                                              DecodeSchedule<true, 256>{batch, num_q_heads, num_kv_heads, block_size,
+                                                                        num_splits, max_tokens, workspace_bytes})
+               : with_decode_shape<false, 256>(decode_hpw<false, 256>(num_kv_heads),
+                                               DecodeSchedule<false, 256>{batch, num_q_heads, num_kv_heads,
+                                                                          block_size, num_splits, max_tokens,
+                                                                          workspace_bytes});
+  }
+  return fp8 ? with_decode_shape<true, 128>(decode_hpw<true, 128>(num_kv_heads),
+                                            DecodeSchedule<true, 128>{batch, num_q_heads, num_kv_heads, block_size,
+                                                                      num_splits, max_tokens, workspace_bytes})
+             : with_decode_shape<false, 128>(decode_hpw<false, 128>(num_kv_heads),
+                                             DecodeSchedule<false, 128>{batch, num_q_heads, num_kv_heads, block_size,
+                                                                        num_splits, max_tokens, workspace_bytes});
 }
 
 extern "C" int64_t nq_decode_workspace_bytes(int batch, int num_q_heads, int head_dim, int num_splits) {

@@ -27,8 +27,6 @@
 //    operand reads are bank-conflict free.
 //  * Online softmax in the log2 domain with lazy rescaling: O and l are only
 //    rescaled when a row maximum grows by more than 2^8, so P <= 256.
-#include <stdlib.h>
-
 #include <type_traits>
 
 #include "nq_device.hpp"
@@ -101,11 +99,10 @@ inline int64_t work_grid(int64_t n_x, int64_t U) { return U >= 8 ? 8 * ((U + 7) 
 // fetches.
 //
 // Shapes (PShape): NW waves per workgroup, each wave QS x 16 query rows of
-// one head, WPE waves per SIMD.  A = one 8-wave workgroup per CU; B = one
-// 4-wave workgroup per CU with 64-row waves (every K/V operand read and
-// per-tile step serves twice the rows); C = two independent 4-wave
-// workgroups per CU, whose barriers, prologues and epilogues do not line up,
-// so one's stalls overlap the other's work.
+// one head, WPE waves per SIMD.  C = two independent 4-wave workgroups per
+// CU, whose barriers, prologues and epilogues do not line up, so one's
+// stalls overlap the other's work (measured faster than one 8-wave
+// workgroup per CU); D = head_dim 256.
 template <class T, int D>
 struct DTile {
   static_assert(D == 128 || D == 256, "head_dim 128 or 256");
@@ -132,14 +129,10 @@ struct PShape {
   static_assert(WPE == 2, "two waves per SIMD");
   static_assert(WG_PER_CU * LDS_BYTES <= 160 * 1024, "LDS of the resident workgroups");
 };
-using ShapeA = PShape<8, 2, 2, 5>;  // one workgroup per CU, two 32-row waves per SIMD
 using ShapeC = PShape<4, 2, 2, 4>;  // two independent workgroups per CU, 32-row waves
 // head_dim 256: one workgroup per CU, two 16-row waves per SIMD (a 32 KiB
 // ring slot; the 16-row wave keeps O, Q and a tile's operands in 256 VGPRs)
 using ShapeD = PShape<8, 1, 2, 4, 256>;
-// Launch shapes built with the output gate in their store (the default ones).
-template <class S>
-constexpr bool GATED_OK = std::is_same<S, ShapeC>::value || std::is_same<S, ShapeD>::value;
 
 // A work item of the persistent kernel: query tile qt (S::ITEM_ROWS/G4 rows
 // of G4 heads) of kv-head slot y of sequence s, described by wave-uniform
@@ -1147,17 +1140,6 @@ void varlen_prefill_dma_kernel(const PrefillArgs a) {
   prefill_persistent<T, D, S, GATED, FP8>(a);
 }
 
-// Launch shape of the 16-bit kernel: C (two independent 4-wave workgroups
-// per CU) measured fastest at cfg3 on MI355X; NQ_PREFILL_SHAPE = a | c
-// selects one for measurements.
-char prefill_shape() {
-  static char shape = [] {
-    const char *e = getenv("NQ_PREFILL_SHAPE");
-    return (e && (e[0] == 'a' || e[0] == 'c')) ? e[0] : 'c';
-  }();
-  return shape;
-}
-
 template <class T, int D, class S, bool FP8>
 int launch_prefill_dma(PrefillArgs a, hipStream_t st) {
   const int rows_per_item = S::ITEM_ROWS / a.G4;
@@ -1178,11 +1160,9 @@ int launch_prefill_dma(PrefillArgs a, hipStream_t st) {
   // items; a multiple of 8 so every XCD gets the same count.
   int64_t grid = (static_cast<int64_t>(device_cus()) * S::WG_PER_CU + 7) / 8 * 8;
   if (grid > total) grid = total;  // work_grid() is a multiple of 8 when pinned
-  if constexpr (GATED_OK<S>) {
-    if (a.gate) {
-      varlen_prefill_dma_kernel<T, D, S, true, FP8><<<static_cast<int>(grid), 64 * S::NW, S::LDS_BYTES, st>>>(a);
-      return check_launch("varlen_prefill(gated)");
-    }
+  if (a.gate) {
+    varlen_prefill_dma_kernel<T, D, S, true, FP8><<<static_cast<int>(grid), 64 * S::NW, S::LDS_BYTES, st>>>(a);
+    return check_launch("varlen_prefill(gated)");
   }
   varlen_prefill_dma_kernel<T, D, S, false, FP8><<<static_cast<int>(grid), 64 * S::NW, S::LDS_BYTES, st>>>(a);
   return check_launch("varlen_prefill");
@@ -1192,13 +1172,8 @@ template <class T, bool FP8, int D>
 int launch_prefill(PrefillArgs a, hipStream_t s) {
   if constexpr (D == 256) {
     return launch_prefill_dma<T, D, ShapeD, FP8>(a, s);
-  } else if constexpr (FP8) {
-    return launch_prefill_dma<T, D, ShapeC, true>(a, s);  // fp8 copies: one 1 KiB piece per wave
   } else {
-    switch (prefill_shape()) {
-      case 'c': return launch_prefill_dma<T, D, ShapeC, false>(a, s);
-      default: return launch_prefill_dma<T, D, ShapeA, false>(a, s);
-    }
+    return launch_prefill_dma<T, D, ShapeC, FP8>(a, s);  // fp8 copies: one 1 KiB piece per wave
   }
 }
 
@@ -1274,18 +1249,13 @@ static int varlen_prefill_impl(const void *q, int64_t q_row_stride, int64_t q_he
   a.out = static_cast<uint8_t *>(out);
   a.o_rs = out_row_stride * qsz;
   a.o_hs = out_head_stride * qsz;
-  // The gate rides in the output store of the default launch shapes (C at
-  // head_dim 128, and fp8; D at 256); shape A gets the same arithmetic from
-  // one in-place pass.
-  const bool fused_gate = gate && (fp8 || head_dim == 256 || prefill_shape() == 'c');
+  // The gate rides in the kernel's output store.
   if (gate) {
     if ((gate_row_stride * qsz) % 16 || (gate_head_stride * qsz) % 16 || !aligned(gate, 16))
       return fail(NQ_EINVAL, "varlen_prefill_gated: gate alignment");
     if ((static_cast<int64_t>(max_seqlen_q) + 256) * gate_row_stride * qsz >= (int64_t{1} << 31))
       return fail(NQ_EINVAL, "varlen_prefill_gated: max_seqlen_q x gate row stride too large");
     if (total_q < 0) return fail(NQ_EINVAL, "varlen_prefill_gated: total_q < 0");
-  }
-  if (fused_gate) {
     a.gate = static_cast<const uint8_t *>(gate);
     a.g_rs = gate_row_stride * qsz;
     a.g_hs = gate_head_stride * qsz;
@@ -1315,9 +1285,7 @@ static int varlen_prefill_impl(const void *q, int64_t q_row_stride, int64_t q_he
   } else {
     rc = fp8 ? launch_prefill<F16, true, 128>(a, st) : launch_prefill<F16, false, 128>(a, st);
   }
-  if (rc != NQ_OK || !gate || fused_gate) return rc;
-  return nq_output_gate(out, out_row_stride, out_head_stride, gate, gate_row_stride, gate_head_stride, total_q,
-                        num_q_heads, head_dim, q_dtype, stream);
+  return rc;
 }
 
 extern "C" int nq_varlen_prefill(const void *q, int64_t q_row_stride, int64_t q_head_stride, const void *k,

@@ -13,7 +13,9 @@ TP control plane and the engine loop are out of scope: the caller hands
 fp8 extension: ``allocate_kv_cache(..., kv_cache_dtype=torch.float8_e4m3fn)``
 also creates ``kv_scales [2, L, Hkv]`` float32 (initialised to 1) and binds
 ``module.k_scale = kv_scales[0, l]`` / ``module.v_scale = kv_scales[1, l]``;
-``calibrate_kv_scales`` sets them to absmax/448 per (layer, kv head).
+``calibrate_kv_scales`` sets them to absmax/448 per (layer, kv head).  The
+pool is sized from the memory budget with the *cache* dtype's item size, so
+an fp8 pool holds twice the blocks of a bf16 one in the same budget.
 """
 from __future__ import annotations
 
@@ -25,7 +27,20 @@ from ..utils.context import get_context, reset_context, set_context
 
 class ModelRunner:
 
-    def __init__(self, block_size: int = 256, max_num_seqs: int = 512, device="cuda"):
+    def __init__(self, block_size: int = 256, max_num_seqs: int = 512, device="cuda", config=None):
+        """``config``, when given, is an object with the reference Config's
+        fields (config/config.py:6-24) that ``allocate_kv_cache()`` reads:
+        ``hf_config`` (``num_hidden_layers``, ``num_key_value_heads``,
+        ``head_dim`` or ``hidden_size`` / ``num_attention_heads``, ``dtype``),
+        ``gpu_memory_utilization``, ``kvcache_block_size``, ``max_num_seqs``,
+        ``num_kvcache_blocks`` (set here) and optionally
+        ``tensor_parallel_size`` and ``kv_cache_dtype`` (the fp8 extension).
+        Its block size and sequence count then take precedence."""
+        if config is not None:
+            block_size = config.kvcache_block_size
+            max_num_seqs = config.max_num_seqs
+        self.config = config
+        self.world_size = getattr(config, "tensor_parallel_size", 1) if config is not None else 1
         self.block_size = block_size
         self.max_num_seqs = max_num_seqs
         self.device = torch.device(device)
@@ -45,12 +60,65 @@ class ModelRunner:
         self.allocate_decode_buffers()
 
     # ------------------------------------------------------------- KV pool
-    def allocate_kv_cache(self, model, num_layers: int, num_blocks: int, num_kv_heads: int,
-                          head_dim: int, dtype: torch.dtype, kv_cache_dtype: torch.dtype | None = None):
+    def kv_block_bytes(self, num_layers: int, num_kv_heads: int, head_dim: int, kv_dtype: torch.dtype) -> int:
+        """Bytes of one block of every layer's K and V
+        (engine/model_runner.py:195), with the cache dtype's item size."""
+        item = torch.empty((), dtype=kv_dtype).element_size()
+        return 2 * num_layers * self.block_size * num_kv_heads * head_dim * item
+
+    def budget_blocks(self, block_bytes: int, gpu_memory_utilization: float, mem_info=None, stats=None) -> int:
+        """Blocks that fit the memory budget (engine/model_runner.py:189-196):
+        ``(total * utilization - used - peak + current) // block_bytes``, with
+        ``free, total = mem_get_info()``, ``used = total - free`` and the
+        allocator's peak and current allocated bytes (the peak of the warm-up
+        run is reserved for activations).  ``mem_info`` / ``stats`` stand in
+        for the device queries."""
+        free, total = mem_info if mem_info is not None else torch.cuda.mem_get_info(self.device)
+        used = total - free
+        st = stats if stats is not None else torch.cuda.memory_stats(self.device)
+        peak = st["allocated_bytes.all.peak"]
+        current = st["allocated_bytes.all.current"]
+        return int(total * gpu_memory_utilization - used - peak + current) // block_bytes
+
+    def allocate_kv_cache(self, model=None, num_layers: int | None = None, num_blocks: int | None = None,
+                          num_kv_heads: int | None = None, head_dim: int | None = None,
+                          dtype: torch.dtype | None = None, kv_cache_dtype: torch.dtype | None = None,
+                          gpu_memory_utilization: float | None = None):
         """One tensor ``[2, L, num_blocks, block_size, Hkv, D]`` and per-layer
         views bound to every module with ``k_cache``/``v_cache`` attributes
-        (engine/model_runner.py:198-204)."""
+        (engine/model_runner.py:186-204).
+
+        Called as the reference calls it, ``allocate_kv_cache()``, every
+        argument comes from ``self.config`` and ``self.model``, and the block
+        count from the memory budget (``budget_blocks``), which it also
+        stores in ``config.num_kvcache_blocks``.  Explicit arguments override
+        those; ``num_blocks=None`` sizes from the budget
+        (``gpu_memory_utilization``, default the config's or 0.9).  Returns
+        the number of layers bound."""
+        cfg = self.config
+        hf = getattr(cfg, "hf_config", None)
+        model = model if model is not None else self.model
+        if model is None:
+            raise ValueError("allocate_kv_cache: no model (pass one, or set runner.model)")
+        if hf is not None:
+            num_layers = num_layers if num_layers is not None else hf.num_hidden_layers
+            num_kv_heads = num_kv_heads if num_kv_heads is not None else hf.num_key_value_heads // self.world_size
+            if head_dim is None:
+                head_dim = getattr(hf, "head_dim", None) or hf.hidden_size // hf.num_attention_heads
+            dtype = dtype if dtype is not None else hf.dtype
+            kv_cache_dtype = kv_cache_dtype if kv_cache_dtype is not None else getattr(cfg, "kv_cache_dtype", None)
+        if None in (num_layers, num_kv_heads, head_dim, dtype):
+            raise ValueError("allocate_kv_cache: layers, kv heads, head_dim and dtype are needed "
+                             "(as arguments or from config.hf_config)")
         kv_dtype = kv_cache_dtype or dtype
+        if num_blocks is None:
+            util = gpu_memory_utilization if gpu_memory_utilization is not None else \
+                getattr(cfg, "gpu_memory_utilization", 0.9)
+            num_blocks = self.budget_blocks(self.kv_block_bytes(num_layers, num_kv_heads, head_dim, kv_dtype), util)
+            assert num_blocks > 0, "allocate_kv_cache: the memory budget holds no KV block"
+        if cfg is not None:
+            cfg.num_kvcache_blocks = num_blocks
+        self.model = model
         self.kv_cache = torch.empty(2, num_layers, num_blocks, self.block_size, num_kv_heads, head_dim,
                                     dtype=kv_dtype, device=self.device)
         if kv_dtype == torch.float8_e4m3fn:

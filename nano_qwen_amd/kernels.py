@@ -25,7 +25,10 @@ from ._lib import check, dtype_code, lib, ptr, require_cuda, stream_of
 # on one stream are ordered, so they may share a buffer; calls on different
 # streams get their own.  A buffer that has to grow is replaced, but the old
 # one is kept alive (``_retired``): a HIP graph captured earlier may still
-# hold its address, and replays must keep writing into valid memory.
+# hold its address, and replays must keep writing into valid memory.  The
+# tables therefore grow with the number of streams ever used: callers should
+# launch from a fixed set of streams, and ``release_workspaces`` frees every
+# buffer once no captured graph that used them will be replayed.
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 _prefill_queues: dict[tuple[int, int], torch.Tensor] = {}
 _retired: list[torch.Tensor] = []
@@ -53,6 +56,25 @@ def _grow(table, key, nbytes, dtype, device, zero=False):
         _retired.append(cur)
     table[key] = buf
     return buf
+
+
+def release_workspaces(device=None) -> int:
+    """Drop the kernels' per-stream buffers (decode split-K workspaces,
+    prefill queue counters) and every retired buffer, of ``device`` or of
+    all devices; returns how many were dropped.  Only safe once no HIP graph
+    captured with them will be replayed again: a replay would write freed
+    memory.  Later calls allocate fresh buffers (the prefill counters start
+    at zero again)."""
+    idx = None if device is None else _key(device)[0]
+    n = 0
+    for table in (_workspaces, _prefill_queues):
+        for key in [k for k in table if idx is None or k[0] == idx]:
+            del table[key]
+            n += 1
+    keep = [t for t in _retired if idx is not None and t.device.index != idx]
+    n += len(_retired) - len(keep)
+    _retired[:] = keep
+    return n
 
 
 def store_kvcache(key, value, k_cache, v_cache, slot_mapping, k_scale=None, v_scale=None):
@@ -86,6 +108,18 @@ def decode_plan(batch, num_q_heads, num_kv_heads, max_blocks_per_seq, block_size
                               dtype_code(kv_dtype), ctypes.byref(ns), ctypes.byref(st))
     check(rc, "decode_plan")
     return ns.value, st.value
+
+
+def decode_schedule(batch, num_q_heads, num_kv_heads, head_dim, max_blocks_per_seq, block_size, kv_dtype,
+                    num_splits, workspace_bytes) -> str:
+    """``"stream-K"`` or ``"split-K"``: the schedule ``nq_paged_decode``
+    takes for these shapes, plan and workspace size (a single split reports
+    ``"split-K"``)."""
+    rc = lib().nq_decode_schedule(batch, num_q_heads, num_kv_heads, head_dim, max_blocks_per_seq, block_size,
+                                  dtype_code(kv_dtype), num_splits, int(workspace_bytes))
+    if rc < 0:
+        check(rc, "decode_schedule")
+    return "stream-K" if rc == 1 else "split-K"
 
 
 def decode_workspace(device, nbytes: int) -> torch.Tensor | None:
@@ -471,4 +505,4 @@ def gdn_conv1d(x, weight, conv_state, state_indices, cu_seqlens=None, out=None):
 
 __all__ = ["store_kvcache", "paged_decode", "varlen_prefill", "prepare_decode", "decode_plan", "qk_norm_rope_store",
            "output_gate", "gdn_decode", "gdn_prefill", "gated_rmsnorm", "gdn_conv1d",
-           "decode_workspace", "prefill_workspace", "_lib"]
+           "decode_workspace", "prefill_workspace", "release_workspaces", "decode_schedule", "_lib"]

@@ -102,6 +102,13 @@ def sk_workgroups(cus, occ, groups, batch, max_tokens, block_size):
     return min(W, 65535)
 
 
+def sk_eligible(batch, max_tokens, block_size):
+    """Host rule (sk_eligible): stream-K only where 65535 ranges of at most 61
+    blocks cover batch x max_tokens; split-K otherwise."""
+    total = batch * max_tokens
+    return batch <= 4096 and total < 2 ** 31 and -(-total // (61 * block_size)) <= 65535
+
+
 def check(ctx, W, block_size=256, w_min=1):
     pieces, bnd = kernel_pieces(ctx, W, w_min, block_size)
     # every token of every sequence exactly once
@@ -185,3 +192,23 @@ def test_block_cap_needs_host_rule():
     pieces, _ = kernel_pieces([64 * 256 * 2], 1, 1)
     (w, b, t0, t1, complete, slot), = pieces
     assert (t1 - 1) // 256 - t0 // 256 + 1 > 63
+
+
+def test_range_cap_falls_back_to_split_k():
+    # block_size 32, 2048 sequences of 65536 tokens: 2^27 tokens need more
+    # than 65535 ranges of 61 blocks.  Capped at 65535 workgroups a range
+    # would span 65 blocks (past the 63 table entries a wave holds), so the
+    # host rule sends this plan to split-K.
+    batch, ctx, bs = 2048, 65536, 32
+    W = sk_workgroups(256, 1, 1, batch, ctx, bs)
+    assert W == 65535
+    with pytest.raises(AssertionError):
+        check([ctx] * batch, W, block_size=bs, w_min=256)
+    assert not sk_eligible(batch, ctx, bs)
+    # the largest batch the rule keeps on stream-K stays within 63 blocks
+    b_ok = max(b for b in range(1, batch + 1) if sk_eligible(b, ctx, bs))
+    assert b_ok < batch
+    check([ctx] * b_ok, sk_workgroups(256, 1, 1, b_ok, ctx, bs), block_size=bs, w_min=256)
+    # every plan the rule accepts at these sizes gets W within the cap
+    for b in (1, 64, 512, b_ok):
+        assert -(-(b * ctx) // (61 * bs)) <= sk_workgroups(256, 1, 1, b, ctx, bs) <= 65535

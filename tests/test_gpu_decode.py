@@ -40,6 +40,7 @@ def check(case, seq_ids, tol, all_rows=False):
     if all_rows:
         mx, mn = full_decode_check(case, out, tol)
         print(f"[decode] {case['name']} all {case['batch']} rows: max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
+    case["_out"] = out
     return res
 
 
@@ -188,9 +189,24 @@ def test_decode_cfg4_full_split_k(cuda):
 
 @pytest.mark.slow
 def test_decode_cfg5_full_fp8(cuda):
+    """Every row of cfg5 against the float32 reference over the fp8 codes
+    dequantized in float32, and against the reference the configuration
+    names: attention computed in float32 over K/V dequantized to bf16."""
+    from oracle import sdpa_path
     case = make_decode_case("cfg5", seed=0, device=cuda)
     seqs = np.random.default_rng(1).choice(case["batch"], 10, replace=False).tolist()
     check(case, seqs, TOL_FP8, all_rows=True)
+    out = case["_out"].squeeze(1).float()
+    # the cache now holds the stored new tokens: dequantize code x scale to
+    # bf16, then attention in float32 over the bf16 pools
+    kb = (case["k_cache"].float() * case["k_scale"].view(1, 1, -1, 1)).to(torch.bfloat16)
+    vb = (case["v_cache"].float() * case["v_scale"].view(1, 1, -1, 1)).to(torch.bfloat16)
+    ref = sdpa_path.paged_decode(case["q"], kb, vb, case["block_tables"], case["context_lens"].cpu(), case["scale"])
+    err = (out - ref).abs()
+    mx, mn = float(err.max()), float(err.mean())
+    print(f"[decode] cfg5 all {case['batch']} rows vs bf16-dequantized: max-abs {mx:.2e} mean-abs {mn:.2e}",
+          flush=True)
+    assert mx <= TOL_FP8["max_abs"] and mn <= TOL_FP8["mean_abs"], (mx, mn)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -284,3 +300,15 @@ def test_decode_graph_survives_workspace_growth(cuda):
     ref = decode_reference(dict(case, slot_mapping=torch.full((4,), -1, dtype=torch.int32, device=cuda)),
                            list(range(4)))
     assert_close(f64(out[:, 0]), ref, **TOL_BF16, what="replay after growth vs oracle")
+
+
+def test_release_workspaces_then_decode_again(cuda):
+    """Dropping the per-stream buffers (no graph holds them here) leaves the
+    next decode to allocate a fresh workspace, with the same result."""
+    case = make_decode_case("cfg4", seed=1, device=cuda, batch=2, ctx=(5000, 9000))
+    out1 = run_step(case)
+    assert kernels.release_workspaces(cuda) >= 1
+    out2 = kernels.paged_decode(case["q"].unsqueeze(1), case["k_cache"], case["v_cache"], case["context_lens"],
+                                case["block_tables"], case["scale"])
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)

@@ -29,6 +29,17 @@ def _decode(case, gate=None):
     return out
 
 
+def _schedule(case):
+    """The schedule the shim's next decode of ``case`` takes (same plan and
+    workspace size as kernels.paged_decode uses)."""
+    kc = case["k_cache"]
+    B, hq, d = case["batch"], case["q"].shape[1], case["q"].shape[-1]
+    hkv, bs, W = kc.shape[2], kc.shape[1], case["block_tables"].shape[1]
+    ns, _ = kernels.decode_plan(B, hq, hkv, W, bs, kc.dtype)
+    ws = kernels.decode_workspace(kc.device, kernels._lib.lib().nq_decode_workspace_bytes(B, hq, d, ns))
+    return kernels.decode_schedule(B, hq, hkv, d, W, bs, kc.dtype, ns, 0 if ws is None else ws.numel())
+
+
 def _both_paths(case, tol, monkeypatch, oracle_rows=(0,)):
     """Store, then decode on both paths; every row against the device
     reference, ``oracle_rows`` against the float64 oracle (end to end from
@@ -43,6 +54,8 @@ def _both_paths(case, tol, monkeypatch, oracle_rows=(0,)):
         monkeypatch.setenv("NQ_DECODE_STREAMK", mode)
         print(f"[streamk] {case['name']} B={case['batch']} D={case['d']} kv={case['k_cache'].dtype} "
               f"mode={mode}", flush=True)
+        # the launch must take the schedule under test, not fall back quietly
+        assert _schedule(case) == ("stream-K" if mode == "1" else "split-K")
         out = _decode(case)
         mx, mn = full_decode_check(case, out, tol)
         print(f"[streamk] all rows: max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
@@ -97,6 +110,7 @@ def test_streamk_gated(cuda, monkeypatch):
     g = torch.Generator().manual_seed(3)
     gate = (torch.randn(B, hq, 2 * d, generator=g) * 3).to(torch.bfloat16).to(cuda)[..., d:]
     monkeypatch.setenv("NQ_DECODE_STREAMK", "1")
+    assert _schedule(case) == "stream-K"
     plain = _decode(case).squeeze(1)
     gated = _decode(case, gate=gate).squeeze(1)
     ref = torch.from_numpy(gate_ref(plain.float().cpu().numpy(), gate.float().cpu().numpy(), "bf16"))
@@ -123,6 +137,7 @@ def test_streamk_graph_replay(cuda, monkeypatch):
     side = torch.cuda.Stream()
     with torch.cuda.stream(side):
         step()
+        assert _schedule(case) == "stream-K"
     side.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=side):

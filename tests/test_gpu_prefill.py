@@ -226,7 +226,7 @@ def test_prefill_head_dim_256(cuda, kind):
 
 
 def test_prefill_head_dim_256_gated(cuda):
-    """The output gate at head_dim 256 (in the register-staged kernel's store)."""
+    """The output gate at head_dim 256 (in the persistent kernel's output store, launch shape D)."""
     from oracle.output_gate import output_gate as gate_ref
     case = make_prefill_case("cfg3", seed=24, device=cuda, nseq=3, lq=(50, 500), prefix_blocks=(1, 2),
                              d=256, hq=16, hkv=4)

@@ -173,3 +173,57 @@ def test_calibrated_fp8_store_uses_full_range(cuda):
             x = kv[li][which].float()
             # e4m3 keeps 3 mantissa bits: relative error at most 2^-4, plus the subnormal step
             assert torch.all((deq - x).abs() <= x.abs() * 2.0 ** -4 + runner.kv_scales[which, li].view(1, HKV, 1) * 2.0 ** -10)
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
+def test_runner_pool_from_memory_budget(cuda, kv_dtype):
+    """allocate_kv_cache() sized from the device's memory budget
+    (engine/model_runner.py:186-197): a utilization that leaves room for
+    about 1 GiB of bf16 blocks; fp8 gets twice the blocks of the same
+    budget, and the pool's last block stores and decodes."""
+    from types import SimpleNamespace
+    torch.cuda.synchronize()
+    free, total = torch.cuda.mem_get_info(cuda)
+    st = torch.cuda.memory_stats(cuda)
+    reserve = (total - free) + st["allocated_bytes.all.peak"] - st["allocated_bytes.all.current"]
+    util = (reserve + (1 << 30)) / total
+    hf = SimpleNamespace(num_hidden_layers=2, num_key_value_heads=HKV, head_dim=D, hidden_size=HQ * D,
+                         num_attention_heads=HQ, dtype=torch.bfloat16)
+    cfg = SimpleNamespace(hf_config=hf, gpu_memory_utilization=util, kvcache_block_size=BS, max_num_seqs=4,
+                          num_kvcache_blocks=-1, tensor_parallel_size=1, kv_cache_dtype=kv_dtype)
+    runner = ModelRunner(device=cuda, config=cfg)
+    runner.model = TwoLayers()
+    bf16_bytes = runner.kv_block_bytes(2, HKV, D, torch.bfloat16)
+    print(f"[budget] {kv_dtype} util {util:.4f} of {total / 2**30:.1f} GiB", flush=True)
+    assert runner.allocate_kv_cache() == 2
+    nb = cfg.num_kvcache_blocks
+    want = (1 << 30) // bf16_bytes * (2 if kv_dtype == torch.float8_e4m3fn else 1)
+    assert abs(nb - want) <= 2 + want // 50, (nb, want)   # other allocations may move in between
+    assert runner.kv_cache.shape == (2, 2, nb, BS, HKV, D) and runner.kv_cache.dtype == kv_dtype
+    # one decode step whose only block is the pool's last one
+    attn = runner.model.attn[0]
+    g = torch.Generator().manual_seed(0)
+    k = torch.randn(1, HKV, D, generator=g).to(torch.bfloat16).to(cuda)
+    v = torch.randn(1, HKV, D, generator=g).to(torch.bfloat16).to(cuda)
+    q = torch.randn(1, HQ, D, generator=g).to(torch.bfloat16).to(cuda)
+    if kv_dtype == torch.float8_e4m3fn:
+        runner.kv_scales.fill_(0.02)
+    slot = torch.tensor([(nb - 1) * BS], dtype=torch.int32, device=cuda)
+    store_kvcache(k, v, attn.k_cache, attn.v_cache, slot, attn.k_scale, attn.v_scale)
+    from nano_qwen_amd import kernels
+    out = kernels.paged_decode(q.unsqueeze(1), attn.k_cache, attn.v_cache,
+                               torch.tensor([1], dtype=torch.int32, device=cuda),
+                               torch.tensor([[nb - 1]], dtype=torch.int32, device=cuda), D ** -0.5,
+                               attn.k_scale, attn.v_scale)
+    torch.cuda.synchronize()
+    # one token: every head's output is its kv head's stored V row
+    vs = attn.v_cache[nb - 1, 0].float()
+    if kv_dtype == torch.float8_e4m3fn:
+        vs = vs * attn.v_scale.view(-1, 1)
+    ref = vs.repeat_interleave(HQ // HKV, dim=0)
+    assert torch.allclose(out[0, 0].float(), ref, atol=1e-2, rtol=1e-2)
+    for m in runner.model.attn:
+        m.k_cache = m.v_cache = torch.tensor([])
+    runner.kv_cache = runner.kv_scales = None
+    del attn
+    torch.cuda.empty_cache()

@@ -57,6 +57,9 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert rc == -1 and b"split_tokens" in lib.nq_last_error()
     ns, st = kernels.decode_plan(1, 8, 2, 4096, 256, torch.bfloat16)
     assert st <= 63 * 256
+    # the schedule query refuses bad arguments before any device call
+    assert lib.nq_decode_schedule(0, 32, 8, 128, 16, 256, 2, 2, 0) == -1
+    assert lib.nq_decode_schedule(4, 32, 8, 64, 16, 256, 2, 2, 0) == -2
     # conv1d rows narrower than the channel count overlap: refused
     rc = lib.nq_gdn_conv1d(fake, 512, fake, 4, fake, 2, fake, fake, 4, 0, fake, 1024, 1024, 2, None)
     assert rc == -1 and b"row strides" in lib.nq_last_error()
@@ -232,3 +235,77 @@ def test_calibrate_kv_scales():
     bf.allocate_kv_cache(M(), 3, 4, 2, 16, torch.bfloat16)
     with pytest.raises(RuntimeError):
         bf.calibrate_kv_scales(kv)
+
+
+def test_kv_pool_sized_from_memory_budget():
+    """engine/model_runner.py:186-197: blocks = (total * utilization - used -
+    peak + current) // block_bytes, block_bytes = 2 L block_size Hkv D
+    itemsize -- with the cache dtype's item size, so fp8 gets twice the
+    blocks.  Device queries are stood in for; the arithmetic is the
+    reference's, restated here in plain integers."""
+    from types import SimpleNamespace
+
+    class M(torch.nn.Module):
+        def __init__(self, n=3):
+            super().__init__()
+            self.a = torch.nn.ModuleList([Attention(8, 16, 0.25, 2) for _ in range(n)])
+
+    GiB = 1 << 30
+    mem = (30 * GiB, 80 * GiB)                       # free, total
+    stats = {"allocated_bytes.all.peak": 7 * GiB, "allocated_bytes.all.current": 5 * GiB}
+    L, hkv, d, bs = 3, 2, 16, 16
+    r = ModelRunner(block_size=bs, max_num_seqs=4, device="cpu")
+    bf_bytes = r.kv_block_bytes(L, hkv, d, torch.bfloat16)
+    assert bf_bytes == 2 * L * bs * hkv * d * 2
+    budget = int(80 * GiB * 0.5 - (80 - 30) * GiB - 7 * GiB + 5 * GiB)
+    assert budget < 0  # 50% of 80 GiB is already used
+    assert r.budget_blocks(bf_bytes, 0.5, mem, stats) == budget // bf_bytes
+    want_bf = int(80 * GiB * 0.9 - 50 * GiB - 2 * GiB) // bf_bytes
+    assert r.budget_blocks(bf_bytes, 0.9, mem, stats) == want_bf
+    fp8_bytes = r.kv_block_bytes(L, hkv, d, torch.float8_e4m3fn)
+    assert fp8_bytes * 2 == bf_bytes
+    assert r.budget_blocks(fp8_bytes, 0.9, mem, stats) in (2 * want_bf, 2 * want_bf + 1)
+
+    # allocate_kv_cache() as the reference calls it: everything from the
+    # config and the runner's model, the block count from the budget (a small
+    # budget here: the allocation is real host memory)
+    small = (50 * GiB + 2 * GiB + 10.5 * bf_bytes) / (80 * GiB)
+    hf = SimpleNamespace(num_hidden_layers=L, num_key_value_heads=hkv, head_dim=d, hidden_size=128,
+                         num_attention_heads=8, dtype=torch.bfloat16)
+    for kv_dtype, blocks in ((None, (10,)), (torch.float8_e4m3fn, (20, 21))):
+        cfg = SimpleNamespace(hf_config=hf, gpu_memory_utilization=small, kvcache_block_size=bs, max_num_seqs=4,
+                              num_kvcache_blocks=-1, tensor_parallel_size=1, kv_cache_dtype=kv_dtype)
+        runner = ModelRunner(device="cpu", config=cfg)
+        runner.model = M()
+        real_mem, real_stats = torch.cuda.mem_get_info, torch.cuda.memory_stats
+        torch.cuda.mem_get_info = lambda device=None: mem
+        torch.cuda.memory_stats = lambda device=None: stats
+        try:
+            assert runner.allocate_kv_cache() == L
+        finally:
+            torch.cuda.mem_get_info, torch.cuda.memory_stats = real_mem, real_stats
+        assert cfg.num_kvcache_blocks in blocks
+        assert runner.kv_cache.shape == (2, L, cfg.num_kvcache_blocks, bs, hkv, d)
+        assert runner.kv_cache.dtype == (kv_dtype or torch.bfloat16)
+    # tensor parallel: each rank holds num_key_value_heads // tp heads
+    cfg = SimpleNamespace(hf_config=SimpleNamespace(num_hidden_layers=1, num_key_value_heads=4, hidden_size=64,
+                                                    num_attention_heads=4, dtype=torch.bfloat16),
+                          gpu_memory_utilization=0.9, kvcache_block_size=16, max_num_seqs=2, num_kvcache_blocks=-1,
+                          tensor_parallel_size=2)
+    runner = ModelRunner(device="cpu", config=cfg)
+    assert runner.allocate_kv_cache(M(1), num_blocks=3) == 1
+    assert runner.kv_cache.shape == (2, 1, 3, 16, 2, 16) and cfg.num_kvcache_blocks == 3
+
+
+def test_release_workspaces_drops_per_stream_buffers():
+    kernels._workspaces[(7, 1)] = torch.empty(4)
+    kernels._workspaces[(7, 2)] = torch.empty(4)
+    kernels._prefill_queues[(7, 1)] = torch.empty(4)
+    kernels._retired.append(torch.empty(4))
+    try:
+        assert kernels.release_workspaces() >= 4
+        assert not any(k[0] == 7 for k in kernels._workspaces) and not kernels._retired
+    finally:
+        for t in (kernels._workspaces, kernels._prefill_queues):
+            for k in [k for k in t if k[0] == 7]:
+                del t[k]
