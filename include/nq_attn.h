@@ -164,6 +164,46 @@ int nq_paged_decode_gated(const void *q, int64_t q_batch_stride, int64_t q_head_
                           void *stream);
 
 /*
+ * The decode step of Attention.forward in one launch: the new token's KV
+ * store and the paged decode.  Replaces store_kvcache(k, v, k_cache, v_cache,
+ * slot_mapping) followed by flash_attn_with_kvcache(...)
+ * (layers/attention.py:62-63 then :71-74); with a non-NULL gate, also the
+ * gating of models/qwen3_5.py:140-142 (as nq_paged_decode_gated).
+ *
+ * k_new / v_new [batch, num_kv_heads, head_dim] with row strides
+ * k_new_row_stride / v_new_row_stride (elements of new_dtype), 16-byte
+ * aligned rows contiguous over (head, dim); new_dtype == kv_dtype for a
+ * 16-bit cache, or F32/F16/BF16 for an fp8 cache (quantized with
+ * k_scale/v_scale exactly as nq_store_kvcache does).  slot_mapping [batch]
+ * int32: row b goes to cache row slot_mapping[b] when that lies in
+ * [0, num_blocks * block_size) (-1 skips it).  Every other argument is as
+ * for nq_paged_decode / nq_paged_decode_gated; gate may be NULL.
+ *
+ * Cache bytes and outputs equal those of nq_store_kvcache followed by
+ * nq_paged_decode(_gated) when, for every sequence b, slot_mapping[b] is -1
+ * or the slot of token context_lens[b] - 1 in b's block table (what
+ * engine/decode_init.py writes) and no other sequence of the batch reads
+ * that slot.  The workgroup that reads that token takes it from k_new/v_new
+ * instead of the cache, so the store and the attention need no ordering.
+ */
+int nq_paged_decode_store(const void *q, int64_t q_batch_stride, int64_t q_head_stride,
+                          void *k_cache, void *v_cache,
+                          const int32_t *block_tables, int64_t bt_stride,
+                          int max_blocks_per_seq, const int32_t *context_lens,
+                          const void *k_new, int64_t k_new_row_stride,
+                          const void *v_new, int64_t v_new_row_stride,
+                          const int32_t *slot_mapping, int new_dtype,
+                          void *out, int64_t out_batch_stride, int64_t out_head_stride,
+                          int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                          int block_size, int64_t num_blocks, float softmax_scale,
+                          int num_splits, int split_tokens,
+                          void *workspace, int64_t workspace_bytes,
+                          int q_dtype, int kv_dtype,
+                          const float *k_scale, const float *v_scale,
+                          const void *gate, int64_t gate_batch_stride, int64_t gate_head_stride,
+                          void *stream);
+
+/*
  * nq_paged_decode without a caller workspace, for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  No counterpart in the reference: it is

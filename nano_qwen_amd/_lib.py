@@ -41,6 +41,11 @@ _SIGS = {
                                       c_int, c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_int, c_int,
                                       c_int, c_int64, c_float, c_int, c_int, c_void_p, c_int64, c_int, c_int,
                                       c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
+    "nq_paged_decode_store": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int64,
+                                      c_int, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int,
+                                      c_void_p, c_int64, c_int64, c_int, c_int, c_int, c_int,
+                                      c_int, c_int64, c_float, c_int, c_int, c_void_p, c_int64, c_int, c_int,
+                                      c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "nq_paged_decode_noalloc": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_int,
                                         c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_int, c_int, c_int,
                                         c_int64, c_float, c_int, c_int, c_int, c_int, c_void_p, c_void_p,

@@ -64,6 +64,12 @@ struct DecodeArgs {
   float scale_log2;
   const float *k_scale;
   const float *v_scale;
+  // Fused store of the new token (nq_paged_decode_store); k_new == null: none.
+  const uint8_t *k_new;
+  const uint8_t *v_new;
+  int64_t kn_rs, vn_rs;         // bytes per row (token) of k_new / v_new
+  const int32_t *slot_mapping;  // [batch]
+  int new_dtype;                // element type of k_new / v_new
 };
 
 // Per-head-dim geometry.  K/V are streamed from HBM in "full-line" layout:
@@ -99,7 +105,97 @@ __device__ inline int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1) 
 template <class T, bool FP8, int D>
 struct DecodeWave {
   using Gm = Geo<D, FP8>;
-  static constexpr int LDS_PER_WAVE_B = Gm::TILE_B;
+  // The wave's 32-token tile, then the new token's K and V rows (16-bit,
+  // unswizzled) for the fused store.
+  static constexpr int LDS_PER_WAVE_B = Gm::TILE_B + 2 * Gm::ROWB;
+
+  // 8 elements of the new token's row: row chunk c (elements 8c .. 8c+7) of
+  // kv head kvh in `src` (a k_new / v_new row of type a.new_dtype), as the
+  // cache stores it -- the same bits for a 16-bit cache; for an fp8 cache
+  // the e4m3fn codes of x * (1 / scale) (saturating, RNE, as
+  // nq_store_kvcache), returned widened to 16 bits (exact) in `wide` and as
+  // codes in `codes` (two words).
+  __device__ static inline void new_chunk(const DecodeArgs &a, const uint8_t *src, int kvh, int c, float scale,
+                                          u32x4 &wide, u32x2 &codes) {
+    if constexpr (!FP8) {
+      wide = load16(src + (static_cast<int64_t>(kvh) * D + 8 * c) * 2);
+      codes = u32x2{0, 0};
+    } else {
+      float x[8];
+      if (a.new_dtype == NQ_F32) {
+        const float *f = reinterpret_cast<const float *>(src) + kvh * D + 8 * c;
+        // float vectors: this hipcc miscompiles __builtin_bit_cast of an
+        // ext_vector element (every element reads as [0])
+        const f32x4 w0 = *reinterpret_cast<const f32x4 *>(f), w1 = *reinterpret_cast<const f32x4 *>(f + 4);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          x[t] = w0[t];
+          x[4 + t] = w1[t];
+        }
+      } else {
+        const u32x4 w = load16(src + (static_cast<int64_t>(kvh) * D + 8 * c) * 2);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint16_t lo = static_cast<uint16_t>(w[t] & 0xffffu), hi = static_cast<uint16_t>(w[t] >> 16);
+          x[2 * t] = a.new_dtype == NQ_F16 ? F16::to_float(lo) : BF16::to_float(lo);
+          x[2 * t + 1] = a.new_dtype == NQ_F16 ? F16::to_float(hi) : BF16::to_float(hi);
+        }
+      }
+      const float inv = 1.0f / scale;
+      codes = u32x2{fp8x4(x[0] * inv, x[1] * inv, x[2] * inv, x[3] * inv),
+                    fp8x4(x[4] * inv, x[5] * inv, x[6] * inv, x[7] * inv)};
+      wide = u32x4{T::template fp8x2<false>(codes[0]), T::template fp8x2<true>(codes[0]),
+                   T::template fp8x2<false>(codes[1]), T::template fp8x2<true>(codes[1])};
+    }
+  }
+
+  // Fused store: the new token of sequence b, kv head kvh, to cache row
+  // slot_mapping[b] when that slot lies in the pool (nq_store_kvcache's
+  // rule).  Lanes 0 .. 2 * D / 8 - 1: chunk lane % (D / 8) of K (first half)
+  // or V (second half).
+  __device__ static inline void store_new(const DecodeArgs &a, int b, int kvh, int lane) {
+    const int32_t slot = a.slot_mapping[b];
+    if (slot < 0 || slot >= a.num_blocks * a.block_size) return;
+    constexpr int NC = D / 8;  // 8-element chunks per row
+    if (lane >= 2 * NC) return;
+    const bool is_v = lane >= NC;
+    const int c = is_v ? lane - NC : lane;
+    const uint8_t *src = (is_v ? a.v_new : a.k_new) + b * (is_v ? a.vn_rs : a.kn_rs);
+    u32x4 wide;
+    u32x2 codes;
+    new_chunk(a, src, kvh, c, FP8 ? (is_v ? a.v_scale : a.k_scale)[kvh] : 1.0f, wide, codes);
+    const int64_t elem = (static_cast<int64_t>(slot) * a.Hkv + kvh) * D + 8 * c;
+    uint8_t *dst = is_v ? const_cast<uint8_t *>(a.v_cache) : const_cast<uint8_t *>(a.k_cache);
+    if constexpr (FP8)
+      *reinterpret_cast<u32x2 *>(dst + elem) = codes;
+    else
+      store16(dst + elem * 2, wide);
+  }
+
+  // The new token's K and V rows into the wave's row buffer `nbuf` (K at 0,
+  // V at ROWB), in the tile's 16-bit form.
+  __device__ static inline void stage_new(const DecodeArgs &a, uint8_t *nbuf, int b, int kvh, int lane) {
+    constexpr int NC = D / 8;
+    if (lane >= 2 * NC) return;
+    const bool is_v = lane >= NC;
+    const int c = is_v ? lane - NC : lane;
+    const uint8_t *src = (is_v ? a.v_new : a.k_new) + b * (is_v ? a.vn_rs : a.kn_rs);
+    u32x4 wide;
+    u32x2 codes;
+    new_chunk(a, src, kvh, c, FP8 ? (is_v ? a.v_scale : a.k_scale)[kvh] : 1.0f, wide, codes);
+    *reinterpret_cast<u32x4 *>(nbuf + (is_v ? Gm::ROWB : 0) + 16 * c) = wide;
+  }
+
+  // Overwrite row `row` of a staged tile with a buffered row (same swizzle
+  // as stage): lanes 0 .. CHUNKS - 1, one 16-byte chunk each.  LDS
+  // operations of one wave complete in order, so this write follows the
+  // stage's.
+  __device__ static inline void patch_row(uint8_t *tile, const uint8_t *row_buf, int row, int lane) {
+    if (lane < Gm::CHUNKS) {
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(row_buf + 16 * lane);
+      *reinterpret_cast<u32x4 *>(tile + row * Gm::ROWB + ((lane ^ swz(row)) << 4)) = v;
+    }
+  }
 
   // Cache row of token t0 of a step (t0 % 32 == 0, so the step stays inside
   // one block), or -1 if the table entry is not a valid block.  The split's
@@ -225,6 +321,24 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs &a, uint8_t *tile,
   const int n_blk = (t_end - 1) / a.block_size - first_blk + 1;  // <= 64 (host plan)
   const int bt_lane = lane < n_blk ? bt_row[first_blk + lane] : -1;
   const int voff0 = W::lane_voff(a, kvh, lane);
+
+  // Fused store: the piece that ends at the sequence's last token, when that
+  // token's cache row is the slot the new token is stored to, takes the new
+  // K/V rows from the inputs (as the store writes them) instead of from the
+  // cache, so it needs no ordering against the store.  sub_t0: the step that
+  // holds the token (-1: none).
+  uint8_t *const nbuf = tile + Gm::TILE_B;
+  int sub_t0 = -1, sub_row = 0;
+  if (a.k_new && t_end == a.context_lens[b]) {
+    const int t = t_end - 1;
+    const int blk = __builtin_amdgcn_readlane(bt_lane, t / a.block_size - first_blk);
+    if (blk >= 0 && blk < a.num_blocks &&
+        a.slot_mapping[b] == static_cast<int64_t>(blk) * a.block_size + t % a.block_size) {
+      W::stage_new(a, nbuf, b, kvh, lane);
+      sub_t0 = __builtin_amdgcn_readfirstlane(t_begin + (t - t_begin) / kStep * kStep);
+      sub_row = __builtin_amdgcn_readfirstlane(t - sub_t0);
+    }
+  }
   u32x4 kraw[DEPTH][Gm::RAW], vraw[DEPTH][Gm::RAW];
   int64_t rows[DEPTH];
 #pragma unroll
@@ -247,6 +361,7 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs &a, uint8_t *tile,
     const int64_t rown = (tn < t_end) ? W::step_row(a, bt_lane, first_blk, tn) : -1;
     wave_lds_sync();  // the previous step's V^T reads are issued before the tile is overwritten
     W::stage(tile, kr, lane);
+    if (t0 == sub_t0) W::patch_row(tile, nbuf, sub_row, lane);
     W::load(a.k_cache, a, rown, tn, t_end, voff0, kr);  // empty past t_end
     wave_lds_sync();
     f32x4 s[2];
@@ -258,6 +373,7 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs &a, uint8_t *tile,
     }
     wave_lds_sync();  // K operand reads are issued before V overwrites the tile
     W::stage(tile, vr, lane);
+    if (t0 == sub_t0) W::patch_row(tile, nbuf + Gm::ROWB, sub_row, lane);
     W::load(a.v_cache, a, rown, tn, t_end, voff0, vr);
     float x[8];
     float mloc = kNegInf;
@@ -361,6 +477,8 @@ void paged_decode_kernel(const DecodeArgs a) {
   const int split = blockIdx.x, b = blockIdx.z;
   const int kvh = blockIdx.y * HPW + wave;
   if (kvh >= a.Hkv) return;  // whole wave; the kernel has no workgroup barrier
+  // fused store: split 0's wave of each (sequence, kv head) writes the row
+  if (a.k_new && split == 0) DecodeWave<T, FP8, D>::store_new(a, b, kvh, lane);
   const int ctx = min(a.context_lens[b], a.max_tokens);
   const int t_begin = split * a.split_tokens;
   if (ctx <= 0) {  // padded graph row: defined zeros, no KV reads
@@ -429,10 +547,18 @@ void paged_decode_sk_kernel(const DecodeArgs a, int batch, int grid_w, int w_min
   const int w = blockIdx.x;
   const int kvh = blockIdx.y * HPW + wave;
   if (kvh >= a.Hkv) return;  // whole wave; the kernel has no workgroup barrier
+  // fused store: workgroup w's wave of kv head kvh writes the rows of
+  // sequences w, w + grid_w, ... after its pieces (the piece that reads a
+  // new token takes it from the inputs, so the order does not matter)
+  auto store_rows = [&]() {
+    if (a.k_new)
+      for (int b = w; b < batch; b += grid_w) DecodeWave<T, FP8, D>::store_new(a, b, kvh, lane);
+  };
   const int total = sk_total(a, batch, lane);
   const int W = min(grid_w, max(w_min, max(total / kSkMinPiece, (total + 61 * a.block_size - 1) / (61 * a.block_size))));
   if (w >= W) {
     if (blockIdx.y == 0 && wave == 0 && lane == 0) a.sk_bnd[w] = int2{batch, 0};
+    store_rows();
     return;
   }
   const int2 lo = sk_boundary(a, batch, total, w, W, lane);
@@ -448,6 +574,7 @@ void paged_decode_sk_kernel(const DecodeArgs a, int batch, int grid_w, int w_min
     decode_piece<T, FP8, D, DEPTH>(a, tile, b, kvh, t0, t1, t0 == 0 && t1 == ctx,
                                    (static_cast<int64_t>(w) * 2 + slot) * a.Hq, 1);
   }
+  store_rows();
 }
 
 int env_int(const char *name, int dflt) {
@@ -842,7 +969,10 @@ static int paged_decode_impl(const void *q, int64_t q_batch_stride, int64_t q_he
                              int64_t num_blocks, float softmax_scale, int num_splits, int split_tokens,
                              void *workspace, int64_t workspace_bytes, int q_dtype, int kv_dtype,
                              const float *k_scale, const float *v_scale, const void *gate,
-                             int64_t gate_batch_stride, int64_t gate_head_stride, void *stream) {
+                             int64_t gate_batch_stride, int64_t gate_head_stride, void *stream,
+                             const void *k_new = nullptr, int64_t k_new_row_stride = 0, const void *v_new = nullptr,
+                             int64_t v_new_row_stride = 0, const int32_t *slot_mapping = nullptr,
+                             int new_dtype = -1) {
   if (batch == 0) return NQ_OK;
   if (batch < 0 || batch > 65535 || num_q_heads <= 0 || num_kv_heads <= 0 || num_kv_heads > 65535)
     return fail(NQ_EINVAL, "paged_decode: bad batch/head counts");
@@ -906,6 +1036,24 @@ static int paged_decode_impl(const void *q, int64_t q_batch_stride, int64_t q_he
   a.scale_log2 = softmax_scale * kLog2e;
   a.k_scale = k_scale;
   a.v_scale = v_scale;
+  if (k_new) {
+    // the fused store (nq_paged_decode_store): rows [batch, Hkv, D]
+    const int nsz = elem_size(new_dtype);
+    if (!v_new || !slot_mapping) return fail(NQ_EINVAL, "paged_decode_store: null k_new/v_new/slot_mapping");
+    if (nsz == 0 || new_dtype == NQ_FP8_E4M3 || (!fp8 && new_dtype != kv_dtype))
+      return fail(NQ_EUNSUPPORTED, "paged_decode_store: new rows of dtype %d into a cache of dtype %d", new_dtype,
+                  kv_dtype);
+    if (k_new_row_stride < static_cast<int64_t>(num_kv_heads) * head_dim ||
+        v_new_row_stride < static_cast<int64_t>(num_kv_heads) * head_dim || (k_new_row_stride * nsz) % 16 ||
+        (v_new_row_stride * nsz) % 16 || !aligned(k_new, 16) || !aligned(v_new, 16))
+      return fail(NQ_EINVAL, "paged_decode_store: k_new/v_new rows must be 16-byte aligned [Hkv, D] rows");
+    a.k_new = static_cast<const uint8_t *>(k_new);
+    a.v_new = static_cast<const uint8_t *>(v_new);
+    a.kn_rs = k_new_row_stride * nsz;
+    a.vn_rs = v_new_row_stride * nsz;
+    a.slot_mapping = slot_mapping;
+    a.new_dtype = new_dtype;
+  }
   if (num_splits > 1) {
     const int64_t need = nq_decode_workspace_bytes(batch, num_q_heads, head_dim, num_splits);
     if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
@@ -958,6 +1106,26 @@ extern "C" int nq_paged_decode_gated(const void *q, int64_t q_batch_stride, int6
                            num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, softmax_scale,
                            num_splits, split_tokens, workspace, workspace_bytes, q_dtype, kv_dtype, k_scale,
                            v_scale, gate, gate_batch_stride, gate_head_stride, stream);
+}
+
+extern "C" int nq_paged_decode_store(const void *q, int64_t q_batch_stride, int64_t q_head_stride,
+                                     void *k_cache, void *v_cache, const int32_t *block_tables, int64_t bt_stride,
+                                     int max_blocks_per_seq, const int32_t *context_lens, const void *k_new,
+                                     int64_t k_new_row_stride, const void *v_new, int64_t v_new_row_stride,
+                                     const int32_t *slot_mapping, int new_dtype, void *out,
+                                     int64_t out_batch_stride, int64_t out_head_stride, int batch,
+                                     int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                                     int64_t num_blocks, float softmax_scale, int num_splits, int split_tokens,
+                                     void *workspace, int64_t workspace_bytes, int q_dtype, int kv_dtype,
+                                     const float *k_scale, const float *v_scale, const void *gate,
+                                     int64_t gate_batch_stride, int64_t gate_head_stride, void *stream) {
+  if (!k_new) return fail(NQ_EINVAL, "paged_decode_store: null k_new");
+  return paged_decode_impl(q, q_batch_stride, q_head_stride, k_cache, v_cache, block_tables, bt_stride,
+                           max_blocks_per_seq, context_lens, out, out_batch_stride, out_head_stride, batch,
+                           num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, softmax_scale,
+                           num_splits, split_tokens, workspace, workspace_bytes, q_dtype, kv_dtype, k_scale,
+                           v_scale, gate, gate_batch_stride, gate_head_stride, stream, k_new, k_new_row_stride,
+                           v_new, v_new_row_stride, slot_mapping, new_dtype);
 }
 
 // ---------------------------------------------------------------------------

@@ -181,7 +181,7 @@ def _gate3(gate, n, hq, d, what):
 
 
 def paged_decode(q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale,
-                 k_scale=None, v_scale=None, out=None, gate=None):
+                 k_scale=None, v_scale=None, out=None, gate=None, k=None, v=None, slot_mapping=None):
     """Paged decode attention: ``q [B, 1, Hq, D]`` (or ``[B, Hq, D]``).
 
     Returns ``out`` shaped like ``q`` (``[B, 1, Hq, D]`` as
@@ -189,6 +189,11 @@ def paged_decode(q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale,
     cached tokens including the new one; ``block_table [B, W] int32``.
     With ``gate [B, Hq, D]`` (Qwen3.5's output gate, models/qwen3_5.py:142)
     the output is ``out * sigmoid(gate)``, applied in the kernel's store.
+    With ``k, v [B, Hkv, D]`` and ``slot_mapping [B] int32`` the new token is
+    stored in the same launch (``nq_paged_decode_store``): the result and the
+    cache equal ``store_kvcache`` followed by this call when each
+    ``slot_mapping[b]`` is -1 or the slot of token ``cache_seqlens[b] - 1``
+    of ``block_table[b]`` (what prepare_decode writes).
     """
     require_cuda(q, k_cache, v_cache, cache_seqlens, block_table, what="paged_decode")
     q3 = q.squeeze(1) if q.dim() == 4 else q
@@ -217,13 +222,34 @@ def paged_decode(q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale,
             B, hq, hkv, d, bs, nb, float(softmax_scale), ns, st, ptr(ws), 0 if ws is None else ws.numel(),
             dtype_code(q.dtype), dtype_code(k_cache.dtype), ptr(k_scale) if fp8 else None,
             ptr(v_scale) if fp8 else None)
-    if gate is None:
-        rc = lib().nq_paged_decode(*args, stream_of(q))
-    else:
+    g3 = None
+    if gate is not None:
         require_cuda(gate, what="paged_decode")
         if gate.dtype != q.dtype:
             raise RuntimeError("paged_decode: gate dtype must match q")
         g3 = _gate3(gate, B, hq, d, "paged_decode")
+    if k is not None:
+        require_cuda(k, v, slot_mapping, what="paged_decode")
+        k3 = k.reshape(B, hkv, d) if k.dim() == 4 else k
+        v3 = v.reshape(B, hkv, d) if v.dim() == 4 else v
+        for t, what in ((k3, "k"), (v3, "v")):
+            if t.shape != (B, hkv, d) or t.stride(-1) != 1 or t.stride(1) != d:
+                raise RuntimeError(f"paged_decode: {what} must be [B, Hkv, D] with contiguous heads")
+        if k3.dtype != v3.dtype or (not fp8 and k3.dtype != k_cache.dtype):
+            raise RuntimeError("paged_decode: k/v dtype must match the cache (or be stored into an fp8 cache)")
+        if slot_mapping.dtype != torch.int32 or slot_mapping.numel() != B:
+            raise RuntimeError("paged_decode: slot_mapping must be int32 [B]")
+        rc = lib().nq_paged_decode_store(
+            ptr(q3), q3.stride(0), q3.stride(1), ptr(k_cache), ptr(v_cache), ptr(block_table),
+            block_table.stride(0), W, ptr(cache_seqlens), ptr(k3), k3.stride(0), ptr(v3), v3.stride(0),
+            ptr(slot_mapping), dtype_code(k3.dtype), ptr(o3), o3.stride(0), o3.stride(1),
+            B, hq, hkv, d, bs, nb, float(softmax_scale), ns, st, ptr(ws), 0 if ws is None else ws.numel(),
+            dtype_code(q.dtype), dtype_code(k_cache.dtype), ptr(k_scale) if fp8 else None,
+            ptr(v_scale) if fp8 else None, ptr(g3) if g3 is not None else None,
+            0 if g3 is None else g3.stride(0), 0 if g3 is None else g3.stride(1), stream_of(q))
+    elif g3 is None:
+        rc = lib().nq_paged_decode(*args, stream_of(q))
+    else:
         rc = lib().nq_paged_decode_gated(*args, ptr(g3), g3.stride(0), g3.stride(1), stream_of(q))
     check(rc, "paged_decode")
     return out

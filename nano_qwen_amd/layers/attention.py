@@ -44,7 +44,8 @@ class Attention(nn.Module):
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_stored: bool = False,
                 gate: torch.Tensor | None = None):
-        """layers/attention.py:59-75: store, then prefill or paged decode.
+        """layers/attention.py:59-75: store, then prefill or paged decode
+        (in decode the store and the attention are one launch).
 
         ``kv_stored=True`` skips the store because the caller already made it
         (``layers.qk_norm_rope_store`` stores in the same launch as the q/k
@@ -54,7 +55,22 @@ class Attention(nn.Module):
         """
         context = get_context()
         k_cache, v_cache = self.k_cache, self.v_cache
-        if k_cache.numel() and v_cache.numel() and not kv_stored:
+        store = k_cache.numel() and v_cache.numel() and not kv_stored
+        if store and not context.is_prefill:
+            # decode: the store rides in the decode launch (nq_paged_decode_store);
+            # the reference's asserts of the store still apply
+            N, num_heads, head_dim = k.shape
+            assert k.stride(-1) == 1 and v.stride(-1) == 1
+            assert k.stride(1) == head_dim and v.stride(1) == head_dim
+            assert k_cache.stride(1) == num_heads * head_dim and v_cache.stride(1) == num_heads * head_dim
+            assert context.slot_mapping.numel() == N
+            return kernels.paged_decode(q.unsqueeze(1), k_cache, v_cache,
+                                        cache_seqlens=context.context_lens,
+                                        block_table=context.block_tables, softmax_scale=self.scale,
+                                        k_scale=self.k_scale, v_scale=self.v_scale,
+                                        gate=None if gate is None else gate.unsqueeze(1),
+                                        k=k, v=v, slot_mapping=context.slot_mapping)
+        if store:
             store_kvcache(k, v, k_cache, v_cache, context.slot_mapping, self.k_scale, self.v_scale)
         if context.is_prefill:
             k_scale = v_scale = None
