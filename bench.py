@@ -10,7 +10,10 @@ A "step" is one pass of the path over one batch of synthetic input:
 Inputs are resident in HBM before timing starts.  Decode steps alternate
 between two independent KV pools (each larger than the 256 MB MALL), so no
 step re-reads KV the previous step left in the Infinity Cache; the same step
-replayed as a HIP graph (the runner's path) is reported as ``graph_ms``.
+replayed as a HIP graph (the runner's path) is reported as ``graph_ms``: the
+time per step in a graph of 4 steps, as the runner's whole-model graphs run
+every layer's step per replay (``graph1_ms``: one step per graph, which also
+carries the replay's own launch time).
 Every measurement warms up for at least 20 ms
 and times its steps back to back in five groups between events:
 ``ms_per_step`` is the mean over all timed steps (the whole-step rates, and
@@ -47,6 +50,7 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0
+GRAPH_LAYERS = 4  # decode steps (layers) captured per graph for graph_ms
 BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -129,20 +133,30 @@ def bench_decode(name, steps, warmup, seed=0, **override):
 
     ms = _events_time(step, steps, warmup)
     ms_mean = _LAST["mean"]
-    # The step as a graph replay (engine run_model's path), one graph per
-    # pool, for comparison.
+    # The step as graph replays (engine run_model's path).  The runner
+    # captures the whole model per batch bucket, so each replay runs every
+    # layer's attention step: graph_ms is the time per step in a graph of
+    # GRAPH_LAYERS steps (alternating pools, as consecutive layers read
+    # different caches); graph1_ms the same with one step per graph, which
+    # also carries the replay's own launch time (a few microseconds of idle
+    # GPU per replay on this ROCm).
     side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        step(0)  # the capture stream's workspace exists before the capture
+    side.synchronize()
+    multi = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(multi, stream=side):
+        for layer in range(GRAPH_LAYERS):
+            step(layer)
     graphs = []
     for p in range(2):
-        with torch.cuda.stream(side):
-            step(p)  # the capture stream's workspace exists before the capture
-        side.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=side):
             step(p)
         graphs.append(g)
     torch.cuda.synchronize()
-    ms_graph = _events_time(lambda i: graphs[i % 2].replay(), steps, warmup)
+    ms_graph = _events_time(lambda i: multi.replay(), max(1, steps // GRAPH_LAYERS), warmup) / GRAPH_LAYERS
+    ms_graph1 = _events_time(lambda i: graphs[i % 2].replay(), steps, warmup)
     ms_attn = _events_time(attn_only, steps, warmup)
     ms_two = _events_time(two_calls, steps, warmup)
     nbytes = decode_bytes(case)
@@ -156,7 +170,8 @@ def bench_decode(name, steps, warmup, seed=0, **override):
         ms_per_step=ms_mean, ms_median=ms, graph_ms=ms_graph, gbs=nbytes / (ms_mean * 1e-3) / 1e9,
         tokens_per_s=case["batch"] / (ms_mean * 1e-3), median_gbs=nbytes / (ms * 1e-3) / 1e9,
         hbm_frac=nbytes / (ms_mean * 1e-3) / 1e9 / HBM_PEAK_GBS, bytes_per_step=nbytes,
-        graph_hbm_frac=nbytes / (ms_graph * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        graph_hbm_frac=nbytes / (ms_graph * 1e-3) / 1e9 / HBM_PEAK_GBS, graph_layers=GRAPH_LAYERS,
+        graph1_ms=ms_graph1, graph1_hbm_frac=nbytes / (ms_graph1 * 1e-3) / 1e9 / HBM_PEAK_GBS,
         tflops=decode_flops(case) / (ms * 1e-3) / 1e12,
         step_median_gbs=nbytes / (ms * 1e-3) / 1e9,
         attn_ms=ms_attn, attn_gbs=attn_bytes / (ms_attn * 1e-3) / 1e9, attn_bytes=attn_bytes,
