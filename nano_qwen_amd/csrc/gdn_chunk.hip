@@ -22,28 +22,39 @@
 // arithmetic.  (W = T diag(beta exp(G)) K of the reference is never formed:
 // W S^T = (T diag(..)) (K S^T).)
 //
-// One 8-wave workgroup (two waves per SIMD) per (sequence, value head) walks
-// the sequence's chunks.  The state lives in MFMA accumulators (wave w owns
-// value rows 32 (w / 2) .. +31 against key columns 64 (w % 2) .. +63), in
-// float32 across the whole sequence, with a 16-bit copy in LDS for the
-// products that read it; every product runs on v_mfma_f32_32x32x16 with
-// 16-bit operands and float32 accumulation, as the reference's kernels do
-// (their tl.dot operands are the input dtype).  The 64x64 triangular inverse
-// runs in float32: its four 16x16 diagonal blocks on the VALU of waves 0-3
-// while waves 4-7 form K S^T and Q S^T, which do not depend on it, then the
-// off-diagonal blocks as float32 products (v_mfma_f32_16x16x4f32).
+// One 4-wave workgroup per (sequence, value head) walks the sequence's
+// chunks; two fit on a CU (70 KiB of LDS, at most 256 VGPRs a wave).  Wave w
+// owns value columns 32 w .. +31 of the state S^T [K][V], all 128 key rows of
+// them, as float32 MFMA accumulators for the whole sequence: every
+// state-dependent product of the chunk (Y = K S^T, Q S^T, the update
+// solve, O += P D and the state update) is the wave's own, with no state
+// copy through LDS and no barrier.  Only the chunk's shared inputs go
+// through LDS: unit keys, scaled unit queries, V, the gates, A and P.
 //
-// LDS tiles are row-major with 16-byte chunks XOR-swizzled per row: tiles
-// read only as row operands (ds_read_b128) use swz_r, tiles also read down
-// their columns (ds_read_b64_tr_b16) use swz_c.
+// The update D = T (diag(beta) V + Tw' Y) is formed as the solution of
+// (I + A) D = Z, Z = diag(beta) (V - diag(exp(G)) Y), by substitution over
+// the four 16-token blocks of the chunk: D_j = T_jj (Z_j - sum_{m<j} A_jm D_m),
+// with the inverses T_jj of the 16x16 diagonal blocks formed in float32 on
+// the VALU (forward substitution, one lane per column) and the products on
+// v_mfma_f32_16x16x16, whose accumulator rows are the next product's
+// B-operand rows.  The other products run on v_mfma_f32_16x16x32 with
+// 16-bit operands and float32 accumulation, as the reference's kernels do.
+// A state block's accumulator row i holds key 32 s + 8 (i / 4) + 4 o + i % 4
+// (block 2 s + o), so that the packed accumulators of blocks 2 s and 2 s + 1
+// are the standard B operand of k-step s; the state update reads K down its
+// columns in that order.
+//
+// LDS tiles are row-major with 16-byte chunks XOR-swizzled per row (128-
+// column tiles: swz_r for row reads only, swz_c for tiles also read down
+// their columns) or 8-byte pieces XOR-swizzled (64-column tiles, t64).
 #include "nq_device.hpp"
 
 namespace nq {
 namespace {
 
-constexpr int kC = 64;       // tokens per chunk
-constexpr int kD = 128;      // K = V
-constexpr int kThreads = 512;  // 8 waves, two per SIMD
+constexpr int kC = 64;         // tokens per chunk
+constexpr int kD = 128;        // K = V
+constexpr int kThreads = 256;  // 4 waves, one per SIMD; two workgroups per CU
 
 struct ChunkArgs {
   const uint8_t *q, *k, *v;  // [T, H, K], [T, H, K], [T, HV, V] (dtype T)
@@ -64,28 +75,21 @@ struct ChunkArgs {
 constexpr int kSortSeqs = 64;  // batches up to this size run their longest sequences first
 
 // LDS layout (bytes).
-constexpr int kTile = kC * kD * 2;           // 64 x 128 16-bit values
-constexpr int kOffK = 0;                     // K (unit keys), swz_c
-constexpr int kOffQ = kOffK + kTile;         // Q (scaled unit queries), swz_r; then the output tile
-constexpr int kOffV = kOffQ + kTile;         // V, swz_c; then D^T ([V][T], 128 x 64, swz_6)
-constexpr int kOffS = kOffV + kTile;         // S^T, 16-bit [K][V], swz_c
-constexpr int kTfStride = 68;                // floats per row of the fp32 64x64 matrix
-constexpr int kOffT = kOffS + kD * kD * 2;   // A, then T (fp32 64 x 68)
-constexpr int kOffTw = kOffT + kC * kTfStride * 4;
-constexpr int kOffTu = kOffTw + kC * kC * 2;  // 64 x 64 16-bit, swz_6
-constexpr int kOffP = kOffTu + kC * kC * 2;  // P^T [j][i], swz_6
-constexpr int kGates = 4 * kC * 4;            // G, beta, exp(G), exp(G_C - G): 64 fp32 each
-constexpr int kOffG = kOffP + kC * kC * 2;    // two gate sets: this chunk's and the next one's
-constexpr int kOffM = kOffG + 2 * kGates;     // 4 x 16 x 16 fp32: block products of the inverse
-constexpr int kOffY = kOffM + 4 * 256 * 4;    // Y^T = S K^T, [V][T] 128 x 64 16-bit, swz_6
-constexpr int kLds = kOffY + kTile;
-static_assert(kLds <= 160 * 1024, "LDS");
+constexpr int kTile = kC * kD * 2;         // 64 x 128 16-bit values
+constexpr int kOffK = 0;                   // K (unit keys) [t][k], swz_c
+constexpr int kOffQ = kOffK + kTile;       // Q (scaled unit queries) [t][k], swz_r
+constexpr int kOffV = kOffQ + kTile;       // V [t][v], swz_c
+constexpr int kOffA = kOffV + kTile;       // 64 x 64 16-bit (t64): -A off the diagonal blocks, T_jj on them
+constexpr int kOffP = kOffA + kC * kC * 2;  // P [i][j] (t64), zero above the diagonal blocks
+constexpr int kOffB = kOffP + kC * kC * 2;  // the four diagonal 16x16 blocks of A, fp32 [b][i][j]
+constexpr int kGates = 4 * kC * 4;          // G, beta, exp(G), exp(G_C - G): 64 fp32 each
+constexpr int kOffG = kOffB + 4 * 256 * 4;  // two gate sets: this chunk's and the next one's
+constexpr int kLds = kOffG + 2 * kGates;
+static_assert(2 * kLds <= 160 * 1024, "two workgroups per CU");
 
-// Chunk swizzles of the 128-column tiles (16 chunks a row) and of the
-// 64-column tiles (8 chunks a row, two rows per 256 bytes).
+// Chunk swizzles of the 128-column tiles (16 chunks a row).
 __device__ inline int swz_r(int row) { return row & 15; }
 __device__ inline int swz_c(int row) { return ((row & 7) << 1) | ((row >> 3) & 1); }
-__device__ inline int swz_6(int row) { return (row >> 1) & 7; }
 
 __device__ inline uint32_t lds_addr(const uint8_t *p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t *)(p)));
@@ -93,7 +97,10 @@ __device__ inline uint32_t lds_addr(const uint8_t *p) {
 __device__ inline uint32_t a128(uint32_t base, int row, int chunk, bool colwise) {
   return base + row * 256 + ((chunk ^ (colwise ? swz_c(row) : swz_r(row))) << 4);
 }
-__device__ inline uint32_t a64(uint32_t base, int row, int chunk) { return base + row * 128 + ((chunk ^ swz_6(row)) << 4); }
+// 8-byte piece `piece` (columns 4 piece .. +3) of row `row` of a 64-column 16-bit tile.
+__device__ inline uint32_t t64(uint32_t base, int row, int piece) {
+  return base + row * 128 + ((piece ^ (row & 15)) << 3);
+}
 __device__ inline void st16(uint32_t addr, uint16_t v) {
   *reinterpret_cast<__attribute__((address_space(3))) uint16_t *>(static_cast<uintptr_t>(addr)) = v;
 }
@@ -109,42 +116,12 @@ __device__ inline f32x4 ldf4(uint32_t addr) {
 __device__ inline void stf4(uint32_t addr, const f32x4 &v) {
   *reinterpret_cast<__attribute__((address_space(3))) f32x4 *>(static_cast<uintptr_t>(addr)) = v;
 }
-
-// Row operand of a 32x32x16 product from a 128-column tile: lane l takes
-// row r0 + l % 32, columns 16 s + 8 (l / 32) .. +7 (k-step s).
-__device__ inline u32x4 row_op(uint32_t base, int r0, int s, int lane, bool colwise) {
-  return lds_load_b128<0>(a128(base, r0 + (lane & 31), 2 * s + (lane >> 5), colwise));
+__device__ inline u32x2 lds_load_b64(uint32_t addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) u32x2 *>(static_cast<uintptr_t>(addr));
 }
-__device__ inline u32x4 row_op64(uint32_t base, int r0, int s, int lane) {
-  return lds_load_b128<0>(a64(base, r0 + (lane & 31), 2 * s + (lane >> 5)));
+__device__ inline void lds_store_b64(uint32_t addr, const u32x2 &v) {
+  *reinterpret_cast<__attribute__((address_space(3))) u32x2 *>(static_cast<uintptr_t>(addr)) = v;
 }
-// Column operand from a 128-column swz_c tile: lane l takes rows
-// 16 s + 8 (l / 32) .. +7 of column c0 + l % 32, by two transposing reads
-// (in a 16-lane group, lane i addresses row + (i >> 2), 8-byte piece i & 3 of
-// the group's 32 bytes, and receives the group's column i).
-__device__ inline u32x4 col_op(uint32_t base, int c0, int s, int lane) {
-  const int i = lane & 15, grp = lane >> 4;
-  const int row = 16 * s + 8 * (lane >> 5) + (i >> 2);
-  const int chunk = (c0 >> 3) + 2 * (grp & 1) + ((i & 3) >> 1);
-  const uint32_t lo_a = a128(base, row, chunk, true) + 8 * (i & 1);
-  const uint32_t hi_a = a128(base, row + 4, chunk, true) + 8 * (i & 1);
-  const u32x2 lo = lds_load_tr16<0>(lo_a), hi = lds_load_tr16<0>(hi_a);
-  return u32x4{lo[0], lo[1], hi[0], hi[1]};
-}
-
-// The same from a 64-column tile (swz_6).
-__device__ inline u32x4 col_op64(uint32_t base, int c0, int s, int lane) {
-  const int i = lane & 15, grp = lane >> 4;
-  const int row = 16 * s + 8 * (lane >> 5) + (i >> 2);
-  const int chunk = (c0 >> 3) + 2 * (grp & 1) + ((i & 3) >> 1);
-  const uint32_t lo_a = a64(base, row, chunk) + 8 * (i & 1);
-  const uint32_t hi_a = a64(base, row + 4, chunk) + 8 * (i & 1);
-  const u32x2 lo = lds_load_tr16<0>(lo_a), hi = lds_load_tr16<0>(hi_a);
-  return u32x4{lo[0], lo[1], hi[0], hi[1]};
-}
-
-// Accumulator element r of lane l: row (r & 3) + 4 (l / 32) + 8 (r / 4), column l % 32.
-__device__ inline int acc_row(int r, int lane) { return (r & 3) + 4 * (lane >> 5) + 8 * (r >> 2); }
 
 __device__ inline float softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
 
@@ -152,12 +129,10 @@ template <int CTRL, int ROW_MASK>
 __device__ inline float dpp_f(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, false));
 }
-// Sum over the 8 lanes of an aligned group (xor 1, xor 2 within quads, then
-// the mirrored quad); every lane of the group gets the same bits.
-__device__ inline float sum8(float v) {
-  v += dpp_f<0xb1, 0xf>(v);   // quad_perm [1, 0, 3, 2]
-  v += dpp_f<0x4e, 0xf>(v);   // quad_perm [2, 3, 0, 1]
-  return v + dpp_f<0x141, 0xf>(v);  // row_half_mirror
+// Sum over the 4 lanes of a quad; every lane gets the same bits.
+__device__ inline float sum4(float v) {
+  v += dpp_f<0xb1, 0xf>(v);       // quad_perm [1, 0, 3, 2]
+  return v + dpp_f<0x4e, 0xf>(v);  // quad_perm [2, 3, 0, 1]
 }
 // Inclusive prefix sum over the wave: shifts by 1, 2, 4, 8 within each
 // 16-lane row, then each row's running total into the rows after it
@@ -176,52 +151,18 @@ template <class T>
 __device__ inline f32x4 unpack2x2(uint32_t w0, uint32_t w1) {
   return f32x4{T::to_float(w0 & 0xffffu), T::to_float(w0 >> 16), T::to_float(w1 & 0xffffu), T::to_float(w1 >> 16)};
 }
-
-// acc + X Y for 16x16 float32 blocks in LDS (row strides xs, ys floats) on
-// v_mfma_f32_16x16x4f32: k-slice q takes X[l % 16][4q + l / 16] and
-// Y[4q + l / 16][l % 16]; element r of lane l of the result is row
-// 4 (l / 16) + r, column l % 16.
-__device__ inline f32x4 prod16(uint32_t x, int xs, uint32_t y, int ys, f32x4 acc, int lane) {
-  float av[4], bv[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    av[q] = ldf(x + 4 * ((lane & 15) * xs + 4 * q + (lane >> 4)));
-    bv[q] = ldf(y + 4 * ((4 * q + (lane >> 4)) * ys + (lane & 15)));
-  }
-#pragma unroll
-  for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[q], bv[q], acc, 0, 0, 0);
-  return acc;
-}
-__device__ inline void store16x16(uint32_t base, int stride, const f32x4 &v, float sign, int lane) {
-#pragma unroll
-  for (int r = 0; r < 4; ++r) stf(base + 4 * ((4 * (lane >> 4) + r) * stride + (lane & 15)), sign * v[r]);
-}
-
-__device__ inline void lds_store_b64(uint32_t addr, const u32x2 &v) {
-  *reinterpret_cast<__attribute__((address_space(3))) u32x2 *>(static_cast<uintptr_t>(addr)) = v;
-}
-// 16-bit copy of a 32x32 accumulator block, transposed: element
-// (m0 + acc_row(r, l), n0 + l % 32) goes to tile row n0 + l % 32, column
-// m0 + acc_row(r, l).  Each lane's runs of 4 consecutive M rows become
-// 8-byte writes.  The tile has 128 columns (swz_c) or 64 (swz_6).
 template <class T>
-__device__ inline void st_acc_t(uint32_t tile, bool c128, int m0, int n0, const f32x16 &acc, int lane) {
-  const int row = n0 + (lane & 31);
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int col = m0 + 8 * q + 4 * (lane >> 5);
-    const u32x2 w = u32x2{T::pack2(acc[4 * q], acc[4 * q + 1]), T::pack2(acc[4 * q + 2], acc[4 * q + 3])};
-    const uint32_t ca = c128 ? a128(tile, row, col >> 3, true) : a64(tile, row, col >> 3);
-    lds_store_b64(ca + 2 * (col & 7), w);
-  }
+__device__ inline u32x2 pack4(const f32x4 &v) {
+  return u32x2{T::pack2(v[0], v[1]), T::pack2(v[2], v[3])};
 }
-// 16-bit copy of a wave's state blocks (value rows 32 vb .. +31, key
-// columns 32 kb0 .. +63) into the S^T tile ([K][V], swz_c).
+// B operand of a 16x16x32 k-step from two 16-row accumulator blocks: rows
+// 4 (l / 16) .. +3 of `lo`, then of `hi` (the contraction order the A
+// operand reads follow).
 template <class T>
-__device__ inline void write_state(uint32_t s_base, const f32x16 (&S)[2], int vb, int kb0, int lane) {
-#pragma unroll
-  for (int j = 0; j < 2; ++j) st_acc_t<T>(s_base, true, 32 * vb, 32 * (kb0 + j), S[j], lane);
+__device__ inline u32x4 pack8(const f32x4 &lo, const f32x4 &hi) {
+  return u32x4{T::pack2(lo[0], lo[1]), T::pack2(lo[2], lo[3]), T::pack2(hi[0], hi[1]), T::pack2(hi[2], hi[3])};
 }
+__device__ inline u32x4 cat(const u32x2 &lo, const u32x2 &hi) { return u32x4{lo[0], lo[1], hi[0], hi[1]}; }
 
 // Workgroup barrier after this wave's LDS writes complete, without the
 // fence of __syncthreads(), which would also wait for the next chunk's
@@ -231,15 +172,40 @@ __device__ inline void lds_sync() {
   raw_barrier();
 }
 
+// A operand of the state update from the K tile read down its columns: lane
+// l (i = l % 16, g = l / 16) takes key 32 sg + 8 (i / 4) + 4 o + i % 4 (row
+// i of state block 2 sg + o) at tokens 32 s + 4 g .. +3 and 32 s + 16 + 4 g
+// .. +3.  In a transposing read, lane 4 rho + p addresses row rho and an
+// 8-byte piece, and lane i receives element i % 4 of the pieces of lanes
+// i / 4, 4 + i / 4, 8 + i / 4, 12 + i / 4: piece p is keys 32 sg + 8 p + 4 o .. +3.
+__device__ inline u32x4 kt_op(uint32_t LK, int sg, int o, int s, int lane) {
+  const int i = lane & 15, g = lane >> 4;
+  const int rho = i >> 2, p = i & 3;
+  const uint32_t lo = a128(LK, 32 * s + 4 * g + rho, 4 * sg + p, true) + 8 * o;
+  const uint32_t hi = a128(LK, 32 * s + 16 + 4 * g + rho, 4 * sg + p, true) + 8 * o;
+  return cat(lds_load_tr16<0>(lo), lds_load_tr16<0>(hi));
+}
+
 template <class T>
-__global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_chunk_kernel(
+    const ChunkArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t L = lds_addr(smem);
-  const uint32_t LK = L + kOffK, LQ = L + kOffQ, LV = L + kOffV, LS = L + kOffS, LT = L + kOffT, LTw = L + kOffTw,
-                 LTu = L + kOffTu, LP = L + kOffP, LM = L + kOffM, LY = L + kOffY;
+  const uint32_t LK = L + kOffK, LQ = L + kOffQ, LV = L + kOffV, LA = L + kOffA, LP = L + kOffP, LBD = L + kOffB;
   const int tid0 = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid0 >> 6);  // uniform: branches on it are scalar
-  const int hv = blockIdx.x;
+  // The value heads of one key head read the same q and k: with enough heads
+  // they get grid columns 8 apart, which the hardware places on the same XCD
+  // (workgroup L on XCD L % 8), so the second reads them from that L2.
+  int hv = blockIdx.x;
+  {
+    const int G = a.HV / a.H;
+    if (G > 1 && a.HV % (8 * G) == 0) {
+      const int i = hv & 7, j = hv >> 3;
+      hv = (i + 8 * (j / G)) * G + j % G;
+    }
+    hv = __builtin_amdgcn_readfirstlane(hv);  // uniform: the head's constants load as scalars
+  }
   // Workgroups start in grid order and a sequence's chunks run one after
   // another, so the longest sequences go first (row y of the grid takes the
   // sequence of rank y by length, ties by index); wave 0 ranks them.
@@ -254,12 +220,12 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
         rank += (l2 > len || (l2 == len && s2 < lane)) ? 1 : 0;
       }
       const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < a.num_seqs && rank == static_cast<int>(blockIdx.y));
-      if (lane == 0) *reinterpret_cast<__attribute__((address_space(3))) int *>(static_cast<uintptr_t>(L + kOffM)) =
+      if (lane == 0) *reinterpret_cast<__attribute__((address_space(3))) int *>(static_cast<uintptr_t>(L + kOffG)) =
           static_cast<int>(__builtin_ctzll(hit));
     }
     lds_sync();
     n = __builtin_amdgcn_readfirstlane(
-        *reinterpret_cast<const __attribute__((address_space(3))) int *>(static_cast<uintptr_t>(L + kOffM)));
+        *reinterpret_cast<const __attribute__((address_space(3))) int *>(static_cast<uintptr_t>(L + kOffG)));
     lds_sync();  // read by every wave before the region is reused
   }
   const int h = hv / (a.HV / a.H);
@@ -267,46 +233,72 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
   const int slot = a.idx[n];
   const bool has = slot >= 0 && slot < a.num_slots;
   float *st = has ? a.state + (static_cast<int64_t>(slot) * a.HV + hv) * kD * kD : nullptr;
-  const float neg_a = -expf(a.A_log[hv]), dtb = a.dt_bias[hv];
+  // per-head gate constants, held in scalar registers
+  const float neg_a = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, -expf(a.A_log[hv]))));
+  const float dtb = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, a.dt_bias[hv])));
 
-  // This wave's state blocks: value rows 32 vb .. +31, key columns 32 (kb0 + j) .. +31.
-  const int vb = wave >> 1, kb0 = 2 * (wave & 1);
-  f32x16 S[2];
+  // This wave's state: S^T blocks kb (keys, in the order above) x half hf
+  // (value columns 32 wave + 16 hf .. +15); element r of lane l is key
+  // 32 (kb / 2) + 8 (l / 16) + 4 (kb % 2) + r, value column 32 wave + 16 hf + l % 16.
+  const int m0 = tid0 & 15, g0 = (tid0 >> 4) & 3;
+  f32x4 S[8][2];
+  auto state_at = [&](int kb, int hf) {
+    return reinterpret_cast<f32x4 *>(st + (32 * wave + 16 * hf + m0) * kD + 32 * (kb >> 1) + 8 * g0 + 4 * (kb & 1));
+  };
+  if (has && a.from_slot) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+    for (int kb = 0; kb < 8; ++kb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-      S[j][r] = (has && a.from_slot) ? st[(32 * vb + acc_row(r, tid0 & 63)) * kD + 32 * (kb0 + j) + (tid0 & 31)]
-                                     : 0.f;
+      for (int hf = 0; hf < 2; ++hf) S[kb][hf] = *state_at(kb, hf);
+  } else {
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) S[kb][hf] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
-  if (t1 > t0) write_state<T>(LS, S, vb, kb0, tid0 & 63);
-  // Inputs of a chunk, fetched one chunk ahead: row tid / 8 (columns
-  // 16 (tid % 8) .. +15) of q, k, v, and (wave 0) lane's gate inputs.
-  u32x4 qv[2], kv[2], vv[2];
-  uint32_t gab = 0;  // a (low half) and b (high half) of token lane
+  // Inputs of a chunk: q and k fetched one chunk ahead into registers (row
+  // tid / 4, columns 32 (tid % 4) .. +31), and (wave 0) lane's gate inputs.
   // Through buffer descriptors over the chunk's rows of this head: rows past
   // the sequence are out of range and read as zeros.
+  u32x4 qv[4], kv[4];
+  uint32_t ga = 0, gb = 0;  // a and b of token lane, as 16-bit codes (combined only when used)
   auto fetch = [&](int c0, int tid) {
-    const int r = tid >> 3, e = tid & 7;
+    const int r = tid >> 2, e = tid & 3;
     const int rows = min(kC, t1 - c0);
+    // the gate inputs first: waiting for them does not wait for q and k
+    if (tid < 64) {
+      const int64_t tg = c0 + tid;
+      const bool in = tid < t1 - c0;
+      ga = in ? reinterpret_cast<const uint16_t *>(a.a + tg * a.a_rs)[hv] : 0u;
+      gb = in ? reinterpret_cast<const uint16_t *>(a.b + tg * a.b_rs)[hv] : 0u;
+    }
     const auto rq = make_rsrc(a.q + static_cast<int64_t>(c0) * a.q_rs + h * kD * 2,
                               static_cast<uint32_t>((rows - 1) * a.q_rs + kD * 2));
     const auto rk = make_rsrc(a.k + static_cast<int64_t>(c0) * a.k_rs + h * kD * 2,
                               static_cast<uint32_t>((rows - 1) * a.k_rs + kD * 2));
-    const auto rv = make_rsrc(a.v + static_cast<int64_t>(c0) * a.v_rs + hv * kD * 2,
-                              static_cast<uint32_t>((rows - 1) * a.v_rs + kD * 2));
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col2 = (16 * e + 8 * j) * 2;
+    for (int j = 0; j < 4; ++j) {
+      const int col2 = (32 * e + 8 * j) * 2;
       qv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, r * static_cast<int>(a.q_rs) + col2, 0, 0));
       kv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, r * static_cast<int>(a.k_rs) + col2, 0, 0));
-      vv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, r * static_cast<int>(a.v_rs) + col2, 0, 0));
     }
-    if (tid < 64) {
-      const int64_t tg = c0 + tid;
-      gab = tid < t1 - c0 ? (static_cast<uint32_t>(reinterpret_cast<const uint16_t *>(a.a + tg * a.a_rs)[hv]) |
-                             (static_cast<uint32_t>(reinterpret_cast<const uint16_t *>(a.b + tg * a.b_rs)[hv]) << 16))
-                          : 0u;
+  };
+  // V of the chunk at c0 straight into its LDS tile (no registers): wave w
+  // copies rows 16 w .. +15, four rows per copy; lane l of a copy lands in
+  // chunk position l % 16 of row 4 q + l / 16 and so loads the logical chunk
+  // that the swizzle puts there.  Rows past the sequence read as zeros.
+  // Completed by the vmcnt(0) before the barrier ahead of Z's reads.
+  auto copy_v = [&](int c0, int tid) {
+    const int rows = min(kC, t1 - c0);
+    const u32x4 rv = rsrc_words(a.v + static_cast<int64_t>(c0) * a.v_rs + hv * kD * 2,
+                                static_cast<uint32_t>((rows - 1) * a.v_rs + kD * 2));
+    const int l = tid & 63;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int row0 = 16 * wave + 4 * q4, row = row0 + (l >> 4);  // row0 uniform: M0
+      const int chunk = (l & 15) ^ swz_c(row);
+      dma16_opaque(LV + row0 * 256, rv, static_cast<uint32_t>(row * static_cast<int>(a.v_rs) + 16 * chunk));
     }
   };
   // Gates of the chunk whose inputs gab holds (wave 0; lane = token): G, the
@@ -317,10 +309,8 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
     const uint32_t g0 = L + kOffG + set * kGates;
     float g = 0.f, beta = 0.f;
     if (lane < ck) {
-      const float ga = T::to_float(static_cast<uint16_t>(gab & 0xffffu));
-      const float gb = T::to_float(static_cast<uint16_t>(gab >> 16));
-      g = neg_a * softplus(ga + dtb);
-      beta = 1.0f / (1.0f + expf(-gb));
+      g = neg_a * softplus(T::to_float(static_cast<uint16_t>(ga)) + dtb);
+      beta = 1.0f / (1.0f + expf(-T::to_float(static_cast<uint16_t>(gb))));
     }
     g = wave_scan(g);
     // G_C = G of the chunk's last token (tokens past the sequence add 0)
@@ -333,6 +323,9 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
   if (t1 > t0) {
     fetch(t0, tid0);
     if (wave == 0) gates(min(kC, t1 - t0), 0);
+    // P's blocks (0, 1) and (2, 3), read by O += P D and never written
+    // otherwise: zero once
+    if (wave < 2) lds_store_b64(t64(L + kOffP, 32 * wave + (tid0 & 15), 4 * (2 * wave + 1) + ((tid0 >> 4) & 3)), u32x2{0u, 0u});
   }
   for (int c0 = t0; c0 < t1; c0 += kC) {
     // this chunk's gate set (the next chunk's is written during this one)
@@ -340,335 +333,281 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(const ChunkArgs a) 
     const uint32_t LG = L + kOffG + gset * kGates, LB = LG + kC * 4, LEG = LB + kC * 4, LEC = LEG + kC * 4;
     const int ck = min(kC, t1 - c0);
     // The thread index from an instruction the compiler cannot hoist: the
-    // hundreds of LDS addresses derived from it are recomputed per chunk
-    // instead of each holding a register across the loop.
+    // LDS addresses derived from it are recomputed per chunk instead of each
+    // holding a register across the loop.
     int tid = tid0;
     asm volatile("" : "+v"(tid));
     const int lane = tid & 63;
+    const int m = lane & 15, g = lane >> 4;
     const int wv = tid >> 6;  // the wave index for addresses (branches use the uniform `wave`)
-    // ---- unit keys, scaled unit queries (float32 norms, rounded to 16
-    // bits) and values into LDS; gates and their inclusive sum G.
+    // ---- unit keys and scaled unit queries (float32 norms, rounded to 16
+    // bits) into LDS.
     {
-      const int r = tid >> 3, e = tid & 7;
-      float fq[16], fk[16];
+      const int r = tid >> 2, e = tid & 3;
       float sq = 0.f, sk = 0.f;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < 4; ++j) {
         const f32x4 q0 = unpack2x2<T>(qv[j][0], qv[j][1]), q1 = unpack2x2<T>(qv[j][2], qv[j][3]);
         const f32x4 k0 = unpack2x2<T>(kv[j][0], kv[j][1]), k1 = unpack2x2<T>(kv[j][2], kv[j][3]);
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
-          fq[8 * j + x] = q0[x];
-          fq[8 * j + 4 + x] = q1[x];
-          fk[8 * j + x] = k0[x];
-          fk[8 * j + 4 + x] = k1[x];
+          sq += q0[x] * q0[x] + q1[x] * q1[x];
+          sk += k0[x] * k0[x] + k1[x] * k1[x];
         }
       }
-#pragma unroll
-      for (int x = 0; x < 16; ++x) {
-        sq += fq[x] * fq[x];
-        sk += fk[x] * fk[x];
-      }
-      sq = sum8(sq);
-      sk = sum8(sk);
+      sq = sum4(sq);
+      sk = sum4(sk);
       const float rq = a.scale * __builtin_amdgcn_rsqf(sq + a.eps), rk = __builtin_amdgcn_rsqf(sk + a.eps);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < 4; ++j) {
         u32x4 wq, wk;
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
-          wq[x] = T::pack2(fq[8 * j + 2 * x] * rq, fq[8 * j + 2 * x + 1] * rq);
-          wk[x] = T::pack2(fk[8 * j + 2 * x] * rk, fk[8 * j + 2 * x + 1] * rk);
+          wq[x] = T::pack2(T::to_float(qv[j][x] & 0xffffu) * rq, T::to_float(qv[j][x] >> 16) * rq);
+          wk[x] = T::pack2(T::to_float(kv[j][x] & 0xffffu) * rk, T::to_float(kv[j][x] >> 16) * rk);
         }
-        const int chunk = 2 * e + j;
+        const int chunk = 4 * e + j;
         lds_store_b128(a128(LQ, r, chunk, false), wq);
         lds_store_b128(a128(LK, r, chunk, true), wk);
-        lds_store_b128(a128(LV, r, chunk, true), vv[j]);
       }
     }
-    if (c0 + kC < t1) fetch(c0 + kC, tid);  // in flight while this chunk computes
+    // V: the tile is free (the last chunk's reads ended before its final
+    // barrier); issued after q and k are consumed, so that the compiler's
+    // waits for those do not also wait for these copies
+    copy_v(c0, tid);
     lds_sync();
 
-    // ---- waves 0-3: K K^T -> A (fp32); waves 4-7: Q K^T -> P (16-bit);
-    // block (bm, bn) = ((w / 2) % 2, w % 2).  Each wave's LDS reads are
-    // issued together ahead of their uses, so their latencies overlap.
-    {
-      const int bm = (wv >> 1) & 1, bn = wv & 1;
-      f32x16 acc = f32x16{};
+    // ---- A^T and P^T by 16x16 blocks: pair (I, J), J <= I, gives the block
+    // K_J K_I^T (rows j, columns i) of A and K_J Q_I^T of P, pairs w, w + 4, w + 8.
+    // A[i][j] = beta_i exp(G_i - G_j) (k_i . k_j) for j < i: the diagonal
+    // blocks in float32 for the inverses, -A of the others in 16 bits;
+    // P[i][j] = exp(G_i - G_j) (q_i . k_j) for j <= i (zero above: the two
+    // blocks above the diagonal that O += P D reads are zeroed once).
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {  // two halves of the 8 k-steps
-        u32x4 kb[4], ab[4];
+    for (int pn = 0; pn < 3; ++pn) {
+      const int p = wave + 4 * pn;
+      if (p < 10) {
+        const int I = p < 1 ? 0 : p < 3 ? 1 : p < 6 ? 2 : 3;
+        const int J = p - I * (I + 1) / 2;
+        f32x4 ca = f32x4{0.f, 0.f, 0.f, 0.f}, cp = ca;
+        u32x4 kj[4], ki[4], qi[4];
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-          kb[s4] = row_op(LK, 32 * bn, 4 * h2 + s4, lane, true);
-          ab[s4] = wave < 4 ? row_op(LK, 32 * bm, 4 * h2 + s4, lane, true) : row_op(LQ, 32 * bm, 4 * h2 + s4, lane, false);
+        for (int s = 0; s < 4; ++s) {
+          kj[s] = lds_load_b128<0>(a128(LK, 16 * J + m, 4 * s + g, true));
+          ki[s] = lds_load_b128<0>(a128(LK, 16 * I + m, 4 * s + g, true));
+          qi[s] = lds_load_b128<0>(a128(LQ, 16 * I + m, 4 * s + g, false));
         }
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) acc = T::mfma32x32x16(ab[s4], kb[s4], acc);
-      }
-      // rows i = 32 bm + acc_row(r): four runs of 4 consecutive rows
-      const int j = 32 * bn + (lane & 31);
-      const int i0 = 32 * bm + 4 * (lane >> 5);
-      const float Gj = ldf(LG + 4 * j);
-      f32x4 Gi[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) Gi[q] = ldf4(LG + 4 * (i0 + 8 * q));
-      if (wave < 4) {
-        f32x4 Bi[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) Bi[q] = ldf4(LB + 4 * (i0 + 8 * q));
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int i = i0 + (r & 3) + 8 * (r >> 2);
-          const float dec = __expf(j <= i ? Gi[r >> 2][r & 3] - Gj : 0.f);
-          stf(LT + 4 * (i * kTfStride + j), j < i ? Bi[r >> 2][r & 3] * dec * acc[r] : 0.f);
+        for (int s = 0; s < 4; ++s) {
+          ca = T::mfma16x16x32(kj[s], ki[s], ca);
+          cp = T::mfma16x16x32(kj[s], qi[s], cp);
         }
-      } else {
-        // P^T ([j][i], 8-byte writes), read back by columns as P D's row operand
-        f32x16 pv;
+        // element r: row j = 16 J + 4 g + r, column i = 16 I + m
+        const int i = 16 * I + m, jb = 16 * J + 4 * g;
+        const float Gi = ldf(LG + 4 * i), Bi = ldf(LB + 4 * i);
+        const f32x4 Gj = ldf4(LG + 4 * jb);
+        f32x4 av, pv;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int i = i0 + (r & 3) + 8 * (r >> 2);
-          const float dec = __expf(j <= i ? Gi[r >> 2][r & 3] - Gj : 0.f);
-          pv[r] = j <= i ? dec * acc[r] : 0.f;
+        for (int r = 0; r < 4; ++r) {
+          const int j = jb + r;
+          const float dec = __expf(j <= i ? Gi - Gj[r] : 0.f);
+          av[r] = j < i ? Bi * dec * ca[r] : 0.f;
+          pv[r] = j <= i ? dec * cp[r] : 0.f;
         }
-        st_acc_t<T>(LP, false, 32 * bm, 32 * bn, pv, lane);
+        if (I == J) {
+          stf4(LBD + 4 * (256 * I + 16 * m + 4 * g), av);
+        } else {
+          lds_store_b64(t64(LA, i, 4 * J + g), pack4<T>(-av));
+        }
+        lds_store_b64(t64(LP, i, 4 * J + g), pack4<T>(pv));
       }
     }
     lds_sync();
 
-    // ---- T = (I + A)^-1 in float32, by halves: T_A and T_B, the inverses of
-    // the two diagonal 32x32 halves, and the lower-left half
-    // X = -T_B A_BA T_A.  Waves 0 and 1 invert the diagonal 16x16 blocks
-    // 2w and 2w + 1 by forward substitution (lane = block and column), then
-    // the block between them, T_{2w+1,2w} = -T_{2w+1,2w+1} A_{2w+1,2w} T_{2w,2w};
-    // waves 4-7 meanwhile form Y = K S^T (to LDS) and O = diag(exp(G)) Q S^T
-    // for value columns 32 (w - 4) .. +31.  An off-diagonal block T_{i,j} is
-    // stored at block position (j, i), the unused upper triangle, so A's
-    // lower blocks stay intact.
-    f32x16 O[2];
-    auto blk = [&](int r, int c) { return LT + 4 * (16 * r * kTfStride + 16 * c); };
-    if (wave < 2) {
-      if (lane < 32) {
-        const int b0 = 16 * (2 * wv + (lane >> 4)), c = lane & 15;
-        float x[16];
-        // four rows at a time: their A values are read together, then
-        // consumed; two partial sums per row shorten the dependent chain
+    // ---- wave 0: the inverses T_jj of the diagonal blocks (I + A_jj), lane
+    // = block 16 (l / 16) and column l % 16, by forward substitution in
+    // float32, to the diagonal blocks of the 16-bit tile.  Waves 1-3
+    // meanwhile (and wave 0 after) form Y = K S^T and O = Q S^T.
+    if (wave == 0) {
+      const int b = g, c = m;
+      const uint32_t base = LBD + 4 * 256 * b;
+      float x[16];
+      // four rows at a time: their A values are read together, then
+      // consumed; two partial sums per row shorten the dependent chain
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          f32x4 av[4][4];
+      for (int gq = 0; gq < 4; ++gq) {
+        f32x4 av[4][4];
 #pragma unroll
-          for (int ii = 0; ii < 4; ++ii)
+        for (int ii = 0; ii < 4; ++ii)
 #pragma unroll
-            for (int jc = 0; jc <= g; ++jc) av[ii][jc] = ldf4(LT + 4 * ((b0 + 4 * g + ii) * kTfStride + b0 + 4 * jc));
+          for (int jc = 0; jc <= gq; ++jc) av[ii][jc] = ldf4(base + 4 * (16 * (4 * gq + ii) + 4 * jc));
 #pragma unroll
-          for (int ii = 0; ii < 4; ++ii) {
-            const int i = 4 * g + ii;
-            float acc0 = i == c ? 1.f : 0.f, acc1 = 0.f;
+        for (int ii = 0; ii < 4; ++ii) {
+          const int i = 4 * gq + ii;
+          float acc0 = i == c ? 1.f : 0.f, acc1 = 0.f;
 #pragma unroll
-            for (int j = 0; j < i; ++j) {
-              if (j & 1)
-                acc1 -= av[ii][j >> 2][j & 3] * x[j];
-              else
-                acc0 -= av[ii][j >> 2][j & 3] * x[j];
-            }
-            x[i] = i < c ? 0.f : acc0 + acc1;
+          for (int j = 0; j < i; ++j) {
+            if (j & 1)
+              acc1 -= av[ii][j >> 2][j & 3] * x[j];
+            else
+              acc0 -= av[ii][j >> 2][j & 3] * x[j];
           }
+          x[i] = i < c ? 0.f : acc0 + acc1;
         }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) stf(LT + 4 * ((b0 + i) * kTfStride + b0 + c), x[i]);
       }
-      // the wave's own LDS writes and reads, in order
-      const int d = 2 * wv;
-      const uint32_t lm = LM + 4 * 256 * wv;
-      store16x16(lm, 16, prod16(blk(d + 1, d), kTfStride, blk(d, d), kTfStride, f32x4{0, 0, 0, 0}, lane), 1.f, lane);
-      store16x16(blk(d, d + 1), kTfStride, prod16(blk(d + 1, d + 1), kTfStride, lm, 16, f32x4{0, 0, 0, 0}, lane), -1.f,
-                 lane);
-    } else if (wave >= 4) {
-      const int bn = wv - 4;
-      f32x16 Y[2] = {f32x16{}, f32x16{}};
-      O[0] = f32x16{};
-      O[1] = f32x16{};
-      // operands of two k-steps at a time, read ahead of their products
 #pragma unroll
-      for (int s = 0; s < kD / 16; s += 2) {
-        u32x4 sb[2], kr[2][2], qr[2][2];
+      for (int i = 0; i < 16; ++i) st16(t64(LA, 16 * b + i, 4 * b + (c >> 2)) + 2 * (c & 3), T::from_float(x[i]));
+    }
+    // Y = K S^T, O = Q S^T by 16-row blocks mb and column halves hf (row
+    // 16 mb + 4 g + r, column 32 w + 16 hf + m); B operand of k-step s: the
+    // packed state blocks 2 s and 2 s + 1.
+    f32x4 Y[4][2];
+    auto s_products = [&](uint32_t X, bool colwise, f32x4 (&acc)[4][2]) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          sb[u] = col_op(LS, 32 * bn, s + u, lane);  // S^T operand: keys of column v of the [K][V] tile
+      for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-          for (int bm = 0; bm < 2; ++bm) {
-            kr[u][bm] = row_op(LK, 32 * bm, s + u, lane, true);
-            qr[u][bm] = row_op(LQ, 32 * bm, s + u, lane, false);
-          }
+        for (int hf = 0; hf < 2; ++hf) acc[mb][hf] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const u32x4 sb[2] = {pack8<T>(S[2 * s][0], S[2 * s + 1][0]), pack8<T>(S[2 * s][1], S[2 * s + 1][1])};
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          const u32x4 xr = lds_load_b128<0>(a128(X, 16 * mb + m, 4 * s + g, colwise));
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) acc[mb][hf] = T::mfma16x16x32(xr, sb[hf], acc[mb][hf]);
         }
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-          for (int bm = 0; bm < 2; ++bm) {
-            Y[bm] = T::mfma32x32x16(kr[u][bm], sb[u], Y[bm]);
-            O[bm] = T::mfma32x32x16(qr[u][bm], sb[u], O[bm]);
-          }
       }
-      // exp(G) of the rows: runs of 4 consecutive tokens at 8q + 4 (l / 32)
-      f32x4 eg[2][4];
-#pragma unroll
-      for (int bm = 0; bm < 2; ++bm)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) eg[bm][q] = ldf4(LEG + 4 * (32 * bm + 8 * q + 4 * (lane >> 5)));
-#pragma unroll
-      for (int bm = 0; bm < 2; ++bm) {
-        st_acc_t<T>(LY, false, 32 * bm, 32 * bn, Y[bm], lane);  // Y^T: [V][T]
-#pragma unroll
-        for (int r = 0; r < 16; ++r) O[bm][r] *= eg[bm][r >> 2][r & 3];
-      }
-    }
+    };
+    if (wave != 0) s_products(LK, true, Y);
+    wait_vmcnt<0>();  // this wave's V copies (nothing else is in flight here)
     lds_sync();
-    // Lower-left half: waves 0-3 each own block (p, q) = (2 + w / 2, w % 2),
-    // Y_pq = sum_r A_{p,r} T_{r,q} (r = q, 1), then X_pq = -sum_r T_{p,r} Y_{r,q}
-    // (r = 2 .. p).
-    if (wave < 4) {
-      const int p = 2 + (wv >> 1), q = wv & 1;
-      f32x4 y = prod16(blk(p, 1), kTfStride, q == 1 ? blk(1, 1) : blk(0, 1), kTfStride, f32x4{0, 0, 0, 0}, lane);
-      if (q == 0) y = prod16(blk(p, 0), kTfStride, blk(0, 0), kTfStride, y, lane);
-      store16x16(LM + 4 * 256 * wv, 16, y, 1.f, lane);
-    }
-    lds_sync();
-    if (wave < 4) {
-      const int p = 2 + (wv >> 1), q = wv & 1;
-      // Y_{2,q} is block q of LM, Y_{3,q} block 2 + q
-      f32x4 x = prod16(p == 2 ? blk(2, 2) : blk(2, 3), kTfStride, LM + 4 * 256 * q, 16, f32x4{0, 0, 0, 0}, lane);
-      if (p == 3) x = prod16(blk(3, 3), kTfStride, LM + 4 * 256 * (2 + q), 16, x, lane);
-      store16x16(blk(q, p), kTfStride, x, -1.f, lane);
-    }
-    lds_sync();
-    // Tw = -T diag(beta exp(G)), Tu = T diag(beta): row tid / 8, columns 8 (tid % 8) .. +7,
-    // which lie in one block of T: a diagonal block in place (zero above its
-    // diagonal), a lower one at the transposed block position, an upper one
-    // zero.
-    {
-      const int i = tid >> 3, j0 = 8 * (tid & 7);
-      const int bi_ = i >> 4, bj_ = j0 >> 4;
-      const uint32_t src = bj_ == bi_ ? LT + 4 * (i * kTfStride + j0)
-                                      : LT + 4 * ((16 * bj_ + (i & 15)) * kTfStride + 16 * bi_ + (j0 & 15));
-      f32x4 t4[2] = {ldf4(src), ldf4(src + 16)};
-      if (bj_ > bi_) t4[0] = t4[1] = f32x4{0, 0, 0, 0};
-      const f32x4 b4[2] = {ldf4(LB + 4 * j0), ldf4(LB + 4 * j0 + 16)};
-      const f32x4 e4[2] = {ldf4(LEG + 4 * j0), ldf4(LEG + 4 * j0 + 16)};
-      u32x4 ww, wu;
-#pragma unroll
-      for (int x = 0; x < 4; ++x) {
-        float tw[2], tu[2];
-#pragma unroll
-        for (int z = 0; z < 2; ++z) {
-          const int e = 2 * x + z;
-          const float tb = t4[e >> 2][e & 3] * b4[e >> 2][e & 3];
-          tu[z] = tb;
-          tw[z] = -tb * e4[e >> 2][e & 3];
-        }
-        ww[x] = T::pack2(tw[0], tw[1]);
-        wu[x] = T::pack2(tu[0], tu[1]);
-      }
-      lds_store_b128(a64(LTw, i, j0 >> 3), ww);
-      lds_store_b128(a64(LTu, i, j0 >> 3), wu);
-    }
-    lds_sync();
+    if (wave == 0) s_products(LK, true, Y);
+    // the next chunk's inputs, in flight while this one finishes (issued
+    // here, not at the top, so that their registers are not live beside Y's
+    // products)
+    if (c0 + kC < t1) fetch(c0 + kC, tid);
 
-    // ---- D = Tu V + Tw Y: block (bm, bn) = (w / 4, w % 4); D takes V's place.
+    // ---- Z = diag(beta) (V - diag(exp(G)) Y) for rows 16 mb + 4 g + r,
+    // then D by substitution over the blocks, per half of the columns.
+    f32x4 D[4][2];
     {
-      const int bm = wv >> 2, bn = wv & 3;
-      f32x16 Dv = f32x16{};
-      u32x4 tu[4], tw[4], vc[4], yc[4];
+      f32x4 Bt[4], Et[4];
 #pragma unroll
-      for (int s = 0; s < kC / 16; ++s) {
-        tu[s] = row_op64(LTu, 32 * bm, s, lane);
-        vc[s] = col_op(LV, 32 * bn, s, lane);
-        tw[s] = row_op64(LTw, 32 * bm, s, lane);
-        yc[s] = row_op64(LY, 32 * bn, s, lane);
+      for (int mb = 0; mb < 4; ++mb) {
+        Bt[mb] = ldf4(LB + 4 * (16 * mb + 4 * g));
+        Et[mb] = ldf4(LEG + 4 * (16 * mb + 4 * g));
       }
+      // V rows 16 mb + 4 g .. +3 at column 32 w + 16 hf + m, by transposing reads
+      const int i = m, rho = i >> 2, pc = i & 3;
 #pragma unroll
-      for (int s = 0; s < kC / 16; ++s) {
-        Dv = T::mfma32x32x16(tu[s], vc[s], Dv);
-        Dv = T::mfma32x32x16(tw[s], yc[s], Dv);
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const uint32_t va = a128(LV, 16 * mb + 4 * g + rho, 4 * wv + 2 * hf + (pc >> 1), true) + 8 * (pc & 1);
+          const u32x2 vw = lds_load_tr16<0>(va);
+          const f32x4 vf = unpack2x2<T>(vw[0], vw[1]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) Y[mb][hf][r] = Bt[mb][r] * (vf[r] - Et[mb][r] * Y[mb][hf][r]);
+        }
+      u32x2 Tb[4], Am[6];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) Tb[j] = lds_load_b64(t64(LA, 16 * j + m, 4 * j + g));
+      Am[0] = lds_load_b64(t64(LA, 16 * 1 + m, 4 * 0 + g));
+      Am[1] = lds_load_b64(t64(LA, 16 * 2 + m, 4 * 0 + g));
+      Am[2] = lds_load_b64(t64(LA, 16 * 2 + m, 4 * 1 + g));
+      Am[3] = lds_load_b64(t64(LA, 16 * 3 + m, 4 * 0 + g));
+      Am[4] = lds_load_b64(t64(LA, 16 * 3 + m, 4 * 1 + g));
+      Am[5] = lds_load_b64(t64(LA, 16 * 3 + m, 4 * 2 + g));
+      const f32x4 z4 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        D[0][hf] = T::mfma16x16x16(Tb[0], pack4<T>(Y[0][hf]), z4);
+        const u32x2 d0 = pack4<T>(D[0][hf]);
+        f32x4 w1 = T::mfma16x16x16(Am[0], d0, Y[1][hf]);
+        f32x4 w2 = T::mfma16x16x16(Am[1], d0, Y[2][hf]);
+        f32x4 w3 = T::mfma16x16x16(Am[3], d0, Y[3][hf]);
+        D[1][hf] = T::mfma16x16x16(Tb[1], pack4<T>(w1), z4);
+        const u32x2 d1 = pack4<T>(D[1][hf]);
+        w2 = T::mfma16x16x16(Am[2], d1, w2);
+        w3 = T::mfma16x16x16(Am[4], d1, w3);
+        D[2][hf] = T::mfma16x16x16(Tb[2], pack4<T>(w2), z4);
+        w3 = T::mfma16x16x16(Am[5], pack4<T>(D[2][hf]), w3);
+        D[3][hf] = T::mfma16x16x16(Tb[3], pack4<T>(w3), z4);
       }
-      lds_sync();  // V read by every wave
-      st_acc_t<T>(LV, false, 32 * bm, 32 * bn, Dv, lane);  // D^T: [V][T]
     }
-    lds_sync();
-
-    // ---- waves 4-7: O += P D, stored as 16-bit values straight from the
-    // accumulators (rows past the sequence fall outside the descriptor).
-    if (wave >= 4) {
-      const int bn = wv - 4;
-      u32x4 db[4], pr[4][2];
+    // D as the B operands of P D and of the state update (with the factors
+    // exp(G_C - G) of its rows).
+    u32x4 bd[2][2], bt[2][2];
 #pragma unroll
-      for (int s = 0; s < kC / 16; ++s) {
-        db[s] = row_op64(LV, 32 * bn, s, lane);
+    for (int s = 0; s < 2; ++s) {
+      const f32x4 flo = ldf4(LEC + 4 * (32 * s + 4 * g)), fhi = ldf4(LEC + 4 * (32 * s + 16 + 4 * g));
 #pragma unroll
-        for (int bm = 0; bm < 2; ++bm) pr[s][bm] = col_op64(LP, 32 * bm, s, lane);
+      for (int hf = 0; hf < 2; ++hf) {
+        bd[s][hf] = pack8<T>(D[2 * s][hf], D[2 * s + 1][hf]);
+        bt[s][hf] = pack8<T>(D[2 * s][hf] * flo, D[2 * s + 1][hf] * fhi);
+      }
+    }
+    // ---- O = diag(exp(G)) Q S^T + P D, stored as 16-bit values (rows past
+    // the sequence fall outside the descriptor).
+    {
+      f32x4 O[4][2];
+      s_products(LQ, false, O);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const f32x4 e4 = ldf4(LEG + 4 * (16 * mb + 4 * g));
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) O[mb][hf][r] *= e4[r];
       }
 #pragma unroll
-      for (int s = 0; s < kC / 16; ++s)
+      for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-        for (int bm = 0; bm < 2; ++bm) O[bm] = T::mfma32x32x16(pr[s][bm], db[s], O[bm]);
+        for (int s = 0; s <= (mb >> 1); ++s) {
+          const u32x4 pa = cat(lds_load_b64(t64(LP, 16 * mb + m, 8 * s + g)), lds_load_b64(t64(LP, 16 * mb + m, 8 * s + 4 + g)));
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) O[mb][hf] = T::mfma16x16x32(pa, bd[s][hf], O[mb][hf]);
+        }
       const auto ro = make_rsrc(a.out + static_cast<int64_t>(c0) * a.o_rs + hv * kD * 2,
                                 static_cast<uint32_t>((ck - 1) * a.o_rs + kD * 2));
-      // row t = 32 bm + (r & 3) + 8 (r >> 2) + 4 (l / 32): the lane's part in the
-      // vector offset, the rest (uniform) in the scalar one
+      // row t = 16 mb + 4 g + r: the lane's part in the vector offset, the
+      // rest (uniform) in the scalar one
       const int ors = static_cast<int>(a.o_rs);
-      const int voff = 4 * (lane >> 5) * ors + 2 * (32 * bn + (lane & 31));
 #pragma unroll
-      for (int bm = 0; bm < 2; ++bm)
+      for (int hf = 0; hf < 2; ++hf) {
+        const int voff = 4 * g * ors + 2 * (32 * wv + 16 * hf + m);
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          __builtin_amdgcn_raw_buffer_store_b16(T::from_float(O[bm][r]), ro, voff,
-                                                (32 * bm + (r & 3) + 8 * (r >> 2)) * ors, 0);
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            __builtin_amdgcn_raw_buffer_store_b16(T::from_float(O[mb][hf][r]), ro, voff, (16 * mb + r) * ors, 0);
+      }
     }
-    // ---- S <- exp(G_C) S + (diag(exp(G_C - G)) D)^T K, this wave's blocks.
+    // ---- S^T <- exp(G_C) S^T + K^T diag(exp(G_C - G)) D, this wave's columns.
     {
       const float eC = ldf(LEG + 4 * (kC - 1));
 #pragma unroll
-      for (int j = 0; j < 2; ++j) S[j] *= eC;
-      // two k-steps at a time: operands and factors read ahead of the products
+      for (int kb = 0; kb < 8; ++kb) {
 #pragma unroll
-      for (int s = 0; s < kC / 16; s += 2) {
-        u32x4 d[2], kc[2][2];
-        f32x4 f[2][2];
+        for (int hf = 0; hf < 2; ++hf) S[kb][hf] *= eC;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          // A operand: value row 32 vb + l % 32, tokens 16 (s + u) + 8 (l / 32) .. +7, scaled.
-          d[u] = row_op64(LV, 32 * vb, s + u, lane);
-          const int tb = 16 * (s + u) + 8 * (lane >> 5);
-          f[u][0] = ldf4(LEC + 4 * tb);
-          f[u][1] = ldf4(LEC + 4 * (tb + 4));
+        for (int s = 0; s < 2; ++s) {
+          const u32x4 ka = kt_op(LK, kb >> 1, kb & 1, s, lane);
 #pragma unroll
-          for (int j = 0; j < 2; ++j) kc[u][j] = col_op(LK, 32 * (kb0 + j), s + u, lane);
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          u32x4 da;
-#pragma unroll
-          for (int x = 0; x < 4; ++x)
-            da[x] = T::pack2(T::to_float(d[u][x] & 0xffffu) * f[u][x >> 1][2 * (x & 1)],
-                             T::to_float(d[u][x] >> 16) * f[u][x >> 1][2 * (x & 1) + 1]);
-#pragma unroll
-          for (int j = 0; j < 2; ++j) S[j] = T::mfma32x32x16(da, kc[u][j], S[j]);
+          for (int hf = 0; hf < 2; ++hf) S[kb][hf] = T::mfma16x16x32(ka, bt[s][hf], S[kb][hf]);
         }
       }
     }
     // wave 0: the next chunk's gates (its inputs arrived with the prefetch),
-    // into the other gate set, while waves 4-7 finish the output
+    // into the other gate set
     if (wave == 0 && c0 + kC < t1) gates(min(kC, t1 - c0 - kC), gset ^ 1);
-    // The S^T tile was last read by the Y and Q S^T products, barriers ago.
-    write_state<T>(LS, S, vb, kb0, lane);
-    lds_sync();  // the next chunk overwrites K, Q, V; every read of K and D of this chunk is done
+    lds_sync();  // the next chunk overwrites K, Q, V, A, P; every read of this chunk's is done
   }
   if (has) {
-    const int lane = tid0 & 63;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int kb = 0; kb < 8; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) st[(32 * vb + acc_row(r, lane)) * kD + 32 * (kb0 + j) + (lane & 31)] = S[j][r];
+      for (int hf = 0; hf < 2; ++hf) *state_at(kb, hf) = S[kb][hf];
   }
 }
 

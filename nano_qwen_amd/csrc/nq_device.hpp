@@ -54,6 +54,13 @@ struct BF16 {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
+  // 16x16x16: lane l holds row (A) / column (B) l % 16, k = 4 (l / 16) .. +3,
+  // the layout of the accumulator's rows, so a result feeds the next B operand
+  __device__ static inline f32x4 mfma16x16x16(const u32x2 &a, const u32x2 &b, const f32x4 &c) {
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4, a), __builtin_bit_cast(bf16x4, b), c,
+                                                     0, 0, 0);
+  }
 };
 
 struct F16 {
@@ -66,8 +73,10 @@ struct F16 {
     return static_cast<float>(__builtin_bit_cast(_Float16, h));
   }
   static constexpr uint32_t kOne2 = 0x3c003c00u;  // two 1.0
+  // two fp32 -> packed pair (lo = a), one v_cvt_pk_f16_f32 (RNE)
   __device__ static inline uint32_t pack2(float a, float b) {
-    return static_cast<uint32_t>(from_float(a)) | (static_cast<uint32_t>(from_float(b)) << 16);
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
   }
   template <bool HI>
   __device__ static inline uint32_t fp8x2(uint32_t w) {
@@ -80,6 +89,11 @@ struct F16 {
   __device__ static inline f32x16 mfma32x32x16(const u32x4 &a, const u32x4 &b, const f32x16 &c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline f32x4 mfma16x16x16(const u32x2 &a, const u32x2 &b, const f32x4 &c) {
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0,
+                                                 0);
   }
 };
 
