@@ -258,21 +258,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 
   // Inputs of a chunk: q and k fetched one chunk ahead into registers (row
-  // tid / 4, columns 32 (tid % 4) .. +31), and (wave 0) lane's gate inputs.
-  // Through buffer descriptors over the chunk's rows of this head: rows past
-  // the sequence are out of range and read as zeros.
+  // tid / 4, columns 32 (tid % 4) .. +31), through buffer descriptors over
+  // the chunk's rows of this head: rows past the sequence are out of range
+  // and read as zeros.
   u32x4 qv[4], kv[4];
-  uint32_t ga = 0, gb = 0;  // a and b of token lane, as 16-bit codes (combined only when used)
   auto fetch = [&](int c0, int tid) {
     const int r = tid >> 2, e = tid & 3;
     const int rows = min(kC, t1 - c0);
-    // the gate inputs first: waiting for them does not wait for q and k
-    if (tid < 64) {
-      const int64_t tg = c0 + tid;
-      const bool in = tid < t1 - c0;
-      ga = in ? reinterpret_cast<const uint16_t *>(a.a + tg * a.a_rs)[hv] : 0u;
-      gb = in ? reinterpret_cast<const uint16_t *>(a.b + tg * a.b_rs)[hv] : 0u;
-    }
     const auto rq = make_rsrc(a.q + static_cast<int64_t>(c0) * a.q_rs + h * kD * 2,
                               static_cast<uint32_t>((rows - 1) * a.q_rs + kD * 2));
     const auto rk = make_rsrc(a.k + static_cast<int64_t>(c0) * a.k_rs + h * kD * 2,
@@ -287,8 +279,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // V of the chunk at c0 straight into its LDS tile (no registers): wave w
   // copies rows 16 w .. +15, four rows per copy; lane l of a copy lands in
   // chunk position l % 16 of row 4 q + l / 16 and so loads the logical chunk
-  // that the swizzle puts there.  Rows past the sequence read as zeros.
-  // Completed by the vmcnt(0) before the barrier ahead of Z's reads.
+  // the swizzle puts there.  Rows past the sequence read as zeros.
   auto copy_v = [&](int c0, int tid) {
     const int rows = min(kC, t1 - c0);
     const u32x4 rv = rsrc_words(a.v + static_cast<int64_t>(c0) * a.v_rs + hv * kD * 2,
@@ -301,34 +292,51 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       dma16_opaque(LV + row0 * 256, rv, static_cast<uint32_t>(row * static_cast<int>(a.v_rs) + 16 * chunk));
     }
   };
-  // Gates of the chunk whose inputs gab holds (wave 0; lane = token): G, the
-  // in-chunk inclusive sum of the log decays, beta, exp(G) and exp(G_C - G)
-  // into gate set `set`.
-  auto gates = [&](int ck, int set) {
-    const int lane = tid0 & 63;
-    const uint32_t g0 = L + kOffG + set * kGates;
-    float g = 0.f, beta = 0.f;
-    if (lane < ck) {
-      g = neg_a * softplus(T::to_float(static_cast<uint16_t>(ga)) + dtb);
-      beta = 1.0f / (1.0f + expf(-T::to_float(static_cast<uint16_t>(gb))));
-    }
-    g = wave_scan(g);
-    // G_C = G of the chunk's last token (tokens past the sequence add 0)
-    const float gc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, g), 63));
-    stf(g0 + 4 * lane, g);
-    stf(g0 + 4 * (kC + lane), beta);
-    stf(g0 + 4 * (2 * kC + lane), __expf(g));
-    stf(g0 + 4 * (3 * kC + lane), __expf(gc - g));
+  // The gates of the chunk at c0 into gate set `set`: wave w copies field w
+  // of the 64 tokens (one dword per lane) from the output rows; tokens past
+  // the sequence read as zeros.
+  auto copy_gates = [&](int c0, int set, int tid) {
+    const int rows = min(kC, t1 - c0);
+    const u32x4 rg = rsrc_words(a.out + static_cast<int64_t>(c0) * a.o_rs + hv * kD * 2,
+                                static_cast<uint32_t>((rows - 1) * a.o_rs + 16));
+    dma4_opaque(L + kOffG + set * kGates + kC * 4 * wave, rg,
+                static_cast<uint32_t>((tid & 63) * static_cast<int>(a.o_rs) + 4 * wave));
   };
+  // Gates of every chunk of the sequence up front (wave w: chunks w, w + 4,
+  // ...; lane = token), into the first 16 bytes of each token's output row:
+  // G, the in-chunk inclusive sum of the log decays, beta, exp(G) and
+  // exp(G_C - G).  A chunk's copy reads them before its output overwrites
+  // the row.
   if (t1 > t0) {
+    const int lane = tid0 & 63;
+    for (int c0 = t0 + kC * wave; c0 < t1; c0 += 4 * kC) {
+      const int ck = min(kC, t1 - c0);
+      float g = 0.f, beta = 0.f;
+      const int64_t t = c0 + lane;
+      if (lane < ck) {
+        const float xa = T::to_float(reinterpret_cast<const uint16_t *>(a.a + t * a.a_rs)[hv]);
+        const float xb = T::to_float(reinterpret_cast<const uint16_t *>(a.b + t * a.b_rs)[hv]);
+        g = neg_a * softplus(xa + dtb);
+        beta = 1.0f / (1.0f + expf(-xb));
+      }
+      g = wave_scan(g);
+      // G_C = G of the chunk's last token (tokens past the sequence add 0)
+      const float gc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, g), 63));
+      if (lane < ck)
+        *reinterpret_cast<f32x4 *>(a.out + t * a.o_rs + hv * kD * 2) = f32x4{g, beta, __expf(g), __expf(gc - g)};
+    }
+    // stores complete and seen by every wave, then the first chunk's gates
+    // (the compiler's wait for the q and k fetched after them covers the copy)
+    wait_vmcnt<0>();
+    raw_barrier();
+    copy_gates(t0, 0, tid0);
     fetch(t0, tid0);
-    if (wave == 0) gates(min(kC, t1 - t0), 0);
     // P's blocks (0, 1) and (2, 3), read by O += P D and never written
     // otherwise: zero once
     if (wave < 2) lds_store_b64(t64(L + kOffP, 32 * wave + (tid0 & 15), 4 * (2 * wave + 1) + ((tid0 >> 4) & 3)), u32x2{0u, 0u});
   }
   for (int c0 = t0; c0 < t1; c0 += kC) {
-    // this chunk's gate set (the next chunk's is written during this one)
+    // this chunk's gate set (the next chunk's is copied during this one)
     const int gset = ((c0 - t0) / kC) & 1;
     const uint32_t LG = L + kOffG + gset * kGates, LB = LG + kC * 4, LEG = LB + kC * 4, LEC = LEG + kC * 4;
     const int ck = min(kC, t1 - c0);
@@ -371,97 +379,137 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         lds_store_b128(a128(LK, r, chunk, true), wk);
       }
     }
-    // V: the tile is free (the last chunk's reads ended before its final
-    // barrier); issued after q and k are consumed, so that the compiler's
-    // waits for those do not also wait for these copies
+    // V, and the next chunk's gates: their regions are free (the last
+    // chunk's reads ended before its final barrier); issued after q and k are
+    // consumed, so that the compiler's waits for those do not also wait for
+    // these copies.  Completed by the vmcnt(0) before the barrier ahead of Z.
     copy_v(c0, tid);
+    if (c0 + kC < t1) copy_gates(c0 + kC, gset ^ 1, tid);
     lds_sync();
 
-    // ---- A^T and P^T by 16x16 blocks: pair (I, J), J <= I, gives the block
-    // K_J K_I^T (rows j, columns i) of A and K_J Q_I^T of P, pairs w, w + 4, w + 8.
-    // A[i][j] = beta_i exp(G_i - G_j) (k_i . k_j) for j < i: the diagonal
-    // blocks in float32 for the inverses, -A of the others in 16 bits;
-    // P[i][j] = exp(G_i - G_j) (q_i . k_j) for j <= i (zero above: the two
-    // blocks above the diagonal that O += P D reads are zeroed once).
+    // ---- A and P by 16x16 blocks, formed transposed (rows j, columns i):
+    // A[i][j] = beta_i exp(G_i - G_j) (k_i . k_j) for j < i, P[i][j] =
+    // exp(G_i - G_j) (q_i . k_j) for j <= i (P's two blocks above the
+    // diagonal that O += P D reads are zeroed once).  Wave 0 forms the four
+    // diagonal blocks of A (K_b K_b^T: one operand read per k-step) in
+    // float32 and inverts them: T_bb = (I + A_bb)^-1 by forward substitution,
+    // lane = block l / 16 and column l % 16, stored transposed in the
+    // diagonal blocks of the 16-bit tile.  Waves 1-3 form -A below the
+    // diagonal blocks (16 bits) and P.
+    // Element r of a block's accumulator: row j = 16 J + 4 g + r, column i = 16 I + m.
+    auto decay = [&](int I, int J, f32x4 &dec, float &Bi) {
+      const int i = 16 * I + m, jb = 16 * J + 4 * g;
+      const float Gi = ldf(LG + 4 * i);
+      Bi = ldf(LB + 4 * i);
+      const f32x4 Gj = ldf4(LG + 4 * jb);
 #pragma unroll
-    for (int pn = 0; pn < 3; ++pn) {
-      const int p = wave + 4 * pn;
-      if (p < 10) {
-        const int I = p < 1 ? 0 : p < 3 ? 1 : p < 6 ? 2 : 3;
-        const int J = p - I * (I + 1) / 2;
-        f32x4 ca = f32x4{0.f, 0.f, 0.f, 0.f}, cp = ca;
-        u32x4 kj[4], ki[4], qi[4];
+      for (int r = 0; r < 4; ++r)
+        // G_i <= G_j for tokens j <= i of the sequence; past it G reads 0
+        dec[r] = __expf(jb + r <= i ? fminf(Gi - Gj[r], 0.f) : 0.f);
+    };
+    // A^T and P^T of the pair (I, J), J < I: operands K_J, K_I, Q_I
+    auto pair_job = [&](int I, int J) {
+      f32x4 ca = f32x4{0.f, 0.f, 0.f, 0.f}, cp = ca;
+      u32x4 kj[4], ki[4], qi[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          kj[s] = lds_load_b128<0>(a128(LK, 16 * J + m, 4 * s + g, true));
-          ki[s] = lds_load_b128<0>(a128(LK, 16 * I + m, 4 * s + g, true));
-          qi[s] = lds_load_b128<0>(a128(LQ, 16 * I + m, 4 * s + g, false));
-        }
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          ca = T::mfma16x16x32(kj[s], ki[s], ca);
-          cp = T::mfma16x16x32(kj[s], qi[s], cp);
-        }
-        // element r: row j = 16 J + 4 g + r, column i = 16 I + m
-        const int i = 16 * I + m, jb = 16 * J + 4 * g;
-        const float Gi = ldf(LG + 4 * i), Bi = ldf(LB + 4 * i);
-        const f32x4 Gj = ldf4(LG + 4 * jb);
-        f32x4 av, pv;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = jb + r;
-          const float dec = __expf(j <= i ? Gi - Gj[r] : 0.f);
-          av[r] = j < i ? Bi * dec * ca[r] : 0.f;
-          pv[r] = j <= i ? dec * cp[r] : 0.f;
-        }
-        if (I == J) {
-          stf4(LBD + 4 * (256 * I + 16 * m + 4 * g), av);
-        } else {
-          lds_store_b64(t64(LA, i, 4 * J + g), pack4<T>(-av));
-        }
-        lds_store_b64(t64(LP, i, 4 * J + g), pack4<T>(pv));
+      for (int s = 0; s < 4; ++s) {
+        kj[s] = lds_load_b128<0>(a128(LK, 16 * J + m, 4 * s + g, true));
+        ki[s] = lds_load_b128<0>(a128(LK, 16 * I + m, 4 * s + g, true));
+        qi[s] = lds_load_b128<0>(a128(LQ, 16 * I + m, 4 * s + g, false));
       }
-    }
-    lds_sync();
-
-    // ---- wave 0: the inverses T_jj of the diagonal blocks (I + A_jj), lane
-    // = block 16 (l / 16) and column l % 16, by forward substitution in
-    // float32, to the diagonal blocks of the 16-bit tile.  Waves 1-3
-    // meanwhile (and wave 0 after) form Y = K S^T and O = Q S^T.
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        ca = T::mfma16x16x32(kj[s], ki[s], ca);
+        cp = T::mfma16x16x32(kj[s], qi[s], cp);
+      }
+      f32x4 dec;
+      float Bi;
+      decay(I, J, dec, Bi);
+      const int i = 16 * I + m;
+      lds_store_b64(t64(LA, i, 4 * J + g), pack4<T>(-(Bi * dec * ca)));
+      lds_store_b64(t64(LP, i, 4 * J + g), pack4<T>(dec * cp));
+    };
+    // P^T of the diagonal block I: operands K_I, Q_I
+    auto diag_p_job = [&](int I) {
+      f32x4 cp = f32x4{0.f, 0.f, 0.f, 0.f};
+      u32x4 ki[4], qi[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        ki[s] = lds_load_b128<0>(a128(LK, 16 * I + m, 4 * s + g, true));
+        qi[s] = lds_load_b128<0>(a128(LQ, 16 * I + m, 4 * s + g, false));
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) cp = T::mfma16x16x32(ki[s], qi[s], cp);
+      f32x4 dec;
+      float Bi;
+      decay(I, I, dec, Bi);
+      f32x4 pv;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pv[r] = 4 * g + r <= m ? dec[r] * cp[r] : 0.f;
+      lds_store_b64(t64(LP, 16 * I + m, 4 * I + g), pack4<T>(pv));
+    };
     if (wave == 0) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        f32x4 ca = f32x4{0.f, 0.f, 0.f, 0.f};
+        u32x4 kb[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) kb[s] = lds_load_b128<0>(a128(LK, 16 * b + m, 4 * s + g, true));
+#pragma unroll
+        for (int s = 0; s < 4; ++s) ca = T::mfma16x16x32(kb[s], kb[s], ca);
+        f32x4 dec, av;
+        float Bi;
+        decay(b, b, dec, Bi);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) av[r] = 4 * g + r < m ? Bi * dec[r] * ca[r] : 0.f;
+        stf4(LBD + 4 * (256 * b + 16 * m + 4 * g), av);  // row m, columns 4 g .. +3 of block b
+      }
+      wave_lds_sync();
       const int b = g, c = m;
       const uint32_t base = LBD + 4 * 256 * b;
       float x[16];
-      // four rows at a time: their A values are read together, then
-      // consumed; two partial sums per row shorten the dependent chain
+      // row by row (the reads of later rows may be issued early); two partial
+      // sums per row shorten the dependent chain
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        f32x4 av[4][4];
+      for (int i = 0; i < 16; ++i) {
+        f32x4 av[4];
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii)
+        for (int jc = 0; jc < 4; ++jc)
+          if (4 * jc < i) av[jc] = ldf4(base + 4 * (16 * i + 4 * jc));
+        float acc0 = i == c ? 1.f : 0.f, acc1 = 0.f;
 #pragma unroll
-          for (int jc = 0; jc <= gq; ++jc) av[ii][jc] = ldf4(base + 4 * (16 * (4 * gq + ii) + 4 * jc));
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const int i = 4 * gq + ii;
-          float acc0 = i == c ? 1.f : 0.f, acc1 = 0.f;
-#pragma unroll
-          for (int j = 0; j < i; ++j) {
-            if (j & 1)
-              acc1 -= av[ii][j >> 2][j & 3] * x[j];
-            else
-              acc0 -= av[ii][j >> 2][j & 3] * x[j];
-          }
-          x[i] = i < c ? 0.f : acc0 + acc1;
+        for (int j = 0; j < i; ++j) {
+          if (j & 1)
+            acc1 -= av[j >> 2][j & 3] * x[j];
+          else
+            acc0 -= av[j >> 2][j & 3] * x[j];
         }
+        x[i] = i < c ? 0.f : acc0 + acc1;
       }
+      // column c of T_bb is row c of its transpose: four 8-byte pieces
 #pragma unroll
-      for (int i = 0; i < 16; ++i) st16(t64(LA, 16 * b + i, 4 * b + (c >> 2)) + 2 * (c & 3), T::from_float(x[i]));
+      for (int q4 = 0; q4 < 4; ++q4)
+        lds_store_b64(t64(LA, 16 * b + c, 4 * b + q4), pack4<T>(f32x4{x[4 * q4], x[4 * q4 + 1], x[4 * q4 + 2], x[4 * q4 + 3]}));
+    } else if (wave == 1) {
+      pair_job(1, 0);
+      pair_job(2, 0);
+      diag_p_job(0);
+    } else if (wave == 2) {
+      pair_job(2, 1);
+      pair_job(3, 0);
+      diag_p_job(1);
+    } else {
+      pair_job(3, 1);
+      pair_job(3, 2);
+      diag_p_job(2);
+      diag_p_job(3);
     }
+    lds_sync();
+
     // Y = K S^T, O = Q S^T by 16-row blocks mb and column halves hf (row
     // 16 mb + 4 g + r, column 32 w + 16 hf + m); B operand of k-step s: the
     // packed state blocks 2 s and 2 s + 1.
-    f32x4 Y[4][2];
+    f32x4 Y[4][2], O[4][2];
     auto s_products = [&](uint32_t X, bool colwise, f32x4 (&acc)[4][2]) {
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
@@ -478,13 +526,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
       }
     };
-    if (wave != 0) s_products(LK, true, Y);
-    wait_vmcnt<0>();  // this wave's V copies (nothing else is in flight here)
+    s_products(LK, true, Y);
+    s_products(LQ, false, O);
+    wait_vmcnt<0>();  // this wave's V and gate copies (nothing else is in flight here)
     lds_sync();
-    if (wave == 0) s_products(LK, true, Y);
     // the next chunk's inputs, in flight while this one finishes (issued
-    // here, not at the top, so that their registers are not live beside Y's
-    // products)
+    // here, not at the top, so that their registers are not live beside the
+    // products above)
     if (c0 + kC < t1) fetch(c0 + kC, tid);
 
     // ---- Z = diag(beta) (V - diag(exp(G)) Y) for rows 16 mb + 4 g + r,
@@ -511,7 +559,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
       u32x2 Tb[4], Am[6];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) Tb[j] = lds_load_b64(t64(LA, 16 * j + m, 4 * j + g));
+      // T_jj is stored transposed: a transposing read gives lane (g, m) row m,
+      // columns 4 g .. +3 (lane 4 rho + p addresses row 4 g + rho, piece p)
+      for (int j = 0; j < 4; ++j) Tb[j] = lds_load_tr16<0>(t64(LA, 16 * j + 4 * g + (m >> 2), 4 * j + (m & 3)));
       Am[0] = lds_load_b64(t64(LA, 16 * 1 + m, 4 * 0 + g));
       Am[1] = lds_load_b64(t64(LA, 16 * 2 + m, 4 * 0 + g));
       Am[2] = lds_load_b64(t64(LA, 16 * 2 + m, 4 * 1 + g));
@@ -547,11 +597,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         bt[s][hf] = pack8<T>(D[2 * s][hf] * flo, D[2 * s + 1][hf] * fhi);
       }
     }
-    // ---- O = diag(exp(G)) Q S^T + P D, stored as 16-bit values (rows past
-    // the sequence fall outside the descriptor).
+    // ---- O = diag(exp(G)) Q S^T + P D, stored as 16-bit values.
     {
-      f32x4 O[4][2];
-      s_products(LQ, false, O);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         const f32x4 e4 = ldf4(LEG + 4 * (16 * mb + 4 * g));
@@ -571,7 +618,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       const auto ro = make_rsrc(a.out + static_cast<int64_t>(c0) * a.o_rs + hv * kD * 2,
                                 static_cast<uint32_t>((ck - 1) * a.o_rs + kD * 2));
       // row t = 16 mb + 4 g + r: the lane's part in the vector offset, the
-      // rest (uniform) in the scalar one
+      // rest (uniform) in the scalar one; rows past the sequence fall outside
+      // the descriptor
       const int ors = static_cast<int>(a.o_rs);
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
@@ -585,7 +633,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
     // ---- S^T <- exp(G_C) S^T + K^T diag(exp(G_C - G)) D, this wave's columns.
     {
-      const float eC = ldf(LEG + 4 * (kC - 1));
+      const float eC = ldf(LEG + 4 * (ck - 1));
 #pragma unroll
       for (int kb = 0; kb < 8; ++kb) {
 #pragma unroll
@@ -598,9 +646,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
       }
     }
-    // wave 0: the next chunk's gates (its inputs arrived with the prefetch),
-    // into the other gate set
-    if (wave == 0 && c0 + kC < t1) gates(min(kC, t1 - c0 - kC), gset ^ 1);
     lds_sync();  // the next chunk overwrites K, Q, V, A, P; every read of this chunk's is done
   }
   if (has) {

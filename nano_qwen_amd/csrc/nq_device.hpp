@@ -212,6 +212,14 @@ __device__ inline void dma16_opaque(uint32_t lds_addr, const u32x4 &rsrc, uint32
                : "s"(lds_addr), "v"(voff), "s"(rsrc)
                : "m0");
 }
+// The same for 4 bytes per lane (buffer_load_dword ... lds): lane l's dword
+// lands at lds_addr + 4 * l.
+__device__ inline void dma4_opaque(uint32_t lds_addr, const u32x4 &rsrc, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "m0");
+}
 #pragma clang diagnostic pop
 // LDS reads the compiler schedules and waits for itself, at LDS byte address
 // `addr` + OFF (the constant folds into the instruction's offset).  Only for
