@@ -390,11 +390,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // ---- A and P by 16x16 blocks, formed transposed (rows j, columns i):
     // A[i][j] = beta_i exp(G_i - G_j) (k_i . k_j) for j < i, P[i][j] =
     // exp(G_i - G_j) (q_i . k_j) for j <= i (P's two blocks above the
-    // diagonal that O += P D reads are zeroed once).  Wave 0 forms the four
-    // diagonal blocks of A (K_b K_b^T: one operand read per k-step) in
-    // float32 and inverts them: T_bb = (I + A_bb)^-1 by forward substitution,
+    // diagonal that O += P D reads are zeroed once).  Wave w forms diagonal
+    // block w of A (K_b K_b^T: one operand read per k-step) in float32; then
+    // wave 0 inverts the four: T_bb = (I + A_bb)^-1 by forward substitution,
     // lane = block l / 16 and column l % 16, stored transposed in the
-    // diagonal blocks of the 16-bit tile.  Waves 1-3 form -A below the
+    // diagonal blocks of the 16-bit tile, while waves 1-3 form -A below the
     // diagonal blocks (16 bits) and P.
     // Element r of a block's accumulator: row j = 16 J + 4 g + r, column i = 16 I + m.
     auto decay = [&](int I, int J, f32x4 &dec, float &Bi) {
@@ -448,23 +448,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int r = 0; r < 4; ++r) pv[r] = 4 * g + r <= m ? dec[r] * cp[r] : 0.f;
       lds_store_b64(t64(LP, 16 * I + m, 4 * I + g), pack4<T>(pv));
     };
+    // the diagonal block `wave` of A in float32 (row m, columns 4 g .. +3)
+    {
+      const int b = wave;
+      f32x4 ca = f32x4{0.f, 0.f, 0.f, 0.f};
+      u32x4 kb[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kb[s] = lds_load_b128<0>(a128(LK, 16 * b + m, 4 * s + g, true));
+#pragma unroll
+      for (int s = 0; s < 4; ++s) ca = T::mfma16x16x32(kb[s], kb[s], ca);
+      f32x4 dec, av;
+      float Bi;
+      decay(b, b, dec, Bi);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) av[r] = 4 * g + r < m ? Bi * dec[r] * ca[r] : 0.f;
+      stf4(LBD + 4 * (256 * b + 16 * m + 4 * g), av);
+    }
+    lds_sync();
     if (wave == 0) {
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        f32x4 ca = f32x4{0.f, 0.f, 0.f, 0.f};
-        u32x4 kb[4];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) kb[s] = lds_load_b128<0>(a128(LK, 16 * b + m, 4 * s + g, true));
-#pragma unroll
-        for (int s = 0; s < 4; ++s) ca = T::mfma16x16x32(kb[s], kb[s], ca);
-        f32x4 dec, av;
-        float Bi;
-        decay(b, b, dec, Bi);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) av[r] = 4 * g + r < m ? Bi * dec[r] * ca[r] : 0.f;
-        stf4(LBD + 4 * (256 * b + 16 * m + 4 * g), av);  // row m, columns 4 g .. +3 of block b
-      }
-      wave_lds_sync();
       const int b = g, c = m;
       const uint32_t base = LBD + 4 * 256 * b;
       float x[16];
@@ -494,14 +495,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       pair_job(1, 0);
       pair_job(2, 0);
       diag_p_job(0);
+      diag_p_job(1);
     } else if (wave == 2) {
       pair_job(2, 1);
       pair_job(3, 0);
-      diag_p_job(1);
+      diag_p_job(2);
     } else {
       pair_job(3, 1);
       pair_job(3, 2);
-      diag_p_job(2);
       diag_p_job(3);
     }
     lds_sync();
