@@ -84,7 +84,8 @@ constexpr int kOffP = kOffA + kC * kC * 2;  // P [i][j] (t64), zero above the di
 constexpr int kOffB = kOffP + kC * kC * 2;  // the four diagonal 16x16 blocks of A, fp32 [b][i][j]
 constexpr int kGates = 4 * kC * 4;          // G, beta, exp(G), exp(G_C - G): 64 fp32 each
 constexpr int kOffG = kOffB + 4 * 256 * 4;  // two gate sets: this chunk's and the next one's
-constexpr int kLds = kOffG + 2 * kGates;
+constexpr int kOffR = kOffG + 2 * kGates;    // 1 / |q| x K^-1/2 and 1 / |k| of the chunk's tokens: 64 fp32 each
+constexpr int kLds = kOffR + 2 * kC * 4;
 static_assert(2 * kLds <= 160 * 1024, "two workgroups per CU");
 
 // Chunk swizzles of the 128-column tiles (16 chunks a row).
@@ -150,6 +151,17 @@ __device__ inline float wave_scan(float v) {
 template <class T>
 __device__ inline f32x4 unpack2x2(uint32_t w0, uint32_t w1) {
   return f32x4{T::to_float(w0 & 0xffffu), T::to_float(w0 >> 16), T::to_float(w1 & 0xffffu), T::to_float(w1 >> 16)};
+}
+// a.x * b.x + a.y * b.y + c over packed 16-bit pairs (v_dot2_f32_*)
+template <class T>
+__device__ inline float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (T::dtype == NQ_BF16) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+  } else {
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+  }
 }
 template <class T>
 __device__ inline u32x2 pack4(const f32x4 &v) {
@@ -339,6 +351,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // this chunk's gate set (the next chunk's is copied during this one)
     const int gset = ((c0 - t0) / kC) & 1;
     const uint32_t LG = L + kOffG + gset * kGates, LB = LG + kC * 4, LEG = LB + kC * 4, LEC = LEG + kC * 4;
+    const uint32_t LRQ = L + kOffR, LRK = LRQ + kC * 4;
     const int ck = min(kC, t1 - c0);
     // The thread index from an instruction the compiler cannot hoist: the
     // LDS addresses derived from it are recomputed per chunk instead of each
@@ -348,35 +361,29 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int lane = tid & 63;
     const int m = lane & 15, g = lane >> 4;
     const int wv = tid >> 6;  // the wave index for addresses (branches use the uniform `wave`)
-    // ---- unit keys and scaled unit queries (float32 norms, rounded to 16
-    // bits) into LDS.
+    // ---- q and k rows into LDS as they are; their norms (float32) as
+    // per-token factors 1 / |q| x K^-1/2 and 1 / |k|, which the products'
+    // epilogues apply.
     {
       const int r = tid >> 2, e = tid & 3;
-      float sq = 0.f, sk = 0.f;
+      float sq0 = 0.f, sq1 = 0.f, sk0 = 0.f, sk1 = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const f32x4 q0 = unpack2x2<T>(qv[j][0], qv[j][1]), q1 = unpack2x2<T>(qv[j][2], qv[j][3]);
-        const f32x4 k0 = unpack2x2<T>(kv[j][0], kv[j][1]), k1 = unpack2x2<T>(kv[j][2], kv[j][3]);
-#pragma unroll
-        for (int x = 0; x < 4; ++x) {
-          sq += q0[x] * q0[x] + q1[x] * q1[x];
-          sk += k0[x] * k0[x] + k1[x] * k1[x];
-        }
+        sq0 = dot2<T>(qv[j][0], qv[j][0], dot2<T>(qv[j][1], qv[j][1], sq0));
+        sq1 = dot2<T>(qv[j][2], qv[j][2], dot2<T>(qv[j][3], qv[j][3], sq1));
+        sk0 = dot2<T>(kv[j][0], kv[j][0], dot2<T>(kv[j][1], kv[j][1], sk0));
+        sk1 = dot2<T>(kv[j][2], kv[j][2], dot2<T>(kv[j][3], kv[j][3], sk1));
       }
-      sq = sum4(sq);
-      sk = sum4(sk);
-      const float rq = a.scale * __builtin_amdgcn_rsqf(sq + a.eps), rk = __builtin_amdgcn_rsqf(sk + a.eps);
+      const float sq = sum4(sq0 + sq1), sk = sum4(sk0 + sk1);
+      if (e == 0) {
+        stf(LRQ + 4 * r, a.scale * __builtin_amdgcn_rsqf(sq + a.eps));
+        stf(LRK + 4 * r, __builtin_amdgcn_rsqf(sk + a.eps));
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        u32x4 wq, wk;
-#pragma unroll
-        for (int x = 0; x < 4; ++x) {
-          wq[x] = T::pack2(T::to_float(qv[j][x] & 0xffffu) * rq, T::to_float(qv[j][x] >> 16) * rq);
-          wk[x] = T::pack2(T::to_float(kv[j][x] & 0xffffu) * rk, T::to_float(kv[j][x] >> 16) * rk);
-        }
         const int chunk = 4 * e + j;
-        lds_store_b128(a128(LQ, r, chunk, false), wq);
-        lds_store_b128(a128(LK, r, chunk, true), wk);
+        lds_store_b128(a128(LQ, r, chunk, false), qv[j]);
+        lds_store_b128(a128(LK, r, chunk, true), kv[j]);
       }
     }
     // V, and the next chunk's gates: their regions are free (the last
@@ -397,15 +404,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // diagonal blocks of the 16-bit tile, while waves 1-3 form -A below the
     // diagonal blocks (16 bits) and P.
     // Element r of a block's accumulator: row j = 16 J + 4 g + r, column i = 16 I + m.
-    auto decay = [&](int I, int J, f32x4 &dec, float &Bi) {
+    // dec[r] = exp(G_i - G_j) / |k_j|, fa = beta_i / |k_i|, fp = 1 / |q_i| x K^-1/2
+    auto decay = [&](int I, int J, f32x4 &dec, float &fa, float &fp) {
       const int i = 16 * I + m, jb = 16 * J + 4 * g;
       const float Gi = ldf(LG + 4 * i);
-      Bi = ldf(LB + 4 * i);
-      const f32x4 Gj = ldf4(LG + 4 * jb);
+      fa = ldf(LB + 4 * i) * ldf(LRK + 4 * i);
+      fp = ldf(LRQ + 4 * i);
+      const f32x4 Gj = ldf4(LG + 4 * jb), rkj = ldf4(LRK + 4 * jb);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         // G_i <= G_j for tokens j <= i of the sequence; past it G reads 0
-        dec[r] = __expf(jb + r <= i ? fminf(Gi - Gj[r], 0.f) : 0.f);
+        dec[r] = __expf(jb + r <= i ? fminf(Gi - Gj[r], 0.f) : 0.f) * rkj[r];
     };
     // A^T and P^T of the pair (I, J), J < I: operands K_J, K_I, Q_I
     auto pair_job = [&](int I, int J) {
@@ -423,11 +432,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         cp = T::mfma16x16x32(kj[s], qi[s], cp);
       }
       f32x4 dec;
-      float Bi;
-      decay(I, J, dec, Bi);
+      float fa, fp;
+      decay(I, J, dec, fa, fp);
       const int i = 16 * I + m;
-      lds_store_b64(t64(LA, i, 4 * J + g), pack4<T>(-(Bi * dec * ca)));
-      lds_store_b64(t64(LP, i, 4 * J + g), pack4<T>(dec * cp));
+      lds_store_b64(t64(LA, i, 4 * J + g), pack4<T>(-(fa * dec * ca)));
+      lds_store_b64(t64(LP, i, 4 * J + g), pack4<T>(fp * dec * cp));
     };
     // P^T of the diagonal block I: operands K_I, Q_I
     auto diag_p_job = [&](int I) {
@@ -441,11 +450,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
       for (int s = 0; s < 4; ++s) cp = T::mfma16x16x32(ki[s], qi[s], cp);
       f32x4 dec;
-      float Bi;
-      decay(I, I, dec, Bi);
+      float fa, fp;
+      decay(I, I, dec, fa, fp);
       f32x4 pv;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) pv[r] = 4 * g + r <= m ? dec[r] * cp[r] : 0.f;
+      for (int r = 0; r < 4; ++r) pv[r] = 4 * g + r <= m ? fp * dec[r] * cp[r] : 0.f;
       lds_store_b64(t64(LP, 16 * I + m, 4 * I + g), pack4<T>(pv));
     };
     // the diagonal block `wave` of A in float32 (row m, columns 4 g .. +3)
@@ -458,10 +467,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
       for (int s = 0; s < 4; ++s) ca = T::mfma16x16x32(kb[s], kb[s], ca);
       f32x4 dec, av;
-      float Bi;
-      decay(b, b, dec, Bi);
+      float fa, fp;
+      decay(b, b, dec, fa, fp);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) av[r] = 4 * g + r < m ? Bi * dec[r] * ca[r] : 0.f;
+      for (int r = 0; r < 4; ++r) av[r] = 4 * g + r < m ? fa * dec[r] * ca[r] : 0.f;
       stf4(LBD + 4 * (256 * b + 16 * m + 4 * g), av);
     }
     lds_sync();
@@ -511,24 +520,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // 16 mb + 4 g + r, column 32 w + 16 hf + m); B operand of k-step s: the
     // packed state blocks 2 s and 2 s + 1.
     f32x4 Y[4][2], O[4][2];
-    auto s_products = [&](uint32_t X, bool colwise, f32x4 (&acc)[4][2]) {
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) acc[mb][hf] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int hf = 0; hf < 2; ++hf) Y[mb][hf] = O[mb][hf] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const u32x4 sb[2] = {pack8<T>(S[2 * s][0], S[2 * s + 1][0]), pack8<T>(S[2 * s][1], S[2 * s + 1][1])};
+    for (int s = 0; s < 4; ++s) {
+      // the state packed once for both products
+      const u32x4 sb[2] = {pack8<T>(S[2 * s][0], S[2 * s + 1][0]), pack8<T>(S[2 * s][1], S[2 * s + 1][1])};
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          const u32x4 xr = lds_load_b128<0>(a128(X, 16 * mb + m, 4 * s + g, colwise));
+      for (int mb = 0; mb < 4; ++mb) {
+        const u32x4 kr = lds_load_b128<0>(a128(LK, 16 * mb + m, 4 * s + g, true));
+        const u32x4 qr = lds_load_b128<0>(a128(LQ, 16 * mb + m, 4 * s + g, false));
 #pragma unroll
-          for (int hf = 0; hf < 2; ++hf) acc[mb][hf] = T::mfma16x16x32(xr, sb[hf], acc[mb][hf]);
+        for (int hf = 0; hf < 2; ++hf) {
+          Y[mb][hf] = T::mfma16x16x32(kr, sb[hf], Y[mb][hf]);
+          O[mb][hf] = T::mfma16x16x32(qr, sb[hf], O[mb][hf]);
         }
       }
-    };
-    s_products(LK, true, Y);
-    s_products(LQ, false, O);
+    }
     wait_vmcnt<0>();  // this wave's V and gate copies (nothing else is in flight here)
     lds_sync();
     // the next chunk's inputs, in flight while this one finishes (issued
@@ -544,7 +554,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         Bt[mb] = ldf4(LB + 4 * (16 * mb + 4 * g));
-        Et[mb] = ldf4(LEG + 4 * (16 * mb + 4 * g));
+        Et[mb] = ldf4(LEG + 4 * (16 * mb + 4 * g)) * ldf4(LRK + 4 * (16 * mb + 4 * g));  // Y's rows: raw keys
       }
       // V rows 16 mb + 4 g .. +3 at column 32 w + 16 hf + m, by transposing reads
       const int i = m, rho = i >> 2, pc = i & 3;
@@ -591,7 +601,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     u32x4 bd[2][2], bt[2][2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const f32x4 flo = ldf4(LEC + 4 * (32 * s + 4 * g)), fhi = ldf4(LEC + 4 * (32 * s + 16 + 4 * g));
+      // with 1 / |k_t|: the state update reads the raw keys
+      const f32x4 flo = ldf4(LEC + 4 * (32 * s + 4 * g)) * ldf4(LRK + 4 * (32 * s + 4 * g));
+      const f32x4 fhi = ldf4(LEC + 4 * (32 * s + 16 + 4 * g)) * ldf4(LRK + 4 * (32 * s + 16 + 4 * g));
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         bd[s][hf] = pack8<T>(D[2 * s][hf], D[2 * s + 1][hf]);
@@ -602,7 +614,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     {
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
-        const f32x4 e4 = ldf4(LEG + 4 * (16 * mb + 4 * g));
+        const f32x4 e4 = ldf4(LEG + 4 * (16 * mb + 4 * g)) * ldf4(LRQ + 4 * (16 * mb + 4 * g));
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
