@@ -102,9 +102,6 @@ __device__ inline uint32_t a128(uint32_t base, int row, int chunk, bool colwise)
 __device__ inline uint32_t t64(uint32_t base, int row, int piece) {
   return base + row * 128 + ((piece ^ (row & 15)) << 3);
 }
-__device__ inline void st16(uint32_t addr, uint16_t v) {
-  *reinterpret_cast<__attribute__((address_space(3))) uint16_t *>(static_cast<uintptr_t>(addr)) = v;
-}
 __device__ inline float ldf(uint32_t addr) {
   return *reinterpret_cast<const __attribute__((address_space(3))) float *>(static_cast<uintptr_t>(addr));
 }
@@ -190,12 +187,10 @@ __device__ inline void lds_sync() {
 // .. +3.  In a transposing read, lane 4 rho + p addresses row rho and an
 // 8-byte piece, and lane i receives element i % 4 of the pieces of lanes
 // i / 4, 4 + i / 4, 8 + i / 4, 12 + i / 4: piece p is keys 32 sg + 8 p + 4 o .. +3.
-__device__ inline u32x4 kt_op(uint32_t LK, int sg, int o, int s, int lane) {
-  const int i = lane & 15, g = lane >> 4;
-  const int rho = i >> 2, p = i & 3;
-  const uint32_t lo = a128(LK, 32 * s + 4 * g + rho, 4 * sg + p, true) + 8 * o;
-  const uint32_t hi = a128(LK, 32 * s + 16 + 4 * g + rho, 4 * sg + p, true) + 8 * o;
-  return cat(lds_load_tr16<0>(lo), lds_load_tr16<0>(hi));
+// `base` is the lane's address for s = 0, o = 0 (row 4 g + i / 4, the chunk
+// of piece p; the swizzle depends on neither s nor the +16 rows).
+__device__ inline u32x4 kt_op(uint32_t base, int o, int s) {
+  return cat(lds_load_tr16<0>(base + 8 * o + 32 * 256 * s), lds_load_tr16<0>(base + 8 * o + 32 * 256 * s + 16 * 256));
 }
 
 template <class T>
@@ -203,7 +198,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const ChunkArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t L = lds_addr(smem);
-  const uint32_t LK = L + kOffK, LQ = L + kOffQ, LV = L + kOffV, LA = L + kOffA, LP = L + kOffP, LBD = L + kOffB;
+  const uint32_t LK = L + kOffK, LQ = L + kOffQ, LV = L + kOffV, LA = L + kOffA, LBD = L + kOffB;
   const int tid0 = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid0 >> 6);  // uniform: branches on it are scalar
   // The value heads of one key head read the same q and k: with enough heads
@@ -347,6 +342,30 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // otherwise: zero once
     if (wave < 2) lds_store_b64(t64(L + kOffP, 32 * wave + (tid0 & 15), 4 * (2 * wave + 1) + ((tid0 >> 4) & 3)), u32x2{0u, 0u});
   }
+  // Per-lane LDS addresses of the operand reads, formed once: the tile
+  // swizzles depend only on a row's low four bits, so every block, k-step or
+  // row offset below is an immediate added to one of these.
+  //   bK[x], bQ[x]: row m of the K and Q tiles, chunk 4 x + g (16-byte row reads)
+  //   bKT[x]: the state update's transposing reads of K (kt_op, sg = x)
+  //   bV[hf]: Z's transposing reads of V, columns 32 w + 16 hf ..
+  //   bT[x]: row m, piece 4 x + g of the 64-column tiles (A; P 8 KiB on)
+  uint32_t bK[4], bQ[4], bKT[4], bV[2], bT[4];
+  {
+    const int lane = tid0 & 63, m = lane & 15, g = lane >> 4;
+    const int rr = 4 * g + (m >> 2), p = m & 3;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      bK[x] = a128(L + kOffK, m, 4 * x + g, true);
+      bQ[x] = a128(L + kOffQ, m, 4 * x + g, false);
+      bKT[x] = a128(L + kOffK, rr, 4 * x + p, true);
+      bT[x] = t64(L + kOffA, m, 4 * x + g);
+    }
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) bV[hf] = a128(L + kOffV, rr, 4 * wave + 2 * hf + (p >> 1), true) + 8 * (p & 1);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) asm volatile("" : "+v"(bK[x]), "+v"(bQ[x]), "+v"(bKT[x]), "+v"(bT[x]));
+    asm volatile("" : "+v"(bV[0]), "+v"(bV[1]));
+  }
   for (int c0 = t0; c0 < t1; c0 += kC) {
     // this chunk's gate set (the next chunk's is copied during this one)
     const int gset = ((c0 - t0) / kC) & 1;
@@ -422,9 +441,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       u32x4 kj[4], ki[4], qi[4];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        kj[s] = lds_load_b128<0>(a128(LK, 16 * J + m, 4 * s + g, true));
-        ki[s] = lds_load_b128<0>(a128(LK, 16 * I + m, 4 * s + g, true));
-        qi[s] = lds_load_b128<0>(a128(LQ, 16 * I + m, 4 * s + g, false));
+        kj[s] = lds_load_b128<0>(bK[s] + 16 * 256 * J);
+        ki[s] = lds_load_b128<0>(bK[s] + 16 * 256 * I);
+        qi[s] = lds_load_b128<0>(bQ[s] + 16 * 256 * I);
       }
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -434,9 +453,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       f32x4 dec;
       float fa, fp;
       decay(I, J, dec, fa, fp);
-      const int i = 16 * I + m;
-      lds_store_b64(t64(LA, i, 4 * J + g), pack4<T>(-(fa * dec * ca)));
-      lds_store_b64(t64(LP, i, 4 * J + g), pack4<T>(fp * dec * cp));
+      lds_store_b64(bT[J] + 16 * 128 * I, pack4<T>(-(fa * dec * ca)));                 // A: row 16 I + m, piece 4 J + g
+      lds_store_b64(bT[J] + (kOffP - kOffA) + 16 * 128 * I, pack4<T>(fp * dec * cp));  // P
     };
     // P^T of the diagonal block I: operands K_I, Q_I
     auto diag_p_job = [&](int I) {
@@ -444,8 +462,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       u32x4 ki[4], qi[4];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        ki[s] = lds_load_b128<0>(a128(LK, 16 * I + m, 4 * s + g, true));
-        qi[s] = lds_load_b128<0>(a128(LQ, 16 * I + m, 4 * s + g, false));
+        ki[s] = lds_load_b128<0>(bK[s] + 16 * 256 * I);
+        qi[s] = lds_load_b128<0>(bQ[s] + 16 * 256 * I);
       }
 #pragma unroll
       for (int s = 0; s < 4; ++s) cp = T::mfma16x16x32(ki[s], qi[s], cp);
@@ -455,7 +473,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       f32x4 pv;
 #pragma unroll
       for (int r = 0; r < 4; ++r) pv[r] = 4 * g + r <= m ? fp * dec[r] * cp[r] : 0.f;
-      lds_store_b64(t64(LP, 16 * I + m, 4 * I + g), pack4<T>(pv));
+      lds_store_b64(bT[I] + (kOffP - kOffA) + 16 * 128 * I, pack4<T>(pv));
     };
     // the diagonal block `wave` of A in float32 (row m, columns 4 g .. +3)
     {
@@ -463,7 +481,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       f32x4 ca = f32x4{0.f, 0.f, 0.f, 0.f};
       u32x4 kb[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) kb[s] = lds_load_b128<0>(a128(LK, 16 * b + m, 4 * s + g, true));
+      for (int s = 0; s < 4; ++s) kb[s] = lds_load_b128<0>(bK[s] + 16 * 256 * b);
 #pragma unroll
       for (int s = 0; s < 4; ++s) ca = T::mfma16x16x32(kb[s], kb[s], ca);
       f32x4 dec, av;
@@ -530,8 +548,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       const u32x4 sb[2] = {pack8<T>(S[2 * s][0], S[2 * s + 1][0]), pack8<T>(S[2 * s][1], S[2 * s + 1][1])};
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
-        const u32x4 kr = lds_load_b128<0>(a128(LK, 16 * mb + m, 4 * s + g, true));
-        const u32x4 qr = lds_load_b128<0>(a128(LQ, 16 * mb + m, 4 * s + g, false));
+        const u32x4 kr = lds_load_b128<0>(bK[s] + 16 * 256 * mb);
+        const u32x4 qr = lds_load_b128<0>(bQ[s] + 16 * 256 * mb);
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
           Y[mb][hf] = T::mfma16x16x32(kr, sb[hf], Y[mb][hf]);
@@ -541,10 +559,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
     wait_vmcnt<0>();  // this wave's V and gate copies (nothing else is in flight here)
     lds_sync();
-    // the next chunk's inputs, in flight while this one finishes (issued
-    // here, not at the top, so that their registers are not live beside the
-    // products above)
-    if (c0 + kC < t1) fetch(c0 + kC, tid);
 
     // ---- Z = diag(beta) (V - diag(exp(G)) Y) for rows 16 mb + 4 g + r,
     // then D by substitution over the blocks, per half of the columns.
@@ -557,28 +571,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         Et[mb] = ldf4(LEG + 4 * (16 * mb + 4 * g)) * ldf4(LRK + 4 * (16 * mb + 4 * g));  // Y's rows: raw keys
       }
       // V rows 16 mb + 4 g .. +3 at column 32 w + 16 hf + m, by transposing reads
-      const int i = m, rho = i >> 2, pc = i & 3;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
-          const uint32_t va = a128(LV, 16 * mb + 4 * g + rho, 4 * wv + 2 * hf + (pc >> 1), true) + 8 * (pc & 1);
+          const uint32_t va = bV[hf] + 16 * 256 * mb;
           const u32x2 vw = lds_load_tr16<0>(va);
           const f32x4 vf = unpack2x2<T>(vw[0], vw[1]);
 #pragma unroll
           for (int r = 0; r < 4; ++r) Y[mb][hf][r] = Bt[mb][r] * (vf[r] - Et[mb][r] * Y[mb][hf][r]);
         }
       u32x2 Tb[4], Am[6];
-#pragma unroll
       // T_jj is stored transposed: a transposing read gives lane (g, m) row m,
       // columns 4 g .. +3 (lane 4 rho + p addresses row 4 g + rho, piece p)
+#pragma unroll
       for (int j = 0; j < 4; ++j) Tb[j] = lds_load_tr16<0>(t64(LA, 16 * j + 4 * g + (m >> 2), 4 * j + (m & 3)));
-      Am[0] = lds_load_b64(t64(LA, 16 * 1 + m, 4 * 0 + g));
-      Am[1] = lds_load_b64(t64(LA, 16 * 2 + m, 4 * 0 + g));
-      Am[2] = lds_load_b64(t64(LA, 16 * 2 + m, 4 * 1 + g));
-      Am[3] = lds_load_b64(t64(LA, 16 * 3 + m, 4 * 0 + g));
-      Am[4] = lds_load_b64(t64(LA, 16 * 3 + m, 4 * 1 + g));
-      Am[5] = lds_load_b64(t64(LA, 16 * 3 + m, 4 * 2 + g));
+      // -A_jm: row 16 j + m, piece 4 mm + g
+      Am[0] = lds_load_b64(bT[0] + 16 * 128 * 1);
+      Am[1] = lds_load_b64(bT[0] + 16 * 128 * 2);
+      Am[2] = lds_load_b64(bT[1] + 16 * 128 * 2);
+      Am[3] = lds_load_b64(bT[0] + 16 * 128 * 3);
+      Am[4] = lds_load_b64(bT[1] + 16 * 128 * 3);
+      Am[5] = lds_load_b64(bT[2] + 16 * 128 * 3);
       const f32x4 z4 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
@@ -596,6 +610,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         D[3][hf] = T::mfma16x16x16(Tb[3], pack4<T>(w3), z4);
       }
     }
+    // the next chunk's q and k, in flight while this one finishes (issued
+    // here, not at the top, so that their registers are not live beside the
+    // products and the solve above)
+    if (c0 + kC < t1) fetch(c0 + kC, tid);
     // D as the B operands of P D and of the state update (with the factors
     // exp(G_C - G) of its rows).
     u32x4 bd[2][2], bt[2][2];
@@ -624,7 +642,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
         for (int s = 0; s <= (mb >> 1); ++s) {
-          const u32x4 pa = cat(lds_load_b64(t64(LP, 16 * mb + m, 8 * s + g)), lds_load_b64(t64(LP, 16 * mb + m, 8 * s + 4 + g)));
+          // P: row 16 mb + m, pieces 8 s + g and 8 s + 4 + g
+          const u32x4 pa = cat(lds_load_b64(bT[2 * s] + (kOffP - kOffA) + 16 * 128 * mb),
+                               lds_load_b64(bT[2 * s + 1] + (kOffP - kOffA) + 16 * 128 * mb));
 #pragma unroll
           for (int hf = 0; hf < 2; ++hf) O[mb][hf] = T::mfma16x16x32(pa, bd[s][hf], O[mb][hf]);
         }
@@ -653,7 +673,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         for (int hf = 0; hf < 2; ++hf) S[kb][hf] *= eC;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          const u32x4 ka = kt_op(LK, kb >> 1, kb & 1, s, lane);
+          const u32x4 ka = kt_op(bKT[kb >> 1], kb & 1, s);
 #pragma unroll
           for (int hf = 0; hf < 2; ++hf) S[kb][hf] = T::mfma16x16x32(ka, bt[s][hf], S[kb][hf]);
         }
