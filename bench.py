@@ -309,10 +309,12 @@ def bench_gdn_prefill(steps, warmup, seed=0, H=16, HV=32):
     """Gated DeltaNet prefill (chunked WY form on MFMA) over cfg3's sequence
     lengths (16 sequences, Lq ~ U[256, 2048]): one 4-wave workgroup per
     (sequence, value head) walks its 64-token chunks.  Reported: tokens/s and
-    the MFMA rate of the chunk products -- per chunk and value head K K^T,
-    Q K^T, P D (64x64x128 each), K S^T, Q S^T (64x128x128), Tu V + Tw Y
-    (2 x 64x128x64) and the state update (128x128x64): 11 x 64x64x128
-    multiply-adds, counted over padded chunks."""
+    the rate of the chunked form's nominal product work -- per chunk and
+    value head K K^T, Q K^T, P D (64x64x128 each), K S^T, Q S^T
+    (64x128x128), the update from V and Y (2 x 64x128x64) and the state
+    update (128x128x64): 11 x 64x64x128 multiply-adds, counted over padded
+    chunks (the kernel skips the blocks above the diagonal and solves for the
+    update blockwise, so it executes less)."""
     import torch
     from nano_qwen_amd import kernels
     from oracle.inputs import make_prefill_case

@@ -19,23 +19,24 @@
 //   O = diag(exp(G)) Q S^T + P D
 //   S <- exp(G_C) S + (diag(exp(G_C - G)) D)^T K
 // which unrolls the per-token recurrence of nq_gdn_decode exactly in exact
-// arithmetic.  (W = T diag(beta exp(G)) K of the reference is never formed:
-// W S^T = (T diag(..)) (K S^T).)
+// arithmetic.  (W = T diag(beta exp(G)) K and U = T diag(beta) V of the
+// reference are never formed.)
 //
 // One 4-wave workgroup per (sequence, value head) walks the sequence's
-// chunks; two fit on a CU (70 KiB of LDS, at most 256 VGPRs a wave).  Wave w
+// chunks; two fit on a CU (72 KiB of LDS, at most 256 VGPRs a wave).  Wave w
 // owns value columns 32 w .. +31 of the state S^T [K][V], all 128 key rows of
 // them, as float32 MFMA accumulators for the whole sequence: every
 // state-dependent product of the chunk (Y = K S^T, Q S^T, the update
 // solve, O += P D and the state update) is the wave's own, with no state
 // copy through LDS and no barrier.  Only the chunk's shared inputs go
-// through LDS: unit keys, scaled unit queries, V, the gates, A and P.
+// through LDS: q and k as they are (their norms become per-token factors of
+// the products' epilogues), V, the gates, A and P.
 //
-// The update D = T (diag(beta) V + Tw' Y) is formed as the solution of
+// The update D = Tu V + Tw Y is formed as the solution of
 // (I + A) D = Z, Z = diag(beta) (V - diag(exp(G)) Y), by substitution over
 // the four 16-token blocks of the chunk: D_j = T_jj (Z_j - sum_{m<j} A_jm D_m),
 // with the inverses T_jj of the 16x16 diagonal blocks formed in float32 on
-// the VALU (forward substitution, one lane per column) and the products on
+// the VALU (forward substitution, one lane per block and column) and the products on
 // v_mfma_f32_16x16x16, whose accumulator rows are the next product's
 // B-operand rows.  The other products run on v_mfma_f32_16x16x32 with
 // 16-bit operands and float32 accumulation, as the reference's kernels do.
