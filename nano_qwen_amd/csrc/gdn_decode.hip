@@ -66,31 +66,74 @@ __device__ inline float elem(const uint8_t *p, int i) {
 
 __device__ inline float softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
 
+// Cross-lane steps within a half-wave without the LDS crossbar: the value of
+// the partner lane at step M, which differs from this lane in bit M (and,
+// for M = 8 and 4, in the bits below it): l ^ 16 by a permlane swap, l ^ 15
+// and l ^ 7 by DPP row_mirror and row_half_mirror, l ^ 2 and l ^ 1 by DPP
+// quad permutes.  The five partners' XOR masks are independent, so a
+// butterfly over them covers all 32 lanes once.
+template <int CTRL>
+__device__ inline float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+template <int M>
+__device__ inline float partner(float v, int lane) {
+  if constexpr (M == 16) {
+    // the swap returns {row 2r's value, row 2r + 1's value} of each row pair
+    const auto r = __builtin_amdgcn_permlane16_swap(f2u(v), f2u(v), false, false);
+    return u2f((lane & 16) ? r[0] : r[1]);
+  } else if constexpr (M == 8) {
+    return dpp_mov<0x140>(v);  // row_mirror
+  } else if constexpr (M == 4) {
+    return dpp_mov<0x141>(v);  // row_half_mirror
+  } else if constexpr (M == 2) {
+    return dpp_mov<0x4e>(v);  // quad_perm [2, 3, 0, 1]
+  } else {
+    return dpp_mov<0xb1>(v);  // quad_perm [1, 0, 3, 2]
+  }
+}
+// Sum over the 32 lanes of a half-wave; every lane gets it.
+__device__ inline float hsum32(float v, int lane) {
+  v += partner<16>(v, lane);
+  v += partner<8>(v, lane);
+  v += partner<4>(v, lane);
+  v += partner<2>(v, lane);
+  return v + partner<1>(v, lane);
+}
+
 // Sum of p[i] over the 32 lanes of a half-wave, for N values i per lane
-// (N = 8 or 16): a reduce-scatter over lane bits 4, 3, ... (N/2 + N/4 + ... + 1
-// exchanges) leaves value i = (l >> (5 - log2 N)) & (N - 1) in lane l, and
-// exchanges over the remaining low bits complete the sum in those lanes.
-template <int N>
-__device__ inline float reduce_rows(float (&p)[N], int lane) {
+// (N = 4, 8 or 16): a reduce-scatter over lane bits 4, 3, ... (N/2 + N/4 + ...
+// + 1 exchanges) leaves value i = (l >> (5 - log2 N)) & (N - 1) in lane l
+// (each step keeps the half selected by the lane's bit M and adds the
+// partner's other half), and the remaining steps complete the sum in those
+// lanes.
+template <int M, int C, int N>
+__device__ inline void scatter_step(float (&p)[N], int lane) {
+  if constexpr (C >= 2) {
+    const bool hi = (lane & M) != 0;
 #pragma unroll
-  for (int m = 16, c = N; c >= 2; m >>= 1, c >>= 1) {
-    const bool hi = (lane & m) != 0;
-#pragma unroll
-    for (int j = 0; j < c / 2; ++j) {
+    for (int j = 0; j < C / 2; ++j) {
       // Both elements are first fixed in registers: otherwise the compiler
       // turns the selects into an indexed read of p, a compare-and-select
       // chain over the whole array.
-      float lo = p[j], up = p[j + c / 2];
+      float lo = p[j], up = p[j + C / 2];
       asm volatile("" : "+v"(lo), "+v"(up));
       const float keep = hi ? up : lo;
       const float send = hi ? lo : up;
-      p[j] = keep + __shfl_xor(send, m, 64);
+      p[j] = keep + partner<M>(send, lane);
     }
+    scatter_step<M / 2, C / 2, N>(p, lane);
   }
-  float r = p[0];
-#pragma unroll
-  for (int m = 16 / N; m >= 1; m >>= 1) r += __shfl_xor(r, m, 64);
+}
+template <int M>
+__device__ inline float finish_sum(float r, int lane) {
+  if constexpr (M >= 1) return finish_sum<M / 2>(r + partner<M>(r, lane), lane);
   return r;
+}
+template <int N>
+__device__ inline float reduce_rows(float (&p)[N], int lane) {
+  scatter_step<16, N, N>(p, lane);
+  return finish_sum<16 / N>(p[0], lane);
 }
 
 // A wave owns 2 * NL state rows (NL loads per lane); NL = 4: more, smaller
@@ -134,11 +177,8 @@ __device__ inline void gdn_token(f32x4 (&s)[NL], const TokIn &in, float neg_a, f
   f32x4 qc = unpack4<T>(in.q), kc = unpack4<T>(in.k);
   float sq = qc[0] * qc[0] + qc[1] * qc[1] + qc[2] * qc[2] + qc[3] * qc[3];
   float sk = kc[0] * kc[0] + kc[1] * kc[1] + kc[2] * kc[2] + kc[3] * kc[3];
-#pragma unroll
-  for (int off = 16; off >= 1; off >>= 1) {
-    sq += __shfl_xor(sq, off, 64);
-    sk += __shfl_xor(sk, off, 64);
-  }
+  sq = hsum32(sq, lane);
+  sk = hsum32(sk, lane);
   qc *= scale / sqrtf(sq + eps);
   kc *= 1.0f / sqrtf(sk + eps);
   const float decay = expf(neg_a * softplus(T::to_float(static_cast<uint16_t>(in.ga)) + dt_bias));
