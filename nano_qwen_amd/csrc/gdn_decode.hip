@@ -27,8 +27,8 @@
 // fully coalesced.  Each wave normalizes q and k itself from its lanes' 4
 // columns (a 32-lane reduction).  A row's dot products (S k, S q) are spread
 // over the 32 lanes of a half-wave and summed by a reduce-scatter
-// (reduce_rows); the per-row update factor goes back to the lanes through
-// LDS.
+// (reduce_rows, DPP and permlane swaps); the per-row update factors go back
+// to the lanes by lane reads.
 #include "nq_device.hpp"
 
 namespace nq {
@@ -171,7 +171,7 @@ __device__ inline f32x4 unpack4(const u32x2 &w) {
 // s), writing the token's output for those rows.  neg_a = -exp(A_log[hv]).
 template <class T, int NL>
 __device__ inline void gdn_token(f32x4 (&s)[NL], const TokIn &in, float neg_a, float dt_bias, float eps,
-                                 float scale, int lane, float *urow, int my_row, bool writer, uint16_t *orow) {
+                                 float scale, int lane, int my_row, bool writer, uint16_t *orow) {
   // q and k: this lane's 4 columns, l2-normalized over the 32 lanes that
   // cover all 128 columns; q also carries the scale.
   f32x4 qc = unpack4<T>(in.q), kc = unpack4<T>(in.k);
@@ -191,11 +191,14 @@ __device__ inline void gdn_token(f32x4 (&s)[NL], const TokIn &in, float neg_a, f
     p[i] = s[i][0] * kc[0] + s[i][1] * kc[1] + s[i][2] * kc[2] + s[i][3] * kc[3];
   }
   const float u = beta * (T::to_float(static_cast<uint16_t>(in.v)) - reduce_rows(p, lane));
-  if (writer) urow[my_row] = u;  // one wave: LDS accesses stay in order
-  // S += u k^T, then o = S q.
+  // S += u k^T, then o = S q.  Row 2 i + h's factor is held by every lane of
+  // its group (h, i) (lane bits 5 and kSh ..): read from lane 32 h + (i << kSh).
+  constexpr int kSh = kShOf<NL>;
 #pragma unroll
   for (int i = 0; i < NL; ++i) {
-    const float ui = urow[2 * i + (lane >> 5)];
+    const float u0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, u), i << kSh));
+    const float u1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, u), 32 + (i << kSh)));
+    const float ui = (lane >> 5) ? u1 : u0;
     s[i] += ui * kc;
     p[i] = s[i][0] * qc[0] + s[i][1] * qc[1] + s[i][2] * qc[2] + s[i][3] * qc[3];
   }
@@ -226,9 +229,8 @@ __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(const GdnArgs a) {
   for (int i = 0; i < NL; ++i)
     s[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(sp + 2 * i * kDim));
   const TokIn in = load_tok<T>(a, bi, h, hv, kRowsW * w + my_row, c0);
-  __shared__ float urow[kRowsW];
   uint16_t *orow = reinterpret_cast<uint16_t *>(a.out + bi * a.o_rs + hv * kDim * 2) + kRowsW * w;
-  gdn_token<T, NL>(s, in, -expf(a.A_log[hv]), a.dt_bias[hv], a.eps, a.scale, lane, urow, my_row, writer, orow);
+  gdn_token<T, NL>(s, in, -expf(a.A_log[hv]), a.dt_bias[hv], a.eps, a.scale, lane, my_row, writer, orow);
 #pragma unroll
   for (int i = 0; i < NL; ++i) __builtin_nontemporal_store(s[i], reinterpret_cast<f32x4 *>(sp + 2 * i * kDim));
 }
