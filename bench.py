@@ -286,7 +286,9 @@ def bench_gdn(steps, warmup, seed=0, B=64, H=16, HV=32):
     """Gated DeltaNet decode step for a batch of B sequences (Qwen3.5-style
     linear-attention heads: H key heads, HV value heads, K = V = 128, float32
     state pool).  HBM-bound: each (sequence, value head) state is read and
-    written once."""
+    written once.  The steps rotate over 8 disjoint batches of slots of a
+    1 GiB pool, so no step finds the states of an earlier one in the 256 MB
+    last-level cache (a model's other layers would evict them)."""
     import torch
     from nano_qwen_amd import kernels
 
@@ -295,10 +297,12 @@ def bench_gdn(steps, warmup, seed=0, B=64, H=16, HV=32):
     q, k = r(B, H, 128).bfloat16(), r(B, H, 128).bfloat16()
     v, a, b = r(B, HV, 128).bfloat16(), r(B, HV).bfloat16(), r(B, HV).bfloat16()
     A_log, dt = r(HV) * 0.5, r(HV) * 0.5
-    state = r(2 * B, HV, 128, 128) * 0.05
-    idx = [torch.randperm(2 * B, device="cuda", generator=g)[:B].to(torch.int32) for _ in range(2)]
+    R = 8
+    state = r(R * B, HV, 128, 128) * 0.05
+    perm = torch.randperm(R * B, device="cuda", generator=g).to(torch.int32)
+    idx = [perm[j * B:(j + 1) * B] for j in range(R)]
     out = torch.empty(B, HV, 128, dtype=torch.bfloat16, device="cuda")
-    ms = _events_time(lambda i: kernels.gdn_decode(q, k, v, a, b, A_log, dt, state, idx[i % 2], out=out),
+    ms = _events_time(lambda i: kernels.gdn_decode(q, k, v, a, b, A_log, dt, state, idx[i % R], out=out),
                       steps, max(warmup, 50))
     nb = 2 * B * HV * 128 * 128 * 4 + (2 * B * H * 128 + 2 * B * HV * 128 + 2 * B * HV) * 2 + B * 4
     return dict(ms_per_step=ms, gbs=nb / (ms * 1e-3) / 1e9, hbm_frac=nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
