@@ -422,6 +422,9 @@ int nq_gdn_decode(const void *q, int64_t q_row_stride, const void *k, int64_t k_
  * float32 accumulation, as the reference's kernels do; the state stays
  * float32 between chunks.  Types as for nq_gdn_decode; q, k, v, out and
  * their row strides 16-byte aligned; cu_seqlens int32 [num_seqs + 1].
+ * out is also the kernel's scratch: the first 16 bytes of each (token, value
+ * head) row hold that token's gate values until its output is written, so
+ * out must not overlap q, k, v, a or b.
  */
 int nq_gdn_prefill(const void *q, int64_t q_row_stride, const void *k, int64_t k_row_stride,
                    const void *v, int64_t v_row_stride, const void *a, int64_t a_row_stride,

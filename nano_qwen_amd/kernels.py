@@ -442,6 +442,16 @@ def gdn_decode(query, key, value, a, b, A_log, dt_bias, state, state_indices, ou
     return out
 
 
+def _overlaps(x, y):
+    """Whether the memory spans of two tensors intersect."""
+    def span(t):
+        lo = t.data_ptr()
+        n = sum((d - 1) * st for d, st in zip(t.shape, t.stride())) + 1 if t.numel() else 0
+        return lo, lo + n * t.element_size()
+    (a0, a1), (b0, b1) = span(x), span(y)
+    return a0 < b1 and b0 < a1
+
+
 def gdn_prefill(query, key, value, a, b, A_log, dt_bias, cu_seqlens, state, state_indices,
                 initial_state_from_slot=False, out=None):
     """Gated DeltaNet prefill for packed sequences; final states go to the pool.
@@ -470,6 +480,11 @@ def gdn_prefill(query, key, value, a, b, A_log, dt_bias, cu_seqlens, state, stat
         raise RuntimeError("gdn_prefill: cu_seqlens [N+1] and state_indices [N] must be int32")
     if out is None:
         out = torch.empty(T_, HV, V, dtype=query.dtype, device=query.device)
+    # the kernel keeps each token's gates in its output rows before writing
+    # the output there, so out may not share memory with an input
+    for t, what in ((query, "query"), (key, "key"), (value, "value"), (a2, "a"), (b2, "b")):
+        if _overlaps(out, t):
+            raise RuntimeError(f"gdn_prefill: out must not overlap {what}")
     rc = lib().nq_gdn_prefill(ptr(query), query.stride(0), ptr(key), key.stride(0), ptr(value), value.stride(0),
                               ptr(a2), a2.stride(0), ptr(b2), b2.stride(0), ptr(A_log.contiguous()),
                               ptr(dt_bias.contiguous()), ptr(cu_seqlens), n, ptr(state), ptr(state_indices),

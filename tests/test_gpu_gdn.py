@@ -386,6 +386,17 @@ def test_gdn_prefill_empty_sequences(cuda):
             assert torch.equal(state_dev[slot].cpu(), want)
 
 
+def test_gdn_prefill_rejects_out_over_inputs(cuda):
+    """The output rows double as the kernel's gate scratch, so an out that
+    shares memory with an input is refused before the launch."""
+    c = _prefill_inputs([70, 5], 2, 4, seed=21, slots=4)
+    d = {k: v.to(cuda) for k, v in c.items()}
+    idx = torch.tensor([0, 1], dtype=torch.int32, device=cuda)
+    with pytest.raises(RuntimeError, match="must not overlap value"):
+        kernels.gdn_prefill(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt"], d["cu"], d["state"], idx,
+                            out=d["v"])
+
+
 @pytest.mark.parametrize("nseq", [63, 64, 65, 90])
 def test_gdn_prefill_batch_orders(cuda, nseq):
     """Batches of up to 64 sequences run longest first (the kernel ranks them
