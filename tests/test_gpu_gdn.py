@@ -421,3 +421,49 @@ def test_gdn_prefill_batch_orders(cuda, nseq):
     live = idx.tolist()
     _prefill_close(out.double().cpu().numpy(), ref.cpu().numpy(), state_dev.double().cpu().numpy()[live],
                    ref_state.cpu().numpy()[live])
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_gdn_prefill_random_sweep(cuda, seed):
+    """Random shapes against the float64 chunked form on the device: key heads
+    1-16 with 1, 2 or 4 value heads each (the XCD-paired head order is taken
+    when the value heads are a multiple of 8 per group, and not otherwise),
+    1-6 sequences of 1-400 tokens (chunk multiples among them), zero or pooled
+    initial states, bf16 or f16, and q, k, v as strided views of one fused
+    projection row in half the cases."""
+    rng = np.random.default_rng(1000 + seed)
+    G = int(rng.choice([1, 2, 4]))
+    H = int(rng.choice([1, 2, 4, 8, 16]))
+    HV = H * G
+    nseq = int(rng.integers(1, 7))
+    lens = [int(x) for x in rng.integers(1, 401, nseq)]
+    if nseq > 1:
+        lens[0] = 64 * int(rng.integers(1, 5))
+    dtype = torch.bfloat16 if seed % 2 == 0 else torch.float16
+    from_slot = bool(seed % 3)
+    fused = seed % 4 >= 2
+    c = _prefill_inputs(lens, H, HV, seed=2000 + seed, slots=nseq + 2, dtype=dtype)
+    d = {k: v.to(cuda) for k, v in c.items()}
+    if fused:  # q | k | v of one projection row, as the layer slices them
+        T = int(c["cu"][-1])
+        row = torch.empty(T, (2 * H + HV) * 128, dtype=dtype, device=cuda)
+        q = row[:, :H * 128].view(T, H, 128)
+        k = row[:, H * 128:2 * H * 128].view(T, H, 128)
+        v = row[:, 2 * H * 128:].view(T, HV, 128)
+        q.copy_(d["q"]), k.copy_(d["k"]), v.copy_(d["v"])
+        d["q"], d["k"], d["v"] = q, k, v
+    idx = torch.randperm(nseq + 2, generator=torch.Generator().manual_seed(seed))[:nseq].to(torch.int32)
+    print(f"[gdn] sweep {seed}: H={H} HV={HV} lens={lens} {dtype} from_slot={from_slot} fused={fused}", flush=True)
+    state_dev = d["state"].clone()
+    out = kernels.gdn_prefill(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt"], d["cu"], state_dev,
+                              idx.to(cuda), initial_state_from_slot=from_slot)
+    ref_state = d["state"].double().clone()
+    ref = gdn.gdn_prefill_chunked(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt"], c["cu"], ref_state,
+                                  idx, from_slot=from_slot)
+    torch.cuda.synchronize()
+    live = idx.tolist()
+    _prefill_close(out.double().cpu().numpy(), ref.cpu().numpy(), state_dev.double().cpu().numpy()[live],
+                   ref_state.cpu().numpy()[live])
+    untouched = [sl for sl in range(nseq + 2) if sl not in live]
+    for sl in untouched:  # slots no sequence names keep their contents
+        assert torch.equal(state_dev[sl], d["state"][sl])
