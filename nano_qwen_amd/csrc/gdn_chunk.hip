@@ -497,21 +497,29 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       const int b = g, c = m;
       const uint32_t base = LBD + 4 * 256 * b;
       float x[16];
-      // row by row (the reads of later rows may be issued early); two partial
-      // sums per row shorten the dependent chain
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        f32x4 av[4];
+      // row by row, each row's reads issued three rows ahead (the scheduling
+      // barrier keeps them there); two partial sums per row shorten the
+      // dependent chain
+      constexpr int kAhead = 3;
+      f32x4 av[16][4];
+      auto read_row = [&](int i) {
 #pragma unroll
         for (int jc = 0; jc < 4; ++jc)
-          if (4 * jc < i) av[jc] = ldf4(base + 4 * (16 * i + 4 * jc));
+          if (4 * jc < i) av[i][jc] = ldf4(base + 4 * (16 * i + 4 * jc));
+      };
+#pragma unroll
+      for (int i = 1; i <= kAhead; ++i) read_row(i);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (i + kAhead < 16) read_row(i + kAhead);
+        __builtin_amdgcn_sched_barrier(0);
         float acc0 = i == c ? 1.f : 0.f, acc1 = 0.f;
 #pragma unroll
         for (int j = 0; j < i; ++j) {
           if (j & 1)
-            acc1 -= av[j >> 2][j & 3] * x[j];
+            acc1 -= av[i][j >> 2][j & 3] * x[j];
           else
-            acc0 -= av[j >> 2][j & 3] * x[j];
+            acc0 -= av[i][j >> 2][j & 3] * x[j];
         }
         x[i] = i < c ? 0.f : acc0 + acc1;
       }
@@ -543,19 +551,32 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) Y[mb][hf] = O[mb][hf] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Rolling operand pipeline: block mb's K and Q operands of k-step s + 1
+    // are read as soon as its products of k-step s are issued, so each read
+    // has twelve products to land in; the scheduling barriers keep the
+    // compiler from moving the reads down to their uses.
+    u32x4 kr[4], qr[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      kr[mb] = lds_load_b128<0>(bK[0] + 16 * 256 * mb);
+      qr[mb] = lds_load_b128<0>(bQ[0] + 16 * 256 * mb);
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       // the state packed once for both products
       const u32x4 sb[2] = {pack8<T>(S[2 * s][0], S[2 * s + 1][0]), pack8<T>(S[2 * s][1], S[2 * s + 1][1])};
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
-        const u32x4 kr = lds_load_b128<0>(bK[s] + 16 * 256 * mb);
-        const u32x4 qr = lds_load_b128<0>(bQ[s] + 16 * 256 * mb);
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
-          Y[mb][hf] = T::mfma16x16x32(kr, sb[hf], Y[mb][hf]);
-          O[mb][hf] = T::mfma16x16x32(qr, sb[hf], O[mb][hf]);
+          Y[mb][hf] = T::mfma16x16x32(kr[mb], sb[hf], Y[mb][hf]);
+          O[mb][hf] = T::mfma16x16x32(qr[mb], sb[hf], O[mb][hf]);
         }
+        if (s < 3) {
+          kr[mb] = lds_load_b128<0>(bK[s + 1] + 16 * 256 * mb);
+          qr[mb] = lds_load_b128<0>(bQ[s + 1] + 16 * 256 * mb);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     wait_vmcnt<0>();  // this wave's V and gate copies (nothing else is in flight here)
@@ -571,14 +592,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         Bt[mb] = ldf4(LB + 4 * (16 * mb + 4 * g));
         Et[mb] = ldf4(LEG + 4 * (16 * mb + 4 * g)) * ldf4(LRK + 4 * (16 * mb + 4 * g));  // Y's rows: raw keys
       }
-      // V rows 16 mb + 4 g .. +3 at column 32 w + 16 hf + m, by transposing reads
+      // V rows 16 mb + 4 g .. +3 at column 32 w + 16 hf + m, by transposing
+      // reads, all issued together (the scheduling barrier keeps the compiler
+      // from spreading them out to their uses, one round trip each)
+      u32x2 vw[4][2];
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) vw[mb][hf] = lds_load_tr16<0>(bV[hf] + 16 * 256 * mb);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
-          const uint32_t va = bV[hf] + 16 * 256 * mb;
-          const u32x2 vw = lds_load_tr16<0>(va);
-          const f32x4 vf = unpack2x2<T>(vw[0], vw[1]);
+          const f32x4 vf = unpack2x2<T>(vw[mb][hf][0], vw[mb][hf][1]);
 #pragma unroll
           for (int r = 0; r < 4; ++r) Y[mb][hf][r] = Bt[mb][r] * (vf[r] - Et[mb][r] * Y[mb][hf][r]);
         }
