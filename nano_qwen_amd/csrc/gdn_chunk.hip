@@ -541,6 +541,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       pair_job(3, 2);
       diag_p_job(3);
     }
+    // This wave's V and gate copies (issued with the chunk's inputs; nothing
+    // else is in flight here) complete before this barrier, so that Z, after
+    // the products below (which write no LDS), reads every wave's V rows
+    // without a barrier of its own.
+    wait_vmcnt<0>();
     lds_sync();
 
     // Y = K S^T, O = Q S^T by 16-row blocks mb and column halves hf (row
@@ -579,9 +584,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    wait_vmcnt<0>();  // this wave's V and gate copies (nothing else is in flight here)
-    lds_sync();
-
     // ---- Z = diag(beta) (V - diag(exp(G)) Y) for rows 16 mb + 4 g + r,
     // then D by substitution over the blocks, per half of the columns.
     f32x4 D[4][2];
