@@ -240,6 +240,21 @@ __device__ inline u32x2 lds_load_tr16(uint32_t addr) {
   auto *p = reinterpret_cast<__attribute__((address_space(3))) s16x4 *>(static_cast<uintptr_t>(addr));
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(p + OFF / 8));
 }
+template <int OFF>
+__device__ inline u32x2 lds_load_b64(uint32_t addr) {
+  static_assert(OFF % 8 == 0 && OFF >= 0 && OFF < 65536, "ds offset");
+  const auto *p = reinterpret_cast<const __attribute__((address_space(3))) u32x2 *>(static_cast<uintptr_t>(addr));
+  return p[OFF / 8];
+}
+// Transposing 8-bit read: within each group of 16 lanes, lane 2 rho + p
+// addresses 8 bytes (piece p of row rho, rho < 8), and lane i receives byte
+// i % 8 of the pieces of lanes i / 8, 2 + i / 8, ..., 14 + i / 8 -- column i
+// of the group's 16-column block over its 8 rows (checked on gfx950).
+__device__ inline u32x2 lds_load_tr8(uint32_t addr) {
+  typedef int i32x2 __attribute__((ext_vector_type(2)));
+  auto *p = reinterpret_cast<__attribute__((address_space(3))) i32x2 *>(static_cast<uintptr_t>(addr));
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(p));
+}
 // s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
 template <int N>
 __device__ inline void wait_vmcnt() {

@@ -15,7 +15,9 @@
 //    blocks), resident on every CU and pulling work items from per-XCD
 //    queues; K/V tiles of 32 keys are copied HBM -> LDS by the LDS DMA into
 //    a ring (no VGPRs), the QK products of tile j+1 overlap the softmax of
-//    tile j.  fp8 codes are widened to 16 bits in the ring, in place.
+//    tile j.  fp8 K/V stay codes in the ring: the operand reads take 8
+//    codes per lane (ds_read_b64, ds_read_b64_tr_b8) and widen them in
+//    registers.
 //  * GQA sharing in LDS: the waves of a workgroup are query heads of the SAME
 //    kv head, so every K/V tile staged in LDS serves all of them.
 //  * A tile never crosses a cache block (block_size % 32 == 0), so one buffer
@@ -78,6 +80,18 @@ struct PrefillArgs {
 // the LDS throughput (2-way conflicts) otherwise.
 __device__ inline int swz_k(int row) { return row & 15; }
 __device__ inline int swz_v(int row) { return ((row & 7) << 1) | ((row >> 3) & 1); }
+// fp8 code tiles (rows of D bytes): 8-byte piece c of key row r is stored at
+// piece c ^ 2 swz8(r), i.e. 16-byte unit u at u ^ swz8(r).  Conflict-free
+// (64 banks, 32 lanes a pass) for the K operand reads (rows m and m + 16 x
+// pieces 4 kk + g) and for the V^T reads, whose 16-lane groups g address
+// rows 4 g .. +3 and 16 + 4 g .. +3 (the key order of the P operand).  Row
+// bit 4 enters only through b = bit 3 ^ bit 4, so row m + 16's pieces are
+// row m's with bit 2 (D = 128) or bit 3 (D = 256) of the piece flipped.
+template <int D>
+__device__ inline int swz8(int row) {
+  const int b = ((row >> 3) ^ (row >> 4)) & 1;
+  return D == 128 ? (((row >> 1) & 3) | (b << 2)) : ((row & 7) | (b << 3));
+}
 
 // Groups u = s * n_y + y (kv-head slot y of sequence s) -- the work items
 // that read the same K/V -- are pinned to XCD u % 8 (the hardware places
@@ -330,13 +344,11 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   constexpr int SRC_ROWB = FP8 ? D : 2 * D;  // bytes of one key of one kv head in the cache
   constexpr int COPS = CR * SRC_ROWB / 1024;  // 1 KiB loads per K (or V) per wave and entry
   constexpr int LPR = SRC_ROWB / 16;          // lanes per row in a copy (16 bytes each)
-  // fp8: a wave's copies land in the upper half of its own rows of the slot
-  // (CR rows of 16-bit keys), which it widens in place before the barrier
-  // that publishes the tile.
+  // fp8: a tile's codes are packed rows of D bytes at the start of the K (V)
+  // half of the slot, swizzled by swz8.
   static_assert(S::D == D, "launch shape built for this head_dim");
   static_assert(COPS >= 1 && CR * SRC_ROWB == 1024 * COPS, "a wave copies whole 1 KiB pieces");
   static_assert(!FP8 || COPS == 1, "fp8: one 1 KiB copy of codes per K (or V) per wave");
-  static_assert(!FP8 || kSlots == 4, "fp8: ring slot of a stream entry by mask");
   constexpr int QOPS = QS * DT::NKK;        // Q loads per wave and item
   constexpr int SOPS = QS * (DT::NJ / 2);   // output stores per wave and item
   // Stores that write nothing, after the Q loads: the compiler counts them
@@ -444,13 +456,14 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   int bad_seen = 0, plain_end = 0;
   // This wave's rows of a tile and its 16-byte pieces (the kv head's offset
   // is in the source address).
-  // fp8: rows as they are (widened and swizzled later), 16 codes per lane.
+  // fp8: 16 codes per lane, the 16-byte units of a row swizzled by swz8.
   uint32_t src_k[COPS], src_v[COPS];
 #pragma unroll
   for (int c = 0; c < COPS; ++c) {
     if constexpr (FP8) {
+      // lane l lands in unit l % LPR of row drow: it loads the unit swz8 puts there
       const int drow = CR * wave + lane / LPR;
-      src_k[c] = src_v[c] = static_cast<uint32_t>(drow * kv_rs + ((lane % LPR) << 4));
+      src_k[c] = src_v[c] = static_cast<uint32_t>(drow * kv_rs + (((lane % LPR) ^ swz8<D>(drow)) << 4));
     } else {
       const int drow = CR * wave + (64 / LPR) * c + lane / LPR;
       const uint32_t row_off = static_cast<uint32_t>(drow * kv_rs);
@@ -519,7 +532,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   };
   auto issue = [&]() {
     if (run_left == 0) next_run();
-    const uint32_t dst = st_dst + wave * (CR * DT::ROWB) + (FP8 ? CR * DT::ROWB / 2 : 0);
+    const uint32_t dst = st_dst + wave * (CR * SRC_ROWB);
     const u32x4 rk = rsrc_words(st_src, st_nrec);
     const u32x4 rv = rsrc_words(st_src + v_minus_k, st_nrec);
 #pragma unroll
@@ -532,42 +545,6 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
     --run_left;
     ++st_pos;
   };
-  // fp8: widens this wave's rows of stream entries cv_pos .. upto (whose
-  // copies are complete) to 16 bits, in place.  Lane l holds codes of dims
-  // 16(l % LPR) .. +15 of row CR * wave + l / LPR: the wave reads all its
-  // codes (the upper half of its rows) before it writes any row, and no
-  // other wave touches these rows before the next barrier.  The widening
-  // is exact (every e4m3 value is a bf16 and an f16 value); the scales are
-  // applied to the scores and the output instead.
-  int cv_pos = 0;
-  auto widen = [&](int upto) {
-    if constexpr (FP8) {
-      asm volatile("" ::: "memory");  // after the wait for the copies
-      const int r = CR * wave + lane / LPR, c0 = 2 * (lane % LPR);
-      for (; cv_pos <= upto; ++cv_pos) {
-        const uint32_t slot = lds0 + (cv_pos & (kSlots - 1)) * DT::SLOT_B;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const uint32_t tile = slot + t * DT::TILE_B;
-          const u32x4 raw = lds_load_b128<0>(tile + wave * (CR * DT::ROWB) + CR * DT::ROWB / 2 + 16 * lane);
-          // Every 16-lane store of the K rows covers 16 bank quads (rows 2i
-          // and 2i + 1 take opposite chunk parities under swz_k); the V rows'
-          // (swz_v agrees in bit 0 between them) conflict 2-way.  Choosing the
-          // first chunk per lane removes those conflicts but costs four
-          // selects per lane and tile, measured 1.7% slower on cfg3 over fp8.
-          const u32x4 lo = u32x4{T::template fp8x2<false>(raw[0]), T::template fp8x2<true>(raw[0]),
-                                 T::template fp8x2<false>(raw[1]), T::template fp8x2<true>(raw[1])};
-          const u32x4 hi = u32x4{T::template fp8x2<false>(raw[2]), T::template fp8x2<true>(raw[2]),
-                                 T::template fp8x2<false>(raw[3]), T::template fp8x2<true>(raw[3])};
-          const int sw = t ? swz_v(r) : swz_k(r);
-          const uint32_t row = tile + r * DT::ROWB;
-          lds_store_b128(row + ((c0 ^ sw) << 4), lo);
-          lds_store_b128(row + (((c0 + 1) ^ sw) << 4), hi);
-        }
-      }
-    }
-  };
-
   // ------------------------------------------------------- operand offsets
   // K^T operand kk: key row m (row m + 16 is +16 rows), dims 32kk + 8g.. ;
   // V^T operand j: rows r0 and r0 + 16 (both swizzles ignore row bit 4).
@@ -578,15 +555,34 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   // upper bits, so two registers per lane give every offset (one
   // xor-and-add per read).  unhoist() keeps the compiler from turning them
   // back into one loop-invariant register per operand.
-  const uint32_t kbase_l = m * DT::ROWB + ((g ^ (swz_k(m) & 3)) << 4);
-  uint32_t kx_l = (swz_k(m) & 12) << 4;
-  uint32_t vbase_l, vx_l;
-  {
+  // fp8 code tiles (rows of D bytes, swz8): K^T operand kk of rows m is piece
+  // 4kk + g at (((4kk + g) ^ 2 swz8(m)) << 3) = kbase_l + ((kk << 5) ^ kx_l),
+  // that of rows m + 16 operand kk ^ KF's offset + 16 rows; V^T operand j:
+  // lane (g, rho = (l & 15) >> 1, p = l & 1) addresses row R = 4g + rho
+  // (rho < 4) or 16 + 4g + rho - 4, piece 2j + p: vbase_l + ((j << 4) ^ vx_l).
+  uint32_t kbase_l, kx_l, vbase_l, vx_l;
+  if constexpr (FP8) {
+    const int s8 = 2 * swz8<D>(m);
+    kbase_l = m * D + ((g ^ (s8 & 3)) << 3);
+    kx_l = (s8 & ~3) << 3;
+    const int rho = (lane & 15) >> 1, vp = lane & 1;
+    const int r = rho < 4 ? 4 * g + rho : 12 + 4 * g + rho;
+    vbase_l = r * D + (vp << 3);
+    vx_l = (2 * swz8<D>(r)) << 3;
+  } else {
+    kbase_l = m * DT::ROWB + ((g ^ (swz_k(m) & 3)) << 4);
+    kx_l = (swz_k(m) & 12) << 4;
     const int vg = lane >> 4, vk = (lane >> 2) & 3, vq = lane & 3;
     const int r0 = 4 * vg + vk;
     vbase_l = r0 * DT::ROWB + (((vq >> 1) ^ (swz_v(r0) & 1)) << 4) + (vq & 1) * 8;
     vx_l = (swz_v(r0) & 14) << 4;
   }
+  // eight fp8 codes -> eight 16-bit values (exact: every e4m3 value is a bf16
+  // and an f16 value; the scales are applied to the scores and the output)
+  auto widen8 = [](const u32x2 &w) {
+    return u32x4{T::template fp8x2<false>(w[0]), T::template fp8x2<true>(w[0]), T::template fp8x2<false>(w[1]),
+                 T::template fp8x2<true>(w[1])};
+  };
   auto unhoist = [&]() { asm volatile("" : "+v"(kx_l), "+v"(vx_l)); };
 
   // Q operands of an item for this wave: always QOPS loads, so the count the
@@ -781,8 +777,6 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         wait_vmcnt<2 * COPS * (kAhead - 1) + EOPS>();
       else
         wait_vmcnt<2 * COPS * (kAhead - 1)>();
-      widen(p0);
-      wait_lgkmcnt0();
       raw_barrier();
       if constexpr (FP8) sl2 = a.scale_log2 * ld_const(a.k_scale + cur.kvh);
 
@@ -802,9 +796,15 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
       auto kread = [&](uint32_t kt, u32x4 (&kf)[DT::NKK][2]) {
 #pragma unroll
         for (int kk = 0; kk < DT::NKK; ++kk) {
-          const uint32_t ka = ((kk << 6) ^ kx_l) + (kt + kbase_l);
-          kf[kk][0] = lds_load_b128<0>(ka);
-          kf[kk][1] = lds_load_b128<16 * DT::ROWB>(ka);
+          if constexpr (FP8) {
+            constexpr int KF = D == 128 ? 2 : 4;  // swz8: rows m + 16 flip this bit of kk
+            kf[kk][0] = widen8(lds_load_b64<0>(((kk << 5) ^ kx_l) + (kt + kbase_l)));
+            kf[kk][1] = widen8(lds_load_b64<16 * D>((((kk ^ KF) << 5) ^ kx_l) + (kt + kbase_l)));
+          } else {
+            const uint32_t ka = ((kk << 6) ^ kx_l) + (kt + kbase_l);
+            kf[kk][0] = lds_load_b128<0>(ka);
+            kf[kk][1] = lds_load_b128<16 * DT::ROWB>(ka);
+          }
         }
       };
       auto qk = [&](const u32x4 (&kf)[DT::NKK][2], f32x4 (&sc)[QS][2]) {
@@ -916,11 +916,16 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
 #pragma unroll
           for (int j = 0; j < DT::NJ; ++j) o[qs][j] *= alpha[qs];
       };
-      // V^T operand j of the tile in ring slot `slot`: rows r0 and r0 + 16.
+      // V^T operand j of the tile in ring slot `slot`: rows r0 and r0 + 16
+      // (fp8: one transposing 8-bit read of rows R, widened in registers).
       auto vread = [&](uint32_t slot, int j) {
-        const uint32_t vt = ((j << 5) ^ vx_l) + (slot + DT::TILE_B + vbase_l);
-        const u32x2 lo = lds_load_tr16<0>(vt), hi = lds_load_tr16<16 * DT::ROWB>(vt);
-        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+        if constexpr (FP8) {
+          return widen8(lds_load_tr8(((j << 4) ^ vx_l) + (slot + DT::TILE_B + vbase_l)));
+        } else {
+          const uint32_t vt = ((j << 5) ^ vx_l) + (slot + DT::TILE_B + vbase_l);
+          const u32x2 lo = lds_load_tr16<0>(vt), hi = lds_load_tr16<16 * DT::ROWB>(vt);
+          return u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
       };
       // O^T += V^T P^T of the previous tile (operands vf, pb, read before the
       // barrier), with P of this tile (units of xt) formed in between -- one
@@ -1017,18 +1022,6 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs) pb[qs] = u32x4{pw[qs][0], pw[qs][1], pw[qs][2], pw[qs][3]};
         __builtin_amdgcn_sched_barrier(0);  // the two sections are scheduled apart
-        if constexpr (FP8) {
-          // Widen tile jt + 2 here, while the products run, rather than
-          // before the barrier that publishes it.  Its copies are complete
-          // once at most the entry issued above is younger (plus the item's
-          // start operations, if it preceded them).
-          if (jt + 1 < epi_tiles)
-            wait_vmcnt<2 * COPS + EOPS>();
-          else
-            wait_vmcnt<2 * COPS>();
-          widen(p0 + jt + 2);
-          __builtin_amdgcn_sched_barrier(0);
-        }
         f32x4 sn[QS][2];
         qk_v(kf, sn, slot, vf);
 #pragma unroll
@@ -1045,7 +1038,6 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
           wait_vmcnt<2 * COPS * (kAhead - 2) + EOPS>();
         else
           wait_vmcnt<2 * COPS * (kAhead - 2)>();
-        widen(p0 + jt + 1);
         wait_lgkmcnt0();  // and its reads of tiles jt - 1 and jt are done
         raw_barrier();    // tile jt + 1 complete; slot of tile jt - 1 free
       };
