@@ -583,6 +583,16 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
     return u32x4{T::template fp8x2<false>(w[0]), T::template fp8x2<true>(w[0]), T::template fp8x2<false>(w[1]),
                  T::template fp8x2<true>(w[1])};
   };
+  // K^T and V^T operands as read from LDS: 16-bit values, or fp8 codes that
+  // are widened just before their products (op), so that a read has a whole
+  // section of products to land in and the conversions sit between products.
+  using KV = std::conditional_t<FP8, u32x2, u32x4>;
+  auto op = [&](const KV &x) -> u32x4 {
+    if constexpr (FP8)
+      return widen8(x);
+    else
+      return x;
+  };
   auto unhoist = [&]() { asm volatile("" : "+v"(kx_l), "+v"(vx_l)); };
 
   // Q operands of an item for this wave: always QOPS loads, so the count the
@@ -793,13 +803,13 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
       const int32_t *bt_row = paged ? a.block_tables + static_cast<int64_t>(cur.s) * a.bt_stride : nullptr;
 
       // K^T operands of the tile in ring slot `kt` (its LDS address).
-      auto kread = [&](uint32_t kt, u32x4 (&kf)[DT::NKK][2]) {
+      auto kread = [&](uint32_t kt, KV (&kf)[DT::NKK][2]) {
 #pragma unroll
         for (int kk = 0; kk < DT::NKK; ++kk) {
           if constexpr (FP8) {
             constexpr int KF = D == 128 ? 2 : 4;  // swz8: rows m + 16 flip this bit of kk
-            kf[kk][0] = widen8(lds_load_b64<0>(((kk << 5) ^ kx_l) + (kt + kbase_l)));
-            kf[kk][1] = widen8(lds_load_b64<16 * D>((((kk ^ KF) << 5) ^ kx_l) + (kt + kbase_l)));
+            kf[kk][0] = lds_load_b64<0>(((kk << 5) ^ kx_l) + (kt + kbase_l));
+            kf[kk][1] = lds_load_b64<16 * D>((((kk ^ KF) << 5) ^ kx_l) + (kt + kbase_l));
           } else {
             const uint32_t ka = ((kk << 6) ^ kx_l) + (kt + kbase_l);
             kf[kk][0] = lds_load_b128<0>(ka);
@@ -807,7 +817,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
           }
         }
       };
-      auto qk = [&](const u32x4 (&kf)[DT::NKK][2], f32x4 (&sc)[QS][2]) {
+      auto qk = [&](const KV (&kf)[DT::NKK][2], f32x4 (&sc)[QS][2]) {
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
@@ -817,7 +827,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-            for (int qs = 0; qs < QS; ++qs) sc[qs][ks] = T::mfma16x16x32(kf[kk][ks], qf[qs][kk], sc[qs][ks]);
+            for (int qs = 0; qs < QS; ++qs) sc[qs][ks] = T::mfma16x16x32(op(kf[kk][ks]), qf[qs][kk], sc[qs][ks]);
       };
 
       float m_use[QS];  // running row max, scaled (log2) domain
@@ -837,7 +847,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         for (int kk = 0; kk < DT::NKK; ++kk) asm volatile("" : "+v"(qf[qs][kk]));
       f32x4 sc[QS][2];  // scores of the tile whose P is formed next
       if (wave_nkt > 0) {
-        u32x4 kf[DT::NKK][2];
+        KV kf[DT::NKK][2];
         unhoist();
         kread(lds0 + (p0 % kSlots) * DT::SLOT_B, kf);
         qk(kf, sc);
@@ -917,10 +927,10 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
           for (int j = 0; j < DT::NJ; ++j) o[qs][j] *= alpha[qs];
       };
       // V^T operand j of the tile in ring slot `slot`: rows r0 and r0 + 16
-      // (fp8: one transposing 8-bit read of rows R, widened in registers).
-      auto vread = [&](uint32_t slot, int j) {
+      // (fp8: one transposing 8-bit read of rows R, widened by op at its products).
+      auto vread = [&](uint32_t slot, int j) -> KV {
         if constexpr (FP8) {
-          return widen8(lds_load_tr8(((j << 4) ^ vx_l) + (slot + DT::TILE_B + vbase_l)));
+          return lds_load_tr8(((j << 4) ^ vx_l) + (slot + DT::TILE_B + vbase_l));
         } else {
           const uint32_t vt = ((j << 5) ^ vx_l) + (slot + DT::TILE_B + vbase_l);
           const u32x2 lo = lds_load_tr16<0>(vt), hi = lds_load_tr16<16 * DT::ROWB>(vt);
@@ -932,49 +942,64 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
       // unit, two exponentials and a pack, per two products -- so that the
       // exponentials run while the matrix core works.  The K reads of tile
       // jt + 1 (ring slot slot_next) are issued halfway.
-      auto pv_p = [&](const u32x4 (&vf)[DT::NJ], const u32x4 (&pb)[QS], uint32_t (&pw)[QS][4], uint32_t slot_next,
-                      u32x4 (&kf)[DT::NKK][2]) {
+      auto pv_p = [&](const KV (&vf)[DT::NJ], const u32x4 (&pb)[QS], uint32_t (&pw)[QS][4], uint32_t slot_next,
+                      KV (&kf)[DT::NKK][2]) {
         // 16 products either way: 8 query rows x 2 ... -- PPU products per unit
         // of P (2 with two 16-row blocks at head_dim 128, 4 with one at 256)
         constexpr int NP = DT::NJ * QS, U = 4 * QS, PPU = NP / U;
         static_assert(NP == 16 && (PPU == 2 || PPU == 4), "16 products, 2 or 4 per unit of P");
+        // fp8: conversions per unit -- the next unit's V^T operands, widened
+        // while this unit's products run (the first before the section)
+        constexpr int CV = FP8 ? 4 * DT::NJ / U : 0;
         kread(slot_next, kf);
+        u32x4 vw[DT::NJ];
+        constexpr int JPU = DT::NJ / U > 0 ? DT::NJ / U : 1;  // V^T operands per unit (rounded up)
+#pragma unroll
+        for (int j = 0; j < JPU; ++j) vw[j] = op(vf[j]);
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
           const int j = i / QS, qs = i % QS;
-          o[qs][j] = T::mfma16x16x32(vf[j], pb[qs], o[qs][j]);
+          if (FP8 && i % PPU == 0) {
+            const int u = i / PPU;
+#pragma unroll
+            for (int jn = (u + 1) * DT::NJ / U; jn < (u + 2) * DT::NJ / U && jn < DT::NJ; ++jn)
+              if (jn >= JPU) vw[jn] = op(vf[jn]);
+          }
+          o[qs][j] = T::mfma16x16x32(FP8 ? vw[j] : op(vf[j]), pb[qs], o[qs][j]);
           if (i % PPU == PPU - 1) {
             const int u = i / PPU;
             pw[u / 4][u % 4] = p_unit(u / 4, u % 4);
           }
         }
+        if (FP8) __builtin_amdgcn_sched_group_barrier(0x002, CV, 0);  // VALU: the first operands
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);  // transcendental
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);           // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 2 + CV / 2, 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);           // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);           // transcendental
           if (PPU == 4) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x002, 3 + CV - CV / 2, 0);  // VALU
           if (PPU == 4) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          if (u == U / 2 - 1) __builtin_amdgcn_sched_group_barrier(0x100, 2 * DT::NKK, 0);  // DS read (K)
+          // DS read (K): halfway; fp8 codes (half the registers) after the first unit
+          if (u == (FP8 ? 0 : U / 2 - 1)) __builtin_amdgcn_sched_group_barrier(0x100, 2 * DT::NKK, 0);
         }
       };
       auto p_only = [&](uint32_t (&pw)[QS][4]) {
 #pragma unroll
         for (int u = 0; u < 4 * QS; ++u) pw[u / 4][u % 4] = p_unit(u / 4, u % 4);
       };
-      auto pv_only = [&](const u32x4 (&vf)[DT::NJ], const u32x4 (&pb)[QS]) {
+      auto pv_only = [&](const KV (&vf)[DT::NJ], const u32x4 (&pb)[QS]) {
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
-          for (int j = 0; j < DT::NJ; ++j) o[qs][j] = T::mfma16x16x32(vf[j], pb[qs], o[qs][j]);
+          for (int j = 0; j < DT::NJ; ++j) o[qs][j] = T::mfma16x16x32(op(vf[j]), pb[qs], o[qs][j]);
       };
       // QK products of tile jt + 1 (kf) into sn, with the V^T operands of
       // tile jt (ring slot `slot`) read into vf in between: one transposing
       // read per product.  Products that share an accumulator are 2 QS
       // apart.
-      auto qk_v = [&](const u32x4 (&kf)[DT::NKK][2], f32x4 (&sn)[QS][2], uint32_t slot, u32x4 (&vf)[DT::NJ]) {
+      auto qk_v = [&](const KV (&kf)[DT::NKK][2], f32x4 (&sn)[QS][2], uint32_t slot, KV (&vf)[DT::NJ]) {
         // V^T operands per product: 1/2 at head_dim 128 (two 16-row
         // blocks), 1 at 256 (one); each operand is two transposing reads.
         // K operands die as V operands fill, so the two never hold all
@@ -986,16 +1011,26 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) sn[qs][ks] = f32x4{0, 0, 0, 0};
+        // fp8: each K operand widened while the previous one's products run
+        u32x4 kw[DT::NKK][2];
+        if constexpr (FP8) kw[0][0] = op(kf[0][0]);
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
           const int kk = i / (2 * QS), ks = (i / QS) % 2, qs = i % QS;
-          sn[qs][ks] = T::mfma16x16x32(kf[kk][ks], qf[qs][kk], sn[qs][ks]);
+          if (FP8 && qs == 0 && 2 * kk + ks + 1 < 2 * DT::NKK) {
+            const int n = 2 * kk + ks + 1;
+            kw[n >> 1][n & 1] = op(kf[n >> 1][n & 1]);
+          }
+          sn[qs][ks] = T::mfma16x16x32(FP8 ? kw[kk][ks] : op(kf[kk][ks]), qf[qs][kk], sn[qs][ks]);
           if (i % PPV == 0) vf[i / PPV] = vread(slot, i / PPV);
         }
+        constexpr int CK = FP8 ? 4 / QS : 0;  // conversions per product
+        if (FP8) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU: the first K operand
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // MFMA
           __builtin_amdgcn_sched_group_barrier(0x100, 2 / PPV, 0);  // DS read
+          if (FP8) __builtin_amdgcn_sched_group_barrier(0x002, CK, 0);  // VALU
         }
       };
       // One key tile jt (ring slot `slot`; tile jt + 1 in slot_next), after
@@ -1006,13 +1041,13 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
       // On return vf and pb hold tile jt's operands and sc tile jt + 1's
       // scores.
       auto tile = [&](auto pv_tag, auto mask_tag, int jt, uint32_t slot, uint32_t slot_next, bool blk_ok,
-                      u32x4 (&vf)[DT::NJ], u32x4 (&pb)[QS]) {
+                      KV (&vf)[DT::NJ], u32x4 (&pb)[QS]) {
         unhoist();
         if (pend) rescale(alpha);  // tile jt - 1's maxima, before its products join o
         pend = check(mask_tag, jt, blk_ok, alpha);
         issue();
         uint32_t pw[QS][4];
-        u32x4 kf[DT::NKK][2];  // tile jt + 1 (discarded past the last)
+        KV kf[DT::NKK][2];  // tile jt + 1 (discarded past the last)
         if constexpr (decltype(pv_tag)::value) {
           pv_p(vf, pb, pw, slot_next, kf);
         } else {
@@ -1055,7 +1090,8 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         slot = slot_next;
         slot_next = slot_next == lds_last ? lds0 : slot_next + DT::SLOT_B;
       };
-      u32x4 vf[DT::NJ], pb[QS];  // V^T operands and P of the tile whose products are pending
+      KV vf[DT::NJ];  // V^T operands and P of the tile whose products are pending
+      u32x4 pb[QS];
       int jt = 0;
       plain_end = bad_seen ? 0 : n_plain;
       if (n_kt > 0) {  // tile 0: no earlier tile's products
