@@ -990,10 +990,24 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         for (int u = 0; u < 4 * QS; ++u) pw[u / 4][u % 4] = p_unit(u / 4, u % 4);
       };
       auto pv_only = [&](const KV (&vf)[DT::NJ], const u32x4 (&pb)[QS]) {
+        if constexpr (FP8) {
+          // each operand widened just before its products, so that the
+          // widened operands are never all live at once
 #pragma unroll
-        for (int qs = 0; qs < QS; ++qs)
+          for (int j = 0; j < DT::NJ; ++j)
 #pragma unroll
-          for (int j = 0; j < DT::NJ; ++j) o[qs][j] = T::mfma16x16x32(op(vf[j]), pb[qs], o[qs][j]);
+            for (int qs = 0; qs < QS; ++qs) o[qs][j] = T::mfma16x16x32(op(vf[j]), pb[qs], o[qs][j]);
+#pragma unroll
+          for (int j = 0; j < DT::NJ; ++j) {
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+            __builtin_amdgcn_sched_group_barrier(0x008, QS, 0);  // MFMA
+          }
+        } else {
+#pragma unroll
+          for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+            for (int j = 0; j < DT::NJ; ++j) o[qs][j] = T::mfma16x16x32(vf[j], pb[qs], o[qs][j]);
+        }
       };
       // QK products of tile jt + 1 (kf) into sn, with the V^T operands of
       // tile jt (ring slot `slot`) read into vf in between: one transposing
