@@ -481,11 +481,14 @@ void paged_decode_kernel(const DecodeArgs a) {
   if (a.k_new && split == 0) DecodeWave<T, FP8, D>::store_new(a, b, kvh, lane);
   const int ctx = min(a.context_lens[b], a.max_tokens);
   const int t_begin = split * a.split_tokens;
-  if (ctx <= 0) {  // padded graph row: defined zeros, no KV reads
-    if (split == 0) decode_zero_row<D>(a, b, kvh, lane);
+  if (ctx <= 0 || t_begin >= ctx) {
+    if (ctx <= 0 && split == 0)  // padded graph row: defined zeros, no KV reads
+      decode_zero_row<D>(a, b, kvh, lane);
+    else if (split > 0)  // a split without tokens marks its partials empty for the merge
+      for (int h = lane; h < a.G; h += 64)
+        a.ws_lse[(static_cast<int64_t>(b) * a.Hq + kvh * a.G + h) * a.num_splits + split] = kNegInf;
     return;
   }
-  if (t_begin >= ctx) return;
   const int t_end = min(t_begin + a.split_tokens, ctx);
   decode_piece<T, FP8, D, DEPTH>(a, smem + wave * DecodeWave<T, FP8, D>::LDS_PER_WAVE_B, b, kvh, t_begin, t_end,
                                  ctx <= a.split_tokens,
@@ -584,27 +587,63 @@ int env_int(const char *name, int dflt) {
 }
 
 // Merge the per-split partials of every (sequence, head) with >1 split.
+// nsplit: the splits the main kernel's grid had.  Every split of a row past
+// the first either wrote its partials or marked them empty (lse -inf), so
+// the merge needs no context length: it loads all lse values and partials
+// at once (one round trip), and a row whose later splits are all empty (a
+// single split, or a padded row) was written by the main kernel.
+constexpr int kMergeUnroll = 16;
 template <class T, int D>
-__global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeArgs a, int batch) {
+__global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeArgs a, int batch, int nsplit) {
   constexpr int kPer = D / 4;  // threads per (b, head)
   const int pair = blockIdx.x * (256 / kPer) + threadIdx.x / kPer;
   const int d4 = threadIdx.x % kPer;
   if (pair >= batch * a.Hq) return;
   const int b = pair / a.Hq, head = pair % a.Hq;
-  const int ctx = min(a.context_lens[b], a.max_tokens);
-  if (ctx <= a.split_tokens) return;  // single split or empty: written by the main kernel
-  const int nact = min((ctx + a.split_tokens - 1) / a.split_tokens, a.num_splits);
   const int64_t base = static_cast<int64_t>(pair) * a.num_splits;
-  float M = kNegInf;
-  for (int s = 0; s < nact; ++s) M = fmaxf(M, a.ws_lse[base + s]);
-  float W = 0.f;
   f32x4 acc{0, 0, 0, 0};
-  if (M != kNegInf) {
-    for (int s = 0; s < nact; ++s) {
+  float W = 0.f;
+  if (nsplit <= kMergeUnroll) {
+    float l[kMergeUnroll];
+    f32x4 p[kMergeUnroll];
+#pragma unroll
+    for (int s = 0; s < kMergeUnroll; ++s)
+      if (s < nsplit) {
+        l[s] = a.ws_lse[base + s];
+        p[s] = *reinterpret_cast<const f32x4 *>(a.ws_o + (base + s) * D + 4 * d4);
+      }
+    bool multi = false;
+    float M = l[0];
+#pragma unroll
+    for (int s = 1; s < kMergeUnroll; ++s)
+      if (s < nsplit) {
+        multi |= l[s] != kNegInf;
+        M = fmaxf(M, l[s]);
+      }
+    if (!multi) return;  // written by the main kernel
+#pragma unroll
+    for (int s = 0; s < kMergeUnroll; ++s)
+      if (s < nsplit && l[s] != kNegInf) {  // an empty split's partials are not read: they may be stale
+        const float w = __builtin_amdgcn_exp2f(l[s] - M);
+        W += w;
+        acc += p[s] * w;
+      }
+  } else {
+    bool multi = false;
+    float M = a.ws_lse[base];
+    for (int s = 1; s < nsplit; ++s) {
       const float l = a.ws_lse[base + s];
-      const float w = (l == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(l - M);
-      W += w;
-      acc += *reinterpret_cast<const f32x4 *>(a.ws_o + (base + s) * D + 4 * d4) * w;
+      multi |= l != kNegInf;
+      M = fmaxf(M, l);
+    }
+    if (!multi) return;
+    for (int s = 0; s < nsplit; ++s) {
+      const float l = a.ws_lse[base + s];
+      if (l != kNegInf) {
+        const float w = __builtin_amdgcn_exp2f(l - M);
+        W += w;
+        acc += *reinterpret_cast<const f32x4 *>(a.ws_o + (base + s) * D + 4 * d4) * w;
+      }
     }
   }
   const float inv = W > 0.f ? 1.0f / W : 0.f;
@@ -825,7 +864,7 @@ struct DecodeLaunch {
     paged_decode_kernel<T, FP8, D, H, DP, WP><<<dim3(nsplit, groups, batch), 64 * H, lds, s>>>(a);
     const int rc = check_launch("paged_decode");
     if (rc != NQ_OK || a.num_splits <= 1) return rc;
-    decode_reduce_kernel<T, D><<<rgrid, 256, 0, s>>>(a, batch);
+    decode_reduce_kernel<T, D><<<rgrid, 256, 0, s>>>(a, batch, nsplit);
     return check_launch("paged_decode(reduce)");
   }
 };
