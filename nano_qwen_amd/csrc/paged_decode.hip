@@ -589,9 +589,10 @@ int env_int(const char *name, int dflt) {
 // Merge the per-split partials of every (sequence, head) with >1 split.
 // nsplit: the splits the main kernel's grid had.  Every split of a row past
 // the first either wrote its partials or marked them empty (lse -inf), so
-// the merge needs no context length: it loads all lse values and partials
-// at once (one round trip), and a row whose later splits are all empty (a
-// single split, or a padded row) was written by the main kernel.
+// the merge needs no context length: it loads the lse values and partials
+// of up to kMergeUnroll splits at once (one round trip per chunk of splits),
+// and a row whose later splits are all empty (a single split, or a padded
+// row) was written by the main kernel.
 constexpr int kMergeUnroll = 16;
 template <class T, int D>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeArgs a, int batch, int nsplit) {
@@ -601,51 +602,47 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeArgs a, 
   if (pair >= batch * a.Hq) return;
   const int b = pair / a.Hq, head = pair % a.Hq;
   const int64_t base = static_cast<int64_t>(pair) * a.num_splits;
+  // The splits in chunks of kMergeUnroll, each chunk's loads issued
+  // together; the running maximum rescales the earlier chunks' sums (with
+  // one chunk the weights are exp2(lse - max) directly).
   f32x4 acc{0, 0, 0, 0};
-  float W = 0.f;
-  if (nsplit <= kMergeUnroll) {
+  float W = 0.f, M = kNegInf;
+  bool multi = false;
+#pragma unroll 1
+  for (int c0 = 0; c0 < nsplit; c0 += kMergeUnroll) {
     float l[kMergeUnroll];
     f32x4 p[kMergeUnroll];
 #pragma unroll
-    for (int s = 0; s < kMergeUnroll; ++s)
-      if (s < nsplit) {
-        l[s] = a.ws_lse[base + s];
-        p[s] = *reinterpret_cast<const f32x4 *>(a.ws_o + (base + s) * D + 4 * d4);
+    for (int s = 0; s < kMergeUnroll; ++s) {
+      l[s] = kNegInf;
+      if (c0 + s < nsplit) {
+        l[s] = a.ws_lse[base + c0 + s];
+        p[s] = *reinterpret_cast<const f32x4 *>(a.ws_o + (base + c0 + s) * D + 4 * d4);
       }
-    bool multi = false;
-    float M = l[0];
+    }
+    float mc = kNegInf;
 #pragma unroll
-    for (int s = 1; s < kMergeUnroll; ++s)
-      if (s < nsplit) {
-        multi |= l[s] != kNegInf;
-        M = fmaxf(M, l[s]);
-      }
-    if (!multi) return;  // written by the main kernel
+    for (int s = 0; s < kMergeUnroll; ++s) {
+      if (c0 + s >= 1) multi |= l[s] != kNegInf;
+      mc = fmaxf(mc, l[s]);
+    }
+    if (mc == kNegInf) continue;  // every split of the chunk is empty
+    const float mn = fmaxf(M, mc);
+    if (M != kNegInf) {
+      const float r = __builtin_amdgcn_exp2f(M - mn);
+      W *= r;
+      acc *= r;
+    }
+    M = mn;
 #pragma unroll
     for (int s = 0; s < kMergeUnroll; ++s)
-      if (s < nsplit && l[s] != kNegInf) {  // an empty split's partials are not read: they may be stale
+      if (l[s] != kNegInf) {  // an empty split's partials are not read: they may be stale
         const float w = __builtin_amdgcn_exp2f(l[s] - M);
         W += w;
         acc += p[s] * w;
       }
-  } else {
-    bool multi = false;
-    float M = a.ws_lse[base];
-    for (int s = 1; s < nsplit; ++s) {
-      const float l = a.ws_lse[base + s];
-      multi |= l != kNegInf;
-      M = fmaxf(M, l);
-    }
-    if (!multi) return;
-    for (int s = 0; s < nsplit; ++s) {
-      const float l = a.ws_lse[base + s];
-      if (l != kNegInf) {
-        const float w = __builtin_amdgcn_exp2f(l - M);
-        W += w;
-        acc += *reinterpret_cast<const f32x4 *>(a.ws_o + (base + s) * D + 4 * d4) * w;
-      }
-    }
   }
+  if (!multi) return;  // a single split or a padded row: written by the main kernel
   const float inv = W > 0.f ? 1.0f / W : 0.f;
   acc *= inv;
   uint8_t *op = a.out + b * a.o_bs + head * a.o_hs + d4 * 8;
