@@ -64,10 +64,11 @@ def test_decode_group_sizes(cuda, G):
     check(case, range(3), TOL_BF16)
 
 
-def test_decode_edge_lengths(cuda):
-    # lengths at and around block / step / split boundaries, plus ctx = 1
-    case = make_decode_case("cfg2", seed=4, device=cuda, batch=10, ctx=(1, 1))
-    lens = torch.tensor([1, 2, 31, 32, 33, 255, 256, 257, 512, 513], dtype=torch.int32)
+def _with_lengths(case, lens, cuda):
+    """The case rebuilt over a fresh pool for the given context lengths, each
+    sequence's blocks a random permutation of the pool, table entries past
+    the context stale or out of range (never read)."""
+    n_seq = len(lens)
     bs = case["block_size"]
     pool = case["num_blocks"]
     need = int(sum((int(c) + bs - 1) // bs for c in lens))
@@ -75,7 +76,7 @@ def test_decode_edge_lengths(cuda):
     case["k_cache"] = torch.randn(len(perm), bs, 8, 128, device=cuda).mul_(0.5).to(torch.bfloat16)
     case["v_cache"] = torch.randn(len(perm), bs, 8, 128, device=cuda).mul_(0.5).to(torch.bfloat16)
     W = int(max((int(c) + bs - 1) // bs for c in lens)) + 2
-    bt = torch.full((10, W), -1, dtype=torch.int32)
+    bt = torch.full((n_seq, W), -1, dtype=torch.int32)
     off = 0
     for b, c in enumerate(lens.tolist()):
         n = (c + bs - 1) // bs
@@ -85,7 +86,24 @@ def test_decode_edge_lengths(cuda):
     slot = [int(bt[b, (c - 1) // bs]) * bs + (c - 1) % bs for b, c in enumerate(lens.tolist())]
     case.update(block_tables=bt.to(cuda), context_lens=lens.to(cuda),
                 slot_mapping=torch.tensor(slot, dtype=torch.int32, device=cuda), num_blocks=len(perm))
-    check(case, range(10), TOL_BF16)
+    return case
+
+
+def test_decode_edge_lengths(cuda):
+    # lengths at and around block / step / split boundaries, plus ctx = 1
+    case = make_decode_case("cfg2", seed=4, device=cuda, batch=10, ctx=(1, 1))
+    lens = torch.tensor([1, 2, 31, 32, 33, 255, 256, 257, 512, 513], dtype=torch.int32)
+    check(_with_lengths(case, lens, cuda), range(10), TOL_BF16)
+
+
+def test_decode_many_splits_merge(cuda, monkeypatch):
+    """128-token splits: rows of 1, 16, 17, 32, 33 and 40 splits, so the
+    merge takes its splits in one, two and three chunks of 16, and short rows
+    in the same launch have every later split empty."""
+    monkeypatch.setenv("NQ_DECODE_SPLIT_TOKENS", "128")
+    case = make_decode_case("cfg2", seed=8, device=cuda, batch=8, ctx=(1, 1))
+    lens = torch.tensor([1, 100, 2048, 2049, 4096, 4097, 5000, 300], dtype=torch.int32)
+    check(_with_lengths(case, lens, cuda), range(8), TOL_BF16)
 
 
 def test_decode_ctx1_returns_new_value(cuda):
