@@ -86,7 +86,8 @@ constexpr int kOffB = kOffP + kC * kC * 2;  // the four diagonal 16x16 blocks of
 constexpr int kGates = 4 * kC * 4;          // G, beta, exp(G), exp(G_C - G): 64 fp32 each
 constexpr int kOffG = kOffB + 4 * 256 * 4;  // two gate sets: this chunk's and the next one's
 constexpr int kOffR = kOffG + 2 * kGates;    // 1 / |q| x K^-1/2 and 1 / |k| of the chunk's tokens: 64 fp32 each
-constexpr int kLds = kOffR + 2 * kC * 4;
+constexpr int kOffW = kOffR + 2 * kC * 4;  // 256 bytes the L2 warm-up copies land in (never read)
+constexpr int kLds = kOffW + 256;
 static_assert(2 * kLds <= 160 * 1024, "two workgroups per CU");
 
 // Chunk swizzles of the 128-column tiles (16 chunks a row).
@@ -299,6 +300,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       const int chunk = (l & 15) ^ swz_c(row);
       dma16_opaque(LV + row0 * 256, rv, static_cast<uint32_t>(row * static_cast<int>(a.v_rs) + 16 * chunk));
     }
+  };
+  // The next chunk's q and k rows into L2 ahead of their fetch: one dword
+  // of each 128-byte line, by LDS DMA into a scratch area nobody reads
+  // (waves 0 and 1: q rows 0-31 and 32-63; waves 2 and 3: the same of k).
+  // Rows past the sequence fall outside the descriptor.
+  auto warm = [&](int c0, int tid) {
+    const int rows = min(kC, t1 - c0);
+    const uint8_t *src = wave < 2 ? a.q : a.k;
+    const int64_t rs = wave < 2 ? a.q_rs : a.k_rs;
+    const u32x4 rw = rsrc_words(src + static_cast<int64_t>(c0) * rs + h * kD * 2,
+                                static_cast<uint32_t>((rows - 1) * rs + kD * 2));
+    const int l = tid & 63, row = 32 * (wave & 1) + (l >> 1);
+    dma4_opaque(L + kOffW, rw, static_cast<uint32_t>(row * static_cast<int>(rs) + 128 * (l & 1)));
   };
   // The gates of the chunk at c0 into gate set `set`: wave w copies field w
   // of the 64 tokens (one dword per lane) from the output rows; tokens past
@@ -547,6 +561,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // without a barrier of its own.
     wait_vmcnt<0>();
     lds_sync();
+    // The next chunk's q and k lines into L2 now, about half a chunk before
+    // their fetch: from memory the fetch's latency outlasted the rest of the
+    // chunk.  Issued after the wait above, nothing waits for these copies
+    // before the fetch they precede is consumed.
+    if (c0 + kC < t1) warm(c0 + kC, tid);
 
     // Y = K S^T, O = Q S^T by 16-row blocks mb and column halves hf (row
     // 16 mb + 4 g + r, column 32 w + 16 hf + m); B operand of k-step s: the
