@@ -38,7 +38,13 @@ namespace {
 
 constexpr int kKeys = 32;    // keys per LDS tile
 constexpr float kRescale = 8.0f;  // log2 growth of a row max that forces a rescale
-constexpr int kMaxLevels = 1024;  // work-queue cost levels (key tiles per item, coarsened past it)
+constexpr int kMaxLevels = 1024;  // work-queue cost levels the LDS table holds
+// Cost levels of the queue: key tiles per item, coarsened to at most this
+// many.  Within a level the items of one sequence run together, so its K/V
+// stays in the XCD's L2 for all of them; 16 levels keep the queue longest
+// first in steps of 1/16 of the longest item.
+constexpr int kQueueLevels = 16;
+static_assert(kQueueLevels <= kMaxLevels, "levels fit the table");
 constexpr int kMaxSeqs = 1024;    // sequences whose bounds the persistent kernel keeps in LDS
 constexpr int kQueueWords = 16;   // prefill workspace: 8 per-XCD counters + 1 finish counter (+ pad)
 
@@ -209,9 +215,9 @@ __device__ __forceinline__ Item describe_by_tile(const PrefillArgs &a, int idx, 
 
 // Queue order by cost: the live items of XCD x's groups (see above), by
 // cost level (key tiles >> level_shift) from the highest down, then by
-// sequence, kv-head slot and query tile -- longest first, so the last items
-// a workgroup takes are short ones, and no index is spent on an item
-// without rows.  Each workgroup derives the order from the sequence bounds
+// sequence, kv-head slot and query tile from the last down -- longest
+// first, so the last items a workgroup takes are short ones, and no index
+// is spent on an item without rows.  Each workgroup derives the order from the sequence bounds
 // (kept in LDS) and a table of level starts it builds at launch.
 struct CostQueue {
   const int *lev;  // LDS: first queue index of each level
@@ -291,7 +297,7 @@ __device__ __forceinline__ Item describe_by_cost(const PrefillArgs &a, const Cos
       r -= __builtin_amdgcn_readlane(incl - cnt, ls);
       const int n_t = __builtin_amdgcn_readlane(nqt, ls);
       const int yi = small_div(r, n_t);
-      const int qt = __builtin_amdgcn_readlane(qlo, ls) + (r - yi * n_t);
+      const int qt = __builtin_amdgcn_readlane(qlo, ls) + n_t - 1 - (r - yi * n_t);
       const int y = first_slot(cq, s_it) + cq.ystep * yi;
       const int q0 = cq.cuq[s_it], k0 = cq.cuk[s_it];
       return fill_item(a, s_it, y, qt, cq.rows, q0, cq.cuq[s_it + 1] - q0, k0, cq.cuk[s_it + 1] - k0);
@@ -1196,7 +1202,7 @@ int launch_prefill_dma(PrefillArgs a, hipStream_t st) {
   a.by_cost = a.num_seqs <= kMaxSeqs && static_cast<int64_t>(a.num_seqs) * a.n_qtiles <= 65536;
   const int nkt_max = (a.max_seqlen_k + kKeys - 1) / kKeys;  // key tiles of the longest item
   a.level_shift = 0;
-  while ((nkt_max >> a.level_shift) + 1 > kMaxLevels) ++a.level_shift;
+  while ((nkt_max >> a.level_shift) + 1 > kQueueLevels) ++a.level_shift;
   a.n_levels = (nkt_max >> a.level_shift) + 1;
   // S::WG_PER_CU resident workgroups per CU, never more than there are
   // items; a multiple of 8 so every XCD gets the same count.

@@ -75,7 +75,7 @@ class Shape:
 SHAPES = {"a": Shape(8, 2, 5, 1), "c": Shape(4, 2, 4, 2)}
 
 
-MAX_LEVELS, MAX_SEQS = 1024, 1024  # kMaxLevels, kMaxSeqs
+QUEUE_LEVELS, MAX_SEQS = 16, 1024  # kQueueLevels, kMaxSeqs
 
 
 class Launch:
@@ -104,7 +104,7 @@ class Launch:
         self.by_cost = (n <= MAX_SEQS and n * self.n_x <= 65536) if by_cost is None else by_cost
         nkt_max = (max(lk) + KKEYS - 1) // KKEYS
         self.level_shift = 0
-        while (nkt_max >> self.level_shift) + 1 > MAX_LEVELS:
+        while (nkt_max >> self.level_shift) + 1 > QUEUE_LEVELS:
             self.level_shift += 1
         self.n_levels = (nkt_max >> self.level_shift) + 1
         self.ystep = 8 if self.pin else 1
@@ -185,7 +185,7 @@ class Launch:
             y0 = self.first_slot(x, s)
             cnt = n_t * self.n_slots(y0)
             if r < cnt:
-                return self.item(idx, s, y0 + self.ystep * (r // n_t), qlo + r % n_t)
+                return self.item(idx, s, y0 + self.ystep * (r // n_t), qlo + n_t - 1 - r % n_t)
             r -= cnt
         raise AssertionError("queue index past the live items")
 
@@ -502,14 +502,15 @@ def cost_order_cases():
     yield dict(lq=[5, 40, 300], lk=[0, 40, 900], hkv=1, hq=2)  # a sequence without keys; GQA 2
     yield dict(lq=[20, 300, 77], lk=[276, 300, 77], hkv=1, hq=16)  # 4 head quads
     yield dict(lq=[20, 300], lk=[20, 300], hkv=4, hq=4)  # MHA: 128-row items
-    yield dict(lq=[3000, 10], lk=[40000, 10], hkv=2, hq=8)  # levels coarsened past MAX_LEVELS
+    yield dict(lq=[3000, 10], lk=[40000, 10], hkv=2, hq=8)  # levels coarsened past QUEUE_LEVELS
 
 
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("shape", sorted(SHAPES))
 def test_cost_order_covers_live_items_longest_first(shape, causal):
     """The cost-ordered queue lists every live item of its XCD exactly once,
-    by non-increasing cost level, then sequence, kv-head slot and query tile;
+    by non-increasing cost level, then sequence, kv-head slot and query tile
+    from the last down;
     the arithmetic select matches a plain sort of the live items."""
     for c in cost_order_cases():
         L = Launch(SHAPES[shape], c["lq"], c["lk"], None, 0, 256, c["hkv"], c["hq"], causal=causal, cus=1,
@@ -518,9 +519,9 @@ def test_cost_order_covers_live_items_longest_first(shape, causal):
             _, cx, n = L.queue_of(x)
             got = [L.describe(i, x, cx, n) for i in range(n)]
             assert all(it is not None for it in got)
-            keys = [(-L.cost_level(it["qt"], L.lq[it["s"]], L.lk[it["s"]]), it["s"], it["y"], it["qt"]) for it in got]
-            live = sorted((-L.cost_level(qt, L.lq[s_], L.lk[s_]), s_, y, qt)
+            keys = [(-L.cost_level(it["qt"], L.lq[it["s"]], L.lk[it["s"]]), it["s"], it["y"], -it["qt"]) for it in got]
+            live = sorted((-L.cost_level(qt, L.lq[s_], L.lk[s_]), s_, y, -qt)
                           for s_ in range(len(L.lq)) for y in range(L.n_y) for qt in range(L.n_x)
                           if qt * L.rows < L.lq[s_] and (not L.pin or (s_ * L.n_y + y) % 8 == x))
             assert keys == live
-        assert L.level_shift == 0 or L.n_levels <= MAX_LEVELS
+        assert L.level_shift == 0 or L.n_levels <= QUEUE_LEVELS
