@@ -38,13 +38,11 @@ namespace {
 
 constexpr int kKeys = 32;    // keys per LDS tile
 constexpr float kRescale = 8.0f;  // log2 growth of a row max that forces a rescale
-constexpr int kMaxLevels = 1024;  // work-queue cost levels the LDS table holds
 // Cost levels of the queue: key tiles per item, coarsened to at most this
 // many.  Within a level the items of one sequence run together, so its K/V
 // stays in the XCD's L2 for all of them; 16 levels keep the queue longest
 // first in steps of 1/16 of the longest item.
 constexpr int kQueueLevels = 16;
-static_assert(kQueueLevels <= kMaxLevels, "levels fit the table");
 constexpr int kMaxSeqs = 1024;    // sequences whose bounds the persistent kernel keeps in LDS
 constexpr int kQueueWords = 16;   // prefill workspace: 8 per-XCD counters + 1 finish counter (+ pad)
 
@@ -69,7 +67,8 @@ struct PrefillArgs {
   const float *v_scale;
   uint32_t *queue;  // persistent kernel: kQueueWords work counters (zero between calls)
   int pin;          // work groups pinned to XCDs (>= 8 groups)
-  int by_cost;      // persistent kernel: queue in cost order over live items (num_seqs <= kMaxSeqs)
+  int by_cost;      // persistent kernel: 0 query-tile order; cost order over live items (num_seqs <= kMaxSeqs),
+                    // 1 each item derived when taken, 2 read from a list built at launch
   int level_shift;  // cost level of an item: its key tiles >> level_shift (< n_levels)
   int n_levels;
   const uint8_t *gate;  // null, or Qwen3.5's output gate [total_q, Hq, D] (type of out)
@@ -144,8 +143,14 @@ struct PShape {
   static constexpr int ITEM_ROWS = 16 * QS * NW;  // query rows x heads of one work item
   static constexpr int RING_BYTES = SLOTS * 2 * kKeys * 2 * D;
   // ring, queue item slots (4 words), queue size (4 words), cost-level
-  // starts, sequence bounds (cu_q, cu_k)
-  static constexpr int LDS_BYTES = RING_BYTES + 32 + 4 * kMaxLevels + 8 * (kMaxSeqs + 1);
+  // starts, sequence bounds (cu_q, cu_k), then the items of the queue listed
+  // at launch (one packed word each: sequence << 22 | kv-head slot << 14 |
+  // query tile) in what the CU's LDS has left, at most 4096
+  static constexpr int FIXED_BYTES = RING_BYTES + 32 + 4 * kQueueLevels + 8 * (kMaxSeqs + 1);
+  static constexpr int MAX_ITEMS = (160 * 1024 / WG_PER_CU - FIXED_BYTES) / 4 > 4096
+                                       ? 4096
+                                       : ((160 * 1024 / WG_PER_CU - FIXED_BYTES) / 4) & ~63;
+  static constexpr int LDS_BYTES = FIXED_BYTES + 4 * MAX_ITEMS;
   static_assert(WPE == 2, "two waves per SIMD");
   static_assert(WG_PER_CU * LDS_BYTES <= 160 * 1024, "LDS of the resident workgroups");
 };
@@ -223,6 +228,7 @@ struct CostQueue {
   const int *lev;  // LDS: first queue index of each level
   const int *cuq;  // LDS: cu_seqlens_q, cu_seqlens_k
   const int *cuk;
+  const uint32_t *tab;  // LDS: the queue's items in order (by_cost == 2)
   int x, n_y, rows, ystep;
   int rows_log2, ystep_log2;  // rows and ystep are powers of two
 };
@@ -307,6 +313,18 @@ __device__ __forceinline__ Item describe_by_cost(const PrefillArgs &a, const Cos
   return it;  // not reached for idx < n_items
 }
 
+// Item at queue index idx from the list built at launch (by_cost == 2):
+// one LDS read and the sequence bounds, instead of the search above.
+__device__ __forceinline__ Item describe_by_table(const PrefillArgs &a, const CostQueue &cq, int idx, int n_items) {
+  Item it{};
+  it.live = false;
+  if (idx >= n_items) return it;
+  const uint32_t e = __builtin_amdgcn_readfirstlane(cq.tab[idx]);
+  const int s = e >> 22, y = (e >> 14) & 255, qt = e & 16383;
+  const int q0 = cq.cuq[s], k0 = cq.cuk[s];
+  return fill_item(a, s, y, qt, cq.rows, q0, cq.cuq[s + 1] - q0, k0, cq.cuk[s + 1] - k0);
+}
+
 // Persistent prefill: S::WG_PER_CU workgroups per CU pull work items from
 // per-XCD queues.  The hardware dispatcher keeps only about half of the CUs
 // busy when one-per-CU workgroups of very different lengths are launched as
@@ -341,7 +359,7 @@ __device__ __forceinline__ Item describe_by_cost(const PrefillArgs &a, const Cos
 // waits count only younger stream entries -- except that a new item's first
 // kAhead tiles may precede the Q loads and the previous item's output stores
 // (a fixed count per wave), which the waits then add.
-template <class T, int D, class S, bool GATED, bool FP8>
+template <class T, int D, class S, bool GATED, bool FP8, bool TAB>
 __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   using DT = DTile<T, D>;
   constexpr int NW = S::NW, QS = S::QS, kSlots = S::SLOTS, kAhead = S::AHEAD;
@@ -371,8 +389,9 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   int *lds_item = reinterpret_cast<int *>(smem + S::RING_BYTES);  // fetched queue indices
   int *lds_n = lds_item + 4;                                      // queue size (cost order)
   int *lds_lev = lds_item + 8;                                    // level starts (cost order)
-  int *lds_cuq = lds_lev + kMaxLevels;
+  int *lds_cuq = lds_lev + kQueueLevels;
   int *lds_cuk = lds_cuq + kMaxSeqs + 1;
+  uint32_t *lds_tab = reinterpret_cast<uint32_t *>(lds_cuk + kMaxSeqs + 1);  // the queue's items
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -390,7 +409,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   const int cx = a.pin ? (U - x + 7) >> 3 : U;
   uint32_t *ctr = a.queue + x;
   const int item_rows = 16 * QS * (NW / a.G4);
-  const CostQueue cq{lds_lev,   lds_cuq, lds_cuk, x, n_y, item_rows, a.pin ? 8 : 1, 31 - __builtin_clz(item_rows),
+  const CostQueue cq{lds_lev, lds_cuq,   lds_cuk, lds_tab, x, n_y, item_rows, a.pin ? 8 : 1, 31 - __builtin_clz(item_rows),
                      a.pin ? 3 : 0};
   if (a.by_cost) {
     // Sequence bounds into LDS, then the live items of this queue counted
@@ -419,6 +438,49 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         carry += __builtin_amdgcn_readlane(incl, 63);
       }
       if (lane == 0) *lds_n = carry;
+    }
+    if constexpr (TAB) {
+      // The queue's items listed in order.  First the queue index of each
+      // (level, sequence)'s first item -- a level's sequences in order --
+      // kept in the ring, which no copy has written yet; then every live
+      // (sequence, query tile) writes its items (one per kv-head slot) at
+      // their places: sequence, slot, then query tile from the last down.
+      int *first = reinterpret_cast<int *>(smem);
+      __syncthreads();
+      for (int L = wave; L < a.n_levels; L += NW) {
+        const int lo_v = L << a.level_shift, hi_v = (L + 1) << a.level_shift;
+        int carry = lds_lev[L];
+        for (int base = 0; base < a.num_seqs; base += 64) {
+          const int s = base + lane;
+          int cnt = 0;
+          if (s < a.num_seqs) {
+            const int Lq = lds_cuq[s + 1] - lds_cuq[s], Lk = lds_cuk[s + 1] - lds_cuk[s];
+            const int nq = Lq > 0 ? (Lq + cq.rows - 1) >> cq.rows_log2 : 0;
+            const int qlo = first_tile_with(a, cq, lo_v, nq, Lk, Lk - Lq);
+            const int qhi = L == a.n_levels - 1 ? nq : first_tile_with(a, cq, hi_v, nq, Lk, Lk - Lq);
+            cnt = max(0, qhi - qlo) * n_slots(cq, first_slot(cq, s));
+          }
+          const int incl = wave_iscan(cnt);
+          if (s < a.num_seqs) first[L * a.num_seqs + s] = carry + incl - cnt;
+          carry += __builtin_amdgcn_readlane(incl, 63);
+        }
+      }
+      __syncthreads();
+      for (int i = threadIdx.x; i < a.num_seqs * n_x; i += blockDim.x) {
+        const int sq = i / n_x, qt = i - sq * n_x;
+        const int Lq = lds_cuq[sq + 1] - lds_cuq[sq], Lk = lds_cuk[sq + 1] - lds_cuk[sq];
+        const int y0 = first_slot(cq, sq), w = n_slots(cq, y0);
+        if (qt * cq.rows < Lq && w > 0) {
+          const int L = cost_level(a, cq, qt, Lq, Lk);
+          const int nq = (Lq + cq.rows - 1) >> cq.rows_log2;
+          const int qlo = first_tile_with(a, cq, L << a.level_shift, nq, Lk, Lk - Lq);
+          const int qhi = L == a.n_levels - 1 ? nq : first_tile_with(a, cq, (L + 1) << a.level_shift, nq, Lk, Lk - Lq);
+          int pos = first[L * a.num_seqs + sq] + (qhi - 1 - qt);
+          for (int yi = 0; yi < w; ++yi, pos += qhi - qlo)
+            lds_tab[pos] = (static_cast<uint32_t>(sq) << 22) | (static_cast<uint32_t>(y0 + cq.ystep * yi) << 14) | qt;
+        }
+      }
+      __syncthreads();  // the list is complete, and the ring free for the copies
     }
   }
 
@@ -743,12 +805,24 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
   __syncthreads();
   const int n_items = a.by_cost ? __builtin_amdgcn_readfirstlane(*lds_n) : cx * n_x;
   auto describe = [&](int idx) {
-    return a.by_cost ? describe_by_cost(a, cq, idx, n_items) : describe_by_tile<S>(a, idx, n_items, n_x, n_y, cx, x);
+    if constexpr (TAB) return describe_by_table(a, cq, idx, n_items);
+    else return a.by_cost ? describe_by_cost(a, cq, idx, n_items) : describe_by_tile<S>(a, idx, n_items, n_x, n_y, cx, x);
   };
   int idx_cur = __builtin_amdgcn_readfirstlane(lds_item[0]);
   int idx_nxt = __builtin_amdgcn_readfirstlane(lds_item[1]);
   Item cur = describe(idx_cur);
-  Item nxt = describe(idx_nxt);
+  // The next item: described one ahead and kept, or -- from the list, where
+  // describing is cheap -- described again where it is used, so its fields
+  // hold no registers through the tile loops.  Measured with the list:
+  // describing again is faster at head_dim 128 (cfg3_long -1%, fp8 K/V -0.4%,
+  // 96 fewer scalar spills), keeping the item at 256 (-3%).
+  constexpr bool kRedescribe = TAB && D == 128;
+  Item nxt{};
+  if constexpr (!kRedescribe) nxt = describe(idx_nxt);
+  auto next_item = [&]() -> Item {
+    if constexpr (kRedescribe) return describe(idx_nxt);
+    else return nxt;
+  };
   Item prev{};  // the item whose output is still in o / lsum
   prev.live = false;
   queue_copy(cur);
@@ -785,7 +859,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         if (nx_rem > 0) issue();
         p0 = nx_first;
       }
-      queue_copy(nxt);
+      queue_copy(next_item());
       while (st_pos < p0 + kAhead) issue();
       // Wait for tile 0 (younger: kAhead - 1 stream entries, plus the Q
       // loads and stores above if tile 0 preceded them).
@@ -1152,7 +1226,7 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
         pv_only(vf, pb);
       }
     } else {
-      queue_copy(nxt);
+      queue_copy(next_item());
     }
     // Next item: publish the fetched index (slot k + 2 of 4: a wave still
     // reading slot k + 1 cannot be overtaken, the write comes after the
@@ -1165,8 +1239,12 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
     raw_barrier();
     const int idx_new = __builtin_amdgcn_readfirstlane(lds_item[(k + 2) & 3]);
     prev = cur;
-    cur = nxt;
-    nxt = describe(idx_new);
+    if constexpr (kRedescribe) {
+      cur = describe(idx_nxt);
+    } else {
+      cur = nxt;
+      nxt = describe(idx_new);
+    }
     idx_cur = idx_nxt;
     idx_nxt = idx_new;
   }
@@ -1182,10 +1260,10 @@ __device__ __forceinline__ void prefill_persistent(const PrefillArgs &a) {
 
 // The body lives in a device function: its inline assembly uses register
 // constraints that only the device compilation accepts.
-template <class T, int D, class S, bool GATED, bool FP8>
+template <class T, int D, class S, bool GATED, bool FP8, bool TAB>
 __global__ __launch_bounds__(64 * S::NW) __attribute__((amdgpu_waves_per_eu(S::WPE)))
 void varlen_prefill_dma_kernel(const PrefillArgs a) {
-  prefill_persistent<T, D, S, GATED, FP8>(a);
+  prefill_persistent<T, D, S, GATED, FP8, TAB>(a);
 }
 
 template <class T, int D, class S, bool FP8>
@@ -1204,16 +1282,23 @@ int launch_prefill_dma(PrefillArgs a, hipStream_t st) {
   a.level_shift = 0;
   while ((nkt_max >> a.level_shift) + 1 > kQueueLevels) ++a.level_shift;
   a.n_levels = (nkt_max >> a.level_shift) + 1;
+  // The queue's items listed in LDS at launch when every queue fits the list
+  // (its groups x query tiles bound it), the (level, sequence) starts fit the
+  // ring and the packed words hold the fields.
+  const int64_t cx_max = U >= 8 ? (U + 7) / 8 : U;
+  if (a.by_cost && cx_max * a.n_qtiles <= S::MAX_ITEMS && static_cast<int64_t>(a.num_seqs) * a.n_levels * 4 <= S::RING_BYTES &&
+      U / a.num_seqs <= 256 && a.n_qtiles <= 16384)
+    a.by_cost = 2;
   // S::WG_PER_CU resident workgroups per CU, never more than there are
   // items; a multiple of 8 so every XCD gets the same count.
   int64_t grid = (static_cast<int64_t>(device_cus()) * S::WG_PER_CU + 7) / 8 * 8;
   if (grid > total) grid = total;  // work_grid() is a multiple of 8 when pinned
-  if (a.gate) {
-    varlen_prefill_dma_kernel<T, D, S, true, FP8><<<static_cast<int>(grid), 64 * S::NW, S::LDS_BYTES, st>>>(a);
-    return check_launch("varlen_prefill(gated)");
-  }
-  varlen_prefill_dma_kernel<T, D, S, false, FP8><<<static_cast<int>(grid), 64 * S::NW, S::LDS_BYTES, st>>>(a);
-  return check_launch("varlen_prefill");
+  auto *kern = a.gate ? (a.by_cost == 2 ? varlen_prefill_dma_kernel<T, D, S, true, FP8, true>
+                                        : varlen_prefill_dma_kernel<T, D, S, true, FP8, false>)
+                     : (a.by_cost == 2 ? varlen_prefill_dma_kernel<T, D, S, false, FP8, true>
+                                        : varlen_prefill_dma_kernel<T, D, S, false, FP8, false>);
+  kern<<<static_cast<int>(grid), 64 * S::NW, S::LDS_BYTES, st>>>(a);
+  return check_launch(a.gate ? "varlen_prefill(gated)" : "varlen_prefill");
 }
 
 template <class T, bool FP8, int D>

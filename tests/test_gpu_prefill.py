@@ -192,10 +192,24 @@ def test_prefill_queue_resets_between_calls(cuda):
 
 
 def test_prefill_many_sequences_cost_order(cuda):
-    """70 sequences: the persistent kernel's cost-ordered queue selects items
-    across two 64-sequence steps (and every lane row of the wave scan)."""
+    """70 sequences: the list of each queue's items, built at launch, spans
+    two 64-sequence steps of the wave scan (and every lane row of it)."""
     case = make_prefill_case("cfg3", seed=10, device=cuda, nseq=70, lq=(1, 160), prefix_blocks=(1, 1))
     check(case, range(70), TOL_BF16)
+
+
+@pytest.mark.parametrize("d", [128, 256])
+def test_prefill_cost_order_past_item_list(cuda, d):
+    """Queues whose bound (kv-head groups x query tiles) outgrows the item
+    list the kernel keeps in LDS (1984 items at head_dim 128: 300 sequences
+    of up to 300 rows bound each queue at 300 x 10; 4096 at 256: 1000 x 10 /
+    2) take the cost order derived item by item, across several 64-sequence
+    steps of its select."""
+    nseq = 300 if d == 128 else 1000
+    case = make_prefill_case("cfg3", seed=12, device=cuda, nseq=nseq, lq=(1, 300), prefix_blocks=(0, 1),
+                             **({} if d == 128 else dict(d=256, hq=16, hkv=4)))
+    assert max(case["lq"]) > 288  # 10 query tiles of 32 rows
+    check(case, range(0, nseq, 11 if d == 128 else 37), TOL_BF16)
 
 
 def test_prefill_query_tile_order_past_lds_bounds(cuda):

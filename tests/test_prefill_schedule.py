@@ -71,6 +71,16 @@ class Shape:
     def EOPS(self):
         return self.QOPS + self.SOPS + self.PAD
 
+    @property
+    def RING_BYTES(self):  # K and V tiles of 32 keys, 2 bytes x head_dim 128
+        return self.SLOTS * 2 * KKEYS * 2 * 128
+
+    @property
+    def MAX_ITEMS(self):  # queue items listed in what the CU's LDS has left (PShape::MAX_ITEMS)
+        fixed = self.RING_BYTES + 32 + 4 * QUEUE_LEVELS + 8 * (MAX_SEQS + 1)
+        free = (160 * 1024 // self.WG_PER_CU - fixed) // 4
+        return 4096 if free > 4096 else free & ~63
+
 
 SHAPES = {"a": Shape(8, 2, 5, 1), "c": Shape(4, 2, 4, 2)}
 
@@ -108,6 +118,10 @@ class Launch:
             self.level_shift += 1
         self.n_levels = (nkt_max >> self.level_shift) + 1
         self.ystep = 8 if self.pin else 1
+        cx_max = (self.U + 7) // 8 if self.pin else self.U
+        # launch_prefill_dma: each queue's items listed in LDS at launch (by_cost == 2)
+        self.use_table = bool(self.by_cost and cx_max * self.n_x <= S.MAX_ITEMS
+                              and n * self.n_levels * 4 <= S.RING_BYTES and self.n_y <= 256 and self.n_x <= 16384)
         self.lev = {}  # queue x -> level starts (what each workgroup builds in LDS)
         self.n_live = {}
         if self.by_cost:
@@ -162,6 +176,40 @@ class Launch:
         key_end = self.key_end(qt, Lq, Lk)
         return dict(idx=idx, s=s, y=y, qt=qt, kvh=y // self.quads, key_end=key_end,
                     n_kt=(key_end + KKEYS - 1) // KKEYS)
+
+    def table(self, x):
+        """The list of queue x's items the kernel builds in LDS at launch: the
+        first queue index of each (level, sequence), a level's sequences in
+        order, then each live (sequence, query tile) placing its items (one
+        per kv-head slot) by slot, then query tile from the last down."""
+        start, n = self.lev[x], len(self.lq)
+        first = {}
+        for L in range(self.n_levels):
+            carry = start[L]
+            for s in range(n):
+                Lq, Lk = self.lq[s], self.lk[s]
+                nq = (Lq + self.rows - 1) // self.rows if Lq > 0 else 0
+                qlo = self.first_tile_with(L << self.level_shift, nq, Lk, Lk - Lq)
+                qhi = nq if L == self.n_levels - 1 else self.first_tile_with((L + 1) << self.level_shift, nq, Lk, Lk - Lq)
+                first[L, s] = carry
+                carry += max(0, qhi - qlo) * self.n_slots(self.first_slot(x, s))
+        tab = [None] * self.n_live[x]
+        for s in range(n):
+            Lq, Lk = self.lq[s], self.lk[s]
+            y0 = self.first_slot(x, s)
+            w = self.n_slots(y0)
+            for qt in range(self.n_x):
+                if qt * self.rows < Lq and w > 0:
+                    L = self.cost_level(qt, Lq, Lk)
+                    nq = (Lq + self.rows - 1) // self.rows
+                    qlo = self.first_tile_with(L << self.level_shift, nq, Lk, Lk - Lq)
+                    qhi = nq if L == self.n_levels - 1 else self.first_tile_with((L + 1) << self.level_shift, nq,
+                                                                                   Lk, Lk - Lq)
+                    for yi in range(w):
+                        pos = first[L, s] + yi * (qhi - qlo) + (qhi - 1 - qt)
+                        assert tab[pos] is None, "two items at one place"
+                        tab[pos] = (s << 22) | ((y0 + self.ystep * yi) << 14) | qt
+        return tab
 
     def describe(self, idx, x, cx, n_items):
         """Item idx of queue x (describe_by_cost / describe_by_tile): None when not live."""
@@ -525,3 +573,32 @@ def test_cost_order_covers_live_items_longest_first(shape, causal):
                           if qt * L.rows < L.lq[s_] and (not L.pin or (s_ * L.n_y + y) % 8 == x))
             assert keys == live
         assert L.level_shift == 0 or L.n_levels <= QUEUE_LEVELS
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", sorted(SHAPES))
+def test_item_list_matches_cost_order(shape, causal):
+    """The list of each queue's items built at launch (describe_by_table)
+    holds, at every index, the item describe_by_cost derives there, each
+    field within its bits of the packed word."""
+    for c in cost_order_cases():
+        L = Launch(SHAPES[shape], c["lq"], c["lk"], None, 0, 256, c["hkv"], c["hq"], causal=causal, cus=1,
+                   by_cost=True)
+        for x in range(8 if L.pin else 1):
+            _, cx, n = L.queue_of(x)
+            tab = L.table(x)
+            assert len(tab) == n and all(e is not None for e in tab)
+            for i, e in enumerate(tab):
+                it = L.describe(i, x, cx, n)
+                assert (e >> 22, (e >> 14) & 255, e & 16383) == (it["s"], it["y"], it["qt"])
+
+
+def test_item_list_chosen_for_the_bench_shapes():
+    """launch_prefill_dma lists the items at launch for cfg3's and cfg3_long's
+    batches (every queue's bound fits the LDS left by the ring), and falls
+    back to deriving them when a queue could outgrow the list."""
+    S = SHAPES["c"]
+    c = make_prefill_case("cfg3", seed=0, device="cpu")
+    assert Launch(S, c["lq"], c["lk"], None, 0, 256, c["hkv"], c["hq"]).use_table
+    assert Launch(S, [8192] * 4, [8192] * 4, None, 0, 256, 8, 32).use_table
+    assert not Launch(S, [8192] * 64, [8192] * 64, None, 0, 256, 8, 32).use_table
