@@ -222,8 +222,10 @@ __device__ __forceinline__ Item describe_by_tile(const PrefillArgs &a, int idx, 
 // cost level (key tiles >> level_shift) from the highest down, then by
 // sequence, kv-head slot and query tile from the last down -- longest
 // first, so the last items a workgroup takes are short ones, and no index
-// is spent on an item without rows.  Each workgroup derives the order from the sequence bounds
-// (kept in LDS) and a table of level starts it builds at launch.
+// is spent on an item without rows.  Each workgroup builds, at launch, the
+// sequence bounds and a table of level starts in LDS and, when the queue's
+// whole item list fits, that list (describe_by_table); otherwise each item
+// is derived from the two when taken (describe_by_cost).
 struct CostQueue {
   const int *lev;  // LDS: first queue index of each level
   const int *cuq;  // LDS: cu_seqlens_q, cu_seqlens_k
