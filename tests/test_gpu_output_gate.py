@@ -93,13 +93,18 @@ def test_output_gate_f16_and_errors(cuda):
         kernels.output_gate(out.float(), gate.float())
 
 
-@pytest.mark.parametrize("kind", ["packed", "fp8"])
+@pytest.mark.parametrize("kind", ["packed", "fp8", "past_list"])
 def test_prefill_gated_other_paths(cuda, kind):
-    """Packed K/V (no block table) and paged fp8 K/V on the persistent
-    kernel's fused store: gated == gate(ungated)."""
+    """Packed K/V (no block table), paged fp8 K/V, and a batch whose queues
+    outgrow the item list the kernel keeps in LDS (items derived when taken)
+    on the persistent kernel's fused store: gated == gate(ungated)."""
     from oracle.inputs import make_prefill_case
     if kind == "packed":
         c = make_prefill_case("cfg3", seed=8, device="cuda", prefix_blocks=(0, 0), lq=(100, 700))
+        k, v, bt, ks, vs = c["k_new"], c["v_new"], None, None, None
+    elif kind == "past_list":
+        c = make_prefill_case("cfg3", seed=13, device="cuda", nseq=300, lq=(1, 300), prefix_blocks=(0, 0))
+        assert max(c["lq"]) > 288
         k, v, bt, ks, vs = c["k_new"], c["v_new"], None, None, None
     else:
         c = make_prefill_case("cfg3", seed=9, device="cuda", kv="fp8", lq=(100, 700))

@@ -198,18 +198,18 @@ def test_prefill_many_sequences_cost_order(cuda):
     check(case, range(70), TOL_BF16)
 
 
-@pytest.mark.parametrize("d", [128, 256])
-def test_prefill_cost_order_past_item_list(cuda, d):
+@pytest.mark.parametrize("kind", ["d128", "d256", "fp8"])
+def test_prefill_cost_order_past_item_list(cuda, kind):
     """Queues whose bound (kv-head groups x query tiles) outgrows the item
     list the kernel keeps in LDS (1984 items at head_dim 128: 300 sequences
     of up to 300 rows bound each queue at 300 x 10; 4096 at 256: 1000 x 10 /
-    2) take the cost order derived item by item, across several 64-sequence
-    steps of its select."""
-    nseq = 300 if d == 128 else 1000
-    case = make_prefill_case("cfg3", seed=12, device=cuda, nseq=nseq, lq=(1, 300), prefix_blocks=(0, 1),
-                             **({} if d == 128 else dict(d=256, hq=16, hkv=4)))
+    2) take the cost order derived item by item (the kernels built without
+    the list), across several 64-sequence steps of its select."""
+    nseq = 1000 if kind == "d256" else 300
+    extra = dict(d=256, hq=16, hkv=4) if kind == "d256" else dict(kv="fp8") if kind == "fp8" else {}
+    case = make_prefill_case("cfg3", seed=12, device=cuda, nseq=nseq, lq=(1, 300), prefix_blocks=(0, 1), **extra)
     assert max(case["lq"]) > 288  # 10 query tiles of 32 rows
-    check(case, range(0, nseq, 11 if d == 128 else 37), TOL_BF16)
+    check(case, range(0, nseq, 37 if kind == "d256" else 11), TOL_FP8 if kind == "fp8" else TOL_BF16)
 
 
 def test_prefill_query_tile_order_past_lds_bounds(cuda):
